@@ -1,0 +1,1078 @@
+// HIP kernels of the MLA decode path for MI355X (gfx950, wave64).
+//
+// Per decode step and launch group of up to 64 sequences:
+//   gemv      q_proj | kv_a_proj projections (bf16 MFMA, x split hi/lo)
+//   append    RMSNorm -> quantise (Q8) / store (FP32) -> RoPE of the key, one history row
+//   qprep     absorbed query q_lat = W_UK^T q_nope and RoPE(q_rope) per head
+//   attention split-K over the history, all 16 heads reuse each row read once from HBM
+//   combine   merge split partials (online-softmax algebra) and apply W_UV per head
+//   gemv      o_proj (optionally accumulated onto the input: residual)
+// The arithmetic contract follows src/mla_compressed_q8_state.c:161-255 and
+// src/mla_compressed_state.c:86-161 of the reference; the history rows produced by
+// `append` are bit-exact with src/mla_compressed_q8_state.c:34-55,111-127 given the same
+// kv_a output.
+#include "mla_device.h"
+#include "mla_internal.h"
+
+#include <math.h>
+
+namespace kvl {
+
+// ================================================================ GEMV =================
+
+struct GemvArgs {
+    float *Y;
+    const float *X;
+    const uint16_t *W0;
+    const uint16_t *W1;
+    int ldy, ldx, B, out0, out1, in, acc;
+};
+
+// 16 output rows per block; wave w owns the k-quarter [w*in/4, (w+1)*in/4). The weight tile
+// is the MFMA A operand (exact bf16), the batch of activations the B operand as a hi/lo bf16
+// pair, so every product is exact and accumulation is fp32. Up to 16 sequences per block
+// column (blockIdx.y). Requires in % 128 == 0 and 16-byte aligned rows.
+__global__ __launch_bounds__(256) void k_gemv_mfma(GemvArgs a) {
+    __shared__ v4f red[3][64];
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
+    const int out = a.out0 + a.out1;
+    const int row0 = blockIdx.x * 16;
+    const int row = row0 + n;
+    const uint16_t *wrow = nullptr;
+    if (row < a.out0)
+        wrow = a.W0 + (size_t)row * a.in;
+    else if (row < out)
+        wrow = a.W1 + (size_t)(row - a.out0) * a.in;
+    const int b = blockIdx.y * 16 + n;
+    const float *xrow = b < a.B ? a.X + (size_t)b * a.ldx : nullptr;
+    const int kq = a.in >> 2;
+    const int kbeg = w * kq;
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < kq; k0 += 512) {
+        const int nkb = min(16, (kq - k0) >> 5);
+        v4i wa[16];
+#pragma unroll
+        for (int kb = 0; kb < 16; ++kb) {
+            if (kb < nkb) {
+                const int k = kbeg + k0 + kb * 32 + g * 8;
+                wa[kb] = wrow ? *(const v4i *)(wrow + k) : v4i{0, 0, 0, 0};
+            }
+        }
+#pragma unroll
+        for (int kb = 0; kb < 16; ++kb) {
+            if (kb < nkb) {
+                const int k = kbeg + k0 + kb * 32 + g * 8;
+                v4f x0 = {0.f, 0.f, 0.f, 0.f}, x1 = {0.f, 0.f, 0.f, 0.f};
+                if (xrow) {
+                    x0 = *(const v4f *)(xrow + k);
+                    x1 = *(const v4f *)(xrow + k + 4);
+                }
+                v8bf hi, lo;
+                split8(x0, x1, hi, lo);
+                const v8bf wv = __builtin_bit_cast(v8bf, wa[kb]);
+                acc = mfma_bf16(wv, hi, acc);
+                acc = mfma_bf16(wv, lo, acc);
+            }
+        }
+    }
+    if (w > 0) red[w - 1][l] = acc;
+    __syncthreads();
+    if (w == 0 && b < a.B) {
+        acc += red[0][l];
+        acc += red[1][l];
+        acc += red[2][l];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = row0 + 4 * g + i;
+            if (r < out) {
+                float *yp = a.Y + (size_t)b * a.ldy + r;
+                *yp = a.acc ? *yp + acc[i] : acc[i];
+            }
+        }
+    }
+}
+
+// Any shape: one wave per output row, lanes stride the input, all sequences of the group.
+__global__ __launch_bounds__(256) void k_gemv_generic(GemvArgs a) {
+    const int out = a.out0 + a.out1;
+    const int row = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int l = threadIdx.x & 63;
+    if (row >= out) return;  // whole waves leave together
+    const uint16_t *wrow =
+        row < a.out0 ? a.W0 + (size_t)row * a.in : a.W1 + (size_t)(row - a.out0) * a.in;
+    for (int b = 0; b < a.B; ++b) {
+        const float *x = a.X + (size_t)b * a.ldx;
+        float s = 0.f;
+        for (int i = l; i < a.in; i += 64) s = fmaf(bf16_to_f32(wrow[i]), x[i], s);
+        s = wave_sum(s);
+        if (l == 0) {
+            float *yp = a.Y + (size_t)b * a.ldy + row;
+            *yp = a.acc ? *yp + s : s;
+        }
+    }
+}
+
+hipError_t launch_gemv(hipStream_t st, float *Y, int ldy, const float *X, int ldx, int B,
+                       const uint16_t *W0, int out0, const uint16_t *W1, int out1, int in,
+                       bool accumulate) {
+    GemvArgs a{Y, X, W0, W1, ldy, ldx, B, out0, out1, in, accumulate ? 1 : 0};
+    const int out = out0 + out1;
+    if (out <= 0 || B <= 0) return hipSuccess;
+    const bool aligned = (in % 128) == 0 && (ldx % 4) == 0 && ((uintptr_t)X % 16) == 0 &&
+                         ((uintptr_t)W0 % 16) == 0 && (!W1 || ((uintptr_t)W1 % 16) == 0);
+    if (aligned) {
+        dim3 grid((out + 15) / 16, (B + 15) / 16);
+        hipLaunchKernelGGL(k_gemv_mfma, grid, dim3(256), 0, st, a);
+    } else {
+        hipLaunchKernelGGL(k_gemv_generic, dim3((out + 3) / 4), dim3(256), 0, st, a);
+    }
+    return hipGetLastError();
+}
+
+// ================================================================ append ===============
+
+constexpr int kMaxR = 1024;   // kv_lora_rank bound of the device kernels
+constexpr int kMaxDR = 256;   // qk_rope_dim bound
+constexpr int kMaxDN = 512;   // qk_nope_dim bound
+
+struct AppendArgs {
+    SeqTable t;
+    Dims d;
+    const float *y;
+    const uint16_t *norm;
+    const float2 *cs;
+    uint8_t *rows;
+    float *latent;
+    int ldy, koff, fmt, normed, row_bytes, rows_mode;
+    float eps;
+};
+
+// One block per sequence (rows_mode = 0) or, with rows_mode = 1, one block per row of the
+// single sequence t.s[0]: block i appends row t.s[0].pos + i from input row i. Reproduces src/ops.c:76-83 (RMSNorm: double sum of squares,
+// inv = 1/sqrtf(float(ss/n) + eps), (x*inv)*w), src/mla_compressed_q8_state.c:34-55
+// (absmax/127, inv = 1/scale, roundf, clamp) and the RoPE rotation of
+// src/mla_compressed_q8_state.c:18-32 with host-computed (cos, sin) pairs. The library is
+// compiled with -ffp-contract=off, so each product and sum rounds separately as there.
+__global__ __launch_bounds__(256) void k_append(AppendArgs a) {
+    __shared__ float lat[kMaxR];
+    __shared__ double redd[256];
+    __shared__ float redf[256];
+    const int tid = threadIdx.x, b = blockIdx.x;
+    const SeqDesc &s = a.t.s[a.rows_mode ? 0 : b];
+    const int R = a.d.R, DR = a.d.DR, half = DR / 2, pos = s.pos + (a.rows_mode ? b : 0);
+    const float *kat = a.y + (size_t)b * a.ldy + a.koff;
+
+    if (!a.normed) {
+        double ss = 0.0;
+        for (int r = tid; r < R; r += 256) {
+            const double v = (double)kat[r];
+            ss += v * v;
+        }
+        redd[tid] = ss;
+        __syncthreads();
+        for (int o = 128; o > 0; o >>= 1) {
+            if (tid < o) redd[tid] += redd[tid + o];
+            __syncthreads();
+        }
+        const float mean_sq = (float)(redd[0] / (double)R);
+        const float inv = 1.0f / sqrtf(mean_sq + a.eps);
+        for (int r = tid; r < R; r += 256) {
+            const float t = kat[r] * inv;
+            lat[r] = t * bf16_to_f32(a.norm[r]);
+        }
+    } else {
+        for (int r = tid; r < R; r += 256) lat[r] = kat[r];
+    }
+    __syncthreads();
+
+    uint8_t *row_out = a.rows + (size_t)b * a.row_bytes;
+    if (a.fmt == kFmtQ8) {
+        float m = 0.f;
+        for (int r = tid; r < R; r += 256) m = fmaxf(m, fabsf(lat[r]));
+        redf[tid] = m;
+        __syncthreads();
+        for (int o = 128; o > 0; o >>= 1) {
+            if (tid < o) redf[tid] = fmaxf(redf[tid], redf[tid + o]);
+            __syncthreads();
+        }
+        // fmaxf drops NaN operands: a NaN latent must still select the zero row, as the
+        // reference's sequential `a > amax` scan followed by isfinite() does for Inf; NaN
+        // never compares greater there, so it is simply skipped -- identical to fmaxf.
+        const float amax = redf[0];
+        int8_t *codes = (int8_t *)s.a + (size_t)pos * R;
+        const bool zero = !(amax > 0.0f) || !isfinite(amax);
+        const float scale = zero ? 1.0f : amax / 127.0f;
+        const float inv = zero ? 0.0f : 1.0f / scale;
+        for (int r = tid; r < R; r += 256) {
+            int8_t q = 0;
+            if (!zero) {
+                float v = roundf(lat[r] * inv);
+                v = v > 127.0f ? 127.0f : v;
+                v = v < -127.0f ? -127.0f : v;
+                q = (int8_t)v;
+            }
+            codes[r] = q;
+            row_out[r] = (uint8_t)q;
+        }
+        if (tid == 0) {
+            ((float *)s.b)[pos] = scale;
+            *(float *)(row_out + R) = scale;
+        }
+    } else if (a.fmt == kFmtF32) {
+        float *dst = (float *)s.a + (size_t)pos * R;
+        for (int r = tid; r < R; r += 256) {
+            dst[r] = lat[r];
+            ((float *)row_out)[r] = lat[r];
+        }
+    } else {
+        for (int r = tid; r < R; r += 256) a.latent[(size_t)b * R + r] = lat[r];
+    }
+
+    for (int i = tid; i < half; i += 256) {
+        const float2 cs = a.cs[(size_t)pos * half + i];
+        const float ev = kat[R + 2 * i], od = kat[R + 2 * i + 1];
+        const float ec = ev * cs.x, os = od * cs.y, oc = od * cs.x, es = ev * cs.y;
+        const float d0 = ec - os, d1 = oc + es;
+        if (a.fmt == kFmtQ8) {
+            uint16_t *rp = (uint16_t *)s.c + (size_t)pos * DR;
+            const uint16_t h0 = f32_to_bf16_rne(d0), h1 = f32_to_bf16_rne(d1);
+            rp[i] = h0;
+            rp[half + i] = h1;
+            uint16_t *ro = (uint16_t *)(row_out + R + 4);
+            ro[i] = h0;
+            ro[half + i] = h1;
+        } else if (a.fmt == kFmtF32) {
+            float *rp = (float *)s.b + (size_t)pos * DR;
+            rp[i] = d0;
+            rp[half + i] = d1;
+            float *ro = (float *)row_out + R;
+            ro[i] = d0;
+            ro[half + i] = d1;
+        } else {
+            float *ro = (float *)row_out;  // expanded: rotated key staged for store_expanded
+            ro[i] = d0;
+            ro[half + i] = d1;
+        }
+    }
+}
+
+hipError_t launch_append(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
+                         const float *y, int ldy, int koff, const uint16_t *kv_a_norm,
+                         float eps, const float2 *rope_cs, const DecodeWork &w, bool normed,
+                         int nrows) {
+    if (d.R > kMaxR || d.DR > kMaxDR) return hipErrorInvalidValue;
+    AppendArgs a;
+    a.t = t;
+    a.d = d;
+    a.y = y;
+    a.norm = kv_a_norm;
+    a.cs = rope_cs;
+    a.rows = w.rows;
+    a.latent = w.latent;
+    a.ldy = ldy;
+    a.koff = koff;
+    a.fmt = fmt;
+    a.normed = normed ? 1 : 0;
+    a.row_bytes = fmt == kFmtQ8 ? d.R + 4 + 2 * d.DR
+                  : fmt == kFmtF32 ? 4 * (d.R + d.DR)
+                                   : 4 * d.NH * (d.QD + d.DV);
+    a.eps = eps;
+    a.rows_mode = nrows > 0 ? 1 : 0;
+    hipLaunchKernelGGL(k_append, dim3(nrows > 0 ? nrows : t.n), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+// y = x * (1/sqrtf(float(sum x^2 / n) + eps)) * w for `rows` rows of length n
+// (src/ops.c:76-83). Double sum of squares in a fixed per-thread-then-tree order.
+__global__ __launch_bounds__(256) void k_rmsnorm(float *y, const float *x, const uint16_t *wt,
+                                                 int n, float eps) {
+    __shared__ double redd[256];
+    const int tid = threadIdx.x;
+    const float *xr = x + (size_t)blockIdx.x * n;
+    float *yr = y + (size_t)blockIdx.x * n;
+    double ss = 0.0;
+    for (int i = tid; i < n; i += 256) {
+        const double v = (double)xr[i];
+        ss += v * v;
+    }
+    redd[tid] = ss;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) redd[tid] += redd[tid + o];
+        __syncthreads();
+    }
+    const float mean_sq = (float)(redd[0] / (double)n);
+    const float inv = 1.0f / sqrtf(mean_sq + eps);
+    for (int i = tid; i < n; i += 256) {
+        const float t = xr[i] * inv;
+        yr[i] = t * bf16_to_f32(wt[i]);
+    }
+}
+
+hipError_t launch_rmsnorm(hipStream_t st, float *y, const float *x, const uint16_t *w, int n,
+                          int rows, float eps) {
+    if (rows <= 0 || n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(256), 0, st, y, x, w, n, eps);
+    return hipGetLastError();
+}
+
+// Expanded state: K = [kv_b(latent)[h, :DN] | rotated key], V = kv_b(latent)[h, DN:]
+// (src/mla_state.c:95-115). One block per sequence; rows staged for host write-back.
+struct StoreExpArgs {
+    SeqTable t;
+    Dims d;
+    const float *kv;
+    uint8_t *rows;
+};
+
+__global__ __launch_bounds__(256) void k_store_expanded(StoreExpArgs a) {
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const SeqDesc &s = a.t.s[b];
+    const Dims &d = a.d;
+    const size_t row_bytes = (size_t)4 * d.NH * (d.QD + d.DV);
+    float *stage = (float *)(a.rows + (size_t)b * row_bytes);
+    // the rotated key was staged by k_append at the front of this sequence's row slot
+    __shared__ float rope[kMaxDR];
+    for (int i = tid; i < d.DR; i += 256) rope[i] = stage[i];
+    __syncthreads();
+    float *keys = (float *)s.a + (size_t)s.pos * d.NH * d.QD;
+    float *vals = (float *)s.b + (size_t)s.pos * d.NH * d.DV;
+    const float *kv = a.kv + (size_t)b * d.KVB;
+    const int nk = d.NH * d.QD, nv = d.NH * d.DV;
+    for (int i = tid; i < nk; i += 256) {
+        const int h = i / d.QD, k = i % d.QD;
+        keys[i] = k < d.DN ? kv[h * (d.DN + d.DV) + k] : rope[k - d.DN];
+    }
+    for (int i = tid; i < nv; i += 256) {
+        const int h = i / d.DV, k = i % d.DV;
+        vals[i] = kv[h * (d.DN + d.DV) + d.DN + k];
+    }
+    __syncthreads();
+    for (int i = tid; i < nk; i += 256) stage[i] = keys[i];
+    for (int i = tid; i < nv; i += 256) stage[nk + i] = vals[i];
+}
+
+hipError_t launch_store_expanded(hipStream_t st, const SeqTable &t, const Dims &d,
+                                 const DecodeWork &w) {
+    if (d.DR > kMaxDR) return hipErrorInvalidValue;
+    StoreExpArgs a{t, d, w.kv, w.rows};
+    hipLaunchKernelGGL(k_store_expanded, dim3(t.n), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+// ================================================================ query prep ===========
+
+struct QprepArgs {
+    SeqTable t;
+    Dims d;
+    const float *y;
+    const uint16_t *kv_b;
+    const float2 *cs;
+    float *qf;
+    int8_t *qhi, *qlo;
+    float *qs;
+    uint16_t *qrhi, *qrlo;
+    int ldy, fmt, quantize;
+};
+
+// One block per (sequence, head). Compressed formats: q_lat[r] = sum_d
+// kv_b[h*(DN+DV)+d, r] * q_nope[d] (src/mla_compressed_q8_state.c:206-214), q_rope rotated
+// at the decode position; qf row = [q_lat | q_rope]. Expanded: qf row = [q_nope | q_rope].
+// With `quantize`, q_lat ~= qs * (hi + lo/128) (int8 hi, lo) and q_rope = hi + lo (bf16).
+__global__ __launch_bounds__(256) void k_qprep(QprepArgs a) {
+    __shared__ float qn[kMaxDN];
+    __shared__ float ql[kMaxR];
+    __shared__ float redf[256];
+    const Dims &d = a.d;
+    const int b = blockIdx.x / d.NH, h = blockIdx.x % d.NH, tid = threadIdx.x;
+    const SeqDesc &s = a.t.s[b];
+    const float *qh = a.y + (size_t)b * a.ldy + (size_t)h * d.QD;
+    const int half = d.DR / 2;
+    for (int i = tid; i < d.DN; i += 256) qn[i] = qh[i];
+    __syncthreads();
+    const bool exp = a.fmt == kFmtExp;
+    const int qstride = exp ? d.QD : d.R + d.DR;
+    const int roff = exp ? d.DN : d.R;
+    float *qrow = a.qf + ((size_t)b * d.NH + h) * qstride;
+    if (exp) {
+        for (int i = tid; i < d.DN; i += 256) qrow[i] = qn[i];
+    } else {
+        const uint16_t *wuk = a.kv_b + (size_t)h * (d.DN + d.DV) * d.R;
+        for (int r = tid; r < d.R; r += 256) {
+            float acc = 0.f;
+            for (int k = 0; k < d.DN; ++k) acc = fmaf(bf16_to_f32(wuk[(size_t)k * d.R + r]), qn[k], acc);
+            ql[r] = acc;
+            qrow[r] = acc;
+        }
+    }
+    for (int i = tid; i < half; i += 256) {
+        const float2 cs = a.cs[(size_t)s.pos * half + i];
+        const float ev = qh[d.DN + 2 * i], od = qh[d.DN + 2 * i + 1];
+        const float ec = ev * cs.x, os = od * cs.y, oc = od * cs.x, es = ev * cs.y;
+        const float r0 = ec - os, r1 = oc + es;
+        qrow[roff + i] = r0;
+        qrow[roff + half + i] = r1;
+        if (a.quantize) {
+            uint16_t hi, lo;
+            const size_t o = ((size_t)b * d.NH + h) * d.DR;
+            split_bf16(r0, hi, lo);
+            a.qrhi[o + i] = hi;
+            a.qrlo[o + i] = lo;
+            split_bf16(r1, hi, lo);
+            a.qrhi[o + half + i] = hi;
+            a.qrlo[o + half + i] = lo;
+        }
+    }
+    if (!a.quantize || exp) return;
+    __syncthreads();
+    float m = 0.f;
+    for (int r = tid; r < d.R; r += 256) m = fmaxf(m, fabsf(ql[r]));
+    redf[tid] = m;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) redf[tid] = fmaxf(redf[tid], redf[tid + o]);
+        __syncthreads();
+    }
+    const float amax = redf[0];
+    const bool ok = amax > 0.f && isfinite(amax);
+    const float inv = ok ? 127.0f / amax : 0.f;
+    const size_t o = ((size_t)b * d.NH + h) * d.R;
+    for (int r = tid; r < d.R; r += 256) {
+        const float v = ql[r] * inv;
+        float hi = rintf(v);
+        hi = fminf(fmaxf(hi, -127.f), 127.f);
+        float lo = rintf((v - hi) * 128.0f);
+        lo = fminf(fmaxf(lo, -127.f), 127.f);
+        a.qhi[o + r] = (int8_t)hi;
+        a.qlo[o + r] = (int8_t)lo;
+    }
+    if (tid == 0) a.qs[(size_t)b * d.NH + h] = ok ? amax / 127.0f : 0.f;
+}
+
+hipError_t launch_qprep(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
+                        const uint16_t *kv_b, const float2 *rope_cs, const DecodeWork &w,
+                        bool quantize) {
+    if (d.R > kMaxR || d.DN > kMaxDN || d.DR > kMaxDR) return hipErrorInvalidValue;
+    QprepArgs a;
+    a.t = t;
+    a.d = d;
+    a.y = w.y;
+    a.kv_b = kv_b;
+    a.cs = rope_cs;
+    a.qf = w.qf;
+    a.qhi = w.qhi;
+    a.qlo = w.qlo;
+    a.qs = w.qs;
+    a.qrhi = w.qrhi;
+    a.qrlo = w.qrlo;
+    a.ldy = d.QO + d.KVO;
+    a.fmt = fmt;
+    a.quantize = quantize ? 1 : 0;
+    hipLaunchKernelGGL(k_qprep, dim3(t.n * d.NH), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+// ================================================================ attention ============
+
+struct AttnArgs {
+    SeqTable t;
+    Dims d;
+    float *part;
+    const float *qf;
+    const int8_t *qhi, *qlo;
+    const float *qs;
+    const uint16_t *qrhi, *qrlo;
+    float *scores;
+    int rps, lmax;
+    float smscale;
+};
+
+// Block -> (sequence, split): splits of the sequences are numbered consecutively.
+__device__ __forceinline__ int find_seq(const SeqTable &t, int bid) {
+    int b = 0;
+    for (int i = 1; i < t.n; ++i)
+        if (bid >= t.s[i].split0) b = i;
+    return b;
+}
+
+// ---- generic VALU path: any dims and formats, one block per problem -----------------
+// Problem = one sequence (compressed: all NH heads share the rows) or one (sequence, head)
+// (expanded). Two-pass softmax over the full history; partial written with one split.
+template <int FMT>
+__device__ __forceinline__ float score_elem(const SeqDesc &s, const Dims &d, int h, int j, int k) {
+    if (FMT == kFmtQ8) {
+        if (k < d.R) return (float)((const int8_t *)s.a)[(size_t)j * d.R + k] * ((const float *)s.b)[j];
+        return bf16_to_f32(((const uint16_t *)s.c)[(size_t)j * d.DR + (k - d.R)]);
+    } else if (FMT == kFmtF32) {
+        if (k < d.R) return ((const float *)s.a)[(size_t)j * d.R + k];
+        return ((const float *)s.b)[(size_t)j * d.DR + (k - d.R)];
+    } else {
+        return ((const float *)s.a)[((size_t)j * d.NH + h) * d.QD + k];
+    }
+}
+template <int FMT>
+__device__ __forceinline__ float value_elem(const SeqDesc &s, const Dims &d, int h, int j, int k) {
+    if (FMT == kFmtQ8) return (float)((const int8_t *)s.a)[(size_t)j * d.R + k] * ((const float *)s.b)[j];
+    if (FMT == kFmtF32) return ((const float *)s.a)[(size_t)j * d.R + k];
+    return ((const float *)s.b)[((size_t)j * d.NH + h) * d.DV + k];
+}
+
+template <int FMT>
+__global__ __launch_bounds__(256) void k_attn_generic(AttnArgs a) {
+    __shared__ float red[256];
+    __shared__ float ml[2 * 64];
+    const Dims &d = a.d;
+    const int p = blockIdx.x, tid = threadIdx.x;
+    const bool exp = FMT == kFmtExp;
+    const int b = exp ? p / d.NH : p, h0 = exp ? p % d.NH : 0;
+    const int G = exp ? 1 : d.NH, DS = exp ? d.QD : d.R + d.DR, DVm = exp ? d.DV : d.R;
+    const SeqDesc &s = a.t.s[b];
+    const int L = s.len;
+    const float *q = a.qf + ((size_t)b * d.NH + h0) * DS;
+    float *sc = a.scores + (size_t)p * G * a.lmax;
+    for (int idx = tid; idx < G * L; idx += 256) {
+        const int g = idx / L, j = idx % L;
+        float acc = 0.f;
+        for (int k = 0; k < DS; ++k) acc = fmaf(q[(size_t)g * DS + k], score_elem<FMT>(s, d, h0 + g, j, k), acc);
+        sc[(size_t)g * a.lmax + j] = acc * a.smscale;
+    }
+    __syncthreads();
+    for (int g = 0; g < G; ++g) {
+        float m = -INFINITY;
+        for (int j = tid; j < L; j += 256) m = fmaxf(m, sc[(size_t)g * a.lmax + j]);
+        red[tid] = m;
+        __syncthreads();
+        for (int o = 128; o > 0; o >>= 1) {
+            if (tid < o) red[tid] = fmaxf(red[tid], red[tid + o]);
+            __syncthreads();
+        }
+        m = red[0];
+        __syncthreads();
+        float sum = 0.f;
+        for (int j = tid; j < L; j += 256) {
+            const float e = __expf(sc[(size_t)g * a.lmax + j] - m);
+            sc[(size_t)g * a.lmax + j] = e;
+            sum += e;
+        }
+        red[tid] = sum;
+        __syncthreads();
+        for (int o = 128; o > 0; o >>= 1) {
+            if (tid < o) red[tid] += red[tid + o];
+            __syncthreads();
+        }
+        if (tid == 0) {
+            ml[2 * g] = m;
+            ml[2 * g + 1] = red[0];
+        }
+        __syncthreads();
+    }
+    const int split = exp ? p : s.split0;
+    float *P = a.part + (size_t)split * G * (DVm + 2);
+    for (int idx = tid; idx < G * DVm; idx += 256) {
+        const int g = idx / DVm, k = idx % DVm;
+        float acc = 0.f;
+        for (int j = 0; j < L; ++j) acc = fmaf(sc[(size_t)g * a.lmax + j], value_elem<FMT>(s, d, h0 + g, j, k), acc);
+        P[idx] = acc;
+    }
+    for (int g = tid; g < G; g += 256) {
+        P[(size_t)G * DVm + g] = ml[2 * g];
+        P[(size_t)G * DVm + G + g] = ml[2 * g + 1];
+    }
+}
+
+// ---- fp32 MFMA path (FP32 history, NH=16, R=512, DR=64) -------------------------------
+// Chunks of 16 rows are staged in LDS. Scores: M = 16 heads, N = 16 rows, K = 576 split
+// in four wave-quarters (v_mfma_f32_16x16x4f32, exact fp32 products) and summed through
+// LDS. Softmax statistics are kept per head in every wave (online rescaling). Mix: each
+// wave owns 128 latent columns, M = heads, N = 16 columns, K = 4 rows per instruction.
+constexpr int kF32Ch = 16;
+constexpr int kF32Rs = 580;  // LDS row stride (floats): 576 + 4, conflict-free b128 reads
+
+__global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) float rows[kF32Ch * kF32Rs];
+    __shared__ float sp[4][16][16];
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
+    const int b = find_seq(a.t, blockIdx.x);
+    const SeqDesc &s = a.t.s[b];
+    const int r0 = (blockIdx.x - s.split0) * a.rps;
+    const int r1 = min(r0 + a.rps, s.len);
+    const float *glat = (const float *)s.a;
+    const float *grope = (const float *)s.b;
+
+    float qa[36];
+    {
+        const float *qrow = a.qf + ((size_t)b * 16 + n) * 576 + 144 * w + 36 * g;
+#pragma unroll
+        for (int t = 0; t < 36; t += 4) {
+            const v4f v = *(const v4f *)(qrow + t);
+            qa[t] = v.x;
+            qa[t + 1] = v.y;
+            qa[t + 2] = v.z;
+            qa[t + 3] = v.w;
+        }
+    }
+    float m_run = -INFINITY, l_run = 0.f;
+    v4f acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    v4f pl[8], pr;
+    auto prefetch = [&](int c) {
+        const int base = r0 + c * kF32Ch;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int p = tid + 256 * k, row = p >> 7, c4 = p & 127, gr = base + row;
+            pl[k] = gr < r1 ? *(const v4f *)(glat + (size_t)gr * 512 + 4 * c4) : v4f{0.f, 0.f, 0.f, 0.f};
+        }
+        const int row = tid >> 4, c4 = tid & 15, gr = base + row;
+        pr = gr < r1 ? *(const v4f *)(grope + (size_t)gr * 64 + 4 * c4) : v4f{0.f, 0.f, 0.f, 0.f};
+    };
+    auto stash = [&]() {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int p = tid + 256 * k, row = p >> 7, c4 = p & 127;
+            *(v4f *)(rows + row * kF32Rs + 4 * c4) = pl[k];
+        }
+        const int row = tid >> 4, c4 = tid & 15;
+        *(v4f *)(rows + row * kF32Rs + 512 + 4 * c4) = pr;
+    };
+
+    const int nch = (r1 - r0 + kF32Ch - 1) / kF32Ch;
+    prefetch(0);
+    for (int c = 0; c < nch; ++c) {
+        __syncthreads();
+        stash();
+        __syncthreads();
+        if (c + 1 < nch) prefetch(c + 1);
+        const int base = r0 + c * kF32Ch;
+        v4f dp = {0.f, 0.f, 0.f, 0.f};
+        const float *brow = rows + n * kF32Rs + 144 * w + 36 * g;
+#pragma unroll
+        for (int t = 0; t < 36; t += 4) {
+            const v4f bv = *(const v4f *)(brow + t);
+            dp = mfma_f32(qa[t], bv.x, dp);
+            dp = mfma_f32(qa[t + 1], bv.y, dp);
+            dp = mfma_f32(qa[t + 2], bv.z, dp);
+            dp = mfma_f32(qa[t + 3], bv.w, dp);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sp[w][4 * g + i][n] = dp[i];
+        __syncthreads();
+        float sc[4];
+        float cmax = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int row = 4 * k + g;
+            const float v = ((sp[0][n][row] + sp[1][n][row]) + sp[2][n][row]) + sp[3][n][row];
+            sc[k] = base + row < r1 ? v * a.smscale : -INFINITY;
+            cmax = fmaxf(cmax, sc[k]);
+        }
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+        const float mnew = fmaxf(m_run, cmax);
+        const float alpha = __expf(m_run - mnew);
+        float pr4[4], psum = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            pr4[k] = __expf(sc[k] - mnew);
+            psum += pr4[k];
+        }
+        psum += __shfl_xor(psum, 16);
+        psum += __shfl_xor(psum, 32);
+        l_run = fmaf(l_run, alpha, psum);
+        m_run = mnew;
+        float ad[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ad[i] = __shfl(alpha, 4 * g + i);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[t][i] *= ad[i];
+            const int col = 128 * w + 16 * t + n;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) acc[t] = mfma_f32(pr4[k], rows[(4 * k + g) * kF32Rs + col], acc[t]);
+        }
+    }
+    float *P = a.part + (size_t)blockIdx.x * 16 * 514;
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) P[(4 * g + i) * 512 + 128 * w + 16 * t + n] = acc[t][i];
+    if (w == 0 && g == 0) {
+        P[8192 + n] = m_run;
+        P[8192 + 16 + n] = l_run;
+    }
+}
+
+// ---- int8 MFMA path (Q8 history, NH=16, R=512, DR=64) ---------------------------------
+// Chunks of 64 rows (41 KB) are staged in LDS by all four waves with 16-byte loads.
+// Scores (wave w: rows 16w..16w+15): v_mfma_i32_16x16x64_i8 on the raw int8 codes against
+// the int8 hi/lo split of q_lat (exact integer dot products), plus bf16 MFMA on the bf16
+// RoPE keys against the hi/lo bf16 split of q_rope. The row scale factors out of the dot
+// (score_j = s_j * q_lat . c_j + q_rope . k_j). Mix: the probabilities p_j*s_j are
+// quantised per chunk to int8 hi/lo against the chunk's largest scale (p <= 1 after the
+// running max), and multiplied with the codes, transposed per 4x4 byte block in registers,
+// by v_mfma_i32_16x16x64_i8 (K = 64 rows). Each wave accumulates 128 latent columns.
+constexpr int kQ8Ch = 64;
+constexpr int kQ8Cs = 528;  // LDS bytes per code row (512 + 16)
+constexpr int kQ8Rs = 144;  // LDS bytes per RoPE row (128 + 16)
+constexpr int kQ8Ws = 80;   // LDS bytes per quantised-weight row (64 + 16)
+
+__device__ __forceinline__ void transpose4x4(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
+                                             uint32_t &o0, uint32_t &o1, uint32_t &o2,
+                                             uint32_t &o3) {
+    const uint32_t ab01 = __builtin_amdgcn_perm(b, a, 0x05010400u);
+    const uint32_t ab23 = __builtin_amdgcn_perm(b, a, 0x07030602u);
+    const uint32_t cd01 = __builtin_amdgcn_perm(d, c, 0x05010400u);
+    const uint32_t cd23 = __builtin_amdgcn_perm(d, c, 0x07030602u);
+    o0 = __builtin_amdgcn_perm(cd01, ab01, 0x05040100u);
+    o1 = __builtin_amdgcn_perm(cd01, ab01, 0x07060302u);
+    o2 = __builtin_amdgcn_perm(cd23, ab23, 0x05040100u);
+    o3 = __builtin_amdgcn_perm(cd23, ab23, 0x07060302u);
+}
+
+__global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t codes[kQ8Ch * kQ8Cs];
+    __shared__ __attribute__((aligned(16))) uint8_t ropes[kQ8Ch * kQ8Rs];
+    __shared__ __attribute__((aligned(16))) int8_t wq[2][16 * kQ8Ws];
+    __shared__ float scl[kQ8Ch];
+    __shared__ float mloc[4][16];
+    __shared__ float lsum[4][16];
+    __shared__ float smax_s;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
+    const int b = find_seq(a.t, blockIdx.x);
+    const SeqDesc &s = a.t.s[b];
+    const int r0 = (blockIdx.x - s.split0) * a.rps;
+    const int r1 = min(r0 + a.rps, s.len);
+    const int8_t *gcodes = (const int8_t *)s.a;
+    const float *gscl = (const float *)s.b;
+    const uint16_t *grope = (const uint16_t *)s.c;
+
+    const size_t bh = (size_t)b * 16 + n;
+    v4i qh[8], ql[8];
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) {
+        qh[kb] = *(const v4i *)(a.qhi + bh * 512 + 64 * kb + 16 * g);
+        ql[kb] = *(const v4i *)(a.qlo + bh * 512 + 64 * kb + 16 * g);
+    }
+    v8bf qrh[2], qrl[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        qrh[kb] = *(const v8bf *)(a.qrhi + bh * 64 + 32 * kb + 8 * g);
+        qrl[kb] = *(const v8bf *)(a.qrlo + bh * 64 + 32 * kb + 8 * g);
+    }
+    float qsd[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qsd[i] = a.qs[(size_t)b * 16 + 4 * g + i];
+
+    float m_run[4], l_lane[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        m_run[i] = -INFINITY;
+        l_lane[i] = 0.f;
+    }
+    v4f acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    v4i pc[8], pr[2];
+    float ps = 0.f;
+    auto prefetch = [&](int c) {
+        const int base = r0 + c * kQ8Ch;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int p = tid + 256 * k, row = p >> 5, c16 = p & 31, gr = base + row;
+            pc[k] = gr < r1 ? *(const v4i *)(gcodes + (size_t)gr * 512 + 16 * c16) : v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int p = tid + 256 * k, row = p >> 3, c8 = p & 7, gr = base + row;
+            pr[k] = gr < r1 ? *(const v4i *)(grope + (size_t)gr * 64 + 8 * c8) : v4i{0, 0, 0, 0};
+        }
+        if (tid < kQ8Ch) {
+            const int gr = base + tid;
+            ps = gr < r1 ? gscl[gr] : 0.f;
+        }
+    };
+    auto stash = [&]() {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int p = tid + 256 * k, row = p >> 5, c16 = p & 31;
+            *(v4i *)(codes + row * kQ8Cs + 16 * c16) = pc[k];
+        }
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int p = tid + 256 * k, row = p >> 3, c8 = p & 7;
+            *(v4i *)(ropes + row * kQ8Rs + 16 * c8) = pr[k];
+        }
+        if (tid < kQ8Ch) {  // wave 0, all lanes
+            scl[tid] = ps;
+            const float mx = wave_max(ps);
+            if (tid == 0) smax_s = mx;
+        }
+    };
+
+    const int nch = (r1 - r0 + kQ8Ch - 1) / kQ8Ch;
+    const int rowl = 16 * w + n;
+    prefetch(0);
+    for (int c = 0; c < nch; ++c) {
+        __syncthreads();
+        stash();
+        __syncthreads();
+        if (c + 1 < nch) prefetch(c + 1);
+        const int base = r0 + c * kQ8Ch;
+
+        v4i ih = {0, 0, 0, 0}, il = {0, 0, 0, 0};
+        v4f fr = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) {
+            const v4i bv = *(const v4i *)(codes + rowl * kQ8Cs + 64 * kb + 16 * g);
+            ih = mfma_i8(qh[kb], bv, ih);
+            il = mfma_i8(ql[kb], bv, il);
+        }
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const v8bf bv = *(const v8bf *)(ropes + rowl * kQ8Rs + 64 * kb + 16 * g);
+            fr = mfma_bf16(qrh[kb], bv, fr);
+            fr = mfma_bf16(qrl[kb], bv, fr);
+        }
+        const float sj = scl[rowl];
+        const bool valid = base + rowl < r1;
+        float sc[4], lm[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float dot = (float)ih[i] + (float)il[i] * 0.0078125f;
+            sc[i] = valid ? a.smscale * fmaf(qsd[i] * sj, dot, fr[i]) : -INFINITY;
+            lm[i] = sc[i];
+        }
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) lm[i] = fmaxf(lm[i], __shfl_xor(lm[i], o));
+        if (n == 0)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mloc[w][4 * g + i] = lm[i];
+        __syncthreads();
+
+        const float smax = smax_s;
+        const float wscale = smax > 0.f ? 127.0f / smax : 0.f;
+        float alpha[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int hh = 4 * g + i;
+            const float cm = fmaxf(fmaxf(mloc[0][hh], mloc[1][hh]), fmaxf(mloc[2][hh], mloc[3][hh]));
+            const float mnew = fmaxf(m_run[i], cm);
+            alpha[i] = __expf(m_run[i] - mnew);
+            m_run[i] = mnew;
+            const float p = __expf(sc[i] - mnew);
+            l_lane[i] = fmaf(l_lane[i], alpha[i], p);
+            const float v = p * sj * wscale;
+            float hi = fminf(rintf(v), 127.f);
+            float lo = rintf((v - hi) * 128.0f);
+            lo = fminf(fmaxf(lo, -127.f), 127.f);
+            wq[0][hh * kQ8Ws + rowl] = (int8_t)hi;
+            wq[1][hh * kQ8Ws + rowl] = (int8_t)lo;
+        }
+        __syncthreads();
+
+        const v4i wh = *(const v4i *)(wq[0] + n * kQ8Ws + 16 * g);
+        const v4i wl = *(const v4i *)(wq[1] + n * kQ8Ws + 16 * g);
+        const float wfac = smax * (1.0f / (127.0f * 128.0f));
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+            const int col = 128 * w + 64 * rb + 4 * n;
+            uint32_t dd[16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) dd[k] = *(const uint32_t *)(codes + (16 * g + k) * kQ8Cs + col);
+            uint32_t tt[4][4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                transpose4x4(dd[4 * q], dd[4 * q + 1], dd[4 * q + 2], dd[4 * q + 3], tt[0][q], tt[1][q],
+                             tt[2][q], tt[3][q]);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const v4i bt = {(int)tt[t][0], (int)tt[t][1], (int)tt[t][2], (int)tt[t][3]};
+                const v4i zero = {0, 0, 0, 0};
+                const v4i ih2 = mfma_i8(wh, bt, zero);
+                const v4i il2 = mfma_i8(wl, bt, zero);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[rb * 4 + t][i] = fmaf(acc[rb * 4 + t][i], alpha[i], wfac * (float)(ih2[i] * 128 + il2[i]));
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float v = l_lane[i];
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o);
+        l_lane[i] = v;
+    }
+    if (n == 0)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lsum[w][4 * g + i] = l_lane[i];
+    __syncthreads();
+    float *P = a.part + (size_t)blockIdx.x * 16 * 514;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const int r = 128 * w + 64 * (t >> 2) + 4 * n + (t & 3);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) P[(4 * g + i) * 512 + r] = acc[t][i];
+    }
+    if (w == 0 && n == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int hh = 4 * g + i;
+            P[8192 + hh] = m_run[i];
+            P[8192 + 16 + hh] = (lsum[0][hh] + lsum[1][hh]) + (lsum[2][hh] + lsum[3][hh]);
+        }
+    }
+}
+
+hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t, const Dims &d,
+                            int rows_per_split, int total_splits, int lmax,
+                            const DecodeWork &w) {
+    AttnArgs a;
+    a.t = t;
+    a.d = d;
+    a.part = w.part;
+    a.qf = w.qf;
+    a.qhi = w.qhi;
+    a.qlo = w.qlo;
+    a.qs = w.qs;
+    a.qrhi = w.qrhi;
+    a.qrlo = w.qrlo;
+    a.scores = w.scores;
+    a.rps = rows_per_split;
+    a.lmax = lmax;
+    a.smscale = 1.0f / sqrtf((float)d.QD);
+    if (kind == kAttnQ8Mfma) {
+        hipLaunchKernelGGL(k_attn_q8_mfma, dim3(total_splits), dim3(256), 0, st, a);
+    } else if (kind == kAttnF32Mfma) {
+        hipLaunchKernelGGL(k_attn_f32_mfma, dim3(total_splits), dim3(256), 0, st, a);
+    } else {
+        const int P = fmt == kFmtExp ? t.n * d.NH : t.n;
+        if (fmt == kFmtQ8)
+            hipLaunchKernelGGL(k_attn_generic<kFmtQ8>, dim3(P), dim3(256), 0, st, a);
+        else if (fmt == kFmtF32)
+            hipLaunchKernelGGL(k_attn_generic<kFmtF32>, dim3(P), dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL(k_attn_generic<kFmtExp>, dim3(P), dim3(256), 0, st, a);
+    }
+    return hipGetLastError();
+}
+
+// ================================================================ combine + W_UV =======
+
+struct CombineArgs {
+    SeqTable t;
+    Dims d;
+    const float *part;
+    const uint16_t *kv_b;
+    float *mix;
+    float *ho;
+    int fmt;
+};
+
+// One block per (sequence, head). m* = max_s m_s, denom = sum_s l_s e^(m_s - m*),
+// mix = sum_s acc_s e^(m_s - m*) / denom; then (compressed formats)
+// ho[d] = sum_r kv_b[h*(DN+DV)+DN+d, r] * mix[r] (src/mla_compressed_q8_state.c:239-247).
+__global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
+    __shared__ float mx[kMaxR];
+    const Dims &d = a.d;
+    const int b = blockIdx.x / d.NH, h = blockIdx.x % d.NH, tid = threadIdx.x;
+    const SeqDesc &s = a.t.s[b];
+    const bool exp = a.fmt == kFmtExp;
+    const int G = exp ? 1 : d.NH, DVm = exp ? d.DV : d.R, g = exp ? 0 : h;
+    const int sp0 = exp ? b * d.NH + h : s.split0, ns = exp ? 1 : s.nsplit;
+    const size_t stride = (size_t)G * (DVm + 2);
+    const float *P = a.part + (size_t)sp0 * stride;
+    float M = -INFINITY;
+    for (int i = 0; i < ns; ++i) M = fmaxf(M, P[i * stride + (size_t)G * DVm + g]);
+    float denom = 0.f;
+    for (int i = 0; i < ns; ++i)
+        denom = fmaf(P[i * stride + (size_t)G * DVm + G + g], __expf(P[i * stride + (size_t)G * DVm + g] - M), denom);
+    const float inv = 1.0f / denom;
+    float *mixrow = a.mix + ((size_t)b * d.NH + h) * DVm;
+    for (int k = tid; k < DVm; k += 256) {
+        float v = 0.f;
+        for (int i = 0; i < ns; ++i)
+            v = fmaf(P[i * stride + (size_t)g * DVm + k], __expf(P[i * stride + (size_t)G * DVm + g] - M), v);
+        v *= inv;
+        mixrow[k] = v;
+        if (exp)
+            a.ho[(size_t)b * d.HO + (size_t)h * d.DV + k] = v;
+        else
+            mx[k] = v;
+    }
+    if (exp) return;
+    __syncthreads();
+    const int w = tid >> 6, l = tid & 63;
+    const uint16_t *wuv = a.kv_b + ((size_t)h * (d.DN + d.DV) + d.DN) * d.R;
+    for (int dd = w; dd < d.DV; dd += 4) {
+        const uint16_t *row = wuv + (size_t)dd * d.R;
+        float acc = 0.f;
+        for (int r = l; r < d.R; r += 64) acc = fmaf(bf16_to_f32(row[r]), mx[r], acc);
+        acc = wave_sum(acc);
+        if (l == 0) a.ho[(size_t)b * d.HO + (size_t)h * d.DV + dd] = acc;
+    }
+}
+
+hipError_t launch_combine(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
+                          const uint16_t *kv_b, const DecodeWork &w) {
+    if (d.R > kMaxR) return hipErrorInvalidValue;
+    CombineArgs a{t, d, w.part, kv_b, w.mix, w.ho, fmt};
+    hipLaunchKernelGGL(k_combine, dim3(t.n * d.NH), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+// ================================================================ synthetic history ====
+
+struct FillArgs {
+    void *a, *b, *c;
+    int R, DR, row0, nrows, fmt;
+    uint64_t seed;
+};
+
+// One wave per row. Element e of global row j draws synth_normal(seed, j*(R+DR) + e).
+// Q8: the R latents go through the history quantiser, the DR RoPE values are rounded to
+// bf16. F32: all values are rounded to bf16 first (bf16-representable fp32 history).
+__global__ __launch_bounds__(256) void k_fill_history(FillArgs a) {
+    const int wv = (blockIdx.x * blockDim.x + threadIdx.x) >> 6, l = threadIdx.x & 63;
+    if (wv >= a.nrows) return;
+    const int j = a.row0 + wv;
+    const uint64_t base = (uint64_t)j * (uint64_t)(a.R + a.DR);
+    if (a.fmt == kFmtQ8) {
+        float m = 0.f;
+        for (int e = l; e < a.R; e += 64) m = fmaxf(m, fabsf(synth_normal(a.seed, base + e)));
+        m = wave_max(m);
+        const bool zero = !(m > 0.0f) || !isfinite(m);
+        const float scale = zero ? 1.0f : m / 127.0f;
+        const float inv = zero ? 0.0f : 1.0f / scale;
+        int8_t *codes = (int8_t *)a.a + (size_t)j * a.R;
+        for (int e = l; e < a.R; e += 64) {
+            float v = roundf(synth_normal(a.seed, base + e) * inv);
+            v = fminf(fmaxf(v, -127.f), 127.f);
+            codes[e] = zero ? (int8_t)0 : (int8_t)v;
+        }
+        if (l == 0) ((float *)a.b)[j] = scale;
+        uint16_t *rope = (uint16_t *)a.c + (size_t)j * a.DR;
+        for (int e = l; e < a.DR; e += 64) rope[e] = f32_to_bf16_rne(synth_normal(a.seed, base + a.R + e));
+    } else {
+        float *lat = (float *)a.a + (size_t)j * a.R;
+        float *rope = (float *)a.b + (size_t)j * a.DR;
+        for (int e = l; e < a.R; e += 64) lat[e] = bf16_to_f32(f32_to_bf16_rne(synth_normal(a.seed, base + e)));
+        for (int e = l; e < a.DR; e += 64)
+            rope[e] = bf16_to_f32(f32_to_bf16_rne(synth_normal(a.seed, base + a.R + e)));
+    }
+}
+
+hipError_t launch_fill_history(hipStream_t st, int fmt, void *a, void *b, void *c, int R,
+                               int DR, int row0, int nrows, uint64_t seed) {
+    if (nrows <= 0) return hipSuccess;
+    FillArgs f{a, b, c, R, DR, row0, nrows, fmt, seed};
+    hipLaunchKernelGGL(k_fill_history, dim3((nrows + 3) / 4), dim3(256), 0, st, f);
+    return hipGetLastError();
+}
+
+}  // namespace kvl

@@ -1,0 +1,95 @@
+// Device helpers shared by the MLA kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kvl {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+    return __uint_as_float((uint32_t)h << 16);
+}
+
+// Round-to-nearest-even with the history format's rule: Inf/NaN words are truncated,
+// NaN payloads kept (src/mla_compressed_q8_state.c:9-16).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7f800000u) != 0x7f800000u) u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// x ~= hi + lo with hi, lo bf16: the split keeps ~16 mantissa bits of an fp32 operand
+// for bf16 MFMA (products with bf16-exact operands stay exact in the fp32 accumulator).
+__device__ __forceinline__ void split_bf16(float x, uint16_t &hi, uint16_t &lo) {
+    hi = f32_to_bf16_rne(x);
+    lo = f32_to_bf16_rne(x - bf16_to_f32(hi));
+}
+
+__device__ __forceinline__ uint32_t pack2(uint16_t a, uint16_t b) {
+    return (uint32_t)a | ((uint32_t)b << 16);
+}
+
+// 8 fp32 values -> two bf16x8 MFMA operands (hi, lo).
+__device__ __forceinline__ void split8(const v4f &x0, const v4f &x1, v8bf &hi, v8bf &lo) {
+    uint16_t h[8], l[8];
+    split_bf16(x0.x, h[0], l[0]);
+    split_bf16(x0.y, h[1], l[1]);
+    split_bf16(x0.z, h[2], l[2]);
+    split_bf16(x0.w, h[3], l[3]);
+    split_bf16(x1.x, h[4], l[4]);
+    split_bf16(x1.y, h[5], l[5]);
+    split_bf16(x1.z, h[6], l[6]);
+    split_bf16(x1.w, h[7], l[7]);
+    v4i hv = {(int)pack2(h[0], h[1]), (int)pack2(h[2], h[3]), (int)pack2(h[4], h[5]),
+              (int)pack2(h[6], h[7])};
+    v4i lv = {(int)pack2(l[0], l[1]), (int)pack2(l[2], l[3]), (int)pack2(l[4], l[5]),
+              (int)pack2(l[6], l[7])};
+    hi = __builtin_bit_cast(v8bf, hv);
+    lo = __builtin_bit_cast(v8bf, lv);
+}
+
+__device__ __forceinline__ v4f mfma_bf16(const v8bf &a, const v8bf &b, const v4f &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ v4i mfma_i8(const v4i &a, const v4i &b, const v4i &c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ v4f mfma_f32(float a, float b, const v4f &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// SplitMix64 output k (k >= 1) of the stream seeded by `seed`.
+__device__ __forceinline__ uint64_t splitmix64_at(uint64_t seed, uint64_t k) {
+    uint64_t z = seed + k * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// Approximately N(0,1): Irwin-Hall sum of four 24-bit uniforms, centred and scaled by
+// sqrt(3). Only exactly rounded fp32 operations, so a host mirror reproduces it bit for bit.
+__device__ __forceinline__ float synth_normal(uint64_t seed, uint64_t idx) {
+    float u[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        u[k] = (float)(uint32_t)(splitmix64_at(seed, 4 * idx + k + 1) >> 40) * 5.9604644775390625e-8f;
+    const float s = (u[0] + u[1]) + (u[2] + u[3]);
+    return (s - 2.0f) * 1.7320508f;
+}
+
+}  // namespace kvl

@@ -1,0 +1,128 @@
+// Internal interface between the host runtime (mla_runtime.cpp) and the HIP kernels
+// (mla_decode.hip, mla_prefill.hip) of libkvl_mla. Not installed; the public C ABI is
+// include/kvl/*.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace kvl {
+
+// Sequences handled by one launch group. Per-sequence descriptors travel as kernel
+// arguments (SeqTable, 64 x 48 B), so no per-call descriptor upload is needed.
+constexpr int kMaxBatch = 64;
+
+// Row formats of the latent history on the device.
+enum Fmt : int {
+    kFmtQ8 = 0,   // int8 codes [cap,R], fp32 scale [cap], bf16 RoPE key [cap,DR]
+    kFmtF32 = 1,  // fp32 latent [cap,R], fp32 RoPE key [cap,DR]
+    kFmtExp = 2,  // expanded fp32 keys [cap,NH,QD], values [cap,NH,DV]
+};
+
+struct Dims {
+    int H, NH, DN, DR, DV, R, QD, QO, KVO, KVB, HO;
+};
+
+// One sequence of a batched call. a/b/c are the device arrays of its history
+// (see Fmt), len the number of rows attended (position + 1), pos the row appended
+// by this step. split0/nsplit locate its split-K partials.
+struct SeqDesc {
+    void *a;
+    void *b;
+    void *c;
+    int len;
+    int pos;
+    int split0;
+    int nsplit;
+    int pad0, pad1;
+};
+
+struct SeqTable {
+    SeqDesc s[kMaxBatch];
+    int n;
+};
+
+// Device workspace of one decode launch group (all pointers device memory).
+struct DecodeWork {
+    float *x;        // [B,H]      input hidden states
+    float *y;        // [B,QO+KVO] q_proj | kv_a outputs
+    float *qf;       // [B,NH,QS]  per-head score-space query (fp32)
+    int8_t *qhi;     // [B,NH,R]   Q8 fast path: int8 query, high part
+    int8_t *qlo;     // [B,NH,R]   Q8 fast path: int8 query, low part (x1/128)
+    float *qs;       // [B,NH]     Q8 fast path: query dequant factor
+    uint16_t *qrhi;  // [B,NH,DR]  Q8 fast path: RoPE query, bf16 high part
+    uint16_t *qrlo;  // [B,NH,DR]  Q8 fast path: RoPE query, bf16 low part
+    float *latent;   // [B,R]      expanded state: normalised latent of the new token
+    float *kv;       // [B,KVB]    expanded state: kv_b expansion of the new token
+    float *part;     // [splits, G, DVm+2] split-K partials (acc | m | l)
+    float *scores;   // generic path: [P, G, Lmax] score scratch
+    float *mix;      // [B*NH, DVm] normalised attention mix
+    float *ho;       // [B,HO]     per-head outputs
+    float *out;      // [B,H]      layer output
+    uint8_t *rows;   // [B,row bytes] copy of the appended history rows (host write-back)
+};
+
+// ---- launchers (mla_decode.hip). All are stream-ordered and return hipError_t. ----
+
+// Y[b, o] = (accumulate ? Y[b, o] : 0) + sum_i W[o, i] * X[b, i], for b < B. The output
+// rows are the concatenation of W0 (out0 rows) and W1 (out1 rows, may be 0).
+hipError_t launch_gemv(hipStream_t st, float *Y, int ldy, const float *X, int ldx, int B,
+                       const uint16_t *W0, int out0, const uint16_t *W1, int out1, int in,
+                       bool accumulate);
+
+// RMSNorm of katmp[b] (= y + koff) -> latent row; RoPE of katmp[b][R:] at s.pos. Writes the
+// row into the history at row s.pos (fmt Q8/F32) or, for kFmtExp, the normalised latent
+// into w.latent and the rotated key into the tail of w.rows. A copy of the stored row goes
+// to w.rows for host write-back. rope_cs: [npos, DR/2] (cos, sin) pairs.
+// nrows > 0: rows mode, nrows rows of the single sequence t.s[0] starting at t.s[0].pos,
+// input row i at y + i*ldy, staged row i at w.rows + i*row_bytes.
+hipError_t launch_append(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
+                         const float *y, int ldy, int koff, const uint16_t *kv_a_norm,
+                         float eps, const float2 *rope_cs, const DecodeWork &w, bool normed,
+                         int nrows);
+
+// y[i] = RMSNorm(x[i]) * w for `rows` rows of length n (src/ops.c:76-83).
+hipError_t launch_rmsnorm(hipStream_t st, float *y, const float *x, const uint16_t *w, int n,
+                          int rows, float eps);
+
+// Expanded state: scatter kv_b expansion + rotated key of the new token into keys/values.
+hipError_t launch_store_expanded(hipStream_t st, const SeqTable &t, const Dims &d,
+                                 const DecodeWork &w);
+
+// Query preparation: absorbed q_lat = W_UK^T q_nope and RoPE(q_rope) per head (fmt Q8/F32),
+// or [q_nope | RoPE(q_rope)] (kFmtExp). quantize=true also builds the int8/bf16 split
+// operands of the Q8 MFMA attention kernel.
+hipError_t launch_qprep(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
+                        const uint16_t *kv_b, const float2 *rope_cs, const DecodeWork &w,
+                        bool quantize);
+
+// Split-K attention over the history; writes partials (acc | m | l) per split.
+// kind: 0 = generic VALU (any dims, one split per problem), 1 = fp32 MFMA (Kimi dims),
+// 2 = int8 MFMA (Kimi dims, Q8 rows).
+enum AttnKind : int { kAttnGeneric = 0, kAttnF32Mfma = 1, kAttnQ8Mfma = 2 };
+hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t, const Dims &d,
+                            int rows_per_split, int total_splits, int lmax,
+                            const DecodeWork &w);
+
+// Normalise the split partials into mix[(b*G + g), DVm] and, for the compressed formats,
+// apply W_UV: ho[b, h*DV + d] = sum_r kv_b[h*(DN+DV) + DN + d, r] * mix[b*NH + h, r].
+hipError_t launch_combine(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
+                          const uint16_t *kv_b, const DecodeWork &w);
+
+// Device-side generator of a synthetic Q8 / F32 history (benchmark and test workloads):
+// latents ~ Irwin-Hall(4) normal from SplitMix64, quantised with the history quantiser.
+hipError_t launch_fill_history(hipStream_t st, int fmt, void *a, void *b, void *c, int R,
+                               int DR, int row0, int nrows, uint64_t seed);
+
+// ---- prefill (mla_prefill.hip) ----
+// Device workspace bytes of a causal prefill of S tokens.
+size_t prefill_bytes(const Dims &d, int S);
+// Causal MLA prefill of S tokens: x [S,H] -> out [S,H] (device pointers), ws of
+// prefill_bytes(d, S) bytes, rope_cs table covering positions [0, S).
+hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, const float *x,
+                              float *out, const uint16_t *wq, const uint16_t *wkva,
+                              const uint16_t *wnorm, const uint16_t *wkvb, const uint16_t *wo,
+                              const float2 *rope_cs, void *ws);
+
+}  // namespace kvl

@@ -1,0 +1,1487 @@
+// Host runtime of libkvl_mla: the reference MLA C API (include/kvl/ops.h, mla_state.h,
+// mla_compressed_state.h, mla_compressed_q8_state.h) re-implemented over HIP on one MI355X,
+// plus the extensions of include/kvl/mla_hip.h.
+//
+// Contract kept from the reference (src/mla_compressed_q8_state.c, mla_compressed_state.c,
+// mla_state.c): states own calloc'd host arrays that stay authoritative; every call is
+// synchronous with host buffers; -1 on invalid arguments with the state unchanged; weights
+// are borrowed per call. What the GPU adds:
+//   * a device mirror per state (keyed by the struct address, validated against its host
+//     pointers and capacity) with a watermark of rows already on the device. Appended rows
+//     are produced on the device and written back to the host arrays; rows the caller adds
+//     on the host (len above the watermark) are uploaded before use; truncate/reset lower
+//     the watermark; *_sync forces a full re-upload.
+//   * a device weight cache keyed by host address + size + sampled digest, or pinned by
+//     kvl_mla_bind_weights.
+//   * one HIP stream; kernels are enqueued in order, results copied back, then synchronised.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "kvl/mla_compressed_q8_state.h"
+#include "kvl/mla_compressed_state.h"
+#include "kvl/mla_hip.h"
+#include "kvl/mla_state.h"
+#include "kvl/ops.h"
+#include "mla_internal.h"
+
+using namespace kvl;
+
+namespace {
+
+thread_local std::string g_err;
+
+void set_err(const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+}
+
+#define HIP_TRY(expr)                                                                   \
+    do {                                                                                \
+        hipError_t e_ = (expr);                                                         \
+        if (e_ != hipSuccess) {                                                         \
+            set_err("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__,   \
+                    __LINE__);                                                          \
+            return -1;                                                                  \
+        }                                                                               \
+    } while (0)
+
+// ---------------------------------------------------------------- device buffers --------
+
+struct DevBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+};
+
+int dev_reserve(DevBuf &b, size_t bytes) {
+    if (bytes <= b.bytes) return 0;
+    if (b.p) {
+        hipError_t e = hipFree(b.p);
+        b.p = nullptr;
+        b.bytes = 0;
+        if (e != hipSuccess) {
+            set_err("hipFree: %s", hipGetErrorString(e));
+            return -1;
+        }
+    }
+    size_t want = bytes < 4096 ? 4096 : bytes + bytes / 4;
+    hipError_t e = hipMalloc(&b.p, want);
+    if (e != hipSuccess) {
+        b.p = nullptr;
+        set_err("hipMalloc(%zu): %s", want, hipGetErrorString(e));
+        return -1;
+    }
+    b.bytes = want;
+    return 0;
+}
+
+struct PinBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+};
+
+int pin_reserve(PinBuf &b, size_t bytes) {
+    if (bytes <= b.bytes) return 0;
+    if (b.p) (void)hipHostFree(b.p);
+    b.p = nullptr;
+    b.bytes = 0;
+    size_t want = bytes < 65536 ? 65536 : bytes + bytes / 4;
+    hipError_t e = hipHostMalloc(&b.p, want, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        b.p = nullptr;
+        set_err("hipHostMalloc(%zu): %s", want, hipGetErrorString(e));
+        return -1;
+    }
+    b.bytes = want;
+    return 0;
+}
+
+// ---------------------------------------------------------------- context ---------------
+
+struct WeightEntry {
+    size_t bytes = 0;
+    uint64_t digest = 0;
+    void *dev = nullptr;
+    int pins = 0;
+};
+
+struct Mirror {
+    int fmt = 0;
+    const void *ha = nullptr, *hb = nullptr, *hc = nullptr;  // host arrays at creation
+    int capacity = 0;
+    int d0 = 0, d1 = 0, d2 = 0;  // Q8/F32: R, DR; Exp: NH, QD, DV
+    void *a = nullptr, *b = nullptr, *c = nullptr;
+    int synced = 0;  // rows [0, synced) valid on the device
+};
+
+struct RopeTable {
+    float2 *dev = nullptr;
+    int npos = 0;
+};
+
+struct Ctx {
+    std::recursive_mutex mu;
+    bool ready = false;
+    int device = 0;
+    int ncu = 256;
+    hipStream_t stream = nullptr;
+    std::unordered_map<const void *, WeightEntry> weights;
+    std::unordered_map<const void *, Mirror> mirrors;
+    std::unordered_map<uint64_t, RopeTable> ropes;  // key: theta bits << 16 | DR
+    DevBuf work, part, scores, prefill;
+    PinBuf pin_in, pin_out;
+    bool capturing = false;
+};
+
+Ctx &ctx() {
+    static Ctx *c = new Ctx();  // never destroyed: device memory is released by the driver
+    return *c;
+}
+
+int ensure_ready() {
+    Ctx &c = ctx();
+    if (c.ready) return 0;
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, dev));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        set_err("libkvl_mla is built for gfx950; device %d is %s", dev, prop.gcnArchName);
+        return -1;
+    }
+    HIP_TRY(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
+    c.device = dev;
+    c.ncu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+    c.ready = true;
+    return 0;
+}
+
+// ---------------------------------------------------------------- shapes ----------------
+
+bool dims_of(const KvlMlaConfig *cfg, Dims &d) {
+    if (!cfg || cfg->hidden_size <= 0 || cfg->num_heads <= 0 || cfg->qk_nope_dim <= 0 ||
+        cfg->qk_rope_dim <= 0 || (cfg->qk_rope_dim & 1) || cfg->v_head_dim <= 0 ||
+        cfg->kv_lora_rank <= 0 || cfg->rope_theta <= 0.0f)
+        return false;
+    d.H = cfg->hidden_size;
+    d.NH = cfg->num_heads;
+    d.DN = cfg->qk_nope_dim;
+    d.DR = cfg->qk_rope_dim;
+    d.DV = cfg->v_head_dim;
+    d.R = cfg->kv_lora_rank;
+    d.QD = d.DN + d.DR;
+    d.QO = d.NH * d.QD;
+    d.KVO = d.R + d.DR;
+    d.KVB = d.NH * (d.DN + d.DV);
+    d.HO = d.NH * d.DV;
+    return true;
+}
+
+// Kernel bounds of the device path (kMaxR / kMaxDR / kMaxDN in mla_decode.hip).
+bool dims_supported(const Dims &d) {
+    if (d.R > 1024 || d.DR > 256 || d.DN > 512) {
+        set_err("dims beyond the device kernels' bounds (R<=1024, DR<=256, DN<=512)");
+        return false;
+    }
+    return true;
+}
+
+bool kimi_attn(const Dims &d) { return d.NH == 16 && d.R == 512 && d.DR == 64; }
+
+// ---------------------------------------------------------------- weights ---------------
+
+uint64_t fnv(uint64_t h, const void *p, size_t n) {
+    const unsigned char *b = (const unsigned char *)p;
+    for (size_t i = 0; i < n; ++i) {
+        h ^= b[i];
+        h *= 0x100000001b3ull;
+    }
+    return h;
+}
+
+// Digest of 18 sampled 64-byte windows (first, last and 16 evenly spaced) plus the size.
+uint64_t sample_digest(const void *p, size_t bytes) {
+    uint64_t h = fnv(0xcbf29ce484222325ull, &bytes, sizeof bytes);
+    const unsigned char *b = (const unsigned char *)p;
+    const size_t win = 64;
+    if (bytes <= 18 * win) return fnv(h, b, bytes);
+    h = fnv(h, b, win);
+    h = fnv(h, b + bytes - win, win);
+    for (int i = 1; i <= 16; ++i) {
+        const size_t off = (bytes - win) / 17 * (size_t)i;
+        h = fnv(h, b + off, win);
+    }
+    return h;
+}
+
+int dev_weight(const uint16_t *host, size_t elems, const uint16_t **out) {
+    Ctx &c = ctx();
+    const size_t bytes = elems * sizeof(uint16_t);
+    auto it = c.weights.find(host);
+    if (it != c.weights.end() && it->second.bytes == bytes) {
+        if (it->second.pins > 0 || it->second.digest == sample_digest(host, bytes)) {
+            *out = (const uint16_t *)it->second.dev;
+            return 0;
+        }
+    }
+    WeightEntry e;
+    if (it != c.weights.end()) {
+        e = it->second;
+        if (e.bytes != bytes) {
+            HIP_TRY(hipFree(e.dev));
+            e.dev = nullptr;
+        }
+    }
+    if (!e.dev) HIP_TRY(hipMalloc(&e.dev, bytes));
+    e.bytes = bytes;
+    HIP_TRY(hipMemcpy(e.dev, host, bytes, hipMemcpyHostToDevice));
+    e.digest = sample_digest(host, bytes);
+    c.weights[host] = e;
+    *out = (const uint16_t *)e.dev;
+    return 0;
+}
+
+struct DevWeights {
+    const uint16_t *q, *kva, *norm, *kvb, *o;
+};
+
+int dev_weights(const KvlMlaBF16 *w, const Dims &d, DevWeights &dw) {
+    if (dev_weight(w->q_proj, (size_t)d.QO * d.H, &dw.q) != 0) return -1;
+    if (dev_weight(w->kv_a_proj, (size_t)d.KVO * d.H, &dw.kva) != 0) return -1;
+    if (dev_weight(w->kv_a_norm, (size_t)d.R, &dw.norm) != 0) return -1;
+    if (dev_weight(w->kv_b_proj, (size_t)d.KVB * d.R, &dw.kvb) != 0) return -1;
+    if (dev_weight(w->o_proj, (size_t)d.H * d.HO, &dw.o) != 0) return -1;
+    return 0;
+}
+
+bool weights_ok(const KvlMlaBF16 *w) {
+    return w && w->q_proj && w->kv_a_proj && w->kv_a_norm && w->kv_b_proj && w->o_proj;
+}
+
+// ---------------------------------------------------------------- RoPE table ------------
+
+// (cos, sin) of pos * theta^(-2i/DR) computed exactly as src/mla_compressed_q8_state.c:22-25:
+// double pow/cos/sin, rounded to float. The device kernels only apply the rotation.
+int rope_table(float theta, int DR, int need_pos, const float2 **out) {
+    Ctx &c = ctx();
+    uint32_t tb;
+    memcpy(&tb, &theta, sizeof tb);
+    const uint64_t key = ((uint64_t)tb << 16) | (uint64_t)DR;
+    RopeTable &t = c.ropes[key];
+    if (need_pos > t.npos) {
+        if (c.capturing) {
+            set_err("RoPE table growth during graph capture");
+            return -1;
+        }
+        int npos = 1024;
+        while (npos < need_pos) npos *= 2;
+        const int half = DR / 2;
+        std::vector<float2> h((size_t)npos * half);
+        for (int i = 0; i < half; ++i) {
+            const double freq = pow((double)theta, -((double)(2 * i) / (double)DR));
+            for (int p = 0; p < npos; ++p) {
+                const double ang = (double)p * freq;
+                h[(size_t)p * half + i] = make_float2((float)cos(ang), (float)sin(ang));
+            }
+        }
+        if (t.dev) HIP_TRY(hipFree(t.dev));
+        t.dev = nullptr;
+        t.npos = 0;
+        HIP_TRY(hipMalloc((void **)&t.dev, h.size() * sizeof(float2)));
+        HIP_TRY(hipMemcpy(t.dev, h.data(), h.size() * sizeof(float2), hipMemcpyHostToDevice));
+        t.npos = npos;
+    }
+    *out = t.dev;
+    return 0;
+}
+
+// ---------------------------------------------------------------- state mirrors ---------
+
+size_t row_bytes_of(int fmt, int d0, int d1, int d2) {
+    if (fmt == kFmtQ8) return (size_t)d0 + 4 + 2 * (size_t)d1;
+    if (fmt == kFmtF32) return 4 * ((size_t)d0 + (size_t)d1);
+    return 4 * (size_t)d0 * ((size_t)d1 + (size_t)d2);
+}
+
+void mirror_free(Mirror &m) {
+    if (m.a) (void)hipFree(m.a);
+    if (m.b) (void)hipFree(m.b);
+    if (m.c) (void)hipFree(m.c);
+    m.a = m.b = m.c = nullptr;
+}
+
+void mirror_drop(const void *key) {
+    Ctx &c = ctx();
+    auto it = c.mirrors.find(key);
+    if (it == c.mirrors.end()) return;
+    mirror_free(it->second);
+    c.mirrors.erase(it);
+}
+
+void mirror_lower(const void *key, int len) {
+    Ctx &c = ctx();
+    auto it = c.mirrors.find(key);
+    if (it != c.mirrors.end() && it->second.synced > len) it->second.synced = len;
+}
+
+// Host array sizes (elements) of each component per row.
+struct HostView {
+    int fmt;
+    const void *ha, *hb, *hc;
+    int capacity, len;
+    int d0, d1, d2;
+};
+
+HostView view_of(const KvlMlaCompressedQ8State *s) {
+    return {kFmtQ8, s->latent_q8, s->latent_scale, s->rope_bf16, s->capacity, s->len,
+            s->kv_lora_rank, s->qk_rope_dim, 0};
+}
+HostView view_of(const KvlMlaCompressedState *s) {
+    return {kFmtF32, s->latent, s->rope, nullptr, s->capacity, s->len, s->kv_lora_rank,
+            s->qk_rope_dim, 0};
+}
+HostView view_of(const KvlMlaState *s) {
+    return {kFmtExp, s->keys, s->values, nullptr, s->capacity, s->len, s->num_heads,
+            s->qk_nope_dim + s->qk_rope_dim, s->v_head_dim};
+}
+
+// Element sizes (bytes) of the arrays a/b/c per row.
+void comp_bytes(int fmt, int d0, int d1, int d2, size_t &ea, size_t &eb, size_t &ec) {
+    if (fmt == kFmtQ8) {
+        ea = (size_t)d0;
+        eb = 4;
+        ec = 2 * (size_t)d1;
+    } else if (fmt == kFmtF32) {
+        ea = 4 * (size_t)d0;
+        eb = 4 * (size_t)d1;
+        ec = 0;
+    } else {
+        ea = 4 * (size_t)d0 * d1;
+        eb = 4 * (size_t)d0 * d2;
+        ec = 0;
+    }
+}
+
+int upload_rows(Mirror &m, const HostView &v, int r0, int r1, hipStream_t st) {
+    if (r1 <= r0) return 0;
+    size_t ea, eb, ec;
+    comp_bytes(m.fmt, m.d0, m.d1, m.d2, ea, eb, ec);
+    const size_t n = (size_t)(r1 - r0);
+    HIP_TRY(hipMemcpyAsync((char *)m.a + ea * r0, (const char *)v.ha + ea * r0, ea * n,
+                           hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync((char *)m.b + eb * r0, (const char *)v.hb + eb * r0, eb * n,
+                           hipMemcpyHostToDevice, st));
+    if (ec)
+        HIP_TRY(hipMemcpyAsync((char *)m.c + ec * r0, (const char *)v.hc + ec * r0, ec * n,
+                               hipMemcpyHostToDevice, st));
+    return 0;
+}
+
+// Device mirror of a state, created or re-created when the host arrays changed, and synced
+// up to the host len (unless `no_upload`, used by the synthetic fill).
+int mirror_get(const void *key, const HostView &v, Mirror **out, bool no_upload = false) {
+    Ctx &c = ctx();
+    auto it = c.mirrors.find(key);
+    if (it != c.mirrors.end()) {
+        Mirror &m = it->second;
+        if (m.fmt != v.fmt || m.ha != v.ha || m.hb != v.hb || m.hc != v.hc ||
+            m.capacity != v.capacity || m.d0 != v.d0 || m.d1 != v.d1 || m.d2 != v.d2) {
+            mirror_free(m);
+            c.mirrors.erase(it);
+            it = c.mirrors.end();
+        }
+    }
+    if (it == c.mirrors.end()) {
+        if (c.capturing) {
+            set_err("state mirror creation during graph capture");
+            return -1;
+        }
+        Mirror m;
+        m.fmt = v.fmt;
+        m.ha = v.ha;
+        m.hb = v.hb;
+        m.hc = v.hc;
+        m.capacity = v.capacity;
+        m.d0 = v.d0;
+        m.d1 = v.d1;
+        m.d2 = v.d2;
+        size_t ea, eb, ec;
+        comp_bytes(v.fmt, v.d0, v.d1, v.d2, ea, eb, ec);
+        const size_t cap = (size_t)v.capacity;
+        hipError_t e = hipMalloc(&m.a, ea * cap);
+        if (e == hipSuccess) e = hipMalloc(&m.b, eb * cap);
+        if (e == hipSuccess && ec) e = hipMalloc(&m.c, ec * cap);
+        if (e != hipSuccess) {
+            mirror_free(m);
+            set_err("state mirror allocation (%zu rows): %s", cap, hipGetErrorString(e));
+            return -1;
+        }
+        it = c.mirrors.emplace(key, m).first;
+    }
+    Mirror &m = it->second;
+    if (m.synced > v.len) m.synced = v.len;
+    if (!no_upload && m.synced < v.len) {
+        if (upload_rows(m, v, m.synced, v.len, c.stream) != 0) return -1;
+        m.synced = v.len;
+    }
+    *out = &m;
+    return 0;
+}
+
+// ---------------------------------------------------------------- workspace -------------
+
+struct Layout {
+    size_t off = 0;
+    template <class T>
+    T *take(char *base, size_t n) {
+        off = (off + 255) & ~(size_t)255;
+        T *p = (T *)(base + off);
+        off += n * sizeof(T);
+        return p;
+    }
+};
+
+// Carves DecodeWork for a group of B sequences out of the workspace buffer.
+int decode_work(const Dims &d, int B, int row_bytes, DecodeWork &w) {
+    Ctx &c = ctx();
+    const size_t qs = (size_t)std::max(d.R + d.DR, d.QD);
+    auto carve = [&](char *base, Layout &L) {
+        w.x = L.take<float>(base, (size_t)B * d.H);
+        w.y = L.take<float>(base, (size_t)B * (d.QO + d.KVO));
+        w.qf = L.take<float>(base, (size_t)B * d.NH * qs);
+        w.qhi = L.take<int8_t>(base, (size_t)B * d.NH * d.R);
+        w.qlo = L.take<int8_t>(base, (size_t)B * d.NH * d.R);
+        w.qs = L.take<float>(base, (size_t)B * d.NH);
+        w.qrhi = L.take<uint16_t>(base, (size_t)B * d.NH * d.DR);
+        w.qrlo = L.take<uint16_t>(base, (size_t)B * d.NH * d.DR);
+        w.latent = L.take<float>(base, (size_t)B * d.R);
+        w.kv = L.take<float>(base, (size_t)B * d.KVB);
+        w.mix = L.take<float>(base, (size_t)B * d.NH * std::max(d.R, d.DV));
+        w.ho = L.take<float>(base, (size_t)B * d.HO);
+        w.out = L.take<float>(base, (size_t)B * d.H);
+        w.rows = L.take<uint8_t>(base, (size_t)B * row_bytes);
+    };
+    Layout probe;
+    carve(nullptr, probe);
+    if (c.work.bytes < probe.off) {
+        if (c.capturing) {
+            set_err("workspace growth during graph capture");
+            return -1;
+        }
+        if (dev_reserve(c.work, probe.off) != 0) return -1;
+    }
+    Layout L;
+    carve((char *)c.work.p, L);
+    return 0;
+}
+
+int reserve_part(size_t bytes, float **p) {
+    Ctx &c = ctx();
+    if (c.part.bytes < bytes) {
+        if (c.capturing) {
+            set_err("partials growth during graph capture");
+            return -1;
+        }
+        if (dev_reserve(c.part, bytes) != 0) return -1;
+    }
+    *p = (float *)c.part.p;
+    return 0;
+}
+
+// ---------------------------------------------------------------- decode core -----------
+
+struct SeqIn {
+    Mirror *m;
+    int pos;
+};
+
+// One decode step for a group of B <= kMaxBatch sequences whose mirrors are synced.
+// d_x: device input rows [B,H]; d_out: device output rows [B,H]. Rows appended on the device
+// at each pos; staged copies in w.rows.
+int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeights &dw,
+                 const SeqIn *seqs, int B, const float *d_x, float *d_out, bool residual,
+                 DecodeWork &w) {
+    Ctx &c = ctx();
+    hipStream_t st = c.stream;
+    int maxpos = 0;
+    for (int i = 0; i < B; ++i) maxpos = std::max(maxpos, seqs[i].pos);
+    const float2 *cs = nullptr;
+    if (rope_table(theta, d.DR, maxpos + 1, &cs) != 0) return -1;
+
+    const bool kimi = kimi_attn(d) && fmt != kFmtExp;
+    const int kind = !kimi ? kAttnGeneric : fmt == kFmtQ8 ? kAttnQ8Mfma : kAttnF32Mfma;
+    SeqTable t;
+    memset(&t, 0, sizeof t);
+    t.n = B;
+    long total_rows = 0;
+    int lmax = 0;
+    for (int i = 0; i < B; ++i) {
+        SeqDesc &s = t.s[i];
+        s.a = seqs[i].m->a;
+        s.b = seqs[i].m->b;
+        s.c = seqs[i].m->c;
+        s.pos = seqs[i].pos;
+        s.len = seqs[i].pos + 1;
+        total_rows += s.len;
+        lmax = std::max(lmax, s.len);
+    }
+    // split-K plan: about two workgroups per CU, rows per split a multiple of the chunk
+    int rps = 0, total_splits = 0;
+    if (kind == kAttnGeneric) {
+        for (int i = 0; i < B; ++i) {
+            t.s[i].split0 = fmt == kFmtExp ? i * d.NH : i;
+            t.s[i].nsplit = 1;
+        }
+        total_splits = fmt == kFmtExp ? B * d.NH : B;
+    } else {
+        const int chunk = kind == kAttnQ8Mfma ? 64 : 16;
+        const long target = 2L * c.ncu;
+        long per = (total_rows + target - 1) / target;
+        per = std::max<long>(per, 4L * chunk);
+        rps = (int)((per + chunk - 1) / chunk * chunk);
+        for (int i = 0; i < B; ++i) {
+            t.s[i].split0 = total_splits;
+            t.s[i].nsplit = (t.s[i].len + rps - 1) / rps;
+            total_splits += t.s[i].nsplit;
+        }
+    }
+    const int G = fmt == kFmtExp ? 1 : d.NH;
+    const int DVm = fmt == kFmtExp ? d.DV : d.R;
+    if (reserve_part((size_t)total_splits * G * (DVm + 2) * sizeof(float), &w.part) != 0) return -1;
+    if (kind == kAttnGeneric) {
+        const int P = fmt == kFmtExp ? B * d.NH : B;
+        const size_t bytes = (size_t)P * G * lmax * sizeof(float);
+        if (c.scores.bytes < bytes) {
+            if (c.capturing) {
+                set_err("score scratch growth during graph capture");
+                return -1;
+            }
+            if (dev_reserve(c.scores, bytes) != 0) return -1;
+        }
+        w.scores = (float *)c.scores.p;
+    }
+
+    const int ldy = d.QO + d.KVO;
+    HIP_TRY(launch_gemv(st, w.y, ldy, d_x, d.H, B, dw.q, d.QO, dw.kva, d.KVO, d.H, false));
+    HIP_TRY(launch_append(st, fmt, t, d, w.y, ldy, d.QO, dw.norm, eps, cs, w, false, 0));
+    if (fmt == kFmtExp) {
+        HIP_TRY(launch_gemv(st, w.kv, d.KVB, w.latent, d.R, B, dw.kvb, d.KVB, nullptr, 0, d.R, false));
+        HIP_TRY(launch_store_expanded(st, t, d, w));
+    }
+    HIP_TRY(launch_qprep(st, fmt, t, d, dw.kvb, cs, w, kind == kAttnQ8Mfma));
+    HIP_TRY(launch_attention(st, kind, fmt, t, d, rps, total_splits, lmax, w));
+    HIP_TRY(launch_combine(st, fmt, t, d, dw.kvb, w));
+    HIP_TRY(launch_gemv(st, d_out, d.H, w.ho, d.HO, B, dw.o, d.H, nullptr, 0, d.HO, residual));
+    return 0;
+}
+
+// Write staged appended rows (device w.rows) back into the host arrays.
+void write_back_rows(int fmt, const HostView &v, int pos, const uint8_t *row) {
+    if (fmt == kFmtQ8) {
+        const int R = v.d0, DR = v.d1;
+        memcpy((int8_t *)v.ha + (size_t)pos * R, row, (size_t)R);
+        memcpy((float *)v.hb + pos, row + R, 4);
+        memcpy((uint16_t *)v.hc + (size_t)pos * DR, row + R + 4, 2 * (size_t)DR);
+    } else if (fmt == kFmtF32) {
+        const int R = v.d0, DR = v.d1;
+        memcpy((float *)v.ha + (size_t)pos * R, row, 4 * (size_t)R);
+        memcpy((float *)v.hb + (size_t)pos * DR, row + 4 * (size_t)R, 4 * (size_t)DR);
+    } else {
+        const size_t nk = (size_t)v.d0 * v.d1, nv = (size_t)v.d0 * v.d2;
+        memcpy((float *)v.ha + (size_t)pos * nk, row, 4 * nk);
+        memcpy((float *)v.hb + (size_t)pos * nv, row + 4 * nk, 4 * nv);
+    }
+}
+
+// Validation shared by the host-API decode entry points (reference conditions:
+// src/mla_compressed_q8_state.c:167-180).
+template <class S>
+bool state_dims_ok(const S *s, const KvlMlaConfig *cfg);
+template <>
+bool state_dims_ok(const KvlMlaCompressedQ8State *s, const KvlMlaConfig *cfg) {
+    return s->kv_lora_rank == cfg->kv_lora_rank && s->qk_rope_dim == cfg->qk_rope_dim;
+}
+template <>
+bool state_dims_ok(const KvlMlaCompressedState *s, const KvlMlaConfig *cfg) {
+    return s->kv_lora_rank == cfg->kv_lora_rank && s->qk_rope_dim == cfg->qk_rope_dim;
+}
+template <>
+bool state_dims_ok(const KvlMlaState *s, const KvlMlaConfig *cfg) {
+    return s->num_heads == cfg->num_heads && s->qk_nope_dim == cfg->qk_nope_dim &&
+           s->qk_rope_dim == cfg->qk_rope_dim && s->v_head_dim == cfg->v_head_dim;
+}
+
+template <class S>
+int fmt_of();
+template <>
+int fmt_of<KvlMlaCompressedQ8State>() { return kFmtQ8; }
+template <>
+int fmt_of<KvlMlaCompressedState>() { return kFmtF32; }
+template <>
+int fmt_of<KvlMlaState>() { return kFmtExp; }
+
+// Host-buffer decode of one token for each of B sequences (any B). positions[i] == len.
+template <class S>
+int decode_host(float *out, const float *x, const int *positions, int B, const KvlMlaConfig *cfg,
+                const KvlMlaBF16 *w, S *const *states) {
+    Dims d;
+    if (!out || !x || B <= 0 || !states || !weights_ok(w) || !dims_of(cfg, d)) {
+        set_err("invalid arguments");
+        return -1;
+    }
+    for (int i = 0; i < B; ++i) {
+        const S *s = states[i];
+        const int pos = positions ? positions[i] : (s ? s->len : -1);
+        if (!s || pos != s->len || pos < 0 || pos >= s->capacity || !state_dims_ok(s, cfg)) {
+            set_err("sequence %d: position/capacity/dims check failed", i);
+            return -1;
+        }
+    }
+    if (!dims_supported(d)) return -1;
+    if (ensure_ready() != 0) return -1;
+    Ctx &c = ctx();
+    const int fmt = fmt_of<S>();
+    DevWeights dw;
+    if (dev_weights(w, d, dw) != 0) return -1;
+    const size_t rb = fmt == kFmtExp ? row_bytes_of(fmt, d.NH, d.QD, d.DV)
+                                     : row_bytes_of(fmt, d.R, d.DR, 0);
+    for (int g0 = 0; g0 < B; g0 += kMaxBatch) {
+        const int n = std::min(kMaxBatch, B - g0);
+        DecodeWork wk;
+        if (decode_work(d, n, (int)rb, wk) != 0) return -1;
+        SeqIn seqs[kMaxBatch];
+        for (int i = 0; i < n; ++i) {
+            S *s = states[g0 + i];
+            Mirror *m = nullptr;
+            if (mirror_get(s, view_of(s), &m) != 0) return -1;
+            seqs[i] = {m, s->len};
+        }
+        const size_t xin = (size_t)n * d.H * sizeof(float);
+        const size_t outb = xin + (size_t)n * rb;
+        if (pin_reserve(c.pin_in, xin) != 0 || pin_reserve(c.pin_out, outb) != 0) return -1;
+        memcpy(c.pin_in.p, x + (size_t)g0 * d.H, xin);
+        HIP_TRY(hipMemcpyAsync(wk.x, c.pin_in.p, xin, hipMemcpyHostToDevice, c.stream));
+        if (decode_group(fmt, d, cfg->rms_eps, cfg->rope_theta, dw, seqs, n, wk.x, wk.out, false, wk) != 0)
+            return -1;
+        HIP_TRY(hipMemcpyAsync(c.pin_out.p, wk.out, xin, hipMemcpyDeviceToHost, c.stream));
+        HIP_TRY(hipMemcpyAsync((char *)c.pin_out.p + xin, wk.rows, (size_t)n * rb,
+                               hipMemcpyDeviceToHost, c.stream));
+        HIP_TRY(hipStreamSynchronize(c.stream));
+        memcpy(out + (size_t)g0 * d.H, c.pin_out.p, xin);
+        for (int i = 0; i < n; ++i) {
+            S *s = states[g0 + i];
+            const int pos = s->len;
+            write_back_rows(fmt, view_of(s), pos, (const uint8_t *)c.pin_out.p + xin + (size_t)i * rb);
+            s->len = pos + 1;
+            seqs[i].m->synced = s->len;
+        }
+    }
+    return 0;
+}
+
+// Stream-ordered decode over device buffers (bound weights, synced mirrors).
+template <class S>
+int decode_device(float *d_out, const float *d_x, int B, const KvlMlaConfig *cfg,
+                  const KvlMlaBF16 *w, S *const *states, unsigned flags) {
+    Dims d;
+    if (!d_out || !d_x || B <= 0 || !states || !weights_ok(w) || !dims_of(cfg, d)) {
+        set_err("invalid arguments");
+        return -1;
+    }
+    for (int i = 0; i < B; ++i) {
+        const S *s = states[i];
+        if (!s || s->len < 0 || s->len >= s->capacity || !state_dims_ok(s, cfg)) {
+            set_err("sequence %d: capacity/dims check failed", i);
+            return -1;
+        }
+    }
+    if (!dims_supported(d)) return -1;
+    if (ensure_ready() != 0) return -1;
+    Ctx &c = ctx();
+    const int fmt = fmt_of<S>();
+    DevWeights dw;
+    if (dev_weights(w, d, dw) != 0) return -1;
+    const size_t rb = row_bytes_of(fmt, d.R, d.DR, 0);
+    for (int g0 = 0; g0 < B; g0 += kMaxBatch) {
+        const int n = std::min(kMaxBatch, B - g0);
+        DecodeWork wk;
+        if (decode_work(d, n, (int)rb, wk) != 0) return -1;
+        SeqIn seqs[kMaxBatch];
+        for (int i = 0; i < n; ++i) {
+            S *s = states[g0 + i];
+            Mirror *m = nullptr;
+            if (mirror_get(s, view_of(s), &m) != 0) return -1;
+            seqs[i] = {m, s->len};
+        }
+        if (decode_group(fmt, d, cfg->rms_eps, cfg->rope_theta, dw, seqs, n, d_x + (size_t)g0 * d.H,
+                         d_out + (size_t)g0 * d.H, (flags & KVL_MLA_RESIDUAL) != 0, wk) != 0)
+            return -1;
+        if (!(flags & KVL_MLA_NO_ADVANCE)) {
+            for (int i = 0; i < n; ++i) {
+                S *s = states[g0 + i];
+                s->len += 1;
+                seqs[i].m->synced = s->len;  // host rows of the new position are not written
+            }
+        }
+    }
+    (void)c;
+    return 0;
+}
+
+// State prefill-fill (src/mla_compressed_state.c:52-84, src/mla_compressed_q8_state.c:
+// 129-159): kv_a GEMV of every token, then the append kernel in rows mode.
+template <class S>
+int state_prefill(const float *x, int seq_len, const KvlMlaConfig *cfg, const KvlMlaBF16 *w, S *s) {
+    if (!x || !cfg || !w || !s || !w->kv_a_proj || !w->kv_a_norm || seq_len <= 0 || s->len != 0 ||
+        seq_len > s->capacity || !state_dims_ok(s, cfg)) {
+        set_err("invalid arguments");
+        return -1;
+    }
+    const int H = cfg->hidden_size, R = cfg->kv_lora_rank, DR = cfg->qk_rope_dim;
+    if (H <= 0 || R <= 0 || DR <= 0 || (DR & 1) || !(cfg->rope_theta > 0.0f)) {
+        set_err("invalid config");
+        return -1;
+    }
+    if (R > 1024 || DR > 256) {
+        set_err("dims beyond the device kernels' bounds");
+        return -1;
+    }
+    if (ensure_ready() != 0) return -1;
+    Ctx &c = ctx();
+    const int fmt = fmt_of<S>();
+    Dims d{};
+    d.H = H;
+    d.R = R;
+    d.DR = DR;
+    d.KVO = R + DR;
+    d.NH = 1;
+    const uint16_t *kva = nullptr, *norm = nullptr;
+    if (dev_weight(w->kv_a_proj, (size_t)d.KVO * H, &kva) != 0) return -1;
+    if (dev_weight(w->kv_a_norm, (size_t)R, &norm) != 0) return -1;
+    Mirror *m = nullptr;
+    if (mirror_get(s, view_of(s), &m) != 0) return -1;
+    const float2 *cs = nullptr;
+    if (rope_table(cfg->rope_theta, DR, seq_len, &cs) != 0) return -1;
+    const size_t rb = row_bytes_of(fmt, R, DR, 0);
+    const int chunk = 4096;
+    for (int t0 = 0; t0 < seq_len; t0 += chunk) {
+        const int n = std::min(chunk, seq_len - t0);
+        Layout L;
+        L.take<float>(nullptr, (size_t)n * H);
+        L.take<float>(nullptr, (size_t)n * d.KVO);
+        L.take<uint8_t>(nullptr, (size_t)n * rb);
+        if (dev_reserve(c.prefill, L.off) != 0) return -1;
+        Layout L2;
+        char *base = (char *)c.prefill.p;
+        float *dx = L2.take<float>(base, (size_t)n * H);
+        float *dy = L2.take<float>(base, (size_t)n * d.KVO);
+        uint8_t *drows = L2.take<uint8_t>(base, (size_t)n * rb);
+        HIP_TRY(hipMemcpyAsync(dx, x + (size_t)t0 * H, (size_t)n * H * sizeof(float),
+                               hipMemcpyHostToDevice, c.stream));
+        for (int b0 = 0; b0 < n; b0 += 16 * 65535) {
+            const int nb = std::min(n - b0, 16 * 65535);
+            HIP_TRY(launch_gemv(c.stream, dy + (size_t)b0 * d.KVO, d.KVO, dx + (size_t)b0 * H, H, nb,
+                                kva, d.KVO, nullptr, 0, H, false));
+        }
+        SeqTable t;
+        memset(&t, 0, sizeof t);
+        t.n = 1;
+        t.s[0].a = m->a;
+        t.s[0].b = m->b;
+        t.s[0].c = m->c;
+        t.s[0].pos = t0;
+        DecodeWork wk{};
+        wk.rows = drows;
+        HIP_TRY(launch_append(c.stream, fmt, t, d, dy, d.KVO, 0, norm, cfg->rms_eps, cs, wk, false, n));
+        if (pin_reserve(c.pin_out, (size_t)n * rb) != 0) return -1;
+        HIP_TRY(hipMemcpyAsync(c.pin_out.p, drows, (size_t)n * rb, hipMemcpyDeviceToHost, c.stream));
+        HIP_TRY(hipStreamSynchronize(c.stream));
+        const HostView v = view_of(s);
+        for (int i = 0; i < n; ++i)
+            write_back_rows(fmt, v, t0 + i, (const uint8_t *)c.pin_out.p + (size_t)i * rb);
+    }
+    s->len = seq_len;
+    m->synced = seq_len;
+    return 0;
+}
+
+// Causal prefill (src/mla_prefill_streaming.c:78-206). d_x/d_out device buffers.
+int prefill_device(float *d_out, const float *d_x, int S, const KvlMlaConfig *cfg, const KvlMlaBF16 *w) {
+    Dims d;
+    if (!d_out || !d_x || S <= 0 || !weights_ok(w) || !dims_of(cfg, d)) {
+        set_err("invalid arguments");
+        return -1;
+    }
+    if (ensure_ready() != 0) return -1;
+    Ctx &c = ctx();
+    DevWeights dw;
+    if (dev_weights(w, d, dw) != 0) return -1;
+    const float2 *cs = nullptr;
+    if (rope_table(cfg->rope_theta, d.DR, S, &cs) != 0) return -1;
+    const size_t bytes = prefill_bytes(d, S);
+    if (c.scores.bytes < bytes) {
+        if (c.capturing) {
+            set_err("prefill workspace growth during graph capture");
+            return -1;
+        }
+        if (dev_reserve(c.scores, bytes) != 0) return -1;
+    }
+    HIP_TRY(launch_prefill_all(c.stream, d, S, cfg->rms_eps, d_x, d_out, dw.q, dw.kva, dw.norm, dw.kvb,
+                               dw.o, cs, c.scores.p));
+    return 0;
+}
+
+struct Guard {
+    std::lock_guard<std::recursive_mutex> g;
+    Guard() : g(ctx().mu) { g_err.clear(); }
+};
+
+}  // namespace
+
+// ==================================================================== C ABI ==============
+
+extern "C" {
+
+// ---- include/kvl/ops.h ---------------------------------------------------------------
+
+// src/ops.c:12-17: the BF16 word is the high half of the FP32 word (a bit operation).
+float kvl_bf16_to_f32(uint16_t x) {
+    const uint32_t u = (uint32_t)x << 16;
+    float f;
+    memcpy(&f, &u, sizeof f);
+    return f;
+}
+
+// src/ops.c:53-66 on the GPU (void return as the reference: failures leave y untouched and
+// are reported through kvl_mla_last_error()).
+void kvl_matvec_bf16(float *y, const float *x, const uint16_t *w, int in, int out) {
+    Guard guard;
+    if (!y || !x || !w || in <= 0 || out <= 0) {
+        set_err("invalid arguments");
+        return;
+    }
+    if (ensure_ready() != 0) return;
+    Ctx &c = ctx();
+    const uint16_t *dw = nullptr;
+    if (dev_weight(w, (size_t)in * out, &dw) != 0) return;
+    Layout L;
+    L.take<float>(nullptr, (size_t)in);
+    L.take<float>(nullptr, (size_t)out);
+    if (dev_reserve(c.prefill, L.off) != 0) return;
+    Layout L2;
+    float *dx = L2.take<float>((char *)c.prefill.p, (size_t)in);
+    float *dy = L2.take<float>((char *)c.prefill.p, (size_t)out);
+    if (hipMemcpyAsync(dx, x, (size_t)in * 4, hipMemcpyHostToDevice, c.stream) != hipSuccess ||
+        launch_gemv(c.stream, dy, out, dx, in, 1, dw, out, nullptr, 0, in, false) != hipSuccess ||
+        hipMemcpyAsync(y, dy, (size_t)out * 4, hipMemcpyDeviceToHost, c.stream) != hipSuccess ||
+        hipStreamSynchronize(c.stream) != hipSuccess)
+        set_err("kvl_matvec_bf16: device error");
+}
+
+// src/ops.c:76-83 on the GPU.
+void kvl_rmsnorm_bf16(float *y, const float *x, const uint16_t *weight, int n, float eps) {
+    Guard guard;
+    if (!y || !x || !weight || n <= 0) {
+        set_err("invalid arguments");
+        return;
+    }
+    if (ensure_ready() != 0) return;
+    Ctx &c = ctx();
+    Layout L;
+    L.take<float>(nullptr, (size_t)n);
+    L.take<float>(nullptr, (size_t)n);
+    L.take<uint16_t>(nullptr, (size_t)n);
+    if (dev_reserve(c.prefill, L.off) != 0) return;
+    Layout L2;
+    char *base = (char *)c.prefill.p;
+    float *dx = L2.take<float>(base, (size_t)n);
+    float *dy = L2.take<float>(base, (size_t)n);
+    uint16_t *dwt = L2.take<uint16_t>(base, (size_t)n);
+    if (hipMemcpyAsync(dx, x, (size_t)n * 4, hipMemcpyHostToDevice, c.stream) != hipSuccess ||
+        hipMemcpyAsync(dwt, weight, (size_t)n * 2, hipMemcpyHostToDevice, c.stream) != hipSuccess ||
+        launch_rmsnorm(c.stream, dy, dx, dwt, n, 1, eps) != hipSuccess ||
+        hipMemcpyAsync(y, dy, (size_t)n * 4, hipMemcpyDeviceToHost, c.stream) != hipSuccess ||
+        hipStreamSynchronize(c.stream) != hipSuccess)
+        set_err("kvl_rmsnorm_bf16: device error");
+}
+
+// src/mla_prefill_streaming.c:78-206 (declared at include/kvl/ops.h:63-64), on the GPU.
+int kvl_mla_prefill_bf16(float *out, const float *x, int seq_len, const KvlMlaConfig *cfg,
+                         const KvlMlaBF16 *w) {
+    Guard guard;
+    Dims d;
+    if (!out || !x || seq_len <= 0 || !weights_ok(w) || !dims_of(cfg, d)) {
+        set_err("invalid arguments");
+        return -1;
+    }
+    if (ensure_ready() != 0) return -1;
+    Ctx &c = ctx();
+    const size_t io = (size_t)seq_len * d.H * sizeof(float);
+    if (dev_reserve(c.prefill, 2 * io + 512) != 0) return -1;
+    float *dx = (float *)c.prefill.p;
+    float *dout = (float *)((char *)c.prefill.p + ((io + 255) & ~(size_t)255));
+    HIP_TRY(hipMemcpyAsync(dx, x, io, hipMemcpyHostToDevice, c.stream));
+    if (prefill_device(dout, dx, seq_len, cfg, w) != 0) return -1;
+    HIP_TRY(hipMemcpyAsync(out, dout, io, hipMemcpyDeviceToHost, c.stream));
+    HIP_TRY(hipStreamSynchronize(c.stream));
+    return 0;
+}
+
+int kvl_mla_prefill_device(float *d_out, const float *d_x, int seq_len, const KvlMlaConfig *cfg,
+                           const KvlMlaBF16 *w) {
+    Guard guard;
+    return prefill_device(d_out, d_x, seq_len, cfg, w);
+}
+
+// ---- include/kvl/mla_state.h (expanded state) ------------------------------------------
+
+int kvl_mla_state_init(KvlMlaState *state, const KvlMlaConfig *cfg, int capacity) {
+    Guard guard;
+    if (!state || !cfg || capacity <= 0 || cfg->num_heads <= 0 || cfg->qk_nope_dim <= 0 ||
+        cfg->qk_rope_dim <= 0 || cfg->v_head_dim <= 0)
+        return -1;
+    mirror_drop(state);
+    memset(state, 0, sizeof(*state));
+    const size_t qd = (size_t)cfg->qk_nope_dim + (size_t)cfg->qk_rope_dim;
+    state->keys = (float *)calloc((size_t)capacity * cfg->num_heads * qd, sizeof(float));
+    state->values =
+        (float *)calloc((size_t)capacity * cfg->num_heads * (size_t)cfg->v_head_dim, sizeof(float));
+    if (!state->keys || !state->values) {
+        free(state->keys);
+        free(state->values);
+        memset(state, 0, sizeof(*state));
+        return -1;
+    }
+    state->capacity = capacity;
+    state->num_heads = cfg->num_heads;
+    state->qk_nope_dim = cfg->qk_nope_dim;
+    state->qk_rope_dim = cfg->qk_rope_dim;
+    state->v_head_dim = cfg->v_head_dim;
+    return 0;
+}
+
+void kvl_mla_state_reset(KvlMlaState *state) {
+    Guard guard;
+    if (!state) return;
+    state->len = 0;
+    mirror_lower(state, 0);
+}
+
+void kvl_mla_state_free(KvlMlaState *state) {
+    Guard guard;
+    if (!state) return;
+    mirror_drop(state);
+    free(state->keys);
+    free(state->values);
+    memset(state, 0, sizeof(*state));
+}
+
+size_t kvl_mla_state_bytes(const KvlMlaState *state) {
+    if (!state || state->capacity <= 0) return 0;
+    const size_t qd = (size_t)state->qk_nope_dim + (size_t)state->qk_rope_dim;
+    const size_t per = (size_t)state->num_heads * (qd + (size_t)state->v_head_dim) * sizeof(float);
+    return sizeof(*state) + (size_t)state->capacity * per;
+}
+
+int kvl_mla_decode_bf16(float *out, const float *x, int position, const KvlMlaConfig *cfg,
+                        const KvlMlaBF16 *w, KvlMlaState *state) {
+    Guard guard;
+    KvlMlaState *st[1] = {state};
+    return decode_host(out, x, &position, 1, cfg, w, st);
+}
+
+// ---- include/kvl/mla_compressed_state.h ---------------------------------------------------
+
+int kvl_mla_compressed_state_init(KvlMlaCompressedState *state, const KvlMlaConfig *cfg, int capacity) {
+    Guard guard;
+    if (!state || !cfg || capacity <= 0 || cfg->kv_lora_rank <= 0 || cfg->qk_rope_dim <= 0 ||
+        (cfg->qk_rope_dim & 1))
+        return -1;
+    mirror_drop(state);
+    memset(state, 0, sizeof(*state));
+    state->latent = (float *)calloc((size_t)capacity * cfg->kv_lora_rank, sizeof(float));
+    state->rope = (float *)calloc((size_t)capacity * cfg->qk_rope_dim, sizeof(float));
+    if (!state->latent || !state->rope) {
+        free(state->latent);
+        free(state->rope);
+        memset(state, 0, sizeof(*state));
+        return -1;
+    }
+    state->capacity = capacity;
+    state->kv_lora_rank = cfg->kv_lora_rank;
+    state->qk_rope_dim = cfg->qk_rope_dim;
+    return 0;
+}
+
+void kvl_mla_compressed_state_reset(KvlMlaCompressedState *state) {
+    Guard guard;
+    if (!state) return;
+    state->len = 0;
+    mirror_lower(state, 0);
+}
+
+int kvl_mla_compressed_state_truncate(KvlMlaCompressedState *state, int new_len) {
+    Guard guard;
+    if (!state || new_len < 0 || new_len > state->len) return -1;
+    state->len = new_len;
+    mirror_lower(state, new_len);
+    return 0;
+}
+
+void kvl_mla_compressed_state_free(KvlMlaCompressedState *state) {
+    Guard guard;
+    if (!state) return;
+    mirror_drop(state);
+    free(state->latent);
+    free(state->rope);
+    memset(state, 0, sizeof(*state));
+}
+
+size_t kvl_mla_compressed_state_bytes(const KvlMlaCompressedState *state) {
+    if (!state || state->capacity <= 0) return 0;
+    return sizeof(*state) + (size_t)state->capacity *
+                                ((size_t)state->kv_lora_rank + (size_t)state->qk_rope_dim) * sizeof(float);
+}
+
+int kvl_mla_compressed_state_prefill_bf16(const float *x, int seq_len, const KvlMlaConfig *cfg,
+                                          const KvlMlaBF16 *w, KvlMlaCompressedState *state) {
+    Guard guard;
+    return state_prefill(x, seq_len, cfg, w, state);
+}
+
+int kvl_mla_decode_compressed_bf16(float *out, const float *x, int position, const KvlMlaConfig *cfg,
+                                   const KvlMlaBF16 *w, KvlMlaCompressedState *state) {
+    Guard guard;
+    KvlMlaCompressedState *st[1] = {state};
+    return decode_host(out, x, &position, 1, cfg, w, st);
+}
+
+// src/mla_compressed_state.c:163-184: every token of the block takes the single-token path,
+// so block and serial decode agree exactly.
+int kvl_mla_decode_compressed_block_bf16(float *out, const float *x, int count, int start_position,
+                                         const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                         KvlMlaCompressedState *state) {
+    Guard guard;
+    if (!out || !x || !cfg || !w || !state || count <= 0 || start_position != state->len ||
+        start_position < 0 || count > state->capacity - start_position)
+        return -1;
+    const int H = cfg->hidden_size;
+    if (H <= 0) return -1;
+    for (int t = 0; t < count; ++t) {
+        KvlMlaCompressedState *st[1] = {state};
+        const int pos = start_position + t;
+        if (decode_host(out + (size_t)t * H, x + (size_t)t * H, &pos, 1, cfg, w, st) != 0) return -1;
+    }
+    return 0;
+}
+
+// ---- include/kvl/mla_compressed_q8_state.h ----------------------------------------------
+
+int kvl_mla_compressed_q8_state_init(KvlMlaCompressedQ8State *state, const KvlMlaConfig *cfg,
+                                     int capacity) {
+    Guard guard;
+    if (!state || !cfg || capacity <= 0 || cfg->kv_lora_rank <= 0 || cfg->qk_rope_dim <= 0 ||
+        (cfg->qk_rope_dim & 1))
+        return -1;
+    mirror_drop(state);
+    memset(state, 0, sizeof(*state));
+    state->latent_q8 = (int8_t *)calloc((size_t)capacity * cfg->kv_lora_rank, 1);
+    state->latent_scale = (float *)calloc((size_t)capacity, sizeof(float));
+    state->rope_bf16 = (uint16_t *)calloc((size_t)capacity * cfg->qk_rope_dim, sizeof(uint16_t));
+    if (!state->latent_q8 || !state->latent_scale || !state->rope_bf16) {
+        free(state->latent_q8);
+        free(state->latent_scale);
+        free(state->rope_bf16);
+        memset(state, 0, sizeof(*state));
+        return -1;
+    }
+    state->capacity = capacity;
+    state->kv_lora_rank = cfg->kv_lora_rank;
+    state->qk_rope_dim = cfg->qk_rope_dim;
+    return 0;
+}
+
+void kvl_mla_compressed_q8_state_reset(KvlMlaCompressedQ8State *state) {
+    Guard guard;
+    if (!state) return;
+    state->len = 0;
+    mirror_lower(state, 0);
+}
+
+int kvl_mla_compressed_q8_state_truncate(KvlMlaCompressedQ8State *state, int new_len) {
+    Guard guard;
+    if (!state || new_len < 0 || new_len > state->len) return -1;
+    state->len = new_len;
+    mirror_lower(state, new_len);
+    return 0;
+}
+
+void kvl_mla_compressed_q8_state_free(KvlMlaCompressedQ8State *state) {
+    Guard guard;
+    if (!state) return;
+    mirror_drop(state);
+    free(state->latent_q8);
+    free(state->latent_scale);
+    free(state->rope_bf16);
+    memset(state, 0, sizeof(*state));
+}
+
+size_t kvl_mla_compressed_q8_state_bytes(const KvlMlaCompressedQ8State *state) {
+    if (!state || state->capacity <= 0) return 0;
+    return sizeof(*state) + (size_t)state->capacity * ((size_t)state->kv_lora_rank + sizeof(float) +
+                                                       (size_t)state->qk_rope_dim * sizeof(uint16_t));
+}
+
+int kvl_mla_compressed_q8_state_prefill_bf16(const float *x, int seq_len, const KvlMlaConfig *cfg,
+                                             const KvlMlaBF16 *w, KvlMlaCompressedQ8State *state) {
+    Guard guard;
+    return state_prefill(x, seq_len, cfg, w, state);
+}
+
+int kvl_mla_decode_compressed_q8_bf16(float *out, const float *x, int position,
+                                      const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                      KvlMlaCompressedQ8State *state) {
+    Guard guard;
+    KvlMlaCompressedQ8State *st[1] = {state};
+    return decode_host(out, x, &position, 1, cfg, w, st);
+}
+
+// ---- include/kvl/mla_hip.h ----------------------------------------------------------------
+
+const char *kvl_mla_last_error(void) { return g_err.c_str(); }
+
+int kvl_mla_init(void) {
+    Guard guard;
+    return ensure_ready();
+}
+
+int kvl_mla_bind_weights(const KvlMlaConfig *cfg, const KvlMlaBF16 *w) {
+    Guard guard;
+    Dims d;
+    if (!weights_ok(w) || !dims_of(cfg, d)) {
+        set_err("invalid arguments");
+        return -1;
+    }
+    if (ensure_ready() != 0) return -1;
+    DevWeights dw;
+    if (dev_weights(w, d, dw) != 0) return -1;
+    const void *ptrs[5] = {w->q_proj, w->kv_a_proj, w->kv_a_norm, w->kv_b_proj, w->o_proj};
+    for (const void *p : ptrs) ctx().weights[p].pins += 1;
+    return 0;
+}
+
+int kvl_mla_release_weights(const KvlMlaBF16 *w) {
+    Guard guard;
+    if (!weights_ok(w)) return -1;
+    Ctx &c = ctx();
+    const void *ptrs[5] = {w->q_proj, w->kv_a_proj, w->kv_a_norm, w->kv_b_proj, w->o_proj};
+    for (const void *p : ptrs) {
+        auto it = c.weights.find(p);
+        if (it == c.weights.end()) continue;
+        if (it->second.pins > 0) it->second.pins -= 1;
+        if (it->second.pins == 0) {
+            (void)hipFree(it->second.dev);
+            c.weights.erase(it);
+        }
+    }
+    return 0;
+}
+
+int kvl_mla_compressed_state_sync(KvlMlaCompressedState *state) {
+    Guard guard;
+    if (!state) return -1;
+    mirror_lower(state, 0);
+    return 0;
+}
+int kvl_mla_compressed_q8_state_sync(KvlMlaCompressedQ8State *state) {
+    Guard guard;
+    if (!state) return -1;
+    mirror_lower(state, 0);
+    return 0;
+}
+int kvl_mla_state_sync(KvlMlaState *state) {
+    Guard guard;
+    if (!state) return -1;
+    mirror_lower(state, 0);
+    return 0;
+}
+
+int kvl_mla_decode_compressed_batch_bf16(float *out, const float *x, const int *positions, int batch,
+                                         const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                         KvlMlaCompressedState *const *states) {
+    Guard guard;
+    if (!positions) return -1;
+    return decode_host(out, x, positions, batch, cfg, w, states);
+}
+
+int kvl_mla_decode_compressed_q8_batch_bf16(float *out, const float *x, const int *positions,
+                                            int batch, const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                            KvlMlaCompressedQ8State *const *states) {
+    Guard guard;
+    if (!positions) return -1;
+    return decode_host(out, x, positions, batch, cfg, w, states);
+}
+
+int kvl_mla_decode_compressed_q8_batch_device(float *d_out, const float *d_x, int batch,
+                                              const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                              KvlMlaCompressedQ8State *const *states, unsigned flags) {
+    Guard guard;
+    return decode_device(d_out, d_x, batch, cfg, w, states, flags);
+}
+
+int kvl_mla_decode_compressed_batch_device(float *d_out, const float *d_x, int batch,
+                                           const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                           KvlMlaCompressedState *const *states, unsigned flags) {
+    Guard guard;
+    return decode_device(d_out, d_x, batch, cfg, w, states, flags);
+}
+
+void *kvl_mla_stream(void) {
+    Guard guard;
+    if (ensure_ready() != 0) return nullptr;
+    return (void *)ctx().stream;
+}
+
+int kvl_mla_synchronize(void) {
+    Guard guard;
+    if (ensure_ready() != 0) return -1;
+    HIP_TRY(hipStreamSynchronize(ctx().stream));
+    return 0;
+}
+
+void *kvl_mla_device_alloc(size_t bytes) {
+    Guard guard;
+    if (ensure_ready() != 0) return nullptr;
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+        set_err("hipMalloc(%zu) failed", bytes);
+        return nullptr;
+    }
+    return p;
+}
+
+int kvl_mla_device_free(void *p) {
+    Guard guard;
+    if (!p) return 0;
+    HIP_TRY(hipFree(p));
+    return 0;
+}
+
+int kvl_mla_copy_to_device(void *dst, const void *src, size_t bytes) {
+    Guard guard;
+    if (ensure_ready() != 0) return -1;
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx().stream));
+    HIP_TRY(hipStreamSynchronize(ctx().stream));
+    return 0;
+}
+
+int kvl_mla_copy_to_host(void *dst, const void *src, size_t bytes) {
+    Guard guard;
+    if (ensure_ready() != 0) return -1;
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx().stream));
+    HIP_TRY(hipStreamSynchronize(ctx().stream));
+    return 0;
+}
+
+int kvl_mla_capture_begin(void) {
+    Guard guard;
+    if (ensure_ready() != 0) return -1;
+    HIP_TRY(hipStreamBeginCapture(ctx().stream, hipStreamCaptureModeThreadLocal));
+    ctx().capturing = true;
+    return 0;
+}
+
+int kvl_mla_capture_end(void **graph_exec) {
+    Guard guard;
+    Ctx &c = ctx();
+    if (!c.capturing || !graph_exec) return -1;
+    c.capturing = false;
+    hipGraph_t graph = nullptr;
+    HIP_TRY(hipStreamEndCapture(c.stream, &graph));
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) {
+        set_err("hipGraphInstantiate: %s", hipGetErrorString(e));
+        return -1;
+    }
+    *graph_exec = (void *)exec;
+    return 0;
+}
+
+int kvl_mla_graph_launch(void *graph_exec) {
+    Guard guard;
+    if (!graph_exec) return -1;
+    HIP_TRY(hipGraphLaunch((hipGraphExec_t)graph_exec, ctx().stream));
+    return 0;
+}
+
+int kvl_mla_graph_destroy(void *graph_exec) {
+    Guard guard;
+    if (!graph_exec) return 0;
+    HIP_TRY(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
+    return 0;
+}
+
+int kvl_mla_q8_pack_rows(int8_t *codes, float *scales, uint16_t *rope_bf16, const float *latent,
+                         const float *k_rope_raw, const int *positions, int n, int R, int DR,
+                         float theta) {
+    Guard guard;
+    if (!codes || !scales || !rope_bf16 || !latent || !k_rope_raw || !positions || n <= 0 || R <= 0 ||
+        R > 1024 || DR <= 0 || DR > 256 || (DR & 1) || !(theta > 0.0f)) {
+        set_err("invalid arguments");
+        return -1;
+    }
+    if (ensure_ready() != 0) return -1;
+    Ctx &c = ctx();
+    int maxpos = 0;
+    for (int i = 0; i < n; ++i) {
+        if (positions[i] < 0) {
+            set_err("negative position");
+            return -1;
+        }
+        maxpos = std::max(maxpos, positions[i]);
+    }
+    const float2 *cs = nullptr;
+    if (rope_table(theta, DR, maxpos + 1, &cs) != 0) return -1;
+    const size_t rb = row_bytes_of(kFmtQ8, R, DR, 0);
+    const int KVO = R + DR;
+    // device: input rows [n, R+DR], scratch history (codes/scales/rope) [n], staged rows
+    Layout L;
+    L.take<float>(nullptr, (size_t)n * KVO);
+    L.take<int8_t>(nullptr, (size_t)n * R);
+    L.take<float>(nullptr, (size_t)n);
+    L.take<uint16_t>(nullptr, (size_t)n * DR);
+    L.take<uint8_t>(nullptr, (size_t)n * rb);
+    if (dev_reserve(c.prefill, L.off) != 0) return -1;
+    Layout L2;
+    char *base = (char *)c.prefill.p;
+    float *din = L2.take<float>(base, (size_t)n * KVO);
+    int8_t *dcodes = L2.take<int8_t>(base, (size_t)n * R);
+    float *dscl = L2.take<float>(base, (size_t)n);
+    uint16_t *drope = L2.take<uint16_t>(base, (size_t)n * DR);
+    uint8_t *drows = L2.take<uint8_t>(base, (size_t)n * rb);
+    std::vector<float> hin((size_t)n * KVO);
+    for (int i = 0; i < n; ++i) {
+        memcpy(&hin[(size_t)i * KVO], latent + (size_t)i * R, (size_t)R * 4);
+        memcpy(&hin[(size_t)i * KVO + R], k_rope_raw + (size_t)i * DR, (size_t)DR * 4);
+    }
+    HIP_TRY(hipMemcpyAsync(din, hin.data(), hin.size() * 4, hipMemcpyHostToDevice, c.stream));
+    Dims d{};
+    d.R = R;
+    d.DR = DR;
+    d.NH = 1;
+    // one block per row, each row its own one-row "sequence" at its own position
+    for (int g0 = 0; g0 < n; g0 += kMaxBatch) {
+        const int m = std::min(kMaxBatch, n - g0);
+        SeqTable t;
+        memset(&t, 0, sizeof t);
+        t.n = m;
+        for (int i = 0; i < m; ++i) {
+            // row g0+i of the scratch history is written at "position" positions[g0+i]; point
+            // the arrays so that row pos lands on scratch row g0+i.
+            const long off = (long)(g0 + i) - (long)positions[g0 + i];
+            t.s[i].a = dcodes + off * R;
+            t.s[i].b = dscl + off;
+            t.s[i].c = drope + off * DR;
+            t.s[i].pos = positions[g0 + i];
+        }
+        DecodeWork wk{};
+        wk.rows = drows + (size_t)g0 * rb;
+        HIP_TRY(launch_append(c.stream, kFmtQ8, t, d, din + (size_t)g0 * KVO, KVO, 0, nullptr, 0.f, cs, wk,
+                              true, 0));
+    }
+    std::vector<uint8_t> hrows((size_t)n * rb);
+    HIP_TRY(hipMemcpyAsync(hrows.data(), drows, hrows.size(), hipMemcpyDeviceToHost, c.stream));
+    HIP_TRY(hipStreamSynchronize(c.stream));
+    for (int i = 0; i < n; ++i) {
+        const uint8_t *row = &hrows[(size_t)i * rb];
+        memcpy(codes + (size_t)i * R, row, (size_t)R);
+        memcpy(scales + i, row + R, 4);
+        memcpy(rope_bf16 + (size_t)i * DR, row + R + 4, 2 * (size_t)DR);
+    }
+    return 0;
+}
+
+static int fill_synth(const void *key, const HostView &v, int row0, int nrows, uint64_t seed,
+                      void (*set_len)(const void *, int)) {
+    if (row0 < 0 || nrows <= 0 || row0 + nrows > v.capacity || row0 > v.len) {
+        set_err("invalid row range");
+        return -1;
+    }
+    if (ensure_ready() != 0) return -1;
+    Ctx &c = ctx();
+    Mirror *m = nullptr;
+    if (mirror_get(key, v, &m, true) != 0) return -1;
+    if (m->synced < row0 && upload_rows(*m, v, m->synced, row0, c.stream) != 0) return -1;
+    HIP_TRY(launch_fill_history(c.stream, v.fmt, m->a, m->b, m->c, v.d0, v.d1, row0, nrows, seed));
+    HIP_TRY(hipStreamSynchronize(c.stream));
+    m->synced = row0 + nrows;
+    set_len(key, row0 + nrows);
+    return 0;
+}
+
+int kvl_mla_compressed_q8_state_fill_synthetic(KvlMlaCompressedQ8State *state, int row0, int nrows,
+                                               uint64_t seed) {
+    Guard guard;
+    if (!state) return -1;
+    return fill_synth(state, view_of(state), row0, nrows, seed,
+                      [](const void *k, int len) { ((KvlMlaCompressedQ8State *)k)->len = len; });
+}
+
+int kvl_mla_compressed_state_fill_synthetic(KvlMlaCompressedState *state, int row0, int nrows,
+                                            uint64_t seed) {
+    Guard guard;
+    if (!state) return -1;
+    return fill_synth(state, view_of(state), row0, nrows, seed,
+                      [](const void *k, int len) { ((KvlMlaCompressedState *)k)->len = len; });
+}
+
+static int pull_rows(const void *key, const HostView &v, int row0, int nrows) {
+    Ctx &c = ctx();
+    auto it = c.mirrors.find(key);
+    if (it == c.mirrors.end() || row0 < 0 || nrows <= 0 || row0 + nrows > it->second.synced) {
+        set_err("rows not on the device");
+        return -1;
+    }
+    Mirror &m = it->second;
+    size_t ea, eb, ec;
+    comp_bytes(m.fmt, m.d0, m.d1, m.d2, ea, eb, ec);
+    HIP_TRY(hipMemcpyAsync((char *)v.ha + ea * row0, (char *)m.a + ea * row0, ea * nrows,
+                           hipMemcpyDeviceToHost, c.stream));
+    HIP_TRY(hipMemcpyAsync((char *)v.hb + eb * row0, (char *)m.b + eb * row0, eb * nrows,
+                           hipMemcpyDeviceToHost, c.stream));
+    if (ec)
+        HIP_TRY(hipMemcpyAsync((char *)v.hc + ec * row0, (char *)m.c + ec * row0, ec * nrows,
+                               hipMemcpyDeviceToHost, c.stream));
+    HIP_TRY(hipStreamSynchronize(c.stream));
+    return 0;
+}
+
+int kvl_mla_compressed_q8_state_pull(KvlMlaCompressedQ8State *state, int row0, int nrows) {
+    Guard guard;
+    if (!state) return -1;
+    return pull_rows(state, view_of(state), row0, nrows);
+}
+
+int kvl_mla_compressed_state_pull(KvlMlaCompressedState *state, int row0, int nrows) {
+    Guard guard;
+    if (!state) return -1;
+    return pull_rows(state, view_of(state), row0, nrows);
+}
+
+}  // extern "C"

@@ -110,3 +110,29 @@ def hidden(cfg, seed, n, bf16_exact=False, tag="x"):
     """[n, hidden] float32 hidden states ~ N(0,1); optionally BF16-representable."""
     x = normal_f32(seed, tag, (n, cfg.hidden_size))
     return bf16_bits_to_f32(f32_to_bf16_bits(x)) if bf16_exact else x
+
+
+def synth_normal(seed, idx):
+    """Host mirror of the device history generator: approx. N(0,1) as the Irwin-Hall sum of
+    four 24-bit uniforms (SplitMix64 outputs 4*idx+1 .. 4*idx+4), centred, times sqrt(3).
+    Only exactly rounded float32 operations, so it matches the device bit for bit."""
+    idx = np.asarray(idx, dtype=np.uint64)
+    k = idx[..., None] * np.uint64(4) + np.arange(1, 5, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        z = np.uint64(seed) + k * _GAMMA
+        z = (z ^ (z >> np.uint64(30))) * _M1
+        z = (z ^ (z >> np.uint64(27))) * _M2
+        z = z ^ (z >> np.uint64(31))
+    u = (z >> np.uint64(40)).astype(np.float32) * np.float32(5.9604644775390625e-8)
+    s = (u[..., 0] + u[..., 1]) + (u[..., 2] + u[..., 3])
+    return ((s - np.float32(2.0)) * np.float32(1.7320508)).astype(np.float32)
+
+
+def synth_rows(seed, rows, R, DR):
+    """Raw synthetic history rows (float32 latent [n, R] and RoPE key [n, DR]) of the given
+    global row indices, as the device generator draws them."""
+    rows = np.asarray(rows, dtype=np.uint64)
+    base = rows[:, None] * np.uint64(R + DR)
+    lat = synth_normal(seed, base + np.arange(R, dtype=np.uint64))
+    rope = synth_normal(seed, base + np.uint64(R) + np.arange(DR, dtype=np.uint64))
+    return lat, rope

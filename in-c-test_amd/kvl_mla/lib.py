@@ -1,0 +1,80 @@
+"""Loader of libkvl_mla.so, the MI355X MLA library (C ABI of include/kvl/*.h).
+
+The library is built in-tree by ``__graft_entry__.build()`` (in-c-test_amd/csrc/Makefile).
+There is no fallback: a missing library raises, so nothing silently runs elsewhere.
+"""
+import ctypes as C
+import os
+
+from . import abi
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libkvl_mla.so")
+
+QSP = C.POINTER(abi.QS)
+CSP = C.POINTER(abi.CS)
+
+# include/kvl/mla_hip.h
+EXT_API = {
+    "mla_last_error": (C.c_char_p, []),
+    "mla_init": (C.c_int, []),
+    "mla_bind_weights": (C.c_int, [abi.CFG, abi.W]),
+    "mla_release_weights": (C.c_int, [abi.W]),
+    "mla_compressed_state_sync": (C.c_int, [abi.CS]),
+    "mla_compressed_q8_state_sync": (C.c_int, [abi.QS]),
+    "mla_state_sync": (C.c_int, [abi.ST]),
+    "mla_decode_compressed_batch_bf16": (C.c_int, [abi.f32p, abi.f32p, C.POINTER(C.c_int), C.c_int,
+                                                   abi.CFG, abi.W, CSP]),
+    "mla_decode_compressed_q8_batch_bf16": (C.c_int, [abi.f32p, abi.f32p, C.POINTER(C.c_int),
+                                                      C.c_int, abi.CFG, abi.W, QSP]),
+    "mla_decode_compressed_q8_batch_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, abi.CFG,
+                                                        abi.W, QSP, C.c_uint]),
+    "mla_decode_compressed_batch_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, abi.CFG,
+                                                     abi.W, CSP, C.c_uint]),
+    "mla_prefill_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, abi.CFG, abi.W]),
+    "mla_stream": (C.c_void_p, []),
+    "mla_synchronize": (C.c_int, []),
+    "mla_device_alloc": (C.c_void_p, [C.c_size_t]),
+    "mla_device_free": (C.c_int, [C.c_void_p]),
+    "mla_copy_to_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
+    "mla_copy_to_host": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
+    "mla_capture_begin": (C.c_int, []),
+    "mla_capture_end": (C.c_int, [C.POINTER(C.c_void_p)]),
+    "mla_graph_launch": (C.c_int, [C.c_void_p]),
+    "mla_graph_destroy": (C.c_int, [C.c_void_p]),
+    "mla_q8_pack_rows": (C.c_int, [abi.i8p, abi.f32p, abi.u16p, abi.f32p, abi.f32p,
+                                   C.POINTER(C.c_int), C.c_int, C.c_int, C.c_int, C.c_float]),
+    "mla_compressed_q8_state_fill_synthetic": (C.c_int, [abi.QS, C.c_int, C.c_int, C.c_uint64]),
+    "mla_compressed_state_fill_synthetic": (C.c_int, [abi.CS, C.c_int, C.c_int, C.c_uint64]),
+    "mla_compressed_q8_state_pull": (C.c_int, [abi.QS, C.c_int, C.c_int]),
+    "mla_compressed_state_pull": (C.c_int, [abi.CS, C.c_int, C.c_int]),
+}
+
+RESIDUAL = 1
+NO_ADVANCE = 2
+
+_lib = None
+
+
+def load():
+    """libkvl_mla with every prototype declared; raises when it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run `python __graft_entry__.py` (build)")
+        lib = C.CDLL(LIB_PATH)
+        abi.declare(lib, abi.REFERENCE_API, "kvl_")
+        abi.declare(lib, abi.PREFILL_API, "kvl_")
+        abi.declare(lib, EXT_API, "kvl_")
+        _lib = lib
+    return _lib
+
+
+def last_error():
+    e = load().kvl_mla_last_error()
+    return e.decode() if e else ""
+
+
+def check(rc, what="call"):
+    if rc != 0:
+        raise RuntimeError(f"{what} failed: {last_error()}")

@@ -1,0 +1,121 @@
+#ifndef KVL_MLA_HIP_H
+#define KVL_MLA_HIP_H
+
+/* Extensions of libkvl_mla (MI355X / gfx950) with no counterpart in the reference runtime.
+ *
+ * The reference MLA API (include/kvl/ops.h, mla_state.h, mla_compressed_state.h,
+ * mla_compressed_q8_state.h) keeps its exact semantics: host buffers in and out, host
+ * state arrays authoritative, synchronous calls. These extensions add what a GPU library
+ * needs on top of it:
+ *   - pinned device copies of a layer's weights (the reference borrows them per call);
+ *   - explicit re-synchronisation of a state whose rows were edited in place on the host;
+ *   - batched (ragged) decode over many sequences in one call;
+ *   - stream-ordered device-pointer variants (no host sync), capturable in a HIP graph;
+ *   - the quantiser boundary (fp32 latent -> Q8 row) as a standalone entry point;
+ *   - device-side synthetic histories for benchmarks.
+ * Every int-returning function returns 0 on success and -1 on failure; the reason is then
+ * available from kvl_mla_last_error() (thread-local). Nothing here calls exit(). */
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "kvl/mla_compressed_q8_state.h"
+#include "kvl/mla_compressed_state.h"
+#include "kvl/mla_state.h"
+#include "kvl/ops.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Last error of the calling thread ("" when none). */
+const char *kvl_mla_last_error(void);
+
+/* Optional explicit initialisation on the current HIP device (otherwise lazy). */
+int kvl_mla_init(void);
+
+/* Uploads the five weight arrays of a layer and pins the device copies under their host
+ * addresses, so later calls with the same KvlMlaBF16 skip the content check. Unpinned
+ * weights are cached by address, size and a sampled content digest, and re-uploaded when
+ * the digest changes. */
+int kvl_mla_bind_weights(const KvlMlaConfig *cfg, const KvlMlaBF16 *w);
+int kvl_mla_release_weights(const KvlMlaBF16 *w);
+
+/* Forces a full re-upload of rows [0, len) on the next call (for callers that overwrite
+ * history rows below len in place, without truncate/reset). */
+int kvl_mla_compressed_state_sync(KvlMlaCompressedState *state);
+int kvl_mla_compressed_q8_state_sync(KvlMlaCompressedQ8State *state);
+int kvl_mla_state_sync(KvlMlaState *state);
+
+/* One decode token for each of `batch` sequences: x [batch, hidden], out [batch, hidden],
+ * positions[i] must equal states[i]->len (the reference rule, checked for every sequence
+ * before anything runs). Host buffers; synchronous; host rows written back. */
+int kvl_mla_decode_compressed_batch_bf16(float *out, const float *x, const int *positions,
+                                         int batch, const KvlMlaConfig *cfg,
+                                         const KvlMlaBF16 *w,
+                                         KvlMlaCompressedState *const *states);
+int kvl_mla_decode_compressed_q8_batch_bf16(float *out, const float *x, const int *positions,
+                                            int batch, const KvlMlaConfig *cfg,
+                                            const KvlMlaBF16 *w,
+                                            KvlMlaCompressedQ8State *const *states);
+
+/* Flags of the device-pointer variants. */
+#define KVL_MLA_RESIDUAL 1u   /* out += attention(x) instead of out = attention(x)      */
+#define KVL_MLA_NO_ADVANCE 2u /* append at position len but leave len (and host rows)  */
+
+/* Stream-ordered variants: d_x / d_out are device pointers ([batch, hidden] fp32, d_out may
+ * equal d_x with KVL_MLA_RESIDUAL), the call returns after enqueueing on kvl_mla_stream().
+ * The appended rows stay on the device (host rows are not written); len advances unless
+ * KVL_MLA_NO_ADVANCE. Weights must be bound. No allocation happens once the workspace has
+ * grown to the batch size, so a warm call can be captured in a HIP graph. */
+int kvl_mla_decode_compressed_q8_batch_device(float *d_out, const float *d_x, int batch,
+                                              const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                              KvlMlaCompressedQ8State *const *states,
+                                              unsigned flags);
+int kvl_mla_decode_compressed_batch_device(float *d_out, const float *d_x, int batch,
+                                           const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                           KvlMlaCompressedState *const *states,
+                                           unsigned flags);
+
+/* Stream-ordered causal prefill over device buffers (d_x, d_out [seq_len, hidden] fp32);
+ * same arithmetic as kvl_mla_prefill_bf16. */
+int kvl_mla_prefill_device(float *d_out, const float *d_x, int seq_len, const KvlMlaConfig *cfg,
+                           const KvlMlaBF16 *w);
+
+/* The library's HIP stream (hipStream_t) and helpers for callers without a HIP binding. */
+void *kvl_mla_stream(void);
+int kvl_mla_synchronize(void);
+void *kvl_mla_device_alloc(size_t bytes);
+int kvl_mla_device_free(void *p);
+int kvl_mla_copy_to_device(void *dst, const void *src, size_t bytes);
+int kvl_mla_copy_to_host(void *dst, const void *src, size_t bytes);
+/* HIP graph capture of the calls made between begin and end on kvl_mla_stream(). */
+int kvl_mla_capture_begin(void);
+int kvl_mla_capture_end(void **graph_exec);
+int kvl_mla_graph_launch(void *graph_exec);
+int kvl_mla_graph_destroy(void *graph_exec);
+
+/* Quantiser boundary, computed on the GPU: for row i, latent [n, R] (already normalised) ->
+ * int8 codes [n, R] + fp32 scale [n]; k_rope_raw [n, DR] (before rotation) -> RoPE at
+ * positions[i] -> BF16 RNE [n, DR]. Same rows as src/mla_compressed_q8_state.c:34-55,
+ * 121-125 produce from the same fp32 latent. */
+int kvl_mla_q8_pack_rows(int8_t *codes, float *scales, uint16_t *rope_bf16, const float *latent,
+                         const float *k_rope_raw, const int *positions, int n, int R, int DR,
+                         float theta);
+
+/* Synthetic histories generated on the device (benchmarks): rows [row0, row0 + nrows) of the
+ * state's device copy get latents ~ approx. N(0,1) (Irwin-Hall of four 24-bit uniforms from
+ * SplitMix64(seed)), Q8-quantised (Q8 state) or rounded to BF16 (FP32 state). Sets
+ * len = row0 + nrows. The host arrays are only written by the *_pull calls. */
+int kvl_mla_compressed_q8_state_fill_synthetic(KvlMlaCompressedQ8State *state, int row0,
+                                               int nrows, uint64_t seed);
+int kvl_mla_compressed_state_fill_synthetic(KvlMlaCompressedState *state, int row0, int nrows,
+                                            uint64_t seed);
+int kvl_mla_compressed_q8_state_pull(KvlMlaCompressedQ8State *state, int row0, int nrows);
+int kvl_mla_compressed_state_pull(KvlMlaCompressedState *state, int row0, int nrows);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,93 @@
+"""CPU checks of the drop-in boundary: libkvl_mla loads, exports every function that
+include/kvl/*.h declares, and its structs have the reference's byte layout. No GPU call."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from kvl_mla import abi, inputs, lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INCLUDE = os.path.join(ROOT, "include", "kvl")
+REF_INCLUDE = "/root/reference/include"
+
+
+def declared_functions():
+    names = set()
+    for fn in sorted(os.listdir(INCLUDE)):
+        if not fn.endswith(".h"):
+            continue
+        text = open(os.path.join(INCLUDE, fn)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"^[A-Za-z][\w \*]*?\b(kvl_\w+)\s*\(", text, flags=re.M):
+            names.add(m.group(1))
+    return names
+
+
+def test_library_exports_every_declared_function():
+    L = lib.load()  # dlopen only: no HIP call is made
+    names = declared_functions()
+    assert len(names) >= 40
+    missing = [n for n in sorted(names) if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_reference_api_symbols_declared():
+    # every symbol of the reference MLA API (include/kvl/ops.h:43-64, mla_state.h:24-37,
+    # mla_compressed_state.h:16-44, mla_compressed_q8_state.h:18-38) is part of the boundary
+    names = declared_functions()
+    for n in list(abi.REFERENCE_API) + list(abi.PREFILL_API):
+        assert "kvl_" + n in names, n
+
+
+def test_struct_sizes_ctypes():
+    assert C.sizeof(abi.KvlMlaConfig) == 32
+    assert C.sizeof(abi.KvlMlaBF16) == 40
+    assert C.sizeof(abi.KvlMlaState) == 40
+    assert C.sizeof(abi.KvlMlaCompressedState) == 32
+    assert C.sizeof(abi.KvlMlaCompressedQ8State) == 40
+
+
+LAYOUT_C = r"""
+#include <stdio.h>
+#include <stddef.h>
+#include "kvl/ops.h"
+#include "kvl/mla_state.h"
+#include "kvl/mla_compressed_state.h"
+#include "kvl/mla_compressed_q8_state.h"
+#define P(T, f) printf(#T "." #f " %zu\n", offsetof(T, f));
+int main(void) {
+  printf("cfg %zu bf16 %zu st %zu cs %zu q8 %zu\n", sizeof(KvlMlaConfig), sizeof(KvlMlaBF16),
+         sizeof(KvlMlaState), sizeof(KvlMlaCompressedState), sizeof(KvlMlaCompressedQ8State));
+  P(KvlMlaConfig, rope_theta) P(KvlMlaBF16, o_proj) P(KvlMlaState, values)
+  P(KvlMlaCompressedState, rope) P(KvlMlaCompressedQ8State, rope_bf16)
+  P(KvlMlaCompressedQ8State, latent_scale) P(KvlMlaState, v_head_dim)
+  return 0;
+}
+"""
+
+
+def _layout(include_dir, tmp_path, tag):
+    src = tmp_path / f"layout_{tag}.c"
+    exe = tmp_path / f"layout_{tag}"
+    src.write_text(LAYOUT_C)
+    subprocess.run(["gcc", "-std=c11", "-I", include_dir, str(src), "-o", str(exe)], check=True)
+    return subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+
+
+def test_struct_layout_matches_reference_headers(tmp_path):
+    if not os.path.isdir(REF_INCLUDE):
+        pytest.skip("reference headers not present")
+    ours = _layout(os.path.join(ROOT, "include"), tmp_path, "ours")
+    ref = _layout(REF_INCLUDE, tmp_path, "ref")
+    assert ours == ref
+
+
+def test_synth_normal_moments_and_determinism():
+    v = inputs.synth_normal(0xC4, np.arange(400000))
+    assert abs(float(v.mean())) < 0.01 and abs(float(v.std()) - 1.0) < 0.01
+    assert np.max(np.abs(v)) <= 2.0 * np.sqrt(3.0)
+    np.testing.assert_array_equal(v[1000:1010], inputs.synth_normal(0xC4, np.arange(1000, 1010)))

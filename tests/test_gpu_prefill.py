@@ -1,0 +1,57 @@
+"""Parity of the causal prefill (C ABI kvl_mla_prefill_bf16) with the oracle's restatement of
+src/mla_prefill_streaming.c:78-206. Bar: max|got - ref| / max|ref| <= 2e-3."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import pyoracle
+from helpers import f32, rel_err
+from kvl_mla import inputs, lib
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+ORC = pyoracle.load_oracle()
+L = lib.load()
+
+STREAM = dict(hidden_size=16, num_heads=2, qk_nope_dim=4, qk_rope_dim=4, v_head_dim=8,
+              kv_lora_rank=6, rms_eps=1e-5, rope_theta=800000.0)  # src/mla_streaming_probe.c:39,46
+
+
+def run(dims, S, seed, std, bf16_x):
+    cfg = inputs.config(**dims)
+    layer = inputs.make_layer(cfg, seed, std=std)
+    x = inputs.hidden(cfg, seed, S, bf16_exact=bf16_x)
+    w = layer.struct()
+    a = np.zeros((S, cfg.hidden_size), np.float32)
+    b = np.zeros((S, cfg.hidden_size), np.float32)
+    lib.check(L.kvl_mla_prefill_bf16(f32(a), f32(x), S, C.byref(cfg), C.byref(w)), "prefill")
+    assert ORC.orc_mla_prefill_streaming(f32(b), f32(x), S, C.byref(cfg), C.byref(w)) == 0
+    return a, b
+
+
+@pytest.mark.parametrize("S", [1, 7, 64, 257])
+def test_prefill_small_shapes(S):
+    print(f"[prefill] stream-probe shape S={S}", flush=True)
+    a, b = run(STREAM, S, 50 + S, 0.2, False)
+    assert rel_err(a, b) <= TOL, rel_err(a, b)
+
+
+@pytest.mark.parametrize("S,bf16_x", [(320, True), (130, False)])
+def test_prefill_kimi_shapes(S, bf16_x):
+    """MFMA route; S not a multiple of the 64-token tile exercises the padded last tile."""
+    print(f"[prefill] kimi S={S} bf16_x={bf16_x}", flush=True)
+    a, b = run(inputs.KIMI, S, 0xC3, 0.02, bf16_x)
+    assert np.all(np.isfinite(a))
+    assert rel_err(a, b) <= TOL, rel_err(a, b)
+
+
+def test_prefill_rejects_bad_arguments():
+    cfg = inputs.config(**inputs.KIMI)
+    layer = inputs.make_layer(inputs.config(**STREAM), 1)
+    w = layer.struct()
+    out = np.zeros(16, np.float32)
+    assert L.kvl_mla_prefill_bf16(f32(out), f32(out), 0, C.byref(cfg), C.byref(w)) == -1
+    bad = inputs.config(**dict(STREAM, qk_rope_dim=5))
+    assert L.kvl_mla_prefill_bf16(f32(out), f32(out), 1, C.byref(bad), C.byref(w)) == -1
