@@ -1,0 +1,311 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X MLA library on its headline workload.
+
+Workload (one "step"): one decode token through a 27-layer MLA attention stack (q_proj,
+kv_a_proj + RMSNorm, absorbed kv_b_proj, o_proj, residual; no MoE) for a batch of 8
+sequences, each holding a 32768-token row-wise Q8 latent history per layer (512 int8 + fp32
+scale + 64 bf16 RoPE key = 644 B/token). Weights are random-init bf16 N(0, 0.02), histories
+are generated on the device (synthetic), all resident in HBM before timing. Every step
+appends at position 32768 without advancing, so steps are identical.
+
+value = algorithmic bytes of a step (weights once per layer + every history row read once)
+        / wall-clock time per step, in GB/s.
+Also reported: the attention kernel's roofline (HIP events on the library stream), the
+stage breakdown, causal prefill TFLOP/s at 4096 tokens, and a CPU baseline (the reference
+C path compiled from its sources when available, else the oracle) on a bounded sample,
+whose outputs double as a parity check of the benchmark workload.
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (os.path.join(ROOT, "in-c-test_amd"), os.path.join(ROOT, "oracle"), os.path.join(ROOT, "tests")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+from kvl_mla import abi, inputs, lib  # noqa: E402
+
+METRIC = "MLA decode HBM GB/s (% peak) @32K ctx Q8 cache; prefill TFLOP/s @4K"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+Q8_ROW = 512 + 4 + 2 * 64
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def layer_weights(cfg, seed):
+    """bf16(N(0, 0.02)) matrices and bf16(1 + N(0, 0.02)) kv_a_norm from PCG64(seed)."""
+    rng = np.random.default_rng(seed)
+    H, NH = cfg.hidden_size, cfg.num_heads
+    DN, DR, DV, R = cfg.qk_nope_dim, cfg.qk_rope_dim, cfg.v_head_dim, cfg.kv_lora_rank
+
+    def mat(shape, mean=0.0):
+        return inputs.f32_to_bf16_bits(rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)
+                                       + np.float32(mean))
+    return inputs.Layer(q_proj=mat((NH * (DN + DR), H)), kv_a_proj=mat((R + DR, H)),
+                        kv_a_norm=mat((R,), 1.0), kv_b_proj=mat((NH * (DN + DV), R)),
+                        o_proj=mat((H, NH * DV)))
+
+
+def weight_bytes(cfg):
+    H, NH = cfg.hidden_size, cfg.num_heads
+    DN, DR, DV, R = cfg.qk_nope_dim, cfg.qk_rope_dim, cfg.v_head_dim, cfg.kv_lora_rank
+    return 2 * (NH * (DN + DR) * H + (R + DR) * H + R + NH * (DN + DV) * R + H * NH * DV)
+
+
+def prefill_flops(S, cfg):
+    """Algorithmic flops of the reference's non-absorbed causal prefill
+    (src/mla_prefill_streaming.c:78-206): kv_a, q, kv_b expansion, QK^T and PV over the
+    S(S+1)/2 causal pairs, o_proj. Softmax, RMSNorm and RoPE excluded."""
+    H, NH = cfg.hidden_size, cfg.num_heads
+    DN, DR, DV, R = cfg.qk_nope_dim, cfg.qk_rope_dim, cfg.v_head_dim, cfg.kv_lora_rank
+    pairs = S * (S + 1) // 2
+    return (2 * S * H * (R + DR) + 2 * S * H * NH * (DN + DR) + 2 * S * R * NH * (DN + DV)
+            + 2 * NH * pairs * (DN + DR) + 2 * NH * pairs * DV + 2 * S * NH * DV * H)
+
+
+def omp_threads():
+    try:
+        return int(C.CDLL("libgomp.so.1").omp_get_max_threads())
+    except OSError:
+        return int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=27)
+    ap.add_argument("--batch", type=int, default=8)
+    ap.add_argument("--context", type=int, default=32768)
+    ap.add_argument("--prefill-tokens", type=int, default=4096)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="also run a plain copy kernel of MIB MiB (memory-counter calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: the MLA path here runs on a single GPU "
+              "(multi-GPU sharding is a design note, not part of this build); use --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    L = lib.load()
+    lib.check(L.kvl_mla_init(), "init")
+    cfg = inputs.config(**inputs.KIMI)
+    NL, B, CTX = args.layers, args.batch, args.context
+    H = cfg.hidden_size
+
+    t_setup = time.time()
+    layers, wstructs = [], []
+    for li in range(NL):
+        lw = layer_weights(cfg, 0xC4 + li)
+        layers.append(lw)
+        ws = lw.struct()
+        wstructs.append(ws)
+        lib.check(L.kvl_mla_bind_weights(C.byref(cfg), C.byref(ws)), "bind weights")
+    log(f"[bench] weights bound ({NL} layers) in {time.time() - t_setup:.1f}s")
+    Q8P = C.POINTER(abi.KvlMlaCompressedQ8State)
+    states, arrays = [], []
+    for li in range(NL):
+        row = []
+        for b in range(B):
+            st = abi.KvlMlaCompressedQ8State()
+            if L.kvl_mla_compressed_q8_state_init(C.byref(st), C.byref(cfg), CTX + 1) != 0:
+                raise RuntimeError("state init failed")
+            seed = (0xC4 << 16) ^ (li << 8) ^ b
+            lib.check(L.kvl_mla_compressed_q8_state_fill_synthetic(C.byref(st), 0, CTX, seed), "fill")
+            row.append(st)
+        states.append(row)
+        arrays.append((Q8P * B)(*[C.pointer(s) for s in row]))
+    log(f"[bench] {NL * B} Q8 histories of {CTX} tokens generated in {time.time() - t_setup:.1f}s")
+
+    x0 = np.ascontiguousarray(inputs.hidden(cfg, 0xC4, B, tag="stack_x"))
+    nbytes = x0.nbytes
+    d_x0 = L.kvl_mla_device_alloc(nbytes)
+    d_h = L.kvl_mla_device_alloc(nbytes)
+    d_l0 = L.kvl_mla_device_alloc(nbytes)
+    if not (d_x0 and d_h and d_l0):
+        raise RuntimeError("device alloc failed: " + lib.last_error())
+    lib.check(L.kvl_mla_copy_to_device(d_x0, x0.ctypes.data, nbytes), "h2d")
+    flags = lib.RESIDUAL | lib.NO_ADVANCE
+
+    def step():
+        lib.check(L.kvl_mla_copy_kernel(d_h, d_x0, nbytes), "reset hidden")
+        for li in range(NL):
+            rc = L.kvl_mla_decode_compressed_q8_batch_device(d_h, d_h, B, C.byref(cfg), C.byref(wstructs[li]),
+                                                              arrays[li], flags)
+            if rc != 0:
+                raise RuntimeError("decode: " + lib.last_error())
+
+    for _ in range(max(1, args.warmup)):
+        step()
+    lib.check(L.kvl_mla_synchronize(), "sync")
+
+    # stage breakdown and attention-kernel roofline: events around each launch, eager steps
+    lib.check(L.kvl_mla_timing_enable(1), "timing on")
+    n_prof = 3
+    for _ in range(n_prof):
+        step()
+    lib.check(L.kvl_mla_synchronize(), "sync")
+    ms = (C.c_double * 6)()
+    cnt = (C.c_int * 6)()
+    lib.check(L.kvl_mla_timing_read(ms, cnt), "timing read")
+    lib.check(L.kvl_mla_timing_enable(0), "timing off")
+    stages = {name: {"ms_per_launch": ms[i] / max(cnt[i], 1), "launches": cnt[i]}
+              for i, name in enumerate(lib.STAGES)}
+
+    graph = None
+    if not args.eager:
+        lib.check(L.kvl_mla_capture_begin(), "capture begin")
+        try:
+            step()
+        finally:
+            ge = C.c_void_p()
+            rc = L.kvl_mla_capture_end(C.byref(ge))
+        lib.check(rc, "capture end")
+        graph = ge
+        for _ in range(max(1, args.warmup)):
+            lib.check(L.kvl_mla_graph_launch(graph), "graph launch")
+        lib.check(L.kvl_mla_synchronize(), "sync")
+
+    K = args.steps
+    lib.check(L.kvl_mla_synchronize(), "sync")
+    t0 = time.perf_counter()
+    e0 = L.kvl_mla_event_record()
+    for _ in range(K):
+        if graph is not None:
+            lib.check(L.kvl_mla_graph_launch(graph), "graph launch")
+        else:
+            step()
+    e1 = L.kvl_mla_event_record()
+    lib.check(L.kvl_mla_synchronize(), "sync")
+    t1 = time.perf_counter()
+    ev_ms = L.kvl_mla_event_elapsed_ms(e0, e1) / K
+    L.kvl_mla_event_destroy(e0)
+    L.kvl_mla_event_destroy(e1)
+    ms_step = (t1 - t0) * 1e3 / K
+    wb = weight_bytes(cfg)
+    hist_bytes = B * (CTX + 1) * Q8_ROW
+    step_bytes = NL * (wb + hist_bytes)
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    log(f"[bench] step {ms_step:.3f} ms wall ({ev_ms:.3f} ms events), {value:.1f} GB/s")
+
+    attn = stages["attention"]
+    attn_gbs = hist_bytes / (attn["ms_per_launch"] * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "k_attn_q8_mfma", "algorithmic_bytes_per_launch": hist_bytes,
+                "avg_launch_ms": round(attn["ms_per_launch"], 5)}
+
+    result = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": K,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": f"{NL}-layer MLA attention stack decode, batch {B}, {CTX}-token row-wise Q8 "
+                               f"latent history per layer and sequence", "layers": NL, "batch": B,
+                   "context": CTX, "hidden": H, "heads": cfg.num_heads, "kv_lora_rank": cfg.kv_lora_rank,
+                   "qk_rope_dim": cfg.qk_rope_dim, "history_row_bytes": Q8_ROW,
+                   "bytes_per_step": step_bytes, "mode": "eager" if graph is None else "hip-graph"},
+        "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "roofline": roofline,
+        "stages_ms_per_launch": {k: round(v["ms_per_launch"], 5) for k, v in stages.items()},
+    }
+
+    # ---- parity spot check + CPU baseline on layer 0 -------------------------------------
+    lib.check(L.kvl_mla_decode_compressed_q8_batch_device(d_l0, d_x0, B, C.byref(cfg), C.byref(wstructs[0]),
+                                                          arrays[0], lib.NO_ADVANCE), "layer-0 decode")
+    gpu_l0 = np.zeros_like(x0)
+    lib.check(L.kvl_mla_copy_to_host(gpu_l0.ctypes.data, d_l0, nbytes), "d2h")
+    if not args.no_cpu:
+        import pyoracle
+        from helpers import rel_err
+        ref = pyoracle.load_reference("avx2")
+        kind = "reference" if ref is not None else "port"
+        cpu = ref if ref is not None else pyoracle.load_oracle()
+        fn = cpu.kvl_mla_decode_compressed_q8_bf16 if ref is not None else cpu.orc_mla_decode_compressed_q8_bf16
+        errs, t_cpu, n_done = [], 0.0, 0
+        for b in range(B):
+            st = states[0][b]
+            lib.check(L.kvl_mla_compressed_q8_state_pull(C.byref(st), 0, CTX), "pull")
+            out = np.zeros(H, np.float32)
+            ts = time.perf_counter()
+            rc = fn(out.ctypes.data_as(abi.f32p), x0[b].ctypes.data_as(abi.f32p), CTX, C.byref(cfg),
+                    C.byref(wstructs[0]), C.byref(st))
+            t_cpu += time.perf_counter() - ts
+            st.len = CTX  # the CPU call appended at position CTX; restore
+            if rc != 0:
+                raise RuntimeError("CPU baseline call failed")
+            errs.append(rel_err(gpu_l0[b], out))
+            n_done += 1
+            if t_cpu > 25.0:
+                break
+        sample_bytes = wb + n_done * (CTX + 1) * Q8_ROW
+        result["cpu_baseline"] = {
+            "value": round(sample_bytes / t_cpu / 1e9, 3), "unit": "GB/s", "cores": omp_threads(), "kind": kind,
+            "sample": f"layer 0 of the stack, {n_done} of {B} sequences at {CTX} tokens, one decode token each "
+                      f"({t_cpu:.2f} s; the reference loops its single-sequence API; attention loops are "
+                      f"single-threaded there, GEMVs use OpenMP)"}
+        result["parity"] = {"layer0_max_rel_err_vs_cpu": float(max(errs)), "tolerance": 2e-3,
+                            "sequences": n_done}
+        log(f"[bench] cpu baseline {result['cpu_baseline']['value']} GB/s ({kind}), parity {max(errs):.2e}")
+
+    # ---- causal prefill, 4096 tokens -----------------------------------------------------
+    if not args.no_prefill:
+        S = args.prefill_tokens
+        xs = np.ascontiguousarray(inputs.bf16_bits_to_f32(inputs.f32_to_bf16_bits(
+            np.random.default_rng(0xC3).standard_normal((S, H), dtype=np.float32))))
+        d_px = L.kvl_mla_device_alloc(xs.nbytes)
+        d_po = L.kvl_mla_device_alloc(xs.nbytes)
+        lib.check(L.kvl_mla_copy_to_device(d_px, xs.ctypes.data, xs.nbytes), "h2d")
+        for _ in range(2):
+            lib.check(L.kvl_mla_prefill_device(d_po, d_px, S, C.byref(cfg), C.byref(wstructs[0])), "prefill")
+        lib.check(L.kvl_mla_synchronize(), "sync")
+        reps = 5
+        p0 = L.kvl_mla_event_record()
+        for _ in range(reps):
+            lib.check(L.kvl_mla_prefill_device(d_po, d_px, S, C.byref(cfg), C.byref(wstructs[0])), "prefill")
+        p1 = L.kvl_mla_event_record()
+        pms = L.kvl_mla_event_elapsed_ms(p0, p1) / reps
+        flops = prefill_flops(S, cfg)
+        tf = flops / (pms * 1e-3) / 1e12
+        result["prefill"] = {"tokens": S, "ms": round(pms, 4), "tflops": round(tf, 2),
+                             "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4),
+                             "algorithmic_gflop": round(flops / 1e9, 3)}
+        log(f"[bench] prefill S={S}: {pms:.3f} ms, {tf:.1f} TFLOP/s")
+        L.kvl_mla_device_free(d_px)
+        L.kvl_mla_device_free(d_po)
+
+    if args.calibrate_copy:
+        nb = args.calibrate_copy << 20
+        a = L.kvl_mla_device_alloc(nb)
+        b = L.kvl_mla_device_alloc(nb)
+        for _ in range(3):
+            lib.check(L.kvl_mla_copy_kernel(b, a, nb), "copy")
+        lib.check(L.kvl_mla_synchronize(), "sync")
+        c0 = L.kvl_mla_event_record()
+        lib.check(L.kvl_mla_copy_kernel(b, a, nb), "copy")
+        c1 = L.kvl_mla_event_record()
+        cms = L.kvl_mla_event_elapsed_ms(c0, c1)
+        result["copy_calibration"] = {"bytes_each_way": nb, "ms": round(cms, 4),
+                                      "gbs_read_plus_write": round(2 * nb / (cms * 1e-3) / 1e9, 1)}
+        L.kvl_mla_device_free(a)
+        L.kvl_mla_device_free(b)
+
+    if graph is not None:
+        L.kvl_mla_graph_destroy(graph)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -398,11 +398,36 @@ __global__ __launch_bounds__(256) void k_qprep(QprepArgs a) {
         for (int i = tid; i < d.DN; i += 256) qrow[i] = qn[i];
     } else {
         const uint16_t *wuk = a.kv_b + (size_t)h * (d.DN + d.DV) * d.R;
-        for (int r = tid; r < d.R; r += 256) {
-            float acc = 0.f;
-            for (int k = 0; k < d.DN; ++k) acc = fmaf(bf16_to_f32(wuk[(size_t)k * d.R + r]), qn[k], acc);
-            ql[r] = acc;
-            qrow[r] = acc;
+        if ((d.R & 1) == 0) {
+            // two adjacent latent columns per thread (one 4-byte load per k), 4 k in flight
+            for (int r = 2 * tid; r < d.R; r += 512) {
+                float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
+                int k = 0;
+                for (; k + 2 <= d.DN; k += 2) {
+                    const uint32_t u0 = *(const uint32_t *)(wuk + (size_t)k * d.R + r);
+                    const uint32_t u1 = *(const uint32_t *)(wuk + (size_t)(k + 1) * d.R + r);
+                    a0 = fmaf(__uint_as_float(u0 << 16), qn[k], a0);
+                    a1 = fmaf(__uint_as_float(u0 & 0xffff0000u), qn[k], a1);
+                    b0 = fmaf(__uint_as_float(u1 << 16), qn[k + 1], b0);
+                    b1 = fmaf(__uint_as_float(u1 & 0xffff0000u), qn[k + 1], b1);
+                }
+                for (; k < d.DN; ++k) {
+                    const uint32_t u0 = *(const uint32_t *)(wuk + (size_t)k * d.R + r);
+                    a0 = fmaf(__uint_as_float(u0 << 16), qn[k], a0);
+                    a1 = fmaf(__uint_as_float(u0 & 0xffff0000u), qn[k], a1);
+                }
+                ql[r] = a0 + b0;
+                ql[r + 1] = a1 + b1;
+                qrow[r] = a0 + b0;
+                qrow[r + 1] = a1 + b1;
+            }
+        } else {
+            for (int r = tid; r < d.R; r += 256) {
+                float acc = 0.f;
+                for (int k = 0; k < d.DN; ++k) acc = fmaf(bf16_to_f32(wuk[(size_t)k * d.R + r]), qn[k], acc);
+                ql[r] = acc;
+                qrow[r] = acc;
+            }
         }
     }
     for (int i = tid; i < half; i += 256) {
@@ -594,8 +619,9 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
     const int b = find_seq(a.t, blockIdx.x);
     const SeqDesc &s = a.t.s[b];
-    const int r0 = (blockIdx.x - s.split0) * a.rps;
-    const int r1 = min(r0 + a.rps, s.len);
+    const int split = blockIdx.x - s.split0;
+    const int r0 = split * s.rps;
+    const int r1 = split == s.nsplit - 1 ? s.len : r0 + s.rps;  // last split takes the rest
     const float *glat = (const float *)s.a;
     const float *grope = (const float *)s.b;
 
@@ -742,8 +768,9 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
     const int b = find_seq(a.t, blockIdx.x);
     const SeqDesc &s = a.t.s[b];
-    const int r0 = (blockIdx.x - s.split0) * a.rps;
-    const int r1 = min(r0 + a.rps, s.len);
+    const int split = blockIdx.x - s.split0;
+    const int r0 = split * s.rps;
+    const int r1 = split == s.nsplit - 1 ? s.len : r0 + s.rps;  // last split takes the rest
     const int8_t *gcodes = (const int8_t *)s.a;
     const float *gscl = (const float *)s.b;
     const uint16_t *grope = (const uint16_t *)s.c;
@@ -977,8 +1004,13 @@ struct CombineArgs {
 // One block per (sequence, head). m* = max_s m_s, denom = sum_s l_s e^(m_s - m*),
 // mix = sum_s acc_s e^(m_s - m*) / denom; then (compressed formats)
 // ho[d] = sum_r kv_b[h*(DN+DV)+DN+d, r] * mix[r] (src/mla_compressed_q8_state.c:239-247).
+// Split weights are computed once into LDS; the mix loop issues independent loads.
+constexpr int kMaxSplits = 2048;
+
 __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
     __shared__ float mx[kMaxR];
+    __shared__ float wts[kMaxSplits];
+    __shared__ float red[256];
     const Dims &d = a.d;
     const int b = blockIdx.x / d.NH, h = blockIdx.x % d.NH, tid = threadIdx.x;
     const SeqDesc &s = a.t.s[b];
@@ -987,18 +1019,46 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
     const int sp0 = exp ? b * d.NH + h : s.split0, ns = exp ? 1 : s.nsplit;
     const size_t stride = (size_t)G * (DVm + 2);
     const float *P = a.part + (size_t)sp0 * stride;
-    float M = -INFINITY;
-    for (int i = 0; i < ns; ++i) M = fmaxf(M, P[i * stride + (size_t)G * DVm + g]);
-    float denom = 0.f;
-    for (int i = 0; i < ns; ++i)
-        denom = fmaf(P[i * stride + (size_t)G * DVm + G + g], __expf(P[i * stride + (size_t)G * DVm + g] - M), denom);
-    const float inv = 1.0f / denom;
+    float m = -INFINITY;
+    for (int i = tid; i < ns; i += 256) {
+        const float mi = P[i * stride + (size_t)G * DVm + g];
+        wts[i] = mi;
+        m = fmaxf(m, mi);
+    }
+    red[tid] = m;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) red[tid] = fmaxf(red[tid], red[tid + o]);
+        __syncthreads();
+    }
+    const float M = red[0];
+    __syncthreads();
+    float den = 0.f;
+    for (int i = tid; i < ns; i += 256) {
+        const float e = __expf(wts[i] - M);
+        wts[i] = e;
+        den = fmaf(P[i * stride + (size_t)G * DVm + G + g], e, den);
+    }
+    red[tid] = den;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) red[tid] += red[tid + o];
+        __syncthreads();
+    }
+    const float inv = 1.0f / red[0];
     float *mixrow = a.mix + ((size_t)b * d.NH + h) * DVm;
+    const float *Pg = P + (size_t)g * DVm;
     for (int k = tid; k < DVm; k += 256) {
-        float v = 0.f;
-        for (int i = 0; i < ns; ++i)
-            v = fmaf(P[i * stride + (size_t)g * DVm + k], __expf(P[i * stride + (size_t)G * DVm + g] - M), v);
-        v *= inv;
+        float v0 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f;
+        int i = 0;
+        for (; i + 4 <= ns; i += 4) {
+            v0 = fmaf(Pg[(size_t)i * stride + k], wts[i], v0);
+            v1 = fmaf(Pg[(size_t)(i + 1) * stride + k], wts[i + 1], v1);
+            v2 = fmaf(Pg[(size_t)(i + 2) * stride + k], wts[i + 2], v2);
+            v3 = fmaf(Pg[(size_t)(i + 3) * stride + k], wts[i + 3], v3);
+        }
+        for (; i < ns; ++i) v0 = fmaf(Pg[(size_t)i * stride + k], wts[i], v0);
+        const float v = ((v0 + v1) + (v2 + v3)) * inv;
         mixrow[k] = v;
         if (exp)
             a.ho[(size_t)b * d.HO + (size_t)h * d.DV + k] = v;
@@ -1009,6 +1069,24 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
     __syncthreads();
     const int w = tid >> 6, l = tid & 63;
     const uint16_t *wuv = a.kv_b + ((size_t)h * (d.DN + d.DV) + d.DN) * d.R;
+    if (d.R == 512) {
+        float mv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mv[e] = mx[8 * l + e];
+        for (int dd = w; dd < d.DV; dd += 4) {
+            const v4i wv = *(const v4i *)(wuv + (size_t)dd * 512 + 8 * l);
+            float acc = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t u = (uint32_t)wv[e];
+                acc = fmaf(__uint_as_float(u << 16), mv[2 * e], acc);
+                acc = fmaf(__uint_as_float(u & 0xffff0000u), mv[2 * e + 1], acc);
+            }
+            acc = wave_sum(acc);
+            if (l == 0) a.ho[(size_t)b * d.HO + (size_t)h * d.DV + dd] = acc;
+        }
+        return;
+    }
     for (int dd = w; dd < d.DV; dd += 4) {
         const uint16_t *row = wuv + (size_t)dd * d.R;
         float acc = 0.f;
@@ -1023,6 +1101,20 @@ hipError_t launch_combine(hipStream_t st, int fmt, const SeqTable &t, const Dims
     if (d.R > kMaxR) return hipErrorInvalidValue;
     CombineArgs a{t, d, w.part, kv_b, w.mix, w.ho, fmt};
     hipLaunchKernelGGL(k_combine, dim3(t.n * d.NH), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+// ================================================================ copy =================
+
+__global__ __launch_bounds__(256) void k_copy(v4i *dst, const v4i *src, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        dst[i] = src[i];
+}
+
+hipError_t launch_copy(hipStream_t st, void *dst, const void *src, size_t bytes) {
+    const size_t n = bytes / 16;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_copy, dim3(4096), dim3(256), 0, st, (v4i *)dst, (const v4i *)src, n);
     return hipGetLastError();
 }
 

@@ -26,7 +26,8 @@ struct Dims {
 
 // One sequence of a batched call. a/b/c are the device arrays of its history
 // (see Fmt), len the number of rows attended (position + 1), pos the row appended
-// by this step. split0/nsplit locate its split-K partials.
+// by this step. split0/nsplit locate its split-K partials; each split covers rps rows
+// except the last, which takes the remainder.
 struct SeqDesc {
     void *a;
     void *b;
@@ -35,7 +36,8 @@ struct SeqDesc {
     int pos;
     int split0;
     int nsplit;
-    int pad0, pad1;
+    int rps;
+    int pad1;
 };
 
 struct SeqTable {
@@ -114,6 +116,9 @@ hipError_t launch_combine(hipStream_t st, int fmt, const SeqTable &t, const Dims
 // latents ~ Irwin-Hall(4) normal from SplitMix64, quantised with the history quantiser.
 hipError_t launch_fill_history(hipStream_t st, int fmt, void *a, void *b, void *c, int R,
                                int DR, int row0, int nrows, uint64_t seed);
+
+// Plain 16-byte vector copy (calibration of memory counters against known bytes).
+hipError_t launch_copy(hipStream_t st, void *dst, const void *src, size_t bytes);
 
 // ---- prefill (mla_prefill.hip) ----
 // Device workspace bytes of a causal prefill of S tokens.

@@ -145,7 +145,13 @@ struct Ctx {
     DevBuf work, part, scores, prefill;
     PinBuf pin_in, pin_out;
     bool capturing = false;
+    // per-stage event timing of decode steps (kvl_mla_timing_*)
+    bool timing = false;
+    std::vector<hipEvent_t> ev_pool;
+    std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> ev_used;
 };
+
+constexpr int kStages = 6;  // gemv_in, append, qprep, attention, combine, gemv_out
 
 Ctx &ctx() {
     static Ctx *c = new Ctx();  // never destroyed: device memory is released by the driver
@@ -169,6 +175,37 @@ int ensure_ready() {
     c.ready = true;
     return 0;
 }
+
+hipEvent_t ev_get() {
+    Ctx &c = ctx();
+    if (!c.ev_pool.empty()) {
+        hipEvent_t e = c.ev_pool.back();
+        c.ev_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+// Brackets one launch of stage `st` with events when timing is on (never during capture).
+struct StageTimer {
+    int stage;
+    hipEvent_t a = nullptr, b = nullptr;
+    explicit StageTimer(int s) : stage(s) {
+        Ctx &c = ctx();
+        if (!c.timing || c.capturing) return;
+        a = ev_get();
+        b = ev_get();
+        if (a && b) (void)hipEventRecord(a, c.stream);
+    }
+    ~StageTimer() {
+        Ctx &c = ctx();
+        if (!a || !b) return;
+        (void)hipEventRecord(b, c.stream);
+        c.ev_used.push_back({stage, {a, b}});
+    }
+};
 
 // ---------------------------------------------------------------- shapes ----------------
 
@@ -548,15 +585,26 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
         }
         total_splits = fmt == kFmtExp ? B * d.NH : B;
     } else {
+        // Balanced split-K: about wg_per_cu workgroups per CU in total, shared among the
+        // sequences in proportion to their lengths; rows per split a multiple of the
+        // kernel's chunk (rounded down), the last split of a sequence takes the remainder.
         const int chunk = kind == kAttnQ8Mfma ? 64 : 16;
-        const long target = 2L * c.ncu;
-        long per = (total_rows + target - 1) / target;
-        per = std::max<long>(per, 4L * chunk);
-        rps = (int)((per + chunk - 1) / chunk * chunk);
+        const int wg_per_cu = kind == kAttnQ8Mfma ? 2 : 3;
+        const double target = (double)wg_per_cu * c.ncu;
         for (int i = 0; i < B; ++i) {
-            t.s[i].split0 = total_splits;
-            t.s[i].nsplit = (t.s[i].len + rps - 1) / rps;
-            total_splits += t.s[i].nsplit;
+            SeqDesc &s = t.s[i];
+            const long want = std::max(1L, std::lround(target * (double)s.len / (double)total_rows));
+            long r = (long)s.len / (want * chunk) * chunk;
+            r = std::max<long>(r, 4L * chunk);
+            s.rps = (int)r;
+            s.split0 = total_splits;
+            s.nsplit = std::max(1, (int)(s.len / r));
+            total_splits += s.nsplit;
+            rps = std::max(rps, s.rps);
+        }
+        if (total_splits > 2048) {
+            set_err("split plan exceeds 2048 partials");
+            return -1;
         }
     }
     const int G = fmt == kFmtExp ? 1 : d.NH;
@@ -576,16 +624,34 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
     }
 
     const int ldy = d.QO + d.KVO;
-    HIP_TRY(launch_gemv(st, w.y, ldy, d_x, d.H, B, dw.q, d.QO, dw.kva, d.KVO, d.H, false));
-    HIP_TRY(launch_append(st, fmt, t, d, w.y, ldy, d.QO, dw.norm, eps, cs, w, false, 0));
-    if (fmt == kFmtExp) {
-        HIP_TRY(launch_gemv(st, w.kv, d.KVB, w.latent, d.R, B, dw.kvb, d.KVB, nullptr, 0, d.R, false));
-        HIP_TRY(launch_store_expanded(st, t, d, w));
+    {
+        StageTimer tm(0);
+        HIP_TRY(launch_gemv(st, w.y, ldy, d_x, d.H, B, dw.q, d.QO, dw.kva, d.KVO, d.H, false));
     }
-    HIP_TRY(launch_qprep(st, fmt, t, d, dw.kvb, cs, w, kind == kAttnQ8Mfma));
-    HIP_TRY(launch_attention(st, kind, fmt, t, d, rps, total_splits, lmax, w));
-    HIP_TRY(launch_combine(st, fmt, t, d, dw.kvb, w));
-    HIP_TRY(launch_gemv(st, d_out, d.H, w.ho, d.HO, B, dw.o, d.H, nullptr, 0, d.HO, residual));
+    {
+        StageTimer tm(1);
+        HIP_TRY(launch_append(st, fmt, t, d, w.y, ldy, d.QO, dw.norm, eps, cs, w, false, 0));
+        if (fmt == kFmtExp) {
+            HIP_TRY(launch_gemv(st, w.kv, d.KVB, w.latent, d.R, B, dw.kvb, d.KVB, nullptr, 0, d.R, false));
+            HIP_TRY(launch_store_expanded(st, t, d, w));
+        }
+    }
+    {
+        StageTimer tm(2);
+        HIP_TRY(launch_qprep(st, fmt, t, d, dw.kvb, cs, w, kind == kAttnQ8Mfma));
+    }
+    {
+        StageTimer tm(3);
+        HIP_TRY(launch_attention(st, kind, fmt, t, d, rps, total_splits, lmax, w));
+    }
+    {
+        StageTimer tm(4);
+        HIP_TRY(launch_combine(st, fmt, t, d, dw.kvb, w));
+    }
+    {
+        StageTimer tm(5);
+        HIP_TRY(launch_gemv(st, d_out, d.H, w.ho, d.HO, B, dw.o, d.H, nullptr, 0, d.HO, residual));
+    }
     return 0;
 }
 
@@ -1414,6 +1480,80 @@ int kvl_mla_q8_pack_rows(int8_t *codes, float *scales, uint16_t *rope_bf16, cons
         memcpy(scales + i, row + R, 4);
         memcpy(rope_bf16 + (size_t)i * DR, row + R + 4, 2 * (size_t)DR);
     }
+    return 0;
+}
+
+int kvl_mla_timing_enable(int on) {
+    Guard guard;
+    if (ensure_ready() != 0) return -1;
+    ctx().timing = on != 0;
+    return 0;
+}
+
+// Sums the recorded stage durations (ms) into ms[0..5] and launch counts into count[0..5]
+// (gemv_in, append, qprep, attention, combine, gemv_out), then clears the records.
+int kvl_mla_timing_read(double *ms, int *count) {
+    Guard guard;
+    Ctx &c = ctx();
+    if (!ms || !count) return -1;
+    for (int i = 0; i < kStages; ++i) {
+        ms[i] = 0.0;
+        count[i] = 0;
+    }
+    int rc = 0;
+    for (auto &u : c.ev_used) {
+        float t = 0.f;
+        if (hipEventSynchronize(u.second.second) != hipSuccess ||
+            hipEventElapsedTime(&t, u.second.first, u.second.second) != hipSuccess) {
+            set_err("event timing failed");
+            rc = -1;
+        } else if (u.first >= 0 && u.first < kStages) {
+            ms[u.first] += t;
+            count[u.first] += 1;
+        }
+        c.ev_pool.push_back(u.second.first);
+        c.ev_pool.push_back(u.second.second);
+    }
+    c.ev_used.clear();
+    return rc;
+}
+
+void *kvl_mla_event_record(void) {
+    Guard guard;
+    if (ensure_ready() != 0) return nullptr;
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess || hipEventRecord(e, ctx().stream) != hipSuccess) {
+        set_err("event record failed");
+        return nullptr;
+    }
+    return (void *)e;
+}
+
+double kvl_mla_event_elapsed_ms(void *start, void *end) {
+    Guard guard;
+    float t = -1.f;
+    if (!start || !end || hipEventSynchronize((hipEvent_t)end) != hipSuccess ||
+        hipEventElapsedTime(&t, (hipEvent_t)start, (hipEvent_t)end) != hipSuccess) {
+        set_err("event elapsed failed");
+        return -1.0;
+    }
+    return (double)t;
+}
+
+int kvl_mla_event_destroy(void *ev) {
+    Guard guard;
+    if (ev) HIP_TRY(hipEventDestroy((hipEvent_t)ev));
+    return 0;
+}
+
+int kvl_mla_copy_kernel(void *dst, const void *src, size_t bytes) {
+    Guard guard;
+    if (!dst || !src || (bytes % 16) != 0) {
+        set_err("copy: 16-byte multiple required");
+        return -1;
+    }
+    if (ensure_ready() != 0) return -1;
+    HIP_TRY(launch_copy(ctx().stream, dst, src, bytes));
     return 0;
 }
 

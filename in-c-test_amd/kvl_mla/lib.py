@@ -42,6 +42,12 @@ EXT_API = {
     "mla_capture_end": (C.c_int, [C.POINTER(C.c_void_p)]),
     "mla_graph_launch": (C.c_int, [C.c_void_p]),
     "mla_graph_destroy": (C.c_int, [C.c_void_p]),
+    "mla_timing_enable": (C.c_int, [C.c_int]),
+    "mla_timing_read": (C.c_int, [C.POINTER(C.c_double), C.POINTER(C.c_int)]),
+    "mla_event_record": (C.c_void_p, []),
+    "mla_event_elapsed_ms": (C.c_double, [C.c_void_p, C.c_void_p]),
+    "mla_event_destroy": (C.c_int, [C.c_void_p]),
+    "mla_copy_kernel": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "mla_q8_pack_rows": (C.c_int, [abi.i8p, abi.f32p, abi.u16p, abi.f32p, abi.f32p,
                                    C.POINTER(C.c_int), C.c_int, C.c_int, C.c_int, C.c_float]),
     "mla_compressed_q8_state_fill_synthetic": (C.c_int, [abi.QS, C.c_int, C.c_int, C.c_uint64]),
@@ -50,6 +56,7 @@ EXT_API = {
     "mla_compressed_state_pull": (C.c_int, [abi.CS, C.c_int, C.c_int]),
 }
 
+STAGES = ("gemv_in", "append", "qprep", "attention", "combine", "gemv_out")
 RESIDUAL = 1
 NO_ADVANCE = 2
 

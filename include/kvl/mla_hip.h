@@ -95,6 +95,19 @@ int kvl_mla_capture_end(void **graph_exec);
 int kvl_mla_graph_launch(void *graph_exec);
 int kvl_mla_graph_destroy(void *graph_exec);
 
+/* Measurement helpers. kvl_mla_timing_enable(1) brackets every decode-step kernel with HIP
+ * events on kvl_mla_stream() (not during graph capture); kvl_mla_timing_read() sums the
+ * durations (ms) and launch counts of the six stages (gemv_in, append, qprep, attention,
+ * combine, gemv_out) since the last read. Events: record on the library stream, elapsed
+ * time between two recorded events (waits for the second). kvl_mla_copy_kernel: a plain
+ * 16-byte vector copy kernel (bytes % 16 == 0), for calibrating memory counters. */
+int kvl_mla_timing_enable(int on);
+int kvl_mla_timing_read(double *ms, int *count);
+void *kvl_mla_event_record(void);
+double kvl_mla_event_elapsed_ms(void *start, void *end);
+int kvl_mla_event_destroy(void *event);
+int kvl_mla_copy_kernel(void *dst, const void *src, size_t bytes);
+
 /* Quantiser boundary, computed on the GPU: for row i, latent [n, R] (already normalised) ->
  * int8 codes [n, R] + fp32 scale [n]; k_rope_raw [n, DR] (before rotation) -> RoPE at
  * positions[i] -> BF16 RNE [n, DR]. Same rows as src/mla_compressed_q8_state.c:34-55,
