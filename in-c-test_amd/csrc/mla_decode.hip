@@ -731,7 +731,11 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
 }
 
 // ---- int8 MFMA path (Q8 history, NH=16, R=512, DR=64) ---------------------------------
-// Chunks of 64 rows (41 KB) are staged in LDS by all four waves with 16-byte loads.
+// One workgroup (4 waves) per CU streams its split in chunks of 64 rows through a ring of
+// three LDS chunk buffers (41 KB each) filled by global_load_lds_dwordx4 DMA: while chunk c
+// is computed, chunks c+1 and c+2 are in flight, and no VGPRs stage the stream. The 16-byte
+// slots of each LDS row are XOR-swizzled so that the row reads of the score and the
+// column reads of the mix are both free of bank conflicts.
 // Scores (wave w: rows 16w..16w+15): v_mfma_i32_16x16x64_i8 on the raw int8 codes against
 // the int8 hi/lo split of q_lat (exact integer dot products), plus bf16 MFMA on the bf16
 // RoPE keys against the hi/lo bf16 split of q_rope. The row scale factors out of the dot
@@ -740,9 +744,43 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
 // running max), and multiplied with the codes, transposed per 4x4 byte block in registers,
 // by v_mfma_i32_16x16x64_i8 (K = 64 rows). Each wave accumulates 128 latent columns.
 constexpr int kQ8Ch = 64;
-constexpr int kQ8Cs = 528;  // LDS bytes per code row (512 + 16)
-constexpr int kQ8Rs = 144;  // LDS bytes per RoPE row (128 + 16)
-constexpr int kQ8Ws = 80;   // LDS bytes per quantised-weight row (64 + 16)
+constexpr int kQ8Ring = 3;
+constexpr int kQ8CodeB = kQ8Ch * 512;               // codes of a chunk
+constexpr int kQ8RopeB = kQ8Ch * 128;               // bf16 RoPE keys of a chunk
+constexpr int kQ8SclB = kQ8Ch * 4;                  // scales of a chunk
+constexpr int kQ8ChunkB = kQ8CodeB + kQ8RopeB + kQ8SclB;
+constexpr int kQ8Ws = 80;                           // LDS bytes per quantised-weight row
+constexpr int kQ8SmemB = kQ8Ring * kQ8ChunkB + 2 * 16 * kQ8Ws + 2 * 4 * 16 * 4;
+
+// Slot swizzle of the code rows: physical 16-byte slot = logical slot ^ q8_swz(row).
+__device__ __forceinline__ int q8_swz(int row) { return (row & 7) ^ (((row >> 4) & 1) << 2); }
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)p; }
+
+// Asynchronous global -> LDS copies: lane l's bytes land at lds_base + l * size. The wave
+// must pass a wave-uniform lds_base. M0 is saved and restored around the instruction.
+__device__ __forceinline__ void dma_b128(const void *gptr, uint32_t lds_base) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_base);
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "s"(base), "v"(gptr)
+                 : "memory");
+}
+__device__ __forceinline__ void dma_b32(const void *gptr, uint32_t lds_base) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_base);
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dword %2, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "s"(base), "v"(gptr)
+                 : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Workgroup barrier after this wave's LDS writes have completed.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ void transpose4x4(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
                                              uint32_t &o0, uint32_t &o1, uint32_t &o2,
@@ -758,13 +796,11 @@ __device__ __forceinline__ void transpose4x4(uint32_t a, uint32_t b, uint32_t c,
 }
 
 __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t codes[kQ8Ch * kQ8Cs];
-    __shared__ __attribute__((aligned(16))) uint8_t ropes[kQ8Ch * kQ8Rs];
-    __shared__ __attribute__((aligned(16))) int8_t wq[2][16 * kQ8Ws];
-    __shared__ float scl[kQ8Ch];
-    __shared__ float mloc[4][16];
-    __shared__ float lsum[4][16];
-    __shared__ float smax_s;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[kQ8SmemB];
+    int8_t *wq = (int8_t *)(smem + kQ8Ring * kQ8ChunkB);  // [2][16 heads][kQ8Ws]
+    float *mloc = (float *)(smem + kQ8Ring * kQ8ChunkB + 2 * 16 * kQ8Ws);  // [4][16]
+    float *lsum = mloc + 64;                                                // [4][16]
+    const uint32_t sbase = lds_addr(smem);
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
     const int b = find_seq(a.t, blockIdx.x);
     const SeqDesc &s = a.t.s[b];
@@ -791,6 +827,36 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
     float qsd[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) qsd[i] = a.qs[(size_t)b * 16 + 4 * g + i];
+    // Settle the query loads here: the empty asm consumes each operand, so the compiler
+    // waits for them once now and never again inside the loop, where any vmcnt wait it
+    // inserted would also drain the chunk DMA ring.
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) {
+        asm volatile("" : "+v"(qh[kb]));
+        asm volatile("" : "+v"(ql[kb]));
+    }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        asm volatile("" : "+v"(qrh[kb]));
+        asm volatile("" : "+v"(qrl[kb]));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(qsd[i]));
+
+    // Largest row scale of the split: the common bound of the quantised weights p_j * s_j
+    // (p_j <= 1 after the running max). One reduction per workgroup.
+    float smax;
+    {
+        float m = 0.f;
+        for (int r = r0 + tid; r < r1; r += 256) m = fmaxf(m, gscl[r]);
+        m = wave_max(m);
+        if (l == 0) mloc[w] = m;
+        __syncthreads();
+        smax = fmaxf(fmaxf(mloc[0], mloc[1]), fmaxf(mloc[2], mloc[3]));
+        __syncthreads();
+    }
+    const float wscale = smax > 0.f ? 127.0f / smax : 0.f;
+    const float wfac = smax * (1.0f / (127.0f * 128.0f));
 
     float m_run[4], l_lane[4];
 #pragma unroll
@@ -802,64 +868,68 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    v4i pc[8], pr[2];
-    float ps = 0.f;
-    auto prefetch = [&](int c) {
-        const int base = r0 + c * kQ8Ch;
+    const int nch = (r1 - r0 + kQ8Ch - 1) / kQ8Ch;
+    // DMA of chunk c into ring slot c % 3: each wave copies 8 row pairs of codes, 2 row
+    // octets of RoPE keys (wave 0 also the 64 scales). Rows past the split end re-read the
+    // split's last row (in bounds); their scores are masked.
+    auto issue = [&](int c) {
+        const uint32_t buf = sbase + (uint32_t)((c % kQ8Ring) * kQ8ChunkB);
+        const int rb0 = r0 + c * kQ8Ch;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const int p = tid + 256 * k, row = p >> 5, c16 = p & 31, gr = base + row;
-            pc[k] = gr < r1 ? *(const v4i *)(gcodes + (size_t)gr * 512 + 16 * c16) : v4i{0, 0, 0, 0};
+            const int i = w * 8 + k;
+            const int row = 2 * i + (l >> 5);
+            const int cidx = (l & 31) ^ q8_swz(row);
+            const int gr = min(rb0 + row, r1 - 1);
+            dma_b128(gcodes + (size_t)gr * 512 + 16 * cidx, buf + (uint32_t)(i * 1024));
         }
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-            const int p = tid + 256 * k, row = p >> 3, c8 = p & 7, gr = base + row;
-            pr[k] = gr < r1 ? *(const v4i *)(grope + (size_t)gr * 64 + 8 * c8) : v4i{0, 0, 0, 0};
+            const int i = w * 2 + k;
+            const int row = 8 * i + (l >> 3);
+            const int cidx = (l & 7) ^ (row & 7);
+            const int gr = min(rb0 + row, r1 - 1);
+            dma_b128(grope + (size_t)gr * 64 + 8 * cidx, buf + (uint32_t)(kQ8CodeB + i * 1024));
         }
-        if (tid < kQ8Ch) {
-            const int gr = base + tid;
-            ps = gr < r1 ? gscl[gr] : 0.f;
-        }
+        if (w == 0) dma_b32(gscl + min(rb0 + l, r1 - 1), buf + (uint32_t)(kQ8CodeB + kQ8RopeB));
     };
-    auto stash = [&]() {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int p = tid + 256 * k, row = p >> 5, c16 = p & 31;
-            *(v4i *)(codes + row * kQ8Cs + 16 * c16) = pc[k];
-        }
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int p = tid + 256 * k, row = p >> 3, c8 = p & 7;
-            *(v4i *)(ropes + row * kQ8Rs + 16 * c8) = pr[k];
-        }
-        if (tid < kQ8Ch) {  // wave 0, all lanes
-            scl[tid] = ps;
-            const float mx = wave_max(ps);
-            if (tid == 0) smax_s = mx;
+    // this wave's DMA instructions per chunk: 10, wave 0: 11
+    auto wait_chunk = [&](int later) {
+        if (w == 0) {
+            if (later >= 2) wait_vmcnt<22>();
+            else if (later == 1) wait_vmcnt<11>();
+            else wait_vmcnt<0>();
+        } else {
+            if (later >= 2) wait_vmcnt<20>();
+            else if (later == 1) wait_vmcnt<10>();
+            else wait_vmcnt<0>();
         }
     };
 
-    const int nch = (r1 - r0 + kQ8Ch - 1) / kQ8Ch;
+    issue(0);
+    if (nch > 1) issue(1);
     const int rowl = 16 * w + n;
-    prefetch(0);
+    const int swz_l = q8_swz(rowl);
     for (int c = 0; c < nch; ++c) {
-        __syncthreads();
-        stash();
-        __syncthreads();
-        if (c + 1 < nch) prefetch(c + 1);
+        if (c + 2 < nch) issue(c + 2);  // ring slot of chunk c-1, released at its end barrier
+        wait_chunk(min(2, nch - 1 - c));
+        lds_barrier();
+        const uint8_t *codes = smem + (c % kQ8Ring) * kQ8ChunkB;
+        const uint8_t *ropes = codes + kQ8CodeB;
+        const float *scl = (const float *)(codes + kQ8CodeB + kQ8RopeB);
         const int base = r0 + c * kQ8Ch;
 
         v4i ih = {0, 0, 0, 0}, il = {0, 0, 0, 0};
         v4f fr = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kb = 0; kb < 8; ++kb) {
-            const v4i bv = *(const v4i *)(codes + rowl * kQ8Cs + 64 * kb + 16 * g);
+            const v4i bv = *(const v4i *)(codes + rowl * 512 + 16 * ((4 * kb + g) ^ swz_l));
             ih = mfma_i8(qh[kb], bv, ih);
             il = mfma_i8(ql[kb], bv, il);
         }
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
-            const v8bf bv = *(const v8bf *)(ropes + rowl * kQ8Rs + 64 * kb + 16 * g);
+            const v8bf bv = *(const v8bf *)(ropes + rowl * 128 + 16 * ((4 * kb + g) ^ (rowl & 7)));
             fr = mfma_bf16(qrh[kb], bv, fr);
             fr = mfma_bf16(qrl[kb], bv, fr);
         }
@@ -873,21 +943,17 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
             lm[i] = sc[i];
         }
 #pragma unroll
-        for (int o = 1; o < 16; o <<= 1)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) lm[i] = fmaxf(lm[i], __shfl_xor(lm[i], o));
+        for (int i = 0; i < 4; ++i) lm[i] = row16_max(lm[i]);
         if (n == 0)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) mloc[w][4 * g + i] = lm[i];
-        __syncthreads();
+            for (int i = 0; i < 4; ++i) mloc[w * 16 + 4 * g + i] = lm[i];
+        lds_barrier();
 
-        const float smax = smax_s;
-        const float wscale = smax > 0.f ? 127.0f / smax : 0.f;
         float alpha[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int hh = 4 * g + i;
-            const float cm = fmaxf(fmaxf(mloc[0][hh], mloc[1][hh]), fmaxf(mloc[2][hh], mloc[3][hh]));
+            const float cm = fmaxf(fmaxf(mloc[hh], mloc[16 + hh]), fmaxf(mloc[32 + hh], mloc[48 + hh]));
             const float mnew = fmaxf(m_run[i], cm);
             alpha[i] = __expf(m_run[i] - mnew);
             m_run[i] = mnew;
@@ -897,20 +963,22 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
             float hi = fminf(rintf(v), 127.f);
             float lo = rintf((v - hi) * 128.0f);
             lo = fminf(fmaxf(lo, -127.f), 127.f);
-            wq[0][hh * kQ8Ws + rowl] = (int8_t)hi;
-            wq[1][hh * kQ8Ws + rowl] = (int8_t)lo;
+            wq[hh * kQ8Ws + rowl] = (int8_t)hi;
+            wq[16 * kQ8Ws + hh * kQ8Ws + rowl] = (int8_t)lo;
         }
-        __syncthreads();
+        lds_barrier();
 
-        const v4i wh = *(const v4i *)(wq[0] + n * kQ8Ws + 16 * g);
-        const v4i wl = *(const v4i *)(wq[1] + n * kQ8Ws + 16 * g);
-        const float wfac = smax * (1.0f / (127.0f * 128.0f));
+        const v4i wh = *(const v4i *)(wq + n * kQ8Ws + 16 * g);
+        const v4i wl = *(const v4i *)(wq + 16 * kQ8Ws + n * kQ8Ws + 16 * g);
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb) {
-            const int col = 128 * w + 64 * rb + 4 * n;
+            const int slot = 8 * w + 4 * rb + (n >> 2);
             uint32_t dd[16];
 #pragma unroll
-            for (int k = 0; k < 16; ++k) dd[k] = *(const uint32_t *)(codes + (16 * g + k) * kQ8Cs + col);
+            for (int k = 0; k < 16; ++k) {
+                const int row = 16 * g + k;
+                dd[k] = *(const uint32_t *)(codes + row * 512 + 16 * (slot ^ q8_swz(row)) + 4 * (n & 3));
+            }
             uint32_t tt[4][4];
 #pragma unroll
             for (int q = 0; q < 4; ++q)
@@ -927,18 +995,14 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
                     acc[rb * 4 + t][i] = fmaf(acc[rb * 4 + t][i], alpha[i], wfac * (float)(ih2[i] * 128 + il2[i]));
             }
         }
+        lds_barrier();  // ring slot, mloc and wq free for the next chunk
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float v = l_lane[i];
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o);
-        l_lane[i] = v;
-    }
+    for (int i = 0; i < 4; ++i) l_lane[i] = row16_sum(l_lane[i]);
     if (n == 0)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) lsum[w][4 * g + i] = l_lane[i];
-    __syncthreads();
+        for (int i = 0; i < 4; ++i) lsum[w * 16 + 4 * g + i] = l_lane[i];
+    lds_barrier();
     float *P = a.part + (size_t)blockIdx.x * 16 * 514;
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
@@ -951,7 +1015,7 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
         for (int i = 0; i < 4; ++i) {
             const int hh = 4 * g + i;
             P[8192 + hh] = m_run[i];
-            P[8192 + 16 + hh] = (lsum[0][hh] + lsum[1][hh]) + (lsum[2][hh] + lsum[3][hh]);
+            P[8192 + 16 + hh] = (lsum[hh] + lsum[16 + hh]) + (lsum[32 + hh] + lsum[48 + hh]);
         }
     }
 }

@@ -73,6 +73,27 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Reductions over the 16 lanes of each DPP row (lanes 16r .. 16r+15) with DPP moves:
+// quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_ror:4, row_ror:8.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_f32<0xB1>(v));
+    v = fmaxf(v, dpp_f32<0x4E>(v));
+    v = fmaxf(v, dpp_f32<0x124>(v));
+    v = fmaxf(v, dpp_f32<0x128>(v));
+    return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x124>(v);
+    v += dpp_f32<0x128>(v);
+    return v;
+}
+
 // SplitMix64 output k (k >= 1) of the stream seeded by `seed`.
 __device__ __forceinline__ uint64_t splitmix64_at(uint64_t seed, uint64_t k) {
     uint64_t z = seed + k * 0x9E3779B97F4A7C15ull;

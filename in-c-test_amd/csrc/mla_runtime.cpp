@@ -589,7 +589,7 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
         // sequences in proportion to their lengths; rows per split a multiple of the
         // kernel's chunk (rounded down), the last split of a sequence takes the remainder.
         const int chunk = kind == kAttnQ8Mfma ? 64 : 16;
-        const int wg_per_cu = kind == kAttnQ8Mfma ? 2 : 3;
+        const int wg_per_cu = kind == kAttnQ8Mfma ? 1 : 3;
         const double target = (double)wg_per_cu * c.ncu;
         for (int i = 0; i < B; ++i) {
             SeqDesc &s = t.s[i];
