@@ -16,6 +16,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace kvl {
 
 // ================================================================ GEMV =================
@@ -28,65 +30,78 @@ struct GemvArgs {
     int ldy, ldx, B, out0, out1, in, acc;
 };
 
-// 16 output rows per block; wave w owns the k-quarter [w*in/4, (w+1)*in/4). The weight tile
-// is the MFMA A operand (exact bf16), the batch of activations the B operand as a hi/lo bf16
-// pair, so every product is exact and accumulation is fp32. Up to 16 sequences per block
-// column (blockIdx.y). Requires in % 128 == 0 and 16-byte aligned rows.
-__global__ __launch_bounds__(256) void k_gemv_mfma(GemvArgs a) {
-    __shared__ v4f red[3][64];
+// 32 output rows per block (two 16-row MFMA tiles); wave w of 8 owns the k-eighth
+// [w*in/8, (w+1)*in/8). The weight tiles are the MFMA A operand (exact bf16), the batch of
+// activations the B operand as a hi/lo bf16 pair, so every product is exact and the
+// accumulation is fp32. All weight and activation loads of a wave are issued before the
+// first MFMA (the kernel is latency-bound at decode batch sizes). Up to 16 sequences per
+// block column (blockIdx.y). Requires in % 256 == 0 and 16-byte aligned rows.
+constexpr int kGvKb = 8;  // k-blocks of 32 per wave and pass
+
+__global__ __launch_bounds__(512) void k_gemv_mfma(GemvArgs a) {
+    __shared__ v4f red[7][2][64];
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
     const int out = a.out0 + a.out1;
-    const int row0 = blockIdx.x * 16;
-    const int row = row0 + n;
-    const uint16_t *wrow = nullptr;
-    if (row < a.out0)
-        wrow = a.W0 + (size_t)row * a.in;
-    else if (row < out)
-        wrow = a.W1 + (size_t)(row - a.out0) * a.in;
+    const int row0 = blockIdx.x * 32;
+    const uint16_t *wrow[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int row = row0 + 16 * t + n;
+        wrow[t] = row < a.out0 ? a.W0 + (size_t)row * a.in
+                  : row < out  ? a.W1 + (size_t)(row - a.out0) * a.in
+                               : nullptr;
+    }
     const int b = blockIdx.y * 16 + n;
     const float *xrow = b < a.B ? a.X + (size_t)b * a.ldx : nullptr;
-    const int kq = a.in >> 2;
-    const int kbeg = w * kq;
-    v4f acc = {0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < kq; k0 += 512) {
-        const int nkb = min(16, (kq - k0) >> 5);
-        v4i wa[16];
+    const int kw = a.in >> 3;
+    const int kbeg = w * kw;
+    v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    for (int k0 = 0; k0 < kw; k0 += 32 * kGvKb) {
+        const int nkb = min(kGvKb, (kw - k0) >> 5);
+        v4i wa[2][kGvKb];
+        v4f xa[kGvKb], xb[kGvKb];
 #pragma unroll
-        for (int kb = 0; kb < 16; ++kb) {
+        for (int kb = 0; kb < kGvKb; ++kb) {
             if (kb < nkb) {
                 const int k = kbeg + k0 + kb * 32 + g * 8;
-                wa[kb] = wrow ? *(const v4i *)(wrow + k) : v4i{0, 0, 0, 0};
+#pragma unroll
+                for (int t = 0; t < 2; ++t) wa[t][kb] = wrow[t] ? *(const v4i *)(wrow[t] + k) : v4i{0, 0, 0, 0};
+                xa[kb] = xrow ? *(const v4f *)(xrow + k) : v4f{0.f, 0.f, 0.f, 0.f};
+                xb[kb] = xrow ? *(const v4f *)(xrow + k + 4) : v4f{0.f, 0.f, 0.f, 0.f};
             }
         }
 #pragma unroll
-        for (int kb = 0; kb < 16; ++kb) {
+        for (int kb = 0; kb < kGvKb; ++kb) {
             if (kb < nkb) {
-                const int k = kbeg + k0 + kb * 32 + g * 8;
-                v4f x0 = {0.f, 0.f, 0.f, 0.f}, x1 = {0.f, 0.f, 0.f, 0.f};
-                if (xrow) {
-                    x0 = *(const v4f *)(xrow + k);
-                    x1 = *(const v4f *)(xrow + k + 4);
-                }
                 v8bf hi, lo;
-                split8(x0, x1, hi, lo);
-                const v8bf wv = __builtin_bit_cast(v8bf, wa[kb]);
-                acc = mfma_bf16(wv, hi, acc);
-                acc = mfma_bf16(wv, lo, acc);
+                split8(xa[kb], xb[kb], hi, lo);
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const v8bf wv = __builtin_bit_cast(v8bf, wa[t][kb]);
+                    acc[t] = mfma_bf16(wv, hi, acc[t]);
+                    acc[t] = mfma_bf16(wv, lo, acc[t]);
+                }
             }
         }
     }
-    if (w > 0) red[w - 1][l] = acc;
+    if (w > 0) {
+        red[w - 1][0][l] = acc[0];
+        red[w - 1][1][l] = acc[1];
+    }
     __syncthreads();
     if (w == 0 && b < a.B) {
-        acc += red[0][l];
-        acc += red[1][l];
-        acc += red[2][l];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = row0 + 4 * g + i;
-            if (r < out) {
-                float *yp = a.Y + (size_t)b * a.ldy + r;
-                *yp = a.acc ? *yp + acc[i] : acc[i];
+        for (int t = 0; t < 2; ++t) {
+            v4f s = acc[t];
+#pragma unroll
+            for (int q = 0; q < 7; ++q) s += red[q][t][l];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = row0 + 16 * t + 4 * g + i;
+                if (r < out) {
+                    float *yp = a.Y + (size_t)b * a.ldy + r;
+                    *yp = a.acc ? *yp + s[i] : s[i];
+                }
             }
         }
     }
@@ -118,11 +133,11 @@ hipError_t launch_gemv(hipStream_t st, float *Y, int ldy, const float *X, int ld
     GemvArgs a{Y, X, W0, W1, ldy, ldx, B, out0, out1, in, accumulate ? 1 : 0};
     const int out = out0 + out1;
     if (out <= 0 || B <= 0) return hipSuccess;
-    const bool aligned = (in % 128) == 0 && (ldx % 4) == 0 && ((uintptr_t)X % 16) == 0 &&
+    const bool aligned = (in % 256) == 0 && (ldx % 4) == 0 && ((uintptr_t)X % 16) == 0 &&
                          ((uintptr_t)W0 % 16) == 0 && (!W1 || ((uintptr_t)W1 % 16) == 0);
     if (aligned) {
-        dim3 grid((out + 15) / 16, (B + 15) / 16);
-        hipLaunchKernelGGL(k_gemv_mfma, grid, dim3(256), 0, st, a);
+        dim3 grid((out + 31) / 32, (B + 15) / 16);
+        hipLaunchKernelGGL(k_gemv_mfma, grid, dim3(512), 0, st, a);
     } else {
         hipLaunchKernelGGL(k_gemv_generic, dim3((out + 3) / 4), dim3(256), 0, st, a);
     }
@@ -398,7 +413,39 @@ __global__ __launch_bounds__(256) void k_qprep(QprepArgs a) {
         for (int i = tid; i < d.DN; i += 256) qrow[i] = qn[i];
     } else {
         const uint16_t *wuk = a.kv_b + (size_t)h * (d.DN + d.DV) * d.R;
-        if ((d.R & 1) == 0) {
+        if (d.R == 512 && (d.DN & 3) == 0) {
+            // wave w: k in [w*DN/4, (w+1)*DN/4); lane l: latent columns 8l .. 8l+7
+            __shared__ v4f part[4][64][2];
+            const int w = tid >> 6, l = tid & 63, kq = d.DN >> 2;
+            float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            for (int k0 = 0; k0 < kq; k0 += 8) {
+                v4i wv[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q)
+                    if (k0 + q < kq) wv[q] = *(const v4i *)(wuk + (size_t)(w * kq + k0 + q) * 512 + 8 * l);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    if (k0 + q < kq) {
+                        const float qv = qn[w * kq + k0 + q];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const uint32_t u = (uint32_t)wv[q][e];
+                            acc[2 * e] = fmaf(__uint_as_float(u << 16), qv, acc[2 * e]);
+                            acc[2 * e + 1] = fmaf(__uint_as_float(u & 0xffff0000u), qv, acc[2 * e + 1]);
+                        }
+                    }
+                }
+            }
+            part[w][l][0] = v4f{acc[0], acc[1], acc[2], acc[3]};
+            part[w][l][1] = v4f{acc[4], acc[5], acc[6], acc[7]};
+            __syncthreads();
+            for (int r = tid; r < 512; r += 256) {
+                const int ll = r >> 3, e = r & 7, hv = e >> 2, c = e & 3;
+                const float v = (part[0][ll][hv][c] + part[1][ll][hv][c]) + (part[2][ll][hv][c] + part[3][ll][hv][c]);
+                ql[r] = v;
+                qrow[r] = v;
+            }
+        } else if ((d.R & 1) == 0) {
             // two adjacent latent columns per thread (one 4-byte load per k), 4 k in flight
             for (int r = 2 * tid; r < d.R; r += 512) {
                 float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
@@ -735,14 +782,18 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
 // three LDS chunk buffers (41 KB each) filled by global_load_lds_dwordx4 DMA: while chunk c
 // is computed, chunks c+1 and c+2 are in flight, and no VGPRs stage the stream. The 16-byte
 // slots of each LDS row are XOR-swizzled so that the row reads of the score and the
-// column reads of the mix are both free of bank conflicts.
+// transposing column reads of the mix are free of bank conflicts.
 // Scores (wave w: rows 16w..16w+15): v_mfma_i32_16x16x64_i8 on the raw int8 codes against
 // the int8 hi/lo split of q_lat (exact integer dot products), plus bf16 MFMA on the bf16
 // RoPE keys against the hi/lo bf16 split of q_rope. The row scale factors out of the dot
-// (score_j = s_j * q_lat . c_j + q_rope . k_j). Mix: the probabilities p_j*s_j are
-// quantised per chunk to int8 hi/lo against the chunk's largest scale (p <= 1 after the
-// running max), and multiplied with the codes, transposed per 4x4 byte block in registers,
-// by v_mfma_i32_16x16x64_i8 (K = 64 rows). Each wave accumulates 128 latent columns.
+// (score_j = s_j * q_lat . c_j + q_rope . k_j). Mix: the weights p_j*s_j (p_j <= 1 after
+// the reference max, s_j <= the split's largest scale) are quantised to int8 hi + lo/128
+// against that scale; ds_read_b64_tr_b8 reads the codes transposed (16 rows of one column
+// per lane), and v_mfma_i32_16x16x64_i8 accumulates the exact integer mix in place across
+// chunks. A head's reference max only moves when a chunk exceeds it by more than ln 2
+// (so p_j <= 2 and the weights are bounded by 2 * largest scale); its integer accumulators
+// are then rescaled by alpha = exp(m_old - m_new) (rounded, below 2^-17 of the sums).
+// Each wave accumulates 128 latent columns.
 constexpr int kQ8Ch = 64;
 constexpr int kQ8Ring = 3;
 constexpr int kQ8CodeB = kQ8Ch * 512;               // codes of a chunk
@@ -750,29 +801,29 @@ constexpr int kQ8RopeB = kQ8Ch * 128;               // bf16 RoPE keys of a chunk
 constexpr int kQ8SclB = kQ8Ch * 4;                  // scales of a chunk
 constexpr int kQ8ChunkB = kQ8CodeB + kQ8RopeB + kQ8SclB;
 constexpr int kQ8Ws = 80;                           // LDS bytes per quantised-weight row
-constexpr int kQ8SmemB = kQ8Ring * kQ8ChunkB + 2 * 16 * kQ8Ws + 2 * 4 * 16 * 4;
+constexpr int kQ8WqOff = kQ8Ring * kQ8ChunkB;
+constexpr int kQ8MlOff = kQ8WqOff + 2 * 16 * kQ8Ws;
+constexpr int kQ8SmemB = kQ8MlOff + 2 * 4 * 16 * 4;
 
 // Slot swizzle of the code rows: physical 16-byte slot = logical slot ^ q8_swz(row).
 __device__ __forceinline__ int q8_swz(int row) { return (row & 7) ^ (((row >> 4) & 1) << 2); }
 
 __device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)p; }
 
-// Asynchronous global -> LDS copies: lane l's bytes land at lds_base + l * size. The wave
-// must pass a wave-uniform lds_base. M0 is saved and restored around the instruction.
+// Asynchronous global -> LDS copies: lane l's bytes land at lds_base + l * size. lds_base
+// must be wave-uniform. M0 is saved and restored around the instruction.
 __device__ __forceinline__ void dma_b128(const void *gptr, uint32_t lds_base) {
-    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_base);
     uint32_t saved;
     asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
                  : "=&s"(saved)
-                 : "s"(base), "v"(gptr)
+                 : "s"(lds_base), "v"(gptr)
                  : "memory");
 }
 __device__ __forceinline__ void dma_b32(const void *gptr, uint32_t lds_base) {
-    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_base);
     uint32_t saved;
     asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dword %2, off\n\ts_mov_b32 m0, %0"
                  : "=&s"(saved)
-                 : "s"(base), "v"(gptr)
+                 : "s"(lds_base), "v"(gptr)
                  : "memory");
 }
 template <int N>
@@ -782,26 +833,21 @@ __device__ __forceinline__ void wait_vmcnt() {
 // Workgroup barrier after this wave's LDS writes have completed.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-__device__ __forceinline__ void transpose4x4(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
-                                             uint32_t &o0, uint32_t &o1, uint32_t &o2,
-                                             uint32_t &o3) {
-    const uint32_t ab01 = __builtin_amdgcn_perm(b, a, 0x05010400u);
-    const uint32_t ab23 = __builtin_amdgcn_perm(b, a, 0x07030602u);
-    const uint32_t cd01 = __builtin_amdgcn_perm(d, c, 0x05010400u);
-    const uint32_t cd23 = __builtin_amdgcn_perm(d, c, 0x07030602u);
-    o0 = __builtin_amdgcn_perm(cd01, ab01, 0x05040100u);
-    o1 = __builtin_amdgcn_perm(cd01, ab01, 0x07060302u);
-    o2 = __builtin_amdgcn_perm(cd23, ab23, 0x05040100u);
-    o3 = __builtin_amdgcn_perm(cd23, ab23, 0x07060302u);
+typedef int v2i __attribute__((ext_vector_type(2)));
+// ds_read_b64_tr_b8: within each 16-lane group, destination lane j byte i comes from the
+// 8 bytes addressed by source lane 2i + (j >> 3), at byte j & 7.
+__device__ __forceinline__ v2i lds_read_tr8(const uint8_t *p) {
+    return __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i *)(p));
 }
 
 __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t smem[kQ8SmemB];
-    int8_t *wq = (int8_t *)(smem + kQ8Ring * kQ8ChunkB);  // [2][16 heads][kQ8Ws]
-    float *mloc = (float *)(smem + kQ8Ring * kQ8ChunkB + 2 * 16 * kQ8Ws);  // [4][16]
-    float *lsum = mloc + 64;                                                // [4][16]
+    int8_t *wq = (int8_t *)(smem + kQ8WqOff);  // [hi, lo][16 heads][kQ8Ws]
+    float *mloc = (float *)(smem + kQ8MlOff);  // [4 waves][16]
+    float *lsum = mloc + 64;                   // [4 waves][16]
     const uint32_t sbase = lds_addr(smem);
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
+    const int tid = threadIdx.x, l = tid & 63, n = l & 15, g = l >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int b = find_seq(a.t, blockIdx.x);
     const SeqDesc &s = a.t.s[b];
     const int split = blockIdx.x - s.split0;
@@ -826,10 +872,24 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
     }
     float qsd[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qsd[i] = a.qs[(size_t)b * 16 + 4 * g + i];
-    // Settle the query loads here: the empty asm consumes each operand, so the compiler
-    // waits for them once now and never again inside the loop, where any vmcnt wait it
-    // inserted would also drain the chunk DMA ring.
+    for (int i = 0; i < 4; ++i) qsd[i] = a.qs[(size_t)b * 16 + 4 * g + i] * a.smscale;
+    // Largest row scale of the split: the common bound of the quantised weights.
+    float smax;
+    {
+        float m = 0.f;
+        for (int r = r0 + tid; r < r1; r += 256) m = fmaxf(m, gscl[r]);
+        m = wave_max(m);
+        if (l == 0) mloc[w] = m;
+        __syncthreads();
+        smax = fmaxf(fmaxf(mloc[0], mloc[1]), fmaxf(mloc[2], mloc[3]));
+        __syncthreads();
+    }
+    // p_j <= 2 relative to the reference max (see the lazy max below)
+    const float wscale = smax > 0.f ? 127.0f / (2.0f * smax) : 0.f;
+    const float wfac = 2.0f * smax * (1.0f / (127.0f * 128.0f));
+    // Settle every load issued so far: the empty asm consumes each operand, so the
+    // compiler waits for them here and never inside the loop, where a vmcnt wait would
+    // also drain the chunk DMA ring.
 #pragma unroll
     for (int kb = 0; kb < 8; ++kb) {
         asm volatile("" : "+v"(qh[kb]));
@@ -842,21 +902,7 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(qsd[i]));
-
-    // Largest row scale of the split: the common bound of the quantised weights p_j * s_j
-    // (p_j <= 1 after the running max). One reduction per workgroup.
-    float smax;
-    {
-        float m = 0.f;
-        for (int r = r0 + tid; r < r1; r += 256) m = fmaxf(m, gscl[r]);
-        m = wave_max(m);
-        if (l == 0) mloc[w] = m;
-        __syncthreads();
-        smax = fmaxf(fmaxf(mloc[0], mloc[1]), fmaxf(mloc[2], mloc[3]));
-        __syncthreads();
-    }
-    const float wscale = smax > 0.f ? 127.0f / smax : 0.f;
-    const float wfac = smax * (1.0f / (127.0f * 128.0f));
+    wait_vmcnt<0>();
 
     float m_run[4], l_lane[4];
 #pragma unroll
@@ -864,34 +910,56 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
         m_run[i] = -INFINITY;
         l_lane[i] = 0.f;
     }
-    v4f acc[8];
+    v4i ahi[8], alo[8];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < 8; ++t) {
+        ahi[t] = v4i{0, 0, 0, 0};
+        alo[t] = v4i{0, 0, 0, 0};
+    }
 
     const int nch = (r1 - r0 + kQ8Ch - 1) / kQ8Ch;
-    // DMA of chunk c into ring slot c % 3: each wave copies 8 row pairs of codes, 2 row
-    // octets of RoPE keys (wave 0 also the 64 scales). Rows past the split end re-read the
-    // split's last row (in bounds); their scores are masked.
+    // ---- DMA plan: wave w copies row pairs 8w..8w+7 of the codes, row octets 2w, 2w+1 of
+    // the RoPE keys, wave 0 also the 64 scales. Per-lane global byte offsets relative to
+    // the chunk's first row; rows past the split end (last chunk only) re-read the split's
+    // last row (in bounds) and are masked in the scores.
+    int code_off[8], rope_off[2];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int row = 2 * (w * 8 + k) + (l >> 5);
+        code_off[k] = row * 512 + 16 * ((l & 31) ^ q8_swz(row));
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int row = 8 * (w * 2 + k) + (l >> 3);
+        rope_off[k] = row * 128 + 16 * ((l & 7) ^ (row & 7));
+    }
     auto issue = [&](int c) {
         const uint32_t buf = sbase + (uint32_t)((c % kQ8Ring) * kQ8ChunkB);
         const int rb0 = r0 + c * kQ8Ch;
+        if (rb0 + kQ8Ch <= r1) {
+            const int8_t *gc = gcodes + (size_t)rb0 * 512;
+            const uint8_t *gr = (const uint8_t *)(grope + (size_t)rb0 * 64);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int i = w * 8 + k;
-            const int row = 2 * i + (l >> 5);
-            const int cidx = (l & 31) ^ q8_swz(row);
-            const int gr = min(rb0 + row, r1 - 1);
-            dma_b128(gcodes + (size_t)gr * 512 + 16 * cidx, buf + (uint32_t)(i * 1024));
-        }
+            for (int k = 0; k < 8; ++k) dma_b128(gc + code_off[k], buf + (uint32_t)((w * 8 + k) * 1024));
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int i = w * 2 + k;
-            const int row = 8 * i + (l >> 3);
-            const int cidx = (l & 7) ^ (row & 7);
-            const int gr = min(rb0 + row, r1 - 1);
-            dma_b128(grope + (size_t)gr * 64 + 8 * cidx, buf + (uint32_t)(kQ8CodeB + i * 1024));
+            for (int k = 0; k < 2; ++k) dma_b128(gr + rope_off[k], buf + (uint32_t)(kQ8CodeB + (w * 2 + k) * 1024));
+            if (w == 0) dma_b32(gscl + rb0 + l, buf + (uint32_t)(kQ8CodeB + kQ8RopeB));
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int row = code_off[k] >> 9;
+                const int gro = min(rb0 + row, r1 - 1);
+                dma_b128(gcodes + (size_t)gro * 512 + (code_off[k] & 511), buf + (uint32_t)((w * 8 + k) * 1024));
+            }
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int row = rope_off[k] >> 7;
+                const int gro = min(rb0 + row, r1 - 1);
+                dma_b128((const uint8_t *)(grope + (size_t)gro * 64) + (rope_off[k] & 127),
+                         buf + (uint32_t)(kQ8CodeB + (w * 2 + k) * 1024));
+            }
+            if (w == 0) dma_b32(gscl + min(rb0 + l, r1 - 1), buf + (uint32_t)(kQ8CodeB + kQ8RopeB));
         }
-        if (w == 0) dma_b32(gscl + min(rb0 + l, r1 - 1), buf + (uint32_t)(kQ8CodeB + kQ8RopeB));
     };
     // this wave's DMA instructions per chunk: 10, wave 0: 11
     auto wait_chunk = [&](int later) {
@@ -906,97 +974,118 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
         }
     };
 
-    issue(0);
-    if (nch > 1) issue(1);
-    const int rowl = 16 * w + n;
-    const int swz_l = q8_swz(rowl);
-    for (int c = 0; c < nch; ++c) {
+    // ---- per-lane LDS offsets within a ring slot
+    const int rowl = 16 * w + n;  // score row of this lane
+    int sc_off[8], rp_off[2], tr_off[8][2];
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) sc_off[kb] = rowl * 512 + 16 * ((4 * kb + g) ^ q8_swz(rowl));
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) rp_off[kb] = kQ8CodeB + rowl * 128 + 16 * ((4 * kb + g) ^ (rowl & 7));
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const int row = 16 * g + 8 * hf + (n >> 1);
+            tr_off[t][hf] = row * 512 + 16 * ((8 * w + t) ^ q8_swz(row)) + 8 * (n & 1);
+        }
+    const int wq_off = n * kQ8Ws + 16 * g;
+
+    auto chunk = [&](auto slot_tag, int c) {
+        constexpr int slot = decltype(slot_tag)::value;
+        const uint8_t *buf = smem + slot * kQ8ChunkB;
         if (c + 2 < nch) issue(c + 2);  // ring slot of chunk c-1, released at its end barrier
         wait_chunk(min(2, nch - 1 - c));
         lds_barrier();
-        const uint8_t *codes = smem + (c % kQ8Ring) * kQ8ChunkB;
-        const uint8_t *ropes = codes + kQ8CodeB;
-        const float *scl = (const float *)(codes + kQ8CodeB + kQ8RopeB);
         const int base = r0 + c * kQ8Ch;
+        float *ml = mloc + 64 * 0;
 
         v4i ih = {0, 0, 0, 0}, il = {0, 0, 0, 0};
         v4f fr = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kb = 0; kb < 8; ++kb) {
-            const v4i bv = *(const v4i *)(codes + rowl * 512 + 16 * ((4 * kb + g) ^ swz_l));
+            const v4i bv = *(const v4i *)(buf + sc_off[kb]);
             ih = mfma_i8(qh[kb], bv, ih);
             il = mfma_i8(ql[kb], bv, il);
         }
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
-            const v8bf bv = *(const v8bf *)(ropes + rowl * 128 + 16 * ((4 * kb + g) ^ (rowl & 7)));
+            const v8bf bv = *(const v8bf *)(buf + rp_off[kb]);
             fr = mfma_bf16(qrh[kb], bv, fr);
             fr = mfma_bf16(qrl[kb], bv, fr);
         }
-        const float sj = scl[rowl];
+        const float sj = *(const float *)(buf + kQ8CodeB + kQ8RopeB + 4 * rowl);
         const bool valid = base + rowl < r1;
         float sc[4], lm[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float dot = (float)ih[i] + (float)il[i] * 0.0078125f;
-            sc[i] = valid ? a.smscale * fmaf(qsd[i] * sj, dot, fr[i]) : -INFINITY;
-            lm[i] = sc[i];
+            const float dot = fmaf((float)il[i], 0.0078125f, (float)ih[i]);
+            sc[i] = valid ? fmaf(qsd[i] * sj, dot, fr[i] * a.smscale) : -INFINITY;
+            lm[i] = row16_max(sc[i]);
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) lm[i] = row16_max(lm[i]);
         if (n == 0)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) mloc[w * 16 + 4 * g + i] = lm[i];
+            for (int i = 0; i < 4; ++i) ml[w * 16 + 4 * g + i] = lm[i];
         lds_barrier();
 
         float alpha[4];
+        bool moved = false;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int hh = 4 * g + i;
-            const float cm = fmaxf(fmaxf(mloc[hh], mloc[16 + hh]), fmaxf(mloc[32 + hh], mloc[48 + hh]));
-            const float mnew = fmaxf(m_run[i], cm);
-            alpha[i] = __expf(m_run[i] - mnew);
+            const float cm = fmaxf(fmaxf(ml[hh], ml[16 + hh]), fmaxf(ml[32 + hh], ml[48 + hh]));
+            // lazy reference max: moves only when the chunk max exceeds it by > ln 2
+            const bool mv = cm > m_run[i] + 0.6931472f;
+            const float mnew = mv ? cm : m_run[i];
+            alpha[i] = mv ? __expf(m_run[i] - mnew) : 1.0f;
+            moved |= mv;
             m_run[i] = mnew;
             const float p = __expf(sc[i] - mnew);
             l_lane[i] = fmaf(l_lane[i], alpha[i], p);
             const float v = p * sj * wscale;
-            float hi = fminf(rintf(v), 127.f);
-            float lo = rintf((v - hi) * 128.0f);
-            lo = fminf(fmaxf(lo, -127.f), 127.f);
+            const float hi = fminf(rintf(v), 127.f);
+            const float lo = rintf((v - hi) * 128.0f);
             wq[hh * kQ8Ws + rowl] = (int8_t)hi;
             wq[16 * kQ8Ws + hh * kQ8Ws + rowl] = (int8_t)lo;
         }
-        lds_barrier();
-
-        const v4i wh = *(const v4i *)(wq + n * kQ8Ws + 16 * g);
-        const v4i wl = *(const v4i *)(wq + 16 * kQ8Ws + n * kQ8Ws + 16 * g);
+        if (__any(moved)) {
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-            const int slot = 8 * w + 4 * rb + (n >> 2);
-            uint32_t dd[16];
-#pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                const int row = 16 * g + k;
-                dd[k] = *(const uint32_t *)(codes + row * 512 + 16 * (slot ^ q8_swz(row)) + 4 * (n & 3));
-            }
-            uint32_t tt[4][4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                transpose4x4(dd[4 * q], dd[4 * q + 1], dd[4 * q + 2], dd[4 * q + 3], tt[0][q], tt[1][q],
-                             tt[2][q], tt[3][q]);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const v4i bt = {(int)tt[t][0], (int)tt[t][1], (int)tt[t][2], (int)tt[t][3]};
-                const v4i zero = {0, 0, 0, 0};
-                const v4i ih2 = mfma_i8(wh, bt, zero);
-                const v4i il2 = mfma_i8(wl, bt, zero);
+            for (int t = 0; t < 8; ++t)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    acc[rb * 4 + t][i] = fmaf(acc[rb * 4 + t][i], alpha[i], wfac * (float)(ih2[i] * 128 + il2[i]));
-            }
+                    if (alpha[i] != 1.0f) {
+                        ahi[t][i] = (int)rintf((float)ahi[t][i] * alpha[i]);
+                        alo[t][i] = (int)rintf((float)alo[t][i] * alpha[i]);
+                    }
+        }
+        lds_barrier();
+
+        const v4i wh = *(const v4i *)(wq + wq_off);
+        const v4i wl = *(const v4i *)(wq + 16 * kQ8Ws + wq_off);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const v2i b0 = lds_read_tr8(buf + tr_off[t][0]);
+            const v2i b1 = lds_read_tr8(buf + tr_off[t][1]);
+            const v4i bt = {b0.x, b0.y, b1.x, b1.y};
+            ahi[t] = mfma_i8(wh, bt, ahi[t]);
+            alo[t] = mfma_i8(wl, bt, alo[t]);
         }
         lds_barrier();  // ring slot, mloc and wq free for the next chunk
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+
+    issue(0);
+    if (nch > 1) issue(1);
+    int c = 0;
+    for (; c + 3 <= nch; c += 3) {
+        chunk(S0{}, c);
+        chunk(S1{}, c + 1);
+        chunk(S2{}, c + 2);
     }
+    if (c < nch) chunk(S0{}, c);
+    if (c + 1 < nch) chunk(S1{}, c + 1);
+
 #pragma unroll
     for (int i = 0; i < 4; ++i) l_lane[i] = row16_sum(l_lane[i]);
     if (n == 0)
@@ -1006,9 +1095,10 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
     float *P = a.part + (size_t)blockIdx.x * 16 * 514;
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-        const int r = 128 * w + 64 * (t >> 2) + 4 * n + (t & 3);
+        const int r = 128 * w + 16 * t + n;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) P[(4 * g + i) * 512 + r] = acc[t][i];
+        for (int i = 0; i < 4; ++i)
+            P[(4 * g + i) * 512 + r] = wfac * fmaf((float)ahi[t][i], 128.0f, (float)alo[t][i]);
     }
     if (w == 0 && n == 0) {
 #pragma unroll
@@ -1115,11 +1205,18 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
     for (int k = tid; k < DVm; k += 256) {
         float v0 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f;
         int i = 0;
-        for (; i + 4 <= ns; i += 4) {
-            v0 = fmaf(Pg[(size_t)i * stride + k], wts[i], v0);
-            v1 = fmaf(Pg[(size_t)(i + 1) * stride + k], wts[i + 1], v1);
-            v2 = fmaf(Pg[(size_t)(i + 2) * stride + k], wts[i + 2], v2);
-            v3 = fmaf(Pg[(size_t)(i + 3) * stride + k], wts[i + 3], v3);
+        for (; i + 8 <= ns; i += 8) {
+            float p[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) p[q] = Pg[(size_t)(i + q) * stride + k];
+            v0 = fmaf(p[0], wts[i], v0);
+            v1 = fmaf(p[1], wts[i + 1], v1);
+            v2 = fmaf(p[2], wts[i + 2], v2);
+            v3 = fmaf(p[3], wts[i + 3], v3);
+            v0 = fmaf(p[4], wts[i + 4], v0);
+            v1 = fmaf(p[5], wts[i + 5], v1);
+            v2 = fmaf(p[6], wts[i + 6], v2);
+            v3 = fmaf(p[7], wts[i + 7], v3);
         }
         for (; i < ns; ++i) v0 = fmaf(Pg[(size_t)i * stride + k], wts[i], v0);
         const float v = ((v0 + v1) + (v2 + v3)) * inv;
@@ -1133,22 +1230,36 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
     __syncthreads();
     const int w = tid >> 6, l = tid & 63;
     const uint16_t *wuv = a.kv_b + ((size_t)h * (d.DN + d.DV) + d.DN) * d.R;
-    if (d.R == 512) {
-        float mv[8];
+    if (d.R == 512 && d.DV == 128) {
+        // thread t: output row t/2, latent half t%2 (256 columns streamed as 32 x 16 B)
+        const int dd = tid >> 1, half = tid & 1;
+        const uint16_t *row = wuv + (size_t)dd * 512 + 256 * half;
+        const float *mh = mx + 256 * half;
+        float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) mv[e] = mx[8 * l + e];
-        for (int dd = w; dd < d.DV; dd += 4) {
-            const v4i wv = *(const v4i *)(wuv + (size_t)dd * 512 + 8 * l);
-            float acc = 0.f;
+        for (int q0 = 0; q0 < 32; q0 += 8) {
+            v4i wv[8];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t u = (uint32_t)wv[e];
-                acc = fmaf(__uint_as_float(u << 16), mv[2 * e], acc);
-                acc = fmaf(__uint_as_float(u & 0xffff0000u), mv[2 * e + 1], acc);
+            for (int q = 0; q < 8; ++q) wv[q] = *(const v4i *)(row + 8 * (q0 + q));
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const v4f m0 = *(const v4f *)(mh + 8 * (q0 + q));
+                const v4f m1 = *(const v4f *)(mh + 8 * (q0 + q) + 4);
+                const uint32_t u0 = (uint32_t)wv[q][0], u1 = (uint32_t)wv[q][1];
+                const uint32_t u2 = (uint32_t)wv[q][2], u3 = (uint32_t)wv[q][3];
+                acc0 = fmaf(__uint_as_float(u0 << 16), m0.x, acc0);
+                acc1 = fmaf(__uint_as_float(u0 & 0xffff0000u), m0.y, acc1);
+                acc0 = fmaf(__uint_as_float(u1 << 16), m0.z, acc0);
+                acc1 = fmaf(__uint_as_float(u1 & 0xffff0000u), m0.w, acc1);
+                acc0 = fmaf(__uint_as_float(u2 << 16), m1.x, acc0);
+                acc1 = fmaf(__uint_as_float(u2 & 0xffff0000u), m1.y, acc1);
+                acc0 = fmaf(__uint_as_float(u3 << 16), m1.z, acc0);
+                acc1 = fmaf(__uint_as_float(u3 & 0xffff0000u), m1.w, acc1);
             }
-            acc = wave_sum(acc);
-            if (l == 0) a.ho[(size_t)b * d.HO + (size_t)h * d.DV + dd] = acc;
         }
+        float acc = acc0 + acc1;
+        acc += dpp_f32<0xB1>(acc);  // partner lane t^1 holds the other half
+        if (half == 0) a.ho[(size_t)b * d.HO + (size_t)h * d.DV + dd] = acc;
         return;
     }
     for (int dd = w; dd < d.DV; dd += 4) {
