@@ -796,14 +796,15 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
 // Each wave accumulates 128 latent columns.
 constexpr int kQ8Ch = 64;
 constexpr int kQ8Ring = 3;
+constexpr int kQ8MaxSplitRows = 2048;               // rows of one split (scales table)
 constexpr int kQ8CodeB = kQ8Ch * 512;               // codes of a chunk
 constexpr int kQ8RopeB = kQ8Ch * 128;               // bf16 RoPE keys of a chunk
-constexpr int kQ8SclB = kQ8Ch * 4;                  // scales of a chunk
-constexpr int kQ8ChunkB = kQ8CodeB + kQ8RopeB + kQ8SclB;
+constexpr int kQ8ChunkB = kQ8CodeB + kQ8RopeB;
 constexpr int kQ8Ws = 80;                           // LDS bytes per quantised-weight row
-constexpr int kQ8WqOff = kQ8Ring * kQ8ChunkB;
+constexpr int kQ8SclOff = kQ8Ring * kQ8ChunkB;      // scales of the whole split
+constexpr int kQ8WqOff = kQ8SclOff + 4 * kQ8MaxSplitRows;
 constexpr int kQ8MlOff = kQ8WqOff + 2 * 16 * kQ8Ws;
-constexpr int kQ8SmemB = kQ8MlOff + 2 * 4 * 16 * 4;
+constexpr int kQ8SmemB = kQ8MlOff + 3 * 4 * 16 * 4;
 
 // Slot swizzle of the code rows: physical 16-byte slot = logical slot ^ q8_swz(row).
 __device__ __forceinline__ int q8_swz(int row) { return (row & 7) ^ (((row >> 4) & 1) << 2); }
@@ -846,6 +847,7 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
     float *mloc = (float *)(smem + kQ8MlOff);  // [4 waves][16]
     float *lsum = mloc + 64;                   // [4 waves][16]
     const uint32_t sbase = lds_addr(smem);
+    const float *sclv = (const float *)(smem + kQ8SclOff);  // scales of the split's rows
     const int tid = threadIdx.x, l = tid & 63, n = l & 15, g = l >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int b = find_seq(a.t, blockIdx.x);
@@ -873,36 +875,6 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
     float qsd[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) qsd[i] = a.qs[(size_t)b * 16 + 4 * g + i] * a.smscale;
-    // Largest row scale of the split: the common bound of the quantised weights.
-    float smax;
-    {
-        float m = 0.f;
-        for (int r = r0 + tid; r < r1; r += 256) m = fmaxf(m, gscl[r]);
-        m = wave_max(m);
-        if (l == 0) mloc[w] = m;
-        __syncthreads();
-        smax = fmaxf(fmaxf(mloc[0], mloc[1]), fmaxf(mloc[2], mloc[3]));
-        __syncthreads();
-    }
-    // p_j <= 2 relative to the reference max (see the lazy max below)
-    const float wscale = smax > 0.f ? 127.0f / (2.0f * smax) : 0.f;
-    const float wfac = 2.0f * smax * (1.0f / (127.0f * 128.0f));
-    // Settle every load issued so far: the empty asm consumes each operand, so the
-    // compiler waits for them here and never inside the loop, where a vmcnt wait would
-    // also drain the chunk DMA ring.
-#pragma unroll
-    for (int kb = 0; kb < 8; ++kb) {
-        asm volatile("" : "+v"(qh[kb]));
-        asm volatile("" : "+v"(ql[kb]));
-    }
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-        asm volatile("" : "+v"(qrh[kb]));
-        asm volatile("" : "+v"(qrl[kb]));
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(qsd[i]));
-    wait_vmcnt<0>();
 
     float m_run[4], l_lane[4];
 #pragma unroll
@@ -917,11 +889,13 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
         alo[t] = v4i{0, 0, 0, 0};
     }
 
+    float wscale = 0.f, wfac = 0.f;  // weight quantisation scale, set once the scales are in
     const int nch = (r1 - r0 + kQ8Ch - 1) / kQ8Ch;
-    // ---- DMA plan: wave w copies row pairs 8w..8w+7 of the codes, row octets 2w, 2w+1 of
-    // the RoPE keys, wave 0 also the 64 scales. Per-lane global byte offsets relative to
-    // the chunk's first row; rows past the split end (last chunk only) re-read the split's
-    // last row (in bounds) and are masked in the scores.
+    // ---- DMA plan: wave w copies row pairs 8w..8w+7 of the codes and row octets 2w, 2w+1
+    // of the RoPE keys of each chunk. Per-lane global byte offsets relative to the chunk's
+    // first row; rows past the split end (last chunk only) re-read the split's last row
+    // (in bounds) and are masked in the scores. The scales of the whole split are copied
+    // once, together with the first two chunks.
     int code_off[8], rope_off[2];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -943,7 +917,6 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
             for (int k = 0; k < 8; ++k) dma_b128(gc + code_off[k], buf + (uint32_t)((w * 8 + k) * 1024));
 #pragma unroll
             for (int k = 0; k < 2; ++k) dma_b128(gr + rope_off[k], buf + (uint32_t)(kQ8CodeB + (w * 2 + k) * 1024));
-            if (w == 0) dma_b32(gscl + rb0 + l, buf + (uint32_t)(kQ8CodeB + kQ8RopeB));
         } else {
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
@@ -958,20 +931,13 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
                 dma_b128((const uint8_t *)(grope + (size_t)gro * 64) + (rope_off[k] & 127),
                          buf + (uint32_t)(kQ8CodeB + (w * 2 + k) * 1024));
             }
-            if (w == 0) dma_b32(gscl + min(rb0 + l, r1 - 1), buf + (uint32_t)(kQ8CodeB + kQ8RopeB));
         }
     };
-    // this wave's DMA instructions per chunk: 10, wave 0: 11
+    // this wave's DMA instructions per chunk: 10
     auto wait_chunk = [&](int later) {
-        if (w == 0) {
-            if (later >= 2) wait_vmcnt<22>();
-            else if (later == 1) wait_vmcnt<11>();
-            else wait_vmcnt<0>();
-        } else {
-            if (later >= 2) wait_vmcnt<20>();
-            else if (later == 1) wait_vmcnt<10>();
-            else wait_vmcnt<0>();
-        }
+        if (later >= 2) wait_vmcnt<20>();
+        else if (later == 1) wait_vmcnt<10>();
+        else wait_vmcnt<0>();
     };
 
     // ---- per-lane LDS offsets within a ring slot
@@ -1013,7 +979,7 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
             fr = mfma_bf16(qrh[kb], bv, fr);
             fr = mfma_bf16(qrl[kb], bv, fr);
         }
-        const float sj = *(const float *)(buf + kQ8CodeB + kQ8RopeB + 4 * rowl);
+        const float sj = sclv[c * kQ8Ch + rowl];
         const bool valid = base + rowl < r1;
         float sc[4], lm[4];
 #pragma unroll
@@ -1075,8 +1041,43 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
     using S1 = std::integral_constant<int, 1>;
     using S2 = std::integral_constant<int, 2>;
 
+    {
+        const uint32_t sdst = sbase + (uint32_t)kQ8SclOff;
+        for (int q = w; q * 64 < r1 - r0; q += 4)
+            dma_b32(gscl + min(r0 + 64 * q + l, r1 - 1), sdst + (uint32_t)(256 * q));
+    }
     issue(0);
     if (nch > 1) issue(1);
+    // Settle every load issued so far (query operands, scales, first chunks): the empty
+    // asm consumes each operand, so the compiler waits for them here and never inside the
+    // loop, where a vmcnt wait would also drain the chunk DMA ring.
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) {
+        asm volatile("" : "+v"(qh[kb]));
+        asm volatile("" : "+v"(ql[kb]));
+    }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        asm volatile("" : "+v"(qrh[kb]));
+        asm volatile("" : "+v"(qrl[kb]));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(qsd[i]));
+    wait_vmcnt<0>();
+    lds_barrier();
+    // largest row scale of the split: the common bound of the quantised weights
+    float smax;
+    {
+        float m = 0.f;
+        for (int r = tid; r < r1 - r0; r += 256) m = fmaxf(m, sclv[r]);
+        m = wave_max(m);
+        if (l == 0) mloc[128 + w] = m;
+        lds_barrier();
+        smax = fmaxf(fmaxf(mloc[128], mloc[129]), fmaxf(mloc[130], mloc[131]));
+    }
+    // p_j <= 2 relative to the reference max (see the lazy max below)
+    wscale = smax > 0.f ? 127.0f / (2.0f * smax) : 0.f;
+    wfac = 2.0f * smax * (1.0f / (127.0f * 128.0f));
     int c = 0;
     for (; c + 3 <= nch; c += 3) {
         chunk(S0{}, c);

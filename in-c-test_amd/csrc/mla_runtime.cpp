@@ -596,6 +596,7 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
             const long want = std::max(1L, std::lround(target * (double)s.len / (double)total_rows));
             long r = (long)s.len / (want * chunk) * chunk;
             r = std::max<long>(r, 4L * chunk);
+            if (kind == kAttnQ8Mfma) r = std::min<long>(r, 1024L);  // every split < 2048 rows
             s.rps = (int)r;
             s.split0 = total_splits;
             s.nsplit = std::max(1, (int)(s.len / r));
