@@ -809,31 +809,6 @@ constexpr int kQ8SmemB = kQ8MlOff + 3 * 4 * 16 * 4;
 // Slot swizzle of the code rows: physical 16-byte slot = logical slot ^ q8_swz(row).
 __device__ __forceinline__ int q8_swz(int row) { return (row & 7) ^ (((row >> 4) & 1) << 2); }
 
-__device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)p; }
-
-// Asynchronous global -> LDS copies: lane l's bytes land at lds_base + l * size. lds_base
-// must be wave-uniform. M0 is saved and restored around the instruction.
-__device__ __forceinline__ void dma_b128(const void *gptr, uint32_t lds_base) {
-    uint32_t saved;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
-                 : "=&s"(saved)
-                 : "s"(lds_base), "v"(gptr)
-                 : "memory");
-}
-__device__ __forceinline__ void dma_b32(const void *gptr, uint32_t lds_base) {
-    uint32_t saved;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dword %2, off\n\ts_mov_b32 m0, %0"
-                 : "=&s"(saved)
-                 : "s"(lds_base), "v"(gptr)
-                 : "memory");
-}
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-// Workgroup barrier after this wave's LDS writes have completed.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 typedef int v2i __attribute__((ext_vector_type(2)));
 // ds_read_b64_tr_b8: within each 16-lane group, destination lane j byte i comes from the
 // 8 bytes addressed by source lane 2i + (j >> 3), at byte j & 7.

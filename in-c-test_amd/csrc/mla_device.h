@@ -94,6 +94,32 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
+__device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)p; }
+
+// Asynchronous global -> LDS copies: lane l's bytes land at lds_base + l * size. lds_base
+// must be wave-uniform. M0 is saved and restored around the instruction.
+__device__ __forceinline__ void dma_b128(const void *gptr, uint32_t lds_base) {
+    lds_base = __builtin_amdgcn_readfirstlane(lds_base);
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "s"(lds_base), "v"(gptr)
+                 : "memory");
+}
+__device__ __forceinline__ void dma_b32(const void *gptr, uint32_t lds_base) {
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dword %2, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "s"(lds_base), "v"(gptr)
+                 : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Workgroup barrier after this wave's LDS writes have completed.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // SplitMix64 output k (k >= 1) of the stream seeded by `seed`.
 __device__ __forceinline__ uint64_t splitmix64_at(uint64_t seed, uint64_t k) {
     uint64_t z = seed + k * 0x9E3779B97F4A7C15ull;

@@ -4,11 +4,11 @@
 // MFMA route (H, R, QD multiples of 32, DV multiple of 16, DN multiple of 8):
 //   split     x (fp32) -> bf16 hi + lo operands; a flag records whether any lo is non-zero
 //   gemm      [q | kv_a] = x . W^T           (bf16 MFMA, fp32 accumulate, lo pass skipped
-//                                             when the operand is exactly bf16)
-//   kva_epi   RMSNorm -> latent (hi/lo), RoPE(k_rope) -> bf16, per token (RMSNorm as decode)
-//   gemm      kv = latent . kv_b^T
-//   pack      Q = [q_nope | RoPE(q_rope)] (hi/lo), K = [k_nope | k_rope] (bf16), V^T (bf16)
-//   flash     causal attention per (64-query tile, head), online softmax, P as hi/lo bf16
+//                                             when the operand is exactly bf16); epilogue:
+//                                             Q = [q_nope | RoPE(q_rope)] as hi/lo bf16
+//   kva_pack  RMSNorm -> latent (hi/lo), RoPE(k_rope) -> rope part of K (bf16), per token
+//   gemm      kv = latent . kv_b^T           epilogue: k_nope -> K (bf16), V^T (hi/lo bf16)
+//   flash     causal attention per (128-query tile, head), online softmax
 //   gemm      out = heads . o_proj^T
 // Generic route (any shape): the same stages with VALU kernels.
 #include "mla_device.h"
@@ -16,25 +16,35 @@
 
 #include <math.h>
 
+#include <algorithm>
+#include <type_traits>
+
 namespace kvl {
 
 // ================================================================ split ================
 
 // src[r, c] (fp32, ld_src) -> hi/lo bf16 [rows, cols] (ld_dst); flag |= any lo != 0.
+// Each thread converts 8 consecutive values (cols % 8 == 0, 16-byte aligned rows).
 __global__ __launch_bounds__(256) void k_split(const float *src, int ld_src, uint16_t *hi,
                                                uint16_t *lo, int ld_dst, int rows, int cols,
                                                int *flag) {
-    const size_t n = (size_t)rows * cols;
+    const int c8 = cols / 8;
+    const size_t n = (size_t)rows * c8;
     int any = 0;
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
-        const size_t r = i / cols, c = i % cols;
-        uint16_t h, l;
-        split_bf16(src[r * ld_src + c], h, l);
-        hi[r * ld_dst + c] = h;
-        lo[r * ld_dst + c] = l;
-        any |= (l & 0x7fff) != 0;
+        const size_t r = i / c8, c = (i % c8) * 8;
+        const v4f x0 = *(const v4f *)(src + r * ld_src + c), x1 = *(const v4f *)(src + r * ld_src + c + 4);
+        v8bf h, l;
+        split8(x0, x1, h, l);
+        *(v8bf *)(hi + r * ld_dst + c) = h;
+        *(v8bf *)(lo + r * ld_dst + c) = l;
+        const v4i lv = __builtin_bit_cast(v4i, l);
+        any |= ((lv.x | lv.y | lv.z | lv.w) & 0x7fff7fff) != 0;
     }
-    if (__syncthreads_or(any) && threadIdx.x == 0) atomicOr(flag, 1);
+    // one atomic per block at most, and none once the flag is seen raised
+    if (__syncthreads_or(any) && threadIdx.x == 0 &&
+        __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0)
+        atomicOr(flag, 1);
 }
 
 __global__ void k_zero_int(int *p, int n) {
@@ -44,97 +54,271 @@ __global__ void k_zero_int(int *p, int n) {
 
 // ================================================================ GEMM =================
 
-// C[m, n] = sum_k (Ah + Al)[m, k] * B[n, k], all row-major, bf16 operands, fp32 output.
-// Block tile 128 x 128, k step 32; wave (wm, wn) owns a 64 x 64 quadrant (4 x 4 MFMA tiles
-// of v_mfma_f32_16x16x32_bf16). The lo operand pass runs when Al is given and either no
-// flag is given or *lo_flag != 0 (the flag is raised by the producer of Al).
-// Requires K % 32 == 0 and 16-byte aligned rows (lda, ldb multiples of 8).
-constexpr int kGBm = 128, kGBn = 128, kGBk = 32, kGLd = 40;  // LDS row: 32 + 8 bf16
+// C[m, n] = sum_k (Ah + Al)[m, k] * B[n, k]: row-major bf16 operands, fp32 output. The
+// columns of C may come from two weight matrices (B0 for n < N0, B1 for the N1 after it),
+// so the q and kv_a projections of the same tokens run as one launch.
+//
+// Block tile 256 x BN (BN = 256 or 128), k step 32, eight waves (2 per SIMD) in a WM x WN
+// grid, each owning a (256 / WM) x (BN / WN) quadrant of v_mfma_f32_16x16x32_bf16 tiles.
+// Large tiles keep the L2 traffic at 24-32 bytes per clock per CU at the MFMA rate. A hi,
+// A lo and B stream into a 3-stage LDS ring by global_load_lds_dwordx4 DMA (two stages in
+// flight while one is computed). LDS rows are 64 bytes (4 slots of 16 B); slot s of row r
+// sits at s ^ ((r >> 1) & 3), which spreads the 8 rows one ds_read_b128 phase touches over
+// distinct banks. The lo pass runs when Al is given and either no flag is given or
+// *lo_flag != 0 (the flag is raised by the producer of Al when some lo word is non-zero).
+// Requires K % 32 == 0, lda and ldb multiples of 8 (16-byte rows).
+constexpr int kGBm = 256, kGBk = 32, kGStages = 3;
+constexpr int kGRowB = kGBk * 2;                 // 64-byte LDS rows
 
-struct GemmArgs {
-    const uint16_t *Ah, *Al, *B;
-    float *C;
-    const int *lo_flag;
-    int M, N, K, lda, ldb, ldc;
+template <int BN>
+struct GemmShape {
+    static constexpr int WM = BN == 256 ? 2 : 4, WN = 8 / WM;
+    static constexpr int TM = kGBm / WM / 16, TN = BN / WN / 16;  // 16x16 tiles per wave
+    static constexpr int ATile = kGBm * kGRowB, BTile = BN * kGRowB;
+    static constexpr int Stage = 2 * ATile + BTile;
+    static constexpr int Smem = kGStages * Stage;
 };
 
-__global__ __launch_bounds__(256) void k_gemm_bf16(GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t sah[kGBm * kGLd];
-    __shared__ __attribute__((aligned(16))) uint16_t sal[kGBm * kGLd];
-    __shared__ __attribute__((aligned(16))) uint16_t sb[kGBn * kGLd];
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
-    const int wm = w >> 1, wn = w & 1;
-    const int m0 = blockIdx.y * kGBm, n0 = blockIdx.x * kGBn;
-    const bool use_lo = a.Al && (!a.lo_flag || *a.lo_flag);
-    v4f acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+struct GemmArgs {
+    const uint16_t *Ah, *Al, *B0, *B1;
+    float *C;
+    const int *lo_flag;
+    int M, N0, N1, K, lda, ldb, ldc;
+};
 
-    // each thread stages 2 x 16 B of A hi (and lo) and 2 x 16 B of B per k step
-    v4i pa[2], pl[2], pb[2];
-    auto load = [&](int k0) {
+// Epilogues. kEpiPlain: C fp32. kEpiQ (q | kv_a projection): the N0 = NH * QD q columns go
+// to Q [NH, Sp, QD] as hi/lo bf16 with the rope half rotated (src/mla_prefill_streaming.c:
+// 139-147: pairs (2i, 2i+1) -> i and DR/2 + i), the kv_a columns to C (ldc = N1). kEpiKV
+// (kv_b projection): k_nope -> K [NH, Sp, QD] bf16, values -> V^T [NH, DV, Sp] hi/lo bf16
+// with the keys of each 32-key group in vt_perm order.
+enum { kEpiPlain = 0, kEpiQ = 1, kEpiKV = 2 };
+struct GemmEpi {
+    uint16_t *qh, *ql, *kb, *vh, *vl;
+    const float2 *cs;
+    int Sp, DN, DR, DV;
+};
+
+// Position of key k (0..31 within its 32-key group) in the permuted V^T rows: the 8 keys
+// lane group g of the flash kernel holds for one PV chunk are 4g .. 4g+3 and 16+4g .. 16+4g+3.
+__host__ __device__ __forceinline__ int vt_perm(int k) { return 8 * ((k & 15) >> 2) + 4 * (k >> 4) + (k & 3); }
+
+__device__ __forceinline__ int g_swz(int row) { return (row >> 1) & 3; }
+
+template <int BN, int EPI>
+__global__ __launch_bounds__(512) void k_gemm_bf16(GemmArgs a, GemmEpi e) {
+    using Sh = GemmShape<BN>;
+    constexpr int TM = Sh::TM, TN = Sh::TN;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[Sh::Smem];
+    const uint32_t sbase = lds_addr(smem);
+    const int tid = threadIdx.x, l = tid & 63, n = l & 15, g = l >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = w / Sh::WN, wn = w % Sh::WN;
+    const int M = a.M, N0 = a.N0, N1 = a.N1, K = a.K, lda = a.lda, ldb = a.ldb;
+    const int tn0 = (N0 + BN - 1) / BN, tn = tn0 + (N1 + BN - 1) / BN;
+    const int tm = (M + kGBm - 1) / kGBm, ntiles = tm * tn;
+    // Tiles in row-major order; with ntiles % 8 == 0, XCD b % 8 takes a contiguous eighth
+    // of them (blocks of one XCD share A rows in its L2).
+    int tile = blockIdx.x;
+    if (ntiles % 8 == 0) tile = (blockIdx.x & 7) * (ntiles / 8) + (blockIdx.x >> 3);
+    const int mt = tile / tn, nt = tile % tn;
+    const bool seg1 = nt >= tn0;
+    const uint16_t *B = seg1 ? a.B1 : a.B0;
+    const int Nseg = seg1 ? N1 : N0;
+    const int nb0 = seg1 ? (nt - tn0) * BN : nt * BN;  // first row of B in this tile
+    const int c0 = seg1 ? N0 + nb0 : nb0;              // first column of C
+    const int m0 = mt * kGBm;
+    const bool use_lo = a.Al && (!a.lo_flag || *a.lo_flag);
+
+    // DMA: thread (w, l), instruction i fills slot (8i + w) * 64 + l of a tile: row p >> 2,
+    // physical slot p & 3 holding logical slot (p & 3) ^ g_swz(row). Rows past the end of A
+    // or B are clamped to the last row (their results are never stored).
+    constexpr int NA = Sh::ATile / 8192, NB = Sh::BTile / 8192;  // instructions per thread
+    uint32_t aoff[NA], boff[NB];
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int p = tid + 256 * q, row = p >> 2, c8 = (p & 3) * 8;
-            const int gm = m0 + row, gn = n0 + row;
-            pa[q] = gm < a.M ? *(const v4i *)(a.Ah + (size_t)gm * a.lda + k0 + c8) : v4i{0, 0, 0, 0};
-            if (use_lo)
-                pl[q] = gm < a.M ? *(const v4i *)(a.Al + (size_t)gm * a.lda + k0 + c8) : v4i{0, 0, 0, 0};
-            pb[q] = gn < a.N ? *(const v4i *)(a.B + (size_t)gn * a.ldb + k0 + c8) : v4i{0, 0, 0, 0};
+    for (int i = 0; i < NA; ++i) {
+        const int p = (8 * i + w) * 64 + l, row = p >> 2, s = (p & 3) ^ g_swz(row);
+        aoff[i] = (uint32_t)(min(m0 + row, M - 1) - m0) * lda * 2 + 16 * s;
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const int p = (8 * i + w) * 64 + l, row = p >> 2, s = (p & 3) ^ g_swz(row);
+        boff[i] = (uint32_t)(min(nb0 + row, Nseg - 1) - nb0) * ldb * 2 + 16 * s;
+    }
+    const uint8_t *gah = (const uint8_t *)(a.Ah + (size_t)m0 * lda);
+    const uint8_t *gal = a.Al ? (const uint8_t *)(a.Al + (size_t)m0 * lda) : nullptr;
+    const uint8_t *gb = (const uint8_t *)(B + (size_t)nb0 * ldb);
+    auto issue = [&](int kt, int stage) __attribute__((always_inline)) {
+        const uint32_t dst = sbase + stage * Sh::Stage + (uint32_t)w * 1024;
+        const size_t ko = (size_t)kt * kGBk * 2;
+#pragma unroll
+        for (int i = 0; i < NA; ++i) dma_b128(gah + ko + aoff[i], dst + i * 8192);
+        if (use_lo) {
+#pragma unroll
+            for (int i = 0; i < NA; ++i) dma_b128(gal + ko + aoff[i], dst + Sh::ATile + i * 8192);
         }
-    };
-    auto stash = [&]() {
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int p = tid + 256 * q, row = p >> 2, c8 = (p & 3) * 8;
-            *(v4i *)(sah + row * kGLd + c8) = pa[q];
-            if (use_lo) *(v4i *)(sal + row * kGLd + c8) = pl[q];
-            *(v4i *)(sb + row * kGLd + c8) = pb[q];
+        for (int i = 0; i < NB; ++i) dma_b128(gb + ko + boff[i], dst + 2 * Sh::ATile + i * 8192);
+    };
+    // fragment rows 16 * tile + n (n & 7 = row & 7), logical slot g
+    const int frd = n * kGRowB + 16 * (g ^ g_swz(n));
+
+    v4f acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    const int nk = K / kGBk;
+    issue(0, 0);
+    if (nk > 1) issue(1, 1);
+    for (int kt = 0; kt < nk; ++kt) {
+        // stage kt has landed when at most one later stage is still in flight
+        if (kt + 1 < nk) {
+            if (use_lo) wait_vmcnt<2 * NA + NB>();
+            else wait_vmcnt<NA + NB>();
+        } else {
+            wait_vmcnt<0>();
         }
-    };
-    load(0);
-    for (int k0 = 0; k0 < a.K; k0 += kGBk) {
-        __syncthreads();
-        stash();
-        __syncthreads();
-        if (k0 + kGBk < a.K) load(k0 + kGBk);
-        v8bf bo[4];
+        lds_barrier();
+        if (kt + 2 < nk) issue(kt + 2, (kt + 2) % kGStages);
+        const uint8_t *st = smem + (kt % kGStages) * Sh::Stage;
+        const uint8_t *sa = st + wm * (TM * 16) * kGRowB + frd;
+        const uint8_t *sb = st + 2 * Sh::ATile + wn * (TN * 16) * kGRowB + frd;
+        v8bf bo[TN];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bo[j] = *(const v8bf *)(sb + (64 * wn + 16 * j + n) * kGLd + 8 * g);
+        for (int j = 0; j < TN; ++j) bo[j] = *(const v8bf *)(sb + j * 16 * kGRowB);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const v8bf ah = *(const v8bf *)(sah + (64 * wm + 16 * i + n) * kGLd + 8 * g);
+        for (int i = 0; i < TM; ++i) {
+            const v8bf ah = *(const v8bf *)(sa + i * 16 * kGRowB);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = mfma_bf16(ah, bo[j], acc[i][j]);
-            if (use_lo) {
-                const v8bf al = *(const v8bf *)(sal + (64 * wm + 16 * i + n) * kGLd + 8 * g);
+            for (int j = 0; j < TN; ++j) acc[i][j] = mfma_bf16(ah, bo[j], acc[i][j]);
+        }
+        if (use_lo) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = mfma_bf16(al, bo[j], acc[i][j]);
+            for (int i = 0; i < TM; ++i) {
+                const v8bf al = *(const v8bf *)(sa + Sh::ATile + i * 16 * kGRowB);
+#pragma unroll
+                for (int j = 0; j < TN; ++j) acc[i][j] = mfma_bf16(al, bo[j], acc[i][j]);
             }
         }
     }
+    // Epilogue. D layout: lane (g, n) of tile (i, j) holds rows 4g + r, column n. Row-major
+    // outputs go through a per-wave LDS buffer (16 rows x 64 columns per tile row i) so that
+    // each lane ends up with 16 consecutive columns of one row: wide stores, and the rope
+    // pairs (2p, 2p+1) in one lane. The V^T part of kEpiKV wants 4 consecutive tokens per
+    // lane, which the D layout already gives.
+    const int QD = e.DN + e.DR, KH = e.DN + e.DV, half = e.DR / 2;
+    static_assert(TN == 4, "the staged epilogue assumes 64 columns per wave");
+    lds_barrier();  // every wave is done with the ring
+    float *ep = (float *)smem + w * (16 * 68);
+    const int cw = wn * 64;                      // wave's first column within the tile
+    const bool vt_wave = EPI == kEpiKV && ((nb0 + cw) % KH) >= e.DN;
+    const int rr = l >> 2, cc = (l & 3) * 16;    // staged row / first column of this lane
+    const int nl0 = nb0 + cw + cc;               // segment column of v[0]
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < TM; ++i) {
+        const int rbase = m0 + wm * TM * 16 + 16 * i;
+        if (vt_wave) {
+            const int row0 = rbase + 4 * g;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int col = n0 + 64 * wn + 16 * j + n;
-            if (col >= a.N) continue;
+            for (int j = 0; j < TN; ++j) {
+                const int nl = nb0 + cw + 16 * j + n;
+                if (nl >= Nseg) continue;
+                const int h = nl / KH, d = nl % KH - e.DN;
+                uint16_t hh[4], ll[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = m0 + 64 * wm + 16 * i + 4 * g + r;
-                if (row < a.M) a.C[(size_t)row * a.ldc + col] = acc[i][j][r];
+                for (int r = 0; r < 4; ++r) split_bf16(acc[i][j][r], hh[r], ll[r]);
+                const size_t o = ((size_t)h * e.DV + d) * e.Sp + (row0 & ~31) + vt_perm(row0 & 31);
+                if (row0 + 3 < M) {
+                    *(uint2 *)(e.vh + o) = make_uint2(pack2(hh[0], hh[1]), pack2(hh[2], hh[3]));
+                    *(uint2 *)(e.vl + o) = make_uint2(pack2(ll[0], ll[1]), pack2(ll[2], ll[3]));
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (row0 + r < M) {
+                            e.vh[o + r] = hh[r];
+                            e.vl[o + r] = ll[r];
+                        }
+                }
             }
+            continue;
         }
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ep[(4 * g + r) * 68 + 16 * j + n] = acc[i][j][r];
+        float v[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const v4f x = *(const v4f *)(ep + rr * 68 + cc + 4 * q);
+            v[4 * q] = x.x;
+            v[4 * q + 1] = x.y;
+            v[4 * q + 2] = x.z;
+            v[4 * q + 3] = x.w;
+        }
+        const int t = rbase + rr;
+        if (t >= M || nl0 >= Nseg) continue;
+        if (EPI == kEpiPlain || (EPI == kEpiQ && seg1)) {
+            float *dst = EPI == kEpiPlain ? a.C + (size_t)t * a.ldc + c0 + cw + cc : a.C + (size_t)t * a.ldc + nl0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) *(v4f *)(dst + 4 * q) = v4f{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+        } else if (EPI == kEpiQ) {
+            const int h = nl0 / QD, k0 = nl0 % QD;
+            const size_t o = ((size_t)h * e.Sp + t) * QD;
+            if (k0 < e.DN) {
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    v8bf hi, lo;
+                    split8(v4f{v[8 * q], v[8 * q + 1], v[8 * q + 2], v[8 * q + 3]},
+                           v4f{v[8 * q + 4], v[8 * q + 5], v[8 * q + 6], v[8 * q + 7]}, hi, lo);
+                    *(v8bf *)(e.qh + o + k0 + 8 * q) = hi;
+                    *(v8bf *)(e.ql + o + k0 + 8 * q) = lo;
+                }
+            } else {
+                // pairs (ev, od) = (v[2p], v[2p+1]) of rope index i2 = (k0 - DN) / 2 + p
+                const int i2 = (k0 - e.DN) >> 1;
+                const float2 *cs = e.cs + (size_t)t * half + i2;
+                float r0[8], r1[8];
+#pragma unroll
+                for (int p = 0; p < 8; ++p) {
+                    const float2 c = cs[p];
+                    const float ev = v[2 * p], od = v[2 * p + 1];
+                    r0[p] = ev * c.x - od * c.y;
+                    r1[p] = od * c.x + ev * c.y;
+                }
+                v8bf hi, lo;
+                split8(v4f{r0[0], r0[1], r0[2], r0[3]}, v4f{r0[4], r0[5], r0[6], r0[7]}, hi, lo);
+                *(v8bf *)(e.qh + o + e.DN + i2) = hi;
+                *(v8bf *)(e.ql + o + e.DN + i2) = lo;
+                split8(v4f{r1[0], r1[1], r1[2], r1[3]}, v4f{r1[4], r1[5], r1[6], r1[7]}, hi, lo);
+                *(v8bf *)(e.qh + o + e.DN + half + i2) = hi;
+                *(v8bf *)(e.ql + o + e.DN + half + i2) = lo;
+            }
+        } else {  // kEpiKV, k_nope columns
+            const int h = nl0 / KH, k0 = nl0 % KH;
+            uint16_t b[16];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) b[q] = f32_to_bf16_rne(v[q]);
+            uint16_t *dst = e.kb + ((size_t)h * e.Sp + t) * QD + k0;
+            *(uint4 *)dst = make_uint4(pack2(b[0], b[1]), pack2(b[2], b[3]), pack2(b[4], b[5]), pack2(b[6], b[7]));
+            *(uint4 *)(dst + 8) =
+                make_uint4(pack2(b[8], b[9]), pack2(b[10], b[11]), pack2(b[12], b[13]), pack2(b[14], b[15]));
+        }
+    }
 }
 
+// C = A . [B0; B1]^T with N0 + N1 output columns (N1 = 0: a single weight matrix). The
+// 256 x 256 tile is used when it still gives one tile per CU, else 256 x 128.
+template <int EPI>
 static hipError_t gemm(hipStream_t st, const uint16_t *Ah, const uint16_t *Al, const int *flag,
-                       int lda, const uint16_t *B, int ldb, float *C, int ldc, int M, int N,
-                       int K) {
-    GemmArgs a{Ah, Al, B, C, flag, M, N, K, lda, ldb, ldc};
-    dim3 grid((N + kGBn - 1) / kGBn, (M + kGBm - 1) / kGBm);
-    hipLaunchKernelGGL(k_gemm_bf16, grid, dim3(256), 0, st, a);
+                       int lda, const uint16_t *B0, int N0, const uint16_t *B1, int N1, int ldb,
+                       float *C, int ldc, int M, int K, const GemmEpi &e) {
+    GemmArgs a{Ah, Al, B0, B1 ? B1 : B0, C, flag, M, N0, N1, K, lda, ldb, ldc};
+    const int tm = (M + kGBm - 1) / kGBm;
+    const int t256 = tm * ((N0 + 255) / 256 + (N1 + 255) / 256);
+    const int t128 = tm * ((N0 + 127) / 128 + (N1 + 127) / 128);
+    if (t256 >= 224) hipLaunchKernelGGL((k_gemm_bf16<256, EPI>), dim3(t256), dim3(512), 0, st, a, e);
+    else hipLaunchKernelGGL((k_gemm_bf16<128, EPI>), dim3(t128), dim3(512), 0, st, a, e);
     return hipGetLastError();
 }
 
@@ -195,199 +379,345 @@ __global__ __launch_bounds__(256) void k_kva_epi(KvaEpiArgs a) {
     if (a.lat_flag && __syncthreads_or(any) && tid == 0) atomicOr(a.lat_flag, 1);
 }
 
-// Per (token t, head h): Q = [q_nope | RoPE(q_rope, t)] as hi/lo bf16 [NH, Sp, QD];
-// K = [kv[t, h, :DN] | krope[t]] bf16 [NH, Sp, QD]; V^T bf16 [NH, DV, Sp].
-struct PackArgs {
-    const float *y, *kv, *krope;
+// MFMA route, one wave per token t: latent = RMSNorm(kv_a[t, :R]) * w (as k_kva_epi) as
+// hi/lo bf16 [S, R] for the kv_b GEMM (whose lo pass always runs), and
+// the rotated k_rope (src/mla_prefill_streaming.c:131-138) as bf16 into the rope part of K
+// for every head. Tokens S .. Sp-1 zero their Q, K and V^T entries, so padding keys
+// contribute 0 * 0 in the flash kernel.
+struct KvaPackArgs {
+    const float *y;  // [S, ldy] kv_a projection
+    const uint16_t *norm;
     const float2 *cs;
-    uint16_t *qh, *ql, *kb, *vt;
-    int S, Sp, NH, DN, DR, DV, ldy;
+    uint16_t *lath, *latl, *qh, *ql, *kb, *vh, *vl;
+    int S, Sp, NH, ldy, R, DN, DR, DV;
+    float eps;
 };
 
-__global__ __launch_bounds__(256) void k_pack(PackArgs a) {
-    const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-    const int QD = a.DN + a.DR, half = a.DR / 2;
-    if (t >= a.S) {  // padding rows of the last tile: zero, so masked keys contribute 0 * 0
-        const size_t qo = ((size_t)h * a.Sp + t) * QD;
-        for (int k = tid; k < QD; k += 256) {
-            a.qh[qo + k] = 0;
-            a.ql[qo + k] = 0;
-            a.kb[qo + k] = 0;
+__global__ __launch_bounds__(256) void k_kva_pack(KvaPackArgs a) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+    if (t >= a.Sp) return;
+    const int QD = a.DN + a.DR, half = a.DR / 2, R = a.R;
+    if (t >= a.S) {
+        const int tv = (t & ~31) | vt_perm(t & 31);
+        for (int h = 0; h < a.NH; ++h) {
+            const size_t qo = ((size_t)h * a.Sp + t) * QD;
+            for (int k = l; k < QD; k += 64) {
+                a.qh[qo + k] = 0;
+                a.ql[qo + k] = 0;
+                a.kb[qo + k] = 0;
+            }
+            for (int d = l; d < a.DV; d += 64) {
+                a.vh[((size_t)h * a.DV + d) * a.Sp + tv] = 0;
+                a.vl[((size_t)h * a.DV + d) * a.Sp + tv] = 0;
+            }
         }
-        for (int d = tid; d < a.DV; d += 256) a.vt[((size_t)h * a.DV + d) * a.Sp + t] = 0;
         return;
     }
-    const float *q = a.y + (size_t)t * a.ldy + (size_t)h * QD;
-    const float *kv = a.kv + (size_t)t * a.NH * (a.DN + a.DV) + (size_t)h * (a.DN + a.DV);
-    const size_t qo = ((size_t)h * a.Sp + t) * QD;
-    for (int k = tid; k < QD; k += 256) {
-        float qv;
-        if (k < a.DN) {
-            qv = q[k];
-        } else {
-            const int i = (k - a.DN) % half;
-            const float2 cs = a.cs[(size_t)t * half + i];
-            const float ev = q[a.DN + 2 * i], od = q[a.DN + 2 * i + 1];
-            qv = (k - a.DN) < half ? ev * cs.x - od * cs.y : od * cs.x + ev * cs.y;
-        }
-        uint16_t hh, ll;
-        split_bf16(qv, hh, ll);
-        a.qh[qo + k] = hh;
-        a.ql[qo + k] = ll;
-        const float kvv = k < a.DN ? kv[k] : a.krope[(size_t)t * a.DR + (k - a.DN)];
-        a.kb[qo + k] = f32_to_bf16_rne(kvv);
+    const float *kat = a.y + (size_t)t * a.ldy;
+    double ss = 0.0;
+    for (int r = l; r < R; r += 64) {
+        const double v = (double)kat[r];
+        ss += v * v;
     }
-    for (int d = tid; d < a.DV; d += 256)
-        a.vt[((size_t)h * a.DV + d) * a.Sp + t] = f32_to_bf16_rne(kv[a.DN + d]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    const float mean_sq = (float)(ss / (double)R);
+    const float inv = 1.0f / sqrtf(mean_sq + a.eps);
+    for (int r = l; r < R; r += 64) {
+        const float v = kat[r] * inv;
+        const float y = v * bf16_to_f32(a.norm[r]);
+        uint16_t hh, ll;
+        split_bf16(y, hh, ll);
+        a.lath[(size_t)t * R + r] = hh;
+        a.latl[(size_t)t * R + r] = ll;
+    }
+    for (int i = l; i < half; i += 64) {
+        const float2 cs = a.cs[(size_t)t * half + i];
+        const float ev = kat[R + 2 * i], od = kat[R + 2 * i + 1];
+        const float ec = ev * cs.x, os = od * cs.y, oc = od * cs.x, es = ev * cs.y;
+        const uint16_t r0 = f32_to_bf16_rne(ec - os), r1 = f32_to_bf16_rne(oc + es);
+        for (int h = 0; h < a.NH; ++h) {
+            a.kb[((size_t)h * a.Sp + t) * QD + a.DN + i] = r0;
+            a.kb[((size_t)h * a.Sp + t) * QD + a.DN + half + i] = r1;
+        }
+    }
 }
 
 // ================================================================ flash attention ======
 
-// Causal attention for one head and 64 queries (4 waves x 16). QD = 192, DV = 128 here.
-// S = Q K^T: M = 16 queries, N = 16 keys, K = 192 (6 x 32), Q as hi/lo bf16 (A), K bf16 (B).
-// P = softmax rows (online), written per wave to LDS and re-read as the A operand (hi/lo).
-// O += P V: N = 16 of the 128 value columns (8 tiles), K = 32 keys, V^T rows from LDS.
-// Output rows normalised by l and written as hi/lo bf16 for the o_proj GEMM.
-constexpr int kFQ = 64, kFK = 64;
-constexpr int kFKs = 200;  // LDS K row: 192 + 8 bf16
-constexpr int kFVs = 72;   // LDS V^T row: 64 + 8 bf16
-constexpr int kFPs = 68;   // LDS P row: 64 + 4 fp32
+// Causal attention for one head and 128 queries: 4 waves x 32 queries (two 16-query tiles
+// u = 0, 1), keys in tiles of 64. QD = 192, DV = 128.
+//
+// Scores are computed transposed, S^T = K Q^T (v_mfma_f32_16x16x32_bf16, A = K from LDS,
+// B = Q^T from registers as hi + lo bf16), so lane (g, n) holds S^T[key 16t + 4g + i][query n].
+// Those are exactly the values the lane must supply as the B operand of O^T = V^T P^T
+// when the k-slots of a 32-key chunk c are ordered (16-key tile 2c: i = 0..3, tile 2c+1:
+// i = 0..3) per lane group g; V^T is stored with its keys permuted to that order (kv_b GEMM),
+// so P never leaves the registers. V is split hi + lo (bf16), P is rounded to bf16 once.
+// Softmax is online with a lazy reference max per query: it moves only when a tile's max
+// exceeds it by more than 8 (log2 units), so p <= 256 and most tiles skip the rescale.
+//
+// K and V tiles stream through LDS by global_load_lds_dwordx4 DMA into two offset rings:
+// step j computes QK of tile j+1 (K ring) and softmax + PV of tile j (V ring) while K of
+// tile j+2 and V of tile j+1 are in flight. The 16-byte slots of each LDS row are XOR-
+// swizzled by the row so that the fragment reads are free of bank conflicts.
+constexpr int kFQ = 128, kFK = 64;
+constexpr int kFKB = kFK * 192 * 2;  // K tile: 64 rows x 384 B
+constexpr int kFVB = 128 * kFK * 2;  // V^T tile (hi or lo): 128 rows x 128 B
+constexpr int kFSmem = 2 * kFKB + 4 * kFVB;
+constexpr float kFLazy = 8.0f;       // log2 headroom of the lazy max
 
 struct FlashArgs {
-    const uint16_t *qh, *ql, *kb, *vt;
-    uint16_t *oh, *ol;  // [S, HO] hi/lo
+    const uint16_t *qh, *ql, *kb, *vh, *vl;  // Q, K: [NH, Sp, 192]; V^T: [NH, 128, Sp]
+    uint16_t *oh, *ol;                       // [S, ldo] hi/lo
     int S, Sp, NH, ldo;
-    float smscale;
+    float sl2;                               // softmax scale * log2(e)
 };
 
-__global__ __launch_bounds__(256) void k_flash_prefill(FlashArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t sk[kFK * kFKs];
-    __shared__ __attribute__((aligned(16))) uint16_t sv[128 * kFVs];
-    __shared__ __attribute__((aligned(16))) float sp[4][16 * kFPs];
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
-    const int nqt = (a.S + kFQ - 1) / kFQ;
-    const int qt = nqt - 1 - (int)blockIdx.x;  // longest tiles first
-    const int h = blockIdx.y;
-    const int q0 = qt * kFQ;
-    const size_t hq = (size_t)h * a.Sp;
-    // Q operands: row q0 + 16w + n, dims kb*32 + 8g
-    v8bf qa[6], qb[6];
-    {
-        const int qrow = q0 + 16 * w + n;
-        const uint16_t *ph = a.qh + (hq + qrow) * 192;
-        const uint16_t *pl = a.ql + (hq + qrow) * 192;
+// Max / sum over the four lanes n, n + 16, n + 32, n + 48 (one per 16-lane row).
+__device__ __forceinline__ float xrow_max(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+__device__ __forceinline__ float xrow_sum(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t cvt2_bf16(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f{a, b}), v2bf));
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void k_flash_prefill(FlashArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[kFSmem];
+    const uint32_t sbase = lds_addr(smem);
+    const int tid = threadIdx.x, l = tid & 63, n = l & 15, g = l >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // kernel arguments as locals (the lambdas below must not capture the argument block)
+    const int S = a.S, Sp = a.Sp, NH = a.NH, ldo = a.ldo;
+    const float sl2 = a.sl2;
+    const int nqt = Sp / kFQ;
+    // Longest tiles first; with NH % 8 == 0, block b runs on XCD b % 8 and each XCD keeps
+    // the same NH / 8 heads, so the blocks streaming one head's K/V share an L2.
+    int qt, h;
+    if (NH % 8 == 0) {
+        const int hpx = NH / 8, j = blockIdx.x >> 3;
+        qt = nqt - 1 - j / hpx;
+        h = (blockIdx.x & 7) + 8 * (j % hpx);
+    } else {
+        qt = nqt - 1 - (int)blockIdx.x / NH;
+        h = (int)blockIdx.x % NH;
+    }
+    const int nt = 2 * qt + 2;  // key tiles 0 .. nt-1 (the last two straddle the diagonal)
+    const int qw = qt * kFQ + 32 * w;
+    const size_t hq = (size_t)h * Sp;
+
+    // Q^T B operands: query qw + 16u + n, dims 32kb + 8g .. +7
+    v8bf qa[2][6], qb[2][6];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const uint16_t *ph = a.qh + (hq + qw + 16 * u + n) * 192 + 8 * g;
+        const uint16_t *pl = a.ql + (hq + qw + 16 * u + n) * 192 + 8 * g;
 #pragma unroll
         for (int kb = 0; kb < 6; ++kb) {
-            qa[kb] = *(const v8bf *)(ph + 32 * kb + 8 * g);
-            qb[kb] = *(const v8bf *)(pl + 32 * kb + 8 * g);
+            qa[u][kb] = *(const v8bf *)(ph + 32 * kb);
+            qb[u][kb] = *(const v8bf *)(pl + 32 * kb);
         }
     }
-    float m_run[4], l_run[4];
+
+    // DMA sources. K tile: wave w fills LDS slots (6w + i) * 64 + l (16 B each) of the
+    // 1536-slot tile; slot (row, s') holds logical slot s = s' ^ (row & 7) (within groups
+    // of 8). V^T tile: slots (4w + i) * 64 + l of 1024; row d, slot s' holds s' ^ (d & 7).
+    const uint8_t *gk = (const uint8_t *)(a.kb + hq * 192);
+    const uint8_t *gvh = (const uint8_t *)(a.vh + (size_t)h * 128 * Sp);
+    const uint8_t *gvl = (const uint8_t *)(a.vl + (size_t)h * 128 * Sp);
+    uint32_t koff[6], voff[4];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+        const int p = (6 * w + i) * 64 + l, row = p / 24, sp = p % 24;
+        koff[i] = row * 384 + 16 * ((sp & ~7) | ((sp & 7) ^ (row & 7)));
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        m_run[i] = -INFINITY;
-        l_run[i] = 0.f;
+        const int p = (4 * w + i) * 64 + l, d = p >> 3, sp = p & 7;
+        voff[i] = (uint32_t)d * Sp * 2 + 16 * (sp ^ (d & 7));
     }
-    v4f acc[8];
+    const uint32_t kbuf[2] = {sbase, sbase + kFKB};
+    const uint32_t vbuf[2] = {sbase + 2 * kFKB, sbase + 2 * kFKB + 2 * kFVB};
+    auto issue_k = [&](int t, uint32_t dst) __attribute__((always_inline)) {
+        const uint8_t *src = gk + (size_t)t * kFK * 384;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
-    const float sl2 = a.smscale * 1.4426950408889634f;  // exp(x) = exp2(x * log2 e)
+        for (int i = 0; i < 6; ++i) dma_b128(src + koff[i], dst + (uint32_t)((6 * w + i) * 1024));
+    };
+    auto issue_v = [&](int t, uint32_t dst) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            dma_b128(gvh + (size_t)t * 128 + voff[i], dst + (uint32_t)((4 * w + i) * 1024));
+            dma_b128(gvl + (size_t)t * 128 + voff[i], dst + (uint32_t)(kFVB + (4 * w + i) * 1024));
+        }
+    };
+    // LDS fragment offsets. K (A operand): row 16t + n, logical slot 4kb + g.
+    // V^T (A operand): row 16dt + n, logical slot 4c + g.
+    int krd[6], vrd[2];
+#pragma unroll
+    for (int kb = 0; kb < 6; ++kb) krd[kb] = n * 384 + 16 * (8 * (kb >> 1) + ((4 * (kb & 1) + g) ^ (n & 7)));
+#pragma unroll
+    for (int c = 0; c < 2; ++c) vrd[c] = n * 128 + 16 * ((4 * c + g) ^ (n & 7));
 
-    for (int kt = 0; kt <= qt; ++kt) {
-        const int k0 = kt * kFK;
-        __syncthreads();
-        // K tile: 64 rows x 192 bf16 = 1536 x 16 B; V^T tile: 128 rows x 64 bf16 = 1024 x 16 B
-        for (int p = tid; p < 64 * 24; p += 256) {
-            const int row = p / 24, c8 = (p % 24) * 8;
-            *(v4i *)(sk + row * kFKs + c8) = *(const v4i *)(a.kb + (hq + k0 + row) * 192 + c8);
-        }
-        for (int p = tid; p < 128 * 8; p += 256) {
-            const int row = p >> 3, c8 = (p & 7) * 8;
-            *(v4i *)(sv + row * kFVs + c8) = *(const v4i *)(a.vt + ((size_t)h * 128 + row) * a.Sp + k0 + c8);
-        }
-        __syncthreads();
-        v4f s[4];
+    issue_k(0, kbuf[0]);
+    issue_k(1, kbuf[1]);
+    issue_v(0, vbuf[0]);
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-            s[nt] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int kb = 0; kb < 6; ++kb) {
-                const v8bf bk = *(const v8bf *)(sk + (16 * nt + n) * kFKs + 32 * kb + 8 * g);
-                s[nt] = mfma_bf16(qa[kb], bk, s[nt]);
-                s[nt] = mfma_bf16(qb[kb], bk, s[nt]);
+        for (int kb = 0; kb < 6; ++kb) asm volatile("" : "+v"(qa[u][kb]), "+v"(qb[u][kb]));
+    wait_vmcnt<0>();
+    lds_barrier();
+
+    auto qk = [&](int buf, v4f (&s)[4][2]) __attribute__((always_inline)) {
+        const uint8_t *kt = smem + buf * kFKB;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) s[t][u] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 6; ++kb)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const v8bf ka = *(const v8bf *)(kt + t * 16 * 384 + krd[kb]);
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    s[t][u] = mfma_bf16(ka, qa[u][kb], s[t][u]);
+                    s[t][u] = mfma_bf16(ka, qb[u][kb], s[t][u]);
+                }
             }
-        }
-        // D layout: query q0 + 16w + 4g + i, key k0 + 16nt + n
-        float mx[4];
+    };
+
+    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+    v4f acc[8][2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int qi = q0 + 16 * w + 4 * g + i;
-            float m = -INFINITY;
+    for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-            for (int nt = 0; nt < 4; ++nt) {
-                const int kj = k0 + 16 * nt + n;
-                float v = s[nt][i] * sl2;
-                if (kj > qi || kj >= a.S) v = -INFINITY;
-                s[nt][i] = v;
-                m = fmaxf(m, v);
-            }
+        for (int u = 0; u < 2; ++u) acc[dt][u] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    auto softmax_pv = [&](auto mask_tag, v4f (&s)[4][2], int k0, int buf) __attribute__((always_inline)) {
+        constexpr bool kMask = decltype(mask_tag)::value;
+        v8bf pb[2][2];
+        float alpha[2];
+        bool moved = false;
 #pragma unroll
-            for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
-            mx[i] = m;
-        }
-        float alpha[4];
+        for (int u = 0; u < 2; ++u) {
+            const int q = qw + 16 * u + n;
+            float mx = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float mnew = fmaxf(m_run[i], mx[i]);
-            alpha[i] = exp2f(m_run[i] - mnew);
-            m_run[i] = mnew;
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float v = s[t][u][i];
+                    if constexpr (kMask) {
+                        const int key = k0 + 16 * t + 4 * g + i;
+                        if (key > q || key >= S) v = -INFINITY;
+                        s[t][u][i] = v;
+                    }
+                    mx = fmaxf(mx, v);
+                }
+            mx = xrow_max(mx) * sl2;
+            const float mref = m_run[u];
+            const bool mv = mx > mref + kFLazy;
+            const float mnew = mv ? mx : mref;
+            alpha[u] = __builtin_amdgcn_exp2f(mref - mnew);
+            m_run[u] = mnew;
+            moved |= mv;
             float ps = 0.f;
+            uint32_t pk[4][2];
 #pragma unroll
-            for (int nt = 0; nt < 4; ++nt) {
-                const float p = exp2f(s[nt][i] - mnew);
-                ps += p;
-                sp[w][(4 * g + i) * kFPs + 16 * nt + n] = p;
+            for (int t = 0; t < 4; ++t) {
+                float p[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    p[i] = __builtin_amdgcn_exp2f(fmaf(s[t][u][i], sl2, -mnew));
+                    ps += p[i];
+                }
+                pk[t][0] = cvt2_bf16(p[0], p[1]);
+                pk[t][1] = cvt2_bf16(p[2], p[3]);
             }
+            l_run[u] = fmaf(l_run[u], alpha[u], ps);
 #pragma unroll
-            for (int o = 1; o < 16; o <<= 1) ps += __shfl_xor(ps, o);
-            l_run[i] = fmaf(l_run[i], alpha[i], ps);
+            for (int c = 0; c < 2; ++c) {
+                const v4i pv = {(int)pk[2 * c][0], (int)pk[2 * c][1], (int)pk[2 * c + 1][0],
+                                (int)pk[2 * c + 1][1]};
+                pb[u][c] = __builtin_bit_cast(v8bf, pv);
+            }
         }
+        if (__any(moved)) {
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
+            for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[t][i] *= alpha[i];
-        __syncthreads();  // P rows of this wave are visible in LDS
-        // P as A operand: query n, keys kb2*32 + 8g .. +7
+                for (int u = 0; u < 2; ++u) acc[dt][u] *= alpha[u];
+        }
+        const uint8_t *vt = smem + 2 * kFKB + buf * 2 * kFVB;
 #pragma unroll
-        for (int kb2 = 0; kb2 < 2; ++kb2) {
-            const float *pr = &sp[w][n * kFPs + 32 * kb2 + 8 * g];
-            const v4f p0 = *(const v4f *)pr, p1 = *(const v4f *)(pr + 4);
-            v8bf ph, pl;
-            split8(p0, p1, ph, pl);
+        for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const v8bf bv = *(const v8bf *)(sv + (16 * t + n) * kFVs + 32 * kb2 + 8 * g);
-                acc[t] = mfma_bf16(ph, bv, acc[t]);
-                acc[t] = mfma_bf16(pl, bv, acc[t]);
+            for (int dt = 0; dt < 8; ++dt) {
+                const v8bf vh = *(const v8bf *)(vt + dt * 16 * 128 + vrd[c]);
+                const v8bf vl = *(const v8bf *)(vt + kFVB + dt * 16 * 128 + vrd[c]);
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    acc[dt][u] = mfma_bf16(vh, pb[u][c], acc[dt][u]);
+                    acc[dt][u] = mfma_bf16(vl, pb[u][c], acc[dt][u]);
+                }
             }
+    };
+
+    v4f sc[4][2];
+    qk(0, sc);
+    // step j: QK of tile j+1 (if NEXT), softmax + PV of tile j; DMA of K(j+2), V(j+1).
+    auto step = [&](auto mask_tag, auto next_tag, int j) __attribute__((always_inline)) {
+        constexpr bool kNext = decltype(next_tag)::value;
+        wait_vmcnt<0>();
+        lds_barrier();
+        if (j + 2 < nt) issue_k(j + 2, kbuf[j & 1]);
+        if (j + 1 < nt) issue_v(j + 1, vbuf[(j + 1) & 1]);
+        v4f sn[4][2];
+        if constexpr (kNext) qk((j + 1) & 1, sn);
+        softmax_pv(mask_tag, sc, j * kFK, j & 1);
+        if constexpr (kNext) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int u = 0; u < 2; ++u) sc[t][u] = sn[t][u];
+        }
+    };
+    using F = std::false_type;
+    using T = std::true_type;
+    for (int j = 0; j < nt - 2; ++j) step(F{}, T{}, j);
+    step(T{}, T{}, nt - 2);
+    step(T{}, F{}, nt - 1);
+
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int q = qw + 16 * u + n;
+        const float inv = 1.0f / xrow_sum(l_run[u]);
+        if (q >= S) continue;
+        uint16_t *oh = a.oh + (size_t)q * ldo + (size_t)h * 128 + 4 * g;
+        uint16_t *ol = a.ol + (size_t)q * ldo + (size_t)h * 128 + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            uint16_t hh[4], ll[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) split_bf16(acc[dt][u][i] * inv, hh[i], ll[i]);
+            *(uint2 *)(oh + 16 * dt) = make_uint2(pack2(hh[0], hh[1]), pack2(hh[2], hh[3]));
+            *(uint2 *)(ol + 16 * dt) = make_uint2(pack2(ll[0], ll[1]), pack2(ll[2], ll[3]));
         }
     }
-    float inv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) inv[i] = 1.0f / l_run[i];
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int qi = q0 + 16 * w + 4 * g + i;
-            if (qi >= a.S) continue;
-            const float v = acc[t][i] * inv[i];
-            uint16_t hh, ll;
-            split_bf16(v, hh, ll);
-            const size_t o = (size_t)qi * a.ldo + (size_t)h * 128 + 16 * t + n;
-            a.oh[o] = hh;
-            a.ol[o] = ll;
-        }
 }
 
 // ================================================================ generic route ========
@@ -488,21 +818,23 @@ bool prefill_mfma_shape(const Dims &d) {
 }
 
 size_t prefill_bytes(const Dims &d, int S) {
-    const size_t Sp = (size_t)(S + 63) / 64 * 64;
+    const size_t Sp = (size_t)(S + 127) / 128 * 128;
     size_t b = 0;
     auto add = [&](size_t n) { b += (n + 255) / 256 * 256 + 256; };
     if (prefill_mfma_shape(d)) {
         add(4 * 8);                              // flags
-        add(2 * (size_t)S * d.H * 2);            // x hi/lo
-        add(4 * (size_t)S * (d.QO + d.KVO));     // y
-        add(4 * (size_t)S * d.R);                // latf
-        add(2 * 2 * (size_t)S * d.R);            // lat hi/lo
-        add(4 * (size_t)S * d.DR);               // krope
-        add(4 * (size_t)S * d.KVB);              // kv
-        add(2 * 2 * (size_t)d.NH * Sp * d.QD);   // q hi/lo
+        add(2 * (size_t)S * d.H);                // x hi
+        add(2 * (size_t)S * d.H);                // x lo
+        add(4 * (size_t)S * d.KVO);              // kv_a projection
+        add(2 * (size_t)S * d.R);                // latent hi
+        add(2 * (size_t)S * d.R);                // latent lo
+        add(2 * (size_t)d.NH * Sp * d.QD);       // q hi
+        add(2 * (size_t)d.NH * Sp * d.QD);       // q lo
         add(2 * (size_t)d.NH * Sp * d.QD);       // k
-        add(2 * (size_t)d.NH * d.DV * Sp);       // v^T
-        add(2 * 2 * (size_t)S * d.HO);           // heads hi/lo
+        add(2 * (size_t)d.NH * d.DV * Sp);       // v^T hi
+        add(2 * (size_t)d.NH * d.DV * Sp);       // v^T lo
+        add(2 * (size_t)S * d.HO);               // heads hi
+        add(2 * (size_t)S * d.HO);               // heads lo
     } else {
         add(4 * (size_t)S * (d.QO + d.KVO));
         add(4 * (size_t)S * d.R);
@@ -519,7 +851,7 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
                               float *out, const uint16_t *wq, const uint16_t *wkva,
                               const uint16_t *wnorm, const uint16_t *wkvb, const uint16_t *wo,
                               const float2 *cs, void *ws) {
-    const int Sp = (S + 63) / 64 * 64;
+    const int Sp = (S + 127) / 128 * 128;
     char *base = (char *)ws;
     size_t off = 0;
     auto take = [&](size_t n) {
@@ -535,37 +867,39 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
         int *flags = (int *)take(4 * 8);
         uint16_t *xh = (uint16_t *)take(2 * (size_t)S * d.H);
         uint16_t *xl = (uint16_t *)take(2 * (size_t)S * d.H);
-        float *y = (float *)take(4 * (size_t)S * ldy);
-        float *latf = (float *)take(4 * (size_t)S * d.R);
+        float *ykva = (float *)take(4 * (size_t)S * d.KVO);
         uint16_t *lath = (uint16_t *)take(2 * (size_t)S * d.R);
         uint16_t *latl = (uint16_t *)take(2 * (size_t)S * d.R);
-        float *krope = (float *)take(4 * (size_t)S * d.DR);
-        float *kv = (float *)take(4 * (size_t)S * d.KVB);
         uint16_t *qh = (uint16_t *)take(2 * (size_t)d.NH * Sp * d.QD);
         uint16_t *ql = (uint16_t *)take(2 * (size_t)d.NH * Sp * d.QD);
         uint16_t *kb = (uint16_t *)take(2 * (size_t)d.NH * Sp * d.QD);
-        uint16_t *vt = (uint16_t *)take(2 * (size_t)d.NH * d.DV * Sp);
+        uint16_t *vh = (uint16_t *)take(2 * (size_t)d.NH * d.DV * Sp);
+        uint16_t *vl = (uint16_t *)take(2 * (size_t)d.NH * d.DV * Sp);
         uint16_t *oh = (uint16_t *)take(2 * (size_t)S * d.HO);
         uint16_t *ol = (uint16_t *)take(2 * (size_t)S * d.HO);
+        const GemmEpi ep{qh, ql, kb, vh, vl, cs, Sp, d.DN, d.DR, d.DV};
         hipLaunchKernelGGL(k_zero_int, dim3(1), dim3(64), 0, st, flags, 8);
-        hipLaunchKernelGGL(k_split, dim3(1024), dim3(256), 0, st, x, d.H, xh, xl, d.H, S, d.H, flags + 0);
+        const int split_blocks = (int)std::min<size_t>(2048, ((size_t)S * d.H / 8 + 255) / 256);
+        hipLaunchKernelGGL(k_split, dim3(split_blocks), dim3(256), 0, st, x, d.H, xh, xl, d.H, S, d.H, flags + 0);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        if ((e = gemm(st, xh, xl, flags + 0, d.H, wq, d.H, y, ldy, S, d.QO, d.H)) != hipSuccess) return e;
-        if ((e = gemm(st, xh, xl, flags + 0, d.H, wkva, d.H, y + d.QO, ldy, S, d.KVO, d.H)) != hipSuccess)
+        // q (-> Q hi/lo, rotated) | kv_a (-> ykva)
+        if ((e = gemm<kEpiQ>(st, xh, xl, flags + 0, d.H, wq, d.QO, wkva, d.KVO, d.H, ykva, d.KVO, S, d.H,
+                             ep)) != hipSuccess)
             return e;
-        KvaEpiArgs ea{y, wnorm, cs, latf, lath, latl, krope, flags + 1, ldy, d.QO, d.R, d.DR, eps};
-        hipLaunchKernelGGL(k_kva_epi, dim3(S), dim3(256), 0, st, ea);
+        KvaPackArgs ka{ykva, wnorm, cs, lath, latl, qh, ql, kb, vh, vl, S, Sp, d.NH, d.KVO, d.R, d.DN, d.DR, d.DV, eps};
+        hipLaunchKernelGGL(k_kva_pack, dim3((Sp + 3) / 4), dim3(256), 0, st, ka);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        if ((e = gemm(st, lath, latl, flags + 1, d.R, wkvb, d.R, kv, d.KVB, S, d.KVB, d.R)) != hipSuccess)
+        // kv_b (-> K nope part, V^T hi/lo)
+        if ((e = gemm<kEpiKV>(st, lath, latl, nullptr, d.R, wkvb, d.KVB, nullptr, 0, d.R, nullptr, 0, S, d.R,
+                              ep)) != hipSuccess)
             return e;
-        PackArgs pa{y, kv, krope, cs, qh, ql, kb, vt, S, Sp, d.NH, d.DN, d.DR, d.DV, ldy};
-        hipLaunchKernelGGL(k_pack, dim3(Sp, d.NH), dim3(256), 0, st, pa);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-        FlashArgs fa{qh, ql, kb, vt, oh, ol, S, Sp, d.NH, d.HO, smscale};
-        hipLaunchKernelGGL(k_flash_prefill, dim3(Sp / 64, d.NH), dim3(256), 0, st, fa);
+        FlashArgs fa{qh, ql, kb, vh, vl, oh, ol, S, Sp, d.NH, d.HO, smscale * 1.4426950408889634f};
+        hipLaunchKernelGGL(k_flash_prefill, dim3(Sp / kFQ * d.NH), dim3(256), 0, st, fa);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // attention outputs are never bf16-exact: the lo pass always runs (no flag)
-        if ((e = gemm(st, oh, ol, nullptr, d.HO, wo, d.HO, out, d.H, S, d.H, d.HO)) != hipSuccess) return e;
+        if ((e = gemm<kEpiPlain>(st, oh, ol, nullptr, d.HO, wo, d.H, nullptr, 0, d.HO, out, d.H, S, d.HO, ep)) !=
+            hipSuccess)
+            return e;
         return hipSuccess;
     }
     float *y = (float *)take(4 * (size_t)S * ldy);
