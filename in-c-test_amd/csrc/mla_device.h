@@ -9,6 +9,8 @@ namespace kvl {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
     return __uint_as_float((uint32_t)h << 16);
@@ -54,6 +56,25 @@ __device__ __forceinline__ void split8(const v4f &x0, const v4f &x1, v8bf &hi, v
 
 __device__ __forceinline__ v4f mfma_bf16(const v8bf &a, const v8bf &b, const v4f &c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ v4f mfma_f16(const v8h &a, const v8h &b, const v4f &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// x ~= hi + lo with hi, lo fp16 (round to nearest even): the split keeps ~22 mantissa bits of
+// an fp32 operand of moderate range; products of fp16 operands are exact in fp32.
+__device__ __forceinline__ void split_f16(float x, _Float16 &hi, _Float16 &lo) {
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
+}
+__device__ __forceinline__ void split8_f16(const float *x, v8h &hi, v8h &lo) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        _Float16 h, l;
+        split_f16(x[i], h, l);
+        hi[i] = h;
+        lo[i] = l;
+    }
 }
 __device__ __forceinline__ v4i mfma_i8(const v4i &a, const v4i &b, const v4i &c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);

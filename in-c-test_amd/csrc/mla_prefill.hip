@@ -5,9 +5,9 @@
 //   split     x (fp32) -> bf16 hi + lo operands; a flag records whether any lo is non-zero
 //   gemm      [q | kv_a] = x . W^T           (bf16 MFMA, fp32 accumulate, lo pass skipped
 //                                             when the operand is exactly bf16); epilogue:
-//                                             Q = [q_nope | RoPE(q_rope)] as hi/lo bf16
-//   kva_pack  RMSNorm -> latent (hi/lo), RoPE(k_rope) -> rope part of K (bf16), per token
-//   gemm      kv = latent . kv_b^T           epilogue: k_nope -> K (bf16), V^T (hi/lo bf16)
+//                                             Q = [q_nope | RoPE(q_rope)] as hi/lo fp16
+//   kva_pack  RMSNorm -> latent (hi/lo bf16), RoPE(k_rope) -> rope part of K (hi/lo fp16)
+//   gemm      kv = latent . kv_b^T           epilogue: k_nope -> K (hi/lo fp16), V^T (fp16)
 //   flash     causal attention per (128-query tile, head), online softmax
 //   gemm      out = heads . o_proj^T
 // Generic route (any shape): the same stages with VALU kernels.
@@ -87,13 +87,13 @@ struct GemmArgs {
 };
 
 // Epilogues. kEpiPlain: C fp32. kEpiQ (q | kv_a projection): the N0 = NH * QD q columns go
-// to Q [NH, Sp, QD] as hi/lo bf16 with the rope half rotated (src/mla_prefill_streaming.c:
+// to Q [NH, Sp, QD] as hi/lo fp16 with the rope half rotated (src/mla_prefill_streaming.c:
 // 139-147: pairs (2i, 2i+1) -> i and DR/2 + i), the kv_a columns to C (ldc = N1). kEpiKV
-// (kv_b projection): k_nope -> K [NH, Sp, QD] bf16, values -> V^T [NH, DV, Sp] hi/lo bf16
+// (kv_b projection): k_nope -> K [NH, Sp, QD] hi/lo fp16, values -> V^T [NH, DV, Sp] fp16
 // with the keys of each 32-key group in vt_perm order.
 enum { kEpiPlain = 0, kEpiQ = 1, kEpiKV = 2 };
 struct GemmEpi {
-    uint16_t *qh, *ql, *kb, *vh, *vl;
+    _Float16 *qh, *ql, *kh, *kl, *vt;
     const float2 *cs;
     int Sp, DN, DR, DV;
 };
@@ -225,20 +225,15 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmArgs a, GemmEpi e) {
                 const int nl = nb0 + cw + 16 * j + n;
                 if (nl >= Nseg) continue;
                 const int h = nl / KH, d = nl % KH - e.DN;
-                uint16_t hh[4], ll[4];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) split_bf16(acc[i][j][r], hh[r], ll[r]);
+                const v4h hv = {(_Float16)acc[i][j][0], (_Float16)acc[i][j][1], (_Float16)acc[i][j][2],
+                                (_Float16)acc[i][j][3]};
                 const size_t o = ((size_t)h * e.DV + d) * e.Sp + (row0 & ~31) + vt_perm(row0 & 31);
                 if (row0 + 3 < M) {
-                    *(uint2 *)(e.vh + o) = make_uint2(pack2(hh[0], hh[1]), pack2(hh[2], hh[3]));
-                    *(uint2 *)(e.vl + o) = make_uint2(pack2(ll[0], ll[1]), pack2(ll[2], ll[3]));
+                    *(v4h *)(e.vt + o) = hv;
                 } else {
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        if (row0 + r < M) {
-                            e.vh[o + r] = hh[r];
-                            e.vl[o + r] = ll[r];
-                        }
+                        if (row0 + r < M) e.vt[o + r] = hv[r];
                 }
             }
             continue;
@@ -268,11 +263,10 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmArgs a, GemmEpi e) {
             if (k0 < e.DN) {
 #pragma unroll
                 for (int q = 0; q < 2; ++q) {
-                    v8bf hi, lo;
-                    split8(v4f{v[8 * q], v[8 * q + 1], v[8 * q + 2], v[8 * q + 3]},
-                           v4f{v[8 * q + 4], v[8 * q + 5], v[8 * q + 6], v[8 * q + 7]}, hi, lo);
-                    *(v8bf *)(e.qh + o + k0 + 8 * q) = hi;
-                    *(v8bf *)(e.ql + o + k0 + 8 * q) = lo;
+                    v8h hi, lo;
+                    split8_f16(v + 8 * q, hi, lo);
+                    *(v8h *)(e.qh + o + k0 + 8 * q) = hi;
+                    *(v8h *)(e.ql + o + k0 + 8 * q) = lo;
                 }
             } else {
                 // pairs (ev, od) = (v[2p], v[2p+1]) of rope index i2 = (k0 - DN) / 2 + p
@@ -286,23 +280,24 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmArgs a, GemmEpi e) {
                     r0[p] = ev * c.x - od * c.y;
                     r1[p] = od * c.x + ev * c.y;
                 }
-                v8bf hi, lo;
-                split8(v4f{r0[0], r0[1], r0[2], r0[3]}, v4f{r0[4], r0[5], r0[6], r0[7]}, hi, lo);
-                *(v8bf *)(e.qh + o + e.DN + i2) = hi;
-                *(v8bf *)(e.ql + o + e.DN + i2) = lo;
-                split8(v4f{r1[0], r1[1], r1[2], r1[3]}, v4f{r1[4], r1[5], r1[6], r1[7]}, hi, lo);
-                *(v8bf *)(e.qh + o + e.DN + half + i2) = hi;
-                *(v8bf *)(e.ql + o + e.DN + half + i2) = lo;
+                v8h hi, lo;
+                split8_f16(r0, hi, lo);
+                *(v8h *)(e.qh + o + e.DN + i2) = hi;
+                *(v8h *)(e.ql + o + e.DN + i2) = lo;
+                split8_f16(r1, hi, lo);
+                *(v8h *)(e.qh + o + e.DN + half + i2) = hi;
+                *(v8h *)(e.ql + o + e.DN + half + i2) = lo;
             }
         } else {  // kEpiKV, k_nope columns
             const int h = nl0 / KH, k0 = nl0 % KH;
-            uint16_t b[16];
+            const size_t o = ((size_t)h * e.Sp + t) * QD + k0;
 #pragma unroll
-            for (int q = 0; q < 16; ++q) b[q] = f32_to_bf16_rne(v[q]);
-            uint16_t *dst = e.kb + ((size_t)h * e.Sp + t) * QD + k0;
-            *(uint4 *)dst = make_uint4(pack2(b[0], b[1]), pack2(b[2], b[3]), pack2(b[4], b[5]), pack2(b[6], b[7]));
-            *(uint4 *)(dst + 8) =
-                make_uint4(pack2(b[8], b[9]), pack2(b[10], b[11]), pack2(b[12], b[13]), pack2(b[14], b[15]));
+            for (int q = 0; q < 2; ++q) {
+                v8h hi, lo;
+                split8_f16(v + 8 * q, hi, lo);
+                *(v8h *)(e.kh + o + 8 * q) = hi;
+                *(v8h *)(e.kl + o + 8 * q) = lo;
+            }
         }
     }
 }
@@ -380,15 +375,16 @@ __global__ __launch_bounds__(256) void k_kva_epi(KvaEpiArgs a) {
 }
 
 // MFMA route, one wave per token t: latent = RMSNorm(kv_a[t, :R]) * w (as k_kva_epi) as
-// hi/lo bf16 [S, R] for the kv_b GEMM (whose lo pass always runs), and
-// the rotated k_rope (src/mla_prefill_streaming.c:131-138) as bf16 into the rope part of K
-// for every head. Tokens S .. Sp-1 zero their Q, K and V^T entries, so padding keys
-// contribute 0 * 0 in the flash kernel.
+// hi/lo bf16 [S, R] for the kv_b GEMM (whose lo pass always runs), and the rotated k_rope
+// (src/mla_prefill_streaming.c:131-138) as hi/lo fp16 into the rope part of K for every
+// head. Tokens S .. Sp-1 zero their Q, K and V^T entries, so padding keys contribute 0 * 0
+// in the flash kernel.
 struct KvaPackArgs {
     const float *y;  // [S, ldy] kv_a projection
     const uint16_t *norm;
     const float2 *cs;
-    uint16_t *lath, *latl, *qh, *ql, *kb, *vh, *vl;
+    uint16_t *lath, *latl;
+    _Float16 *qh, *ql, *kh, *kl, *vt;
     int S, Sp, NH, ldy, R, DN, DR, DV;
     float eps;
 };
@@ -404,12 +400,10 @@ __global__ __launch_bounds__(256) void k_kva_pack(KvaPackArgs a) {
             for (int k = l; k < QD; k += 64) {
                 a.qh[qo + k] = 0;
                 a.ql[qo + k] = 0;
-                a.kb[qo + k] = 0;
+                a.kh[qo + k] = 0;
+                a.kl[qo + k] = 0;
             }
-            for (int d = l; d < a.DV; d += 64) {
-                a.vh[((size_t)h * a.DV + d) * a.Sp + tv] = 0;
-                a.vl[((size_t)h * a.DV + d) * a.Sp + tv] = 0;
-            }
+            for (int d = l; d < a.DV; d += 64) a.vt[((size_t)h * a.DV + d) * a.Sp + tv] = 0;
         }
         return;
     }
@@ -435,10 +429,15 @@ __global__ __launch_bounds__(256) void k_kva_pack(KvaPackArgs a) {
         const float2 cs = a.cs[(size_t)t * half + i];
         const float ev = kat[R + 2 * i], od = kat[R + 2 * i + 1];
         const float ec = ev * cs.x, os = od * cs.y, oc = od * cs.x, es = ev * cs.y;
-        const uint16_t r0 = f32_to_bf16_rne(ec - os), r1 = f32_to_bf16_rne(oc + es);
+        _Float16 h0, l0, h1, l1;
+        split_f16(ec - os, h0, l0);
+        split_f16(oc + es, h1, l1);
         for (int h = 0; h < a.NH; ++h) {
-            a.kb[((size_t)h * a.Sp + t) * QD + a.DN + i] = r0;
-            a.kb[((size_t)h * a.Sp + t) * QD + a.DN + half + i] = r1;
+            const size_t o = ((size_t)h * a.Sp + t) * QD + a.DN;
+            a.kh[o + i] = h0;
+            a.kl[o + i] = l0;
+            a.kh[o + half + i] = h1;
+            a.kl[o + half + i] = l1;
         }
     }
 }
@@ -446,30 +445,33 @@ __global__ __launch_bounds__(256) void k_kva_pack(KvaPackArgs a) {
 // ================================================================ flash attention ======
 
 // Causal attention for one head and 128 queries: 4 waves x 32 queries (two 16-query tiles
-// u = 0, 1), keys in tiles of 64. QD = 192, DV = 128.
+// u = 0, 1), keys in tiles of 64. QD = 192, DV = 128. Operands are fp16 (11 significant bits,
+// ample range for these values): Q and K as hi + lo pairs, V and P rounded once.
 //
-// Scores are computed transposed, S^T = K Q^T (v_mfma_f32_16x16x32_bf16, A = K from LDS,
-// B = Q^T from registers as hi + lo bf16), so lane (g, n) holds S^T[key 16t + 4g + i][query n].
-// Those are exactly the values the lane must supply as the B operand of O^T = V^T P^T
-// when the k-slots of a 32-key chunk c are ordered (16-key tile 2c: i = 0..3, tile 2c+1:
-// i = 0..3) per lane group g; V^T is stored with its keys permuted to that order (kv_b GEMM),
-// so P never leaves the registers. V is split hi + lo (bf16), P is rounded to bf16 once.
-// Softmax is online with a lazy reference max per query: it moves only when a tile's max
-// exceeds it by more than 8 (log2 units), so p <= 256 and most tiles skip the rescale.
+// Scores are computed transposed, S^T = K Q^T (v_mfma_f32_16x16x32_f16, A = K from LDS,
+// B = Q^T from registers) in three passes, Kh Qh + Kh Ql + Kl Qh (the Kl Ql term is below
+// 2^-22 of the product): the score error stays near fp32 even for large logits, where a
+// single rounding of K would be amplified by the logit size. Lane (g, n) then holds
+// S^T[key 16t + 4g + i][query n], exactly the values it must supply as the B operand of
+// O^T = V^T P^T when the k-slots of a 32-key chunk c are ordered (16-key tile 2c: i = 0..3,
+// tile 2c+1: i = 0..3) per lane group g; V^T is stored with its keys permuted to that order
+// (kv_b GEMM), so P never leaves the registers. Softmax is online with a lazy reference max
+// per query: it moves only when a tile's max exceeds it by more than 8 (log2 units), so
+// p <= 256 and most tiles skip the rescale.
 //
 // K and V tiles stream through LDS by global_load_lds_dwordx4 DMA into two offset rings:
 // step j computes QK of tile j+1 (K ring) and softmax + PV of tile j (V ring) while K of
 // tile j+2 and V of tile j+1 are in flight. The 16-byte slots of each LDS row are XOR-
 // swizzled by the row so that the fragment reads are free of bank conflicts.
 constexpr int kFQ = 128, kFK = 64;
-constexpr int kFKB = kFK * 192 * 2;  // K tile: 64 rows x 384 B
-constexpr int kFVB = 128 * kFK * 2;  // V^T tile (hi or lo): 128 rows x 128 B
-constexpr int kFSmem = 2 * kFKB + 4 * kFVB;
+constexpr int kFKB = kFK * 192 * 2;  // K tile (hi or lo): 64 rows x 384 B
+constexpr int kFVB = 128 * kFK * 2;  // V^T tile: 128 rows x 128 B
+constexpr int kFSmem = 2 * 2 * kFKB + 2 * kFVB;
 constexpr float kFLazy = 8.0f;       // log2 headroom of the lazy max
 
 struct FlashArgs {
-    const uint16_t *qh, *ql, *kb, *vh, *vl;  // Q, K: [NH, Sp, 192]; V^T: [NH, 128, Sp]
-    uint16_t *oh, *ol;                       // [S, ldo] hi/lo
+    const _Float16 *qh, *ql, *kh, *kl, *vt;  // Q, K: [NH, Sp, 192]; V^T: [NH, 128, Sp]
+    uint16_t *oh, *ol;                       // [S, ldo] hi/lo bf16
     int S, Sp, NH, ldo;
     float sl2;                               // softmax scale * log2(e)
 };
@@ -486,12 +488,6 @@ __device__ __forceinline__ float xrow_sum(float v) {
     v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return __uint_as_float(q[0]) + __uint_as_float(q[1]);
-}
-
-typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
-typedef float v2f __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t cvt2_bf16(float a, float b) {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f{a, b}), v2bf));
 }
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -520,24 +516,24 @@ void k_flash_prefill(FlashArgs a) {
     const size_t hq = (size_t)h * Sp;
 
     // Q^T B operands: query qw + 16u + n, dims 32kb + 8g .. +7
-    v8bf qa[2][6], qb[2][6];
+    v8h qa[2][6], qb[2][6];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-        const uint16_t *ph = a.qh + (hq + qw + 16 * u + n) * 192 + 8 * g;
-        const uint16_t *pl = a.ql + (hq + qw + 16 * u + n) * 192 + 8 * g;
+        const _Float16 *ph = a.qh + (hq + qw + 16 * u + n) * 192 + 8 * g;
+        const _Float16 *pl = a.ql + (hq + qw + 16 * u + n) * 192 + 8 * g;
 #pragma unroll
         for (int kb = 0; kb < 6; ++kb) {
-            qa[u][kb] = *(const v8bf *)(ph + 32 * kb);
-            qb[u][kb] = *(const v8bf *)(pl + 32 * kb);
+            qa[u][kb] = *(const v8h *)(ph + 32 * kb);
+            qb[u][kb] = *(const v8h *)(pl + 32 * kb);
         }
     }
 
     // DMA sources. K tile: wave w fills LDS slots (6w + i) * 64 + l (16 B each) of the
     // 1536-slot tile; slot (row, s') holds logical slot s = s' ^ (row & 7) (within groups
     // of 8). V^T tile: slots (4w + i) * 64 + l of 1024; row d, slot s' holds s' ^ (d & 7).
-    const uint8_t *gk = (const uint8_t *)(a.kb + hq * 192);
-    const uint8_t *gvh = (const uint8_t *)(a.vh + (size_t)h * 128 * Sp);
-    const uint8_t *gvl = (const uint8_t *)(a.vl + (size_t)h * 128 * Sp);
+    const uint8_t *gkh = (const uint8_t *)(a.kh + hq * 192);
+    const uint8_t *gkl = (const uint8_t *)(a.kl + hq * 192);
+    const uint8_t *gv = (const uint8_t *)(a.vt + (size_t)h * 128 * Sp);
     uint32_t koff[6], voff[4];
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
@@ -549,19 +545,20 @@ void k_flash_prefill(FlashArgs a) {
         const int p = (4 * w + i) * 64 + l, d = p >> 3, sp = p & 7;
         voff[i] = (uint32_t)d * Sp * 2 + 16 * (sp ^ (d & 7));
     }
-    const uint32_t kbuf[2] = {sbase, sbase + kFKB};
-    const uint32_t vbuf[2] = {sbase + 2 * kFKB, sbase + 2 * kFKB + 2 * kFVB};
-    auto issue_k = [&](int t, uint32_t dst) __attribute__((always_inline)) {
-        const uint8_t *src = gk + (size_t)t * kFK * 384;
+    // LDS: K ring [2][hi, lo], then V ring [2]
+    auto issue_k = [&](int t) __attribute__((always_inline)) {
+        const uint32_t dst = sbase + (t & 1) * 2 * kFKB + (uint32_t)(6 * w) * 1024;
+        const size_t so = (size_t)t * kFK * 384;
 #pragma unroll
-        for (int i = 0; i < 6; ++i) dma_b128(src + koff[i], dst + (uint32_t)((6 * w + i) * 1024));
-    };
-    auto issue_v = [&](int t, uint32_t dst) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            dma_b128(gvh + (size_t)t * 128 + voff[i], dst + (uint32_t)((4 * w + i) * 1024));
-            dma_b128(gvl + (size_t)t * 128 + voff[i], dst + (uint32_t)(kFVB + (4 * w + i) * 1024));
+        for (int i = 0; i < 6; ++i) {
+            dma_b128(gkh + so + koff[i], dst + i * 1024);
+            dma_b128(gkl + so + koff[i], dst + kFKB + i * 1024);
         }
+    };
+    auto issue_v = [&](int t) __attribute__((always_inline)) {
+        const uint32_t dst = sbase + 4 * kFKB + (t & 1) * kFVB + (uint32_t)(4 * w) * 1024;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dma_b128(gv + (size_t)t * 128 + voff[i], dst + i * 1024);
     };
     // LDS fragment offsets. K (A operand): row 16t + n, logical slot 4kb + g.
     // V^T (A operand): row 16dt + n, logical slot 4c + g.
@@ -571,9 +568,9 @@ void k_flash_prefill(FlashArgs a) {
 #pragma unroll
     for (int c = 0; c < 2; ++c) vrd[c] = n * 128 + 16 * ((4 * c + g) ^ (n & 7));
 
-    issue_k(0, kbuf[0]);
-    issue_k(1, kbuf[1]);
-    issue_v(0, vbuf[0]);
+    issue_k(0);
+    issue_k(1);
+    issue_v(0);
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
@@ -581,8 +578,8 @@ void k_flash_prefill(FlashArgs a) {
     wait_vmcnt<0>();
     lds_barrier();
 
-    auto qk = [&](int buf, v4f (&s)[4][2]) __attribute__((always_inline)) {
-        const uint8_t *kt = smem + buf * kFKB;
+    auto qk = [&](int j, v4f (&s)[4][2]) __attribute__((always_inline)) {
+        const uint8_t *kt = smem + (j & 1) * 2 * kFKB;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -591,11 +588,13 @@ void k_flash_prefill(FlashArgs a) {
         for (int kb = 0; kb < 6; ++kb)
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const v8bf ka = *(const v8bf *)(kt + t * 16 * 384 + krd[kb]);
+                const v8h kh = *(const v8h *)(kt + t * 16 * 384 + krd[kb]);
+                const v8h kl = *(const v8h *)(kt + kFKB + t * 16 * 384 + krd[kb]);
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
-                    s[t][u] = mfma_bf16(ka, qa[u][kb], s[t][u]);
-                    s[t][u] = mfma_bf16(ka, qb[u][kb], s[t][u]);
+                    s[t][u] = mfma_f16(kh, qa[u][kb], s[t][u]);
+                    s[t][u] = mfma_f16(kh, qb[u][kb], s[t][u]);
+                    s[t][u] = mfma_f16(kl, qa[u][kb], s[t][u]);
                 }
             }
     };
@@ -607,9 +606,10 @@ void k_flash_prefill(FlashArgs a) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) acc[dt][u] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    auto softmax_pv = [&](auto mask_tag, v4f (&s)[4][2], int k0, int buf) __attribute__((always_inline)) {
+    auto softmax_pv = [&](auto mask_tag, v4f (&s)[4][2], int j) __attribute__((always_inline)) {
         constexpr bool kMask = decltype(mask_tag)::value;
-        v8bf pb[2][2];
+        const int k0 = j * kFK;
+        v8h pb[2][2];
         float alpha[2];
         bool moved = false;
 #pragma unroll
@@ -636,25 +636,15 @@ void k_flash_prefill(FlashArgs a) {
             m_run[u] = mnew;
             moved |= mv;
             float ps = 0.f;
-            uint32_t pk[4][2];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                float p[4];
+            for (int t = 0; t < 4; ++t)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    p[i] = __builtin_amdgcn_exp2f(fmaf(s[t][u][i], sl2, -mnew));
-                    ps += p[i];
+                    const float p = __builtin_amdgcn_exp2f(fmaf(s[t][u][i], sl2, -mnew));
+                    ps += p;
+                    pb[u][t >> 1][4 * (t & 1) + i] = (_Float16)p;
                 }
-                pk[t][0] = cvt2_bf16(p[0], p[1]);
-                pk[t][1] = cvt2_bf16(p[2], p[3]);
-            }
             l_run[u] = fmaf(l_run[u], alpha[u], ps);
-#pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                const v4i pv = {(int)pk[2 * c][0], (int)pk[2 * c][1], (int)pk[2 * c + 1][0],
-                                (int)pk[2 * c + 1][1]};
-                pb[u][c] = __builtin_bit_cast(v8bf, pv);
-            }
         }
         if (__any(moved)) {
 #pragma unroll
@@ -662,18 +652,14 @@ void k_flash_prefill(FlashArgs a) {
 #pragma unroll
                 for (int u = 0; u < 2; ++u) acc[dt][u] *= alpha[u];
         }
-        const uint8_t *vt = smem + 2 * kFKB + buf * 2 * kFVB;
+        const uint8_t *vt = smem + 4 * kFKB + (j & 1) * kFVB;
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) {
-                const v8bf vh = *(const v8bf *)(vt + dt * 16 * 128 + vrd[c]);
-                const v8bf vl = *(const v8bf *)(vt + kFVB + dt * 16 * 128 + vrd[c]);
+                const v8h vv = *(const v8h *)(vt + dt * 16 * 128 + vrd[c]);
 #pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    acc[dt][u] = mfma_bf16(vh, pb[u][c], acc[dt][u]);
-                    acc[dt][u] = mfma_bf16(vl, pb[u][c], acc[dt][u]);
-                }
+                for (int u = 0; u < 2; ++u) acc[dt][u] = mfma_f16(vv, pb[u][c], acc[dt][u]);
             }
     };
 
@@ -684,11 +670,11 @@ void k_flash_prefill(FlashArgs a) {
         constexpr bool kNext = decltype(next_tag)::value;
         wait_vmcnt<0>();
         lds_barrier();
-        if (j + 2 < nt) issue_k(j + 2, kbuf[j & 1]);
-        if (j + 1 < nt) issue_v(j + 1, vbuf[(j + 1) & 1]);
+        if (j + 2 < nt) issue_k(j + 2);
+        if (j + 1 < nt) issue_v(j + 1);
         v4f sn[4][2];
-        if constexpr (kNext) qk((j + 1) & 1, sn);
-        softmax_pv(mask_tag, sc, j * kFK, j & 1);
+        if constexpr (kNext) qk(j + 1, sn);
+        softmax_pv(mask_tag, sc, j);
         if constexpr (kNext) {
 #pragma unroll
             for (int t = 0; t < 4; ++t)
@@ -828,11 +814,11 @@ size_t prefill_bytes(const Dims &d, int S) {
         add(4 * (size_t)S * d.KVO);              // kv_a projection
         add(2 * (size_t)S * d.R);                // latent hi
         add(2 * (size_t)S * d.R);                // latent lo
-        add(2 * (size_t)d.NH * Sp * d.QD);       // q hi
+        add(2 * (size_t)d.NH * Sp * d.QD);       // q hi (fp16)
         add(2 * (size_t)d.NH * Sp * d.QD);       // q lo
-        add(2 * (size_t)d.NH * Sp * d.QD);       // k
-        add(2 * (size_t)d.NH * d.DV * Sp);       // v^T hi
-        add(2 * (size_t)d.NH * d.DV * Sp);       // v^T lo
+        add(2 * (size_t)d.NH * Sp * d.QD);       // k hi
+        add(2 * (size_t)d.NH * Sp * d.QD);       // k lo
+        add(2 * (size_t)d.NH * d.DV * Sp);       // v^T
         add(2 * (size_t)S * d.HO);               // heads hi
         add(2 * (size_t)S * d.HO);               // heads lo
     } else {
@@ -870,14 +856,14 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
         float *ykva = (float *)take(4 * (size_t)S * d.KVO);
         uint16_t *lath = (uint16_t *)take(2 * (size_t)S * d.R);
         uint16_t *latl = (uint16_t *)take(2 * (size_t)S * d.R);
-        uint16_t *qh = (uint16_t *)take(2 * (size_t)d.NH * Sp * d.QD);
-        uint16_t *ql = (uint16_t *)take(2 * (size_t)d.NH * Sp * d.QD);
-        uint16_t *kb = (uint16_t *)take(2 * (size_t)d.NH * Sp * d.QD);
-        uint16_t *vh = (uint16_t *)take(2 * (size_t)d.NH * d.DV * Sp);
-        uint16_t *vl = (uint16_t *)take(2 * (size_t)d.NH * d.DV * Sp);
+        _Float16 *qh = (_Float16 *)take(2 * (size_t)d.NH * Sp * d.QD);
+        _Float16 *ql = (_Float16 *)take(2 * (size_t)d.NH * Sp * d.QD);
+        _Float16 *kh = (_Float16 *)take(2 * (size_t)d.NH * Sp * d.QD);
+        _Float16 *kl = (_Float16 *)take(2 * (size_t)d.NH * Sp * d.QD);
+        _Float16 *vt = (_Float16 *)take(2 * (size_t)d.NH * d.DV * Sp);
         uint16_t *oh = (uint16_t *)take(2 * (size_t)S * d.HO);
         uint16_t *ol = (uint16_t *)take(2 * (size_t)S * d.HO);
-        const GemmEpi ep{qh, ql, kb, vh, vl, cs, Sp, d.DN, d.DR, d.DV};
+        const GemmEpi ep{qh, ql, kh, kl, vt, cs, Sp, d.DN, d.DR, d.DV};
         hipLaunchKernelGGL(k_zero_int, dim3(1), dim3(64), 0, st, flags, 8);
         const int split_blocks = (int)std::min<size_t>(2048, ((size_t)S * d.H / 8 + 255) / 256);
         hipLaunchKernelGGL(k_split, dim3(split_blocks), dim3(256), 0, st, x, d.H, xh, xl, d.H, S, d.H, flags + 0);
@@ -886,14 +872,14 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
         if ((e = gemm<kEpiQ>(st, xh, xl, flags + 0, d.H, wq, d.QO, wkva, d.KVO, d.H, ykva, d.KVO, S, d.H,
                              ep)) != hipSuccess)
             return e;
-        KvaPackArgs ka{ykva, wnorm, cs, lath, latl, qh, ql, kb, vh, vl, S, Sp, d.NH, d.KVO, d.R, d.DN, d.DR, d.DV, eps};
+        KvaPackArgs ka{ykva, wnorm, cs, lath, latl, qh, ql, kh, kl, vt, S, Sp, d.NH, d.KVO, d.R, d.DN, d.DR, d.DV, eps};
         hipLaunchKernelGGL(k_kva_pack, dim3((Sp + 3) / 4), dim3(256), 0, st, ka);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // kv_b (-> K nope part, V^T hi/lo)
         if ((e = gemm<kEpiKV>(st, lath, latl, nullptr, d.R, wkvb, d.KVB, nullptr, 0, d.R, nullptr, 0, S, d.R,
                               ep)) != hipSuccess)
             return e;
-        FlashArgs fa{qh, ql, kb, vh, vl, oh, ol, S, Sp, d.NH, d.HO, smscale * 1.4426950408889634f};
+        FlashArgs fa{qh, ql, kh, kl, vt, oh, ol, S, Sp, d.NH, d.HO, smscale * 1.4426950408889634f};
         hipLaunchKernelGGL(k_flash_prefill, dim3(Sp / kFQ * d.NH), dim3(256), 0, st, fa);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // attention outputs are never bf16-exact: the lo pass always runs (no flag)

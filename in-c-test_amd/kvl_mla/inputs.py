@@ -95,11 +95,12 @@ class Layer:
                               abi.ptr(self.o_proj, u16))
 
 
-def make_layer(cfg, seed, std=0.02):
-    """Random-init layer: matrices bf16(N(0, std)), kv_a_norm bf16(1 + N(0, std))."""
+def make_layer(cfg, seed, std=0.02, q_std=None):
+    """Random-init layer: matrices bf16(N(0, std)), kv_a_norm bf16(1 + N(0, std)). q_std (default
+    std) scales q_proj alone: larger values give larger attention logits (sharper softmax)."""
     H, NH = cfg.hidden_size, cfg.num_heads
     DN, DR, DV, R = cfg.qk_nope_dim, cfg.qk_rope_dim, cfg.v_head_dim, cfg.kv_lora_rank
-    return Layer(q_proj=normal_bf16(seed, "q_proj", (NH * (DN + DR), H), std=std),
+    return Layer(q_proj=normal_bf16(seed, "q_proj", (NH * (DN + DR), H), std=std if q_std is None else q_std),
                  kv_a_proj=normal_bf16(seed, "kv_a", (R + DR, H), std=std),
                  kv_a_norm=normal_bf16(seed, "kv_norm", (R,), mean=1.0, std=std),
                  kv_b_proj=normal_bf16(seed, "kv_b", (NH * (DN + DV), R), std=std),
