@@ -28,9 +28,9 @@ LAB = dict(hidden_size=64, num_heads=4, qk_nope_dim=8, qk_rope_dim=8, v_head_dim
 KIMI = dict(inputs.KIMI)
 
 
-def model(d, seed, std=0.02, n=8, xstd=1.0):
+def model(d, seed, std=0.02, n=8, xstd=1.0, q_std=None):
     cfg = inputs.config(**d)
-    layer = inputs.make_layer(cfg, seed, std=std)
+    layer = inputs.make_layer(cfg, seed, std=std, q_std=q_std)
     x = (inputs.hidden(cfg, seed, n) * np.float32(xstd)).astype(np.float32)
     return cfg, layer, x
 
@@ -143,6 +143,39 @@ def test_decode_sequence_matches_oracle(name, dims, std, S, kind):
         b, sb = decode_seq(O, kind, cfg, w, x, prefix=prefix)
         assert rel_err(a, b) <= TOL, (prefix, rel_err(a, b))
         compare_states(kind, sa, sb)
+
+
+@pytest.mark.parametrize("kind", ["exp", "f32", "q8"])
+def test_decode_sharp_attention(kind):
+    """Large attention logits (q_proj std 8x the other weights): pins the precision of the
+    score products, whose rounding the logit size amplifies."""
+    print(f"[decode] kimi sharp kind={kind}", flush=True)
+    cfg, layer, x = model(KIMI, 13, n=48, q_std=0.16)
+    w = layer.struct()
+    prefix = 0 if kind == "exp" else 24
+    a, sa = decode_seq(G, kind, cfg, w, x, prefix=prefix)
+    b, sb = decode_seq(O, kind, cfg, w, x, prefix=prefix)
+    print(f"[decode]   max|d|/max|ref| = {rel_err(a, b):.3e}", flush=True)
+    assert rel_err(a, b) <= TOL, rel_err(a, b)
+    compare_states(kind, sa, sb)
+
+
+def test_q8_decode_sharp_8192():
+    """Large logits over a long Q8 history (split-K partials with widely different maxima)."""
+    cfg, layer, _ = model(KIMI, 0xC5, q_std=0.16)
+    w = layer.struct()
+    n = 8192
+    lat, rope = rand_rows(0xC5, n, 512, 64)
+    x = inputs.hidden(cfg, 0xC5, 1, tag="query")[0]
+    outs = []
+    for api in (G, O):
+        st = fill_q8_state(api, cfg, lat, rope, n + 1)
+        out = np.zeros(cfg.hidden_size, np.float32)
+        assert api.mla_decode_compressed_q8_bf16(f32(out), f32(x), n, C.byref(cfg), C.byref(w), C.byref(st)) == 0
+        outs.append(out)
+        api.mla_compressed_q8_state_free(C.byref(st))
+    print(f"[decode]   max|d|/max|ref| = {rel_err(outs[0], outs[1]):.3e}", flush=True)
+    assert rel_err(outs[0], outs[1]) <= TOL, rel_err(outs[0], outs[1])
 
 
 def test_errors_leave_state_unchanged():
