@@ -125,9 +125,15 @@ hipError_t launch_copy(hipStream_t st, void *dst, const void *src, size_t bytes)
 size_t prefill_bytes(const Dims &d, int S);
 // Causal MLA prefill of S tokens: x [S,H] -> out [S,H] (device pointers), ws of
 // prefill_bytes(d, S) bytes, rope_cs table covering positions [0, S).
+// wo16: o_proj converted to fp16 (launch_bf16_to_f16), used by the MFMA route (the attention
+// output enters the o_proj GEMM as fp16).
 hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, const float *x,
                               float *out, const uint16_t *wq, const uint16_t *wkva,
                               const uint16_t *wnorm, const uint16_t *wkvb, const uint16_t *wo,
-                              const float2 *rope_cs, void *ws);
+                              const _Float16 *wo16, const float2 *rope_cs, void *ws);
+// True when the prefill of these dims takes the MFMA route (needs the fp16 o_proj copy).
+bool prefill_mfma_shape(const Dims &d);
+// dst[i] = (fp16) bf16 src[i]: exact for |x| >= 2^-17 (bf16 has 8 significant bits).
+hipError_t launch_bf16_to_f16(hipStream_t st, _Float16 *dst, const uint16_t *src, size_t n);
 
 }  // namespace kvl

@@ -9,7 +9,7 @@
 //   kva_pack  RMSNorm -> latent (hi/lo bf16), RoPE(k_rope) -> rope part of K (hi/lo fp16)
 //   gemm      kv = latent . kv_b^T           epilogue: k_nope -> K (hi/lo fp16), V^T (fp16)
 //   flash     causal attention per (128-query tile, head), online softmax
-//   gemm      out = heads . o_proj^T
+//   gemm      out = heads . o_proj^T          (fp16 heads and fp16 copy of o_proj, one pass)
 // Generic route (any shape): the same stages with VALU kernels.
 #include "mla_device.h"
 #include "mla_internal.h"
@@ -58,25 +58,28 @@ __global__ void k_zero_int(int *p, int n) {
 // columns of C may come from two weight matrices (B0 for n < N0, B1 for the N1 after it),
 // so the q and kv_a projections of the same tokens run as one launch.
 //
-// Block tile 256 x BN (BN = 256 or 128), k step 32, eight waves (2 per SIMD) in a WM x WN
-// grid, each owning a (256 / WM) x (BN / WN) quadrant of v_mfma_f32_16x16x32_bf16 tiles.
-// Large tiles keep the L2 traffic at 24-32 bytes per clock per CU at the MFMA rate. A hi,
-// A lo and B stream into a 3-stage LDS ring by global_load_lds_dwordx4 DMA (two stages in
-// flight while one is computed). LDS rows are 64 bytes (4 slots of 16 B); slot s of row r
-// sits at s ^ ((r >> 1) & 3), which spreads the 8 rows one ds_read_b128 phase touches over
-// distinct banks. The lo pass runs when Al is given and either no flag is given or
-// *lo_flag != 0 (the flag is raised by the producer of Al when some lo word is non-zero).
-// Requires K % 32 == 0, lda and ldb multiples of 8 (16-byte rows).
-constexpr int kGBm = 256, kGBk = 32, kGStages = 3;
-constexpr int kGRowB = kGBk * 2;                 // 64-byte LDS rows
+// Block tile 256 x BN (BN = 256 or 128), eight waves (2 per SIMD) in a WM x WN grid, each
+// owning a (256 / WM) x (BN / WN) quadrant of v_mfma_f32_16x16x32 tiles. Large tiles keep
+// the L2 traffic at 24-32 bytes per clock per CU at the MFMA rate. A hi, A lo and B stream
+// into an LDS ring of 3 stages (2 where 3 do not fit) by global_load_lds_dwordx4 DMA (the
+// later stages in flight while one is computed). With a lo operand possible (LOK) the k step is 32 (64-byte LDS rows, slot s of
+// row r at s ^ ((r >> 1) & 3)); without, the ring has room for a k step of 64 (128-byte
+// rows, slot s at s ^ (r & 7)), twice the MFMAs per barrier. Either swizzle spreads the 8
+// rows one ds_read_b128 phase touches over distinct banks. The lo pass runs when Al is
+// given and either no flag is given or *lo_flag != 0 (the flag is raised by the producer
+// of Al when some lo word is non-zero). Requires K % BK == 0, lda and ldb multiples of 8.
+constexpr int kGBm = 256;
 
-template <int BN>
+template <int BN, bool LOK>
 struct GemmShape {
+    static constexpr int BK = LOK ? 32 : 64, RowB = BK * 2, Spr = BK / 8;  // slots per row
     static constexpr int WM = BN == 256 ? 2 : 4, WN = 8 / WM;
     static constexpr int TM = kGBm / WM / 16, TN = BN / WN / 16;  // 16x16 tiles per wave
-    static constexpr int ATile = kGBm * kGRowB, BTile = BN * kGRowB;
-    static constexpr int Stage = 2 * ATile + BTile;
-    static constexpr int Smem = kGStages * Stage;
+    static constexpr int ATile = kGBm * RowB, BTile = BN * RowB;
+    static constexpr int Stage = (LOK ? 2 : 1) * ATile + BTile;
+    static constexpr int Stages = (160 * 1024) / Stage >= 3 ? 3 : 2;  // ring depth that fits
+    static constexpr int Smem = Stages * Stage;
+    __device__ static int swz(int row) { return LOK ? (row >> 1) & 3 : row & 7; }
 };
 
 struct GemmArgs {
@@ -102,11 +105,17 @@ struct GemmEpi {
 // lane group g of the flash kernel holds for one PV chunk are 4g .. 4g+3 and 16+4g .. 16+4g+3.
 __host__ __device__ __forceinline__ int vt_perm(int k) { return 8 * ((k & 15) >> 2) + 4 * (k >> 4) + (k & 3); }
 
-__device__ __forceinline__ int g_swz(int row) { return (row >> 1) & 3; }
+// F16: the 16-bit operands are fp16 (v_mfma_f32_16x16x32_f16) instead of bf16.
+template <bool F16>
+__device__ __forceinline__ v4f mfma16(const v8bf &a, const v8bf &b, const v4f &c) {
+    if constexpr (F16) return mfma_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c);
+    else return mfma_bf16(a, b, c);
+}
 
-template <int BN, int EPI>
-__global__ __launch_bounds__(512) void k_gemm_bf16(GemmArgs a, GemmEpi e) {
-    using Sh = GemmShape<BN>;
+template <int BN, int EPI, bool F16, bool LOK>
+__global__ __launch_bounds__(512) void k_gemm16(GemmArgs a, GemmEpi e) {
+    using Sh = GemmShape<BN, LOK>;
+    constexpr int BK = Sh::BK, RowB = Sh::RowB, Spr = Sh::Spr;
     constexpr int TM = Sh::TM, TN = Sh::TN;
     __shared__ __attribute__((aligned(16))) uint8_t smem[Sh::Smem];
     const uint32_t sbase = lds_addr(smem);
@@ -127,21 +136,21 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmArgs a, GemmEpi e) {
     const int nb0 = seg1 ? (nt - tn0) * BN : nt * BN;  // first row of B in this tile
     const int c0 = seg1 ? N0 + nb0 : nb0;              // first column of C
     const int m0 = mt * kGBm;
-    const bool use_lo = a.Al && (!a.lo_flag || *a.lo_flag);
+    const bool use_lo = LOK && a.Al && (!a.lo_flag || *a.lo_flag);
 
-    // DMA: thread (w, l), instruction i fills slot (8i + w) * 64 + l of a tile: row p >> 2,
-    // physical slot p & 3 holding logical slot (p & 3) ^ g_swz(row). Rows past the end of A
+    // DMA: thread (w, l), instruction i fills slot (8i + w) * 64 + l of a tile: row p / Spr,
+    // physical slot p % Spr holding logical slot (p % Spr) ^ swz(row). Rows past the end of A
     // or B are clamped to the last row (their results are never stored).
     constexpr int NA = Sh::ATile / 8192, NB = Sh::BTile / 8192;  // instructions per thread
     uint32_t aoff[NA], boff[NB];
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
-        const int p = (8 * i + w) * 64 + l, row = p >> 2, s = (p & 3) ^ g_swz(row);
+        const int p = (8 * i + w) * 64 + l, row = p / Spr, s = (p % Spr) ^ Sh::swz(row);
         aoff[i] = (uint32_t)(min(m0 + row, M - 1) - m0) * lda * 2 + 16 * s;
     }
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-        const int p = (8 * i + w) * 64 + l, row = p >> 2, s = (p & 3) ^ g_swz(row);
+        const int p = (8 * i + w) * 64 + l, row = p / Spr, s = (p % Spr) ^ Sh::swz(row);
         boff[i] = (uint32_t)(min(nb0 + row, Nseg - 1) - nb0) * ldb * 2 + 16 * s;
     }
     const uint8_t *gah = (const uint8_t *)(a.Ah + (size_t)m0 * lda);
@@ -149,7 +158,7 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmArgs a, GemmEpi e) {
     const uint8_t *gb = (const uint8_t *)(B + (size_t)nb0 * ldb);
     auto issue = [&](int kt, int stage) __attribute__((always_inline)) {
         const uint32_t dst = sbase + stage * Sh::Stage + (uint32_t)w * 1024;
-        const size_t ko = (size_t)kt * kGBk * 2;
+        const size_t ko = (size_t)kt * BK * 2;
 #pragma unroll
         for (int i = 0; i < NA; ++i) dma_b128(gah + ko + aoff[i], dst + i * 8192);
         if (use_lo) {
@@ -157,10 +166,12 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmArgs a, GemmEpi e) {
             for (int i = 0; i < NA; ++i) dma_b128(gal + ko + aoff[i], dst + Sh::ATile + i * 8192);
         }
 #pragma unroll
-        for (int i = 0; i < NB; ++i) dma_b128(gb + ko + boff[i], dst + 2 * Sh::ATile + i * 8192);
+        for (int i = 0; i < NB; ++i) dma_b128(gb + ko + boff[i], dst + (LOK ? 2 : 1) * Sh::ATile + i * 8192);
     };
-    // fragment rows 16 * tile + n (n & 7 = row & 7), logical slot g
-    const int frd = n * kGRowB + 16 * (g ^ g_swz(n));
+    // fragment rows 16 * tile + n (n & 7 = row & 7), logical slot 4 ks + g of k-sub ks
+    int frd[BK / 32];
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) frd[ks] = n * RowB + 16 * ((4 * ks + g) ^ Sh::swz(n));
 
     v4f acc[TM][TN];
 #pragma unroll
@@ -168,37 +179,42 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmArgs a, GemmEpi e) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    const int nk = K / kGBk;
-    issue(0, 0);
-    if (nk > 1) issue(1, 1);
+    constexpr int NS = Sh::Stages;
+    const int nk = K / BK;
+#pragma unroll
+    for (int q = 0; q < NS - 1; ++q)
+        if (q < nk) issue(q, q);
     for (int kt = 0; kt < nk; ++kt) {
-        // stage kt has landed when at most one later stage is still in flight
-        if (kt + 1 < nk) {
+        // stage kt has landed when at most min(NS - 2, nk - 1 - kt) later stages are in flight
+        if (NS == 3 && kt + 1 < nk) {
             if (use_lo) wait_vmcnt<2 * NA + NB>();
             else wait_vmcnt<NA + NB>();
         } else {
             wait_vmcnt<0>();
         }
-        lds_barrier();
-        if (kt + 2 < nk) issue(kt + 2, (kt + 2) % kGStages);
-        const uint8_t *st = smem + (kt % kGStages) * Sh::Stage;
-        const uint8_t *sa = st + wm * (TM * 16) * kGRowB + frd;
-        const uint8_t *sb = st + 2 * Sh::ATile + wn * (TN * 16) * kGRowB + frd;
-        v8bf bo[TN];
+        lds_barrier();  // also: every wave is done with stage kt - 1, whose slot is refilled next
+        if (kt + NS - 1 < nk) issue(kt + NS - 1, (kt + NS - 1) % NS);
+        const uint8_t *st = smem + (kt % NS) * Sh::Stage;
 #pragma unroll
-        for (int j = 0; j < TN; ++j) bo[j] = *(const v8bf *)(sb + j * 16 * kGRowB);
+        for (int ks = 0; ks < BK / 32; ++ks) {
+            const uint8_t *sa = st + wm * (TM * 16) * RowB + frd[ks];
+            const uint8_t *sb = st + (LOK ? 2 : 1) * Sh::ATile + wn * (TN * 16) * RowB + frd[ks];
+            v8bf bo[TN];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            const v8bf ah = *(const v8bf *)(sa + i * 16 * kGRowB);
-#pragma unroll
-            for (int j = 0; j < TN; ++j) acc[i][j] = mfma_bf16(ah, bo[j], acc[i][j]);
-        }
-        if (use_lo) {
+            for (int j = 0; j < TN; ++j) bo[j] = *(const v8bf *)(sb + j * 16 * RowB);
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
-                const v8bf al = *(const v8bf *)(sa + Sh::ATile + i * 16 * kGRowB);
+                const v8bf ah = *(const v8bf *)(sa + i * 16 * RowB);
 #pragma unroll
-                for (int j = 0; j < TN; ++j) acc[i][j] = mfma_bf16(al, bo[j], acc[i][j]);
+                for (int j = 0; j < TN; ++j) acc[i][j] = mfma16<F16>(ah, bo[j], acc[i][j]);
+            }
+            if (use_lo) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    const v8bf al = *(const v8bf *)(sa + Sh::ATile + i * 16 * RowB);
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) acc[i][j] = mfma16<F16>(al, bo[j], acc[i][j]);
+                }
             }
         }
     }
@@ -304,7 +320,7 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmArgs a, GemmEpi e) {
 
 // C = A . [B0; B1]^T with N0 + N1 output columns (N1 = 0: a single weight matrix). The
 // 256 x 256 tile is used when it still gives one tile per CU, else 256 x 128.
-template <int EPI>
+template <int EPI, bool F16 = false>
 static hipError_t gemm(hipStream_t st, const uint16_t *Ah, const uint16_t *Al, const int *flag,
                        int lda, const uint16_t *B0, int N0, const uint16_t *B1, int N1, int ldb,
                        float *C, int ldc, int M, int K, const GemmEpi &e) {
@@ -312,8 +328,14 @@ static hipError_t gemm(hipStream_t st, const uint16_t *Ah, const uint16_t *Al, c
     const int tm = (M + kGBm - 1) / kGBm;
     const int t256 = tm * ((N0 + 255) / 256 + (N1 + 255) / 256);
     const int t128 = tm * ((N0 + 127) / 128 + (N1 + 127) / 128);
-    if (t256 >= 224) hipLaunchKernelGGL((k_gemm_bf16<256, EPI>), dim3(t256), dim3(512), 0, st, a, e);
-    else hipLaunchKernelGGL((k_gemm_bf16<128, EPI>), dim3(t128), dim3(512), 0, st, a, e);
+    if (Al) {
+        if (t256 >= 224) hipLaunchKernelGGL((k_gemm16<256, EPI, F16, true>), dim3(t256), dim3(512), 0, st, a, e);
+        else hipLaunchKernelGGL((k_gemm16<128, EPI, F16, true>), dim3(t128), dim3(512), 0, st, a, e);
+    } else {
+        if (K % 64) return hipErrorInvalidValue;
+        if (t256 >= 224) hipLaunchKernelGGL((k_gemm16<256, EPI, F16, false>), dim3(t256), dim3(512), 0, st, a, e);
+        else hipLaunchKernelGGL((k_gemm16<128, EPI, F16, false>), dim3(t128), dim3(512), 0, st, a, e);
+    }
     return hipGetLastError();
 }
 
@@ -471,7 +493,7 @@ constexpr float kFLazy = 8.0f;       // log2 headroom of the lazy max
 
 struct FlashArgs {
     const _Float16 *qh, *ql, *kh, *kl, *vt;  // Q, K: [NH, Sp, 192]; V^T: [NH, 128, Sp]
-    uint16_t *oh, *ol;                       // [S, ldo] hi/lo bf16
+    _Float16 *o;                             // [S, ldo] fp16 (input of the o_proj GEMM)
     int S, Sp, NH, ldo;
     float sl2;                               // softmax scale * log2(e)
 };
@@ -693,16 +715,11 @@ void k_flash_prefill(FlashArgs a) {
         const int q = qw + 16 * u + n;
         const float inv = 1.0f / xrow_sum(l_run[u]);
         if (q >= S) continue;
-        uint16_t *oh = a.oh + (size_t)q * ldo + (size_t)h * 128 + 4 * g;
-        uint16_t *ol = a.ol + (size_t)q * ldo + (size_t)h * 128 + 4 * g;
+        _Float16 *o = a.o + (size_t)q * ldo + (size_t)h * 128 + 4 * g;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-            uint16_t hh[4], ll[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) split_bf16(acc[dt][u][i] * inv, hh[i], ll[i]);
-            *(uint2 *)(oh + 16 * dt) = make_uint2(pack2(hh[0], hh[1]), pack2(hh[2], hh[3]));
-            *(uint2 *)(ol + 16 * dt) = make_uint2(pack2(ll[0], ll[1]), pack2(ll[2], ll[3]));
-        }
+        for (int dt = 0; dt < 8; ++dt)
+            *(v4h *)(o + 16 * dt) = v4h{(_Float16)(acc[dt][u][0] * inv), (_Float16)(acc[dt][u][1] * inv),
+                                        (_Float16)(acc[dt][u][2] * inv), (_Float16)(acc[dt][u][3] * inv)};
     }
 }
 
@@ -798,6 +815,17 @@ hipError_t launch_gemv(hipStream_t st, float *Y, int ldy, const float *X, int ld
                        const uint16_t *W0, int out0, const uint16_t *W1, int out1, int in,
                        bool accumulate);
 
+__global__ __launch_bounds__(256) void k_bf16_to_f16(_Float16 *dst, const uint16_t *src, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        dst[i] = (_Float16)bf16_to_f32(src[i]);
+}
+
+hipError_t launch_bf16_to_f16(hipStream_t st, _Float16 *dst, const uint16_t *src, size_t n) {
+    const int blocks = (int)std::min<size_t>(4096, (n + 255) / 256);
+    hipLaunchKernelGGL(k_bf16_to_f16, dim3(blocks), dim3(256), 0, st, dst, src, n);
+    return hipGetLastError();
+}
+
 bool prefill_mfma_shape(const Dims &d) {
     return d.H % 32 == 0 && d.R % 32 == 0 && d.QD == 192 && d.DV == 128 && d.HO % 32 == 0 &&
            d.DN % 8 == 0;
@@ -819,8 +847,7 @@ size_t prefill_bytes(const Dims &d, int S) {
         add(2 * (size_t)d.NH * Sp * d.QD);       // k hi
         add(2 * (size_t)d.NH * Sp * d.QD);       // k lo
         add(2 * (size_t)d.NH * d.DV * Sp);       // v^T
-        add(2 * (size_t)S * d.HO);               // heads hi
-        add(2 * (size_t)S * d.HO);               // heads lo
+        add(2 * (size_t)S * d.HO);               // heads (fp16)
     } else {
         add(4 * (size_t)S * (d.QO + d.KVO));
         add(4 * (size_t)S * d.R);
@@ -836,7 +863,7 @@ size_t prefill_bytes(const Dims &d, int S) {
 hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, const float *x,
                               float *out, const uint16_t *wq, const uint16_t *wkva,
                               const uint16_t *wnorm, const uint16_t *wkvb, const uint16_t *wo,
-                              const float2 *cs, void *ws) {
+                              const _Float16 *wo16, const float2 *cs, void *ws) {
     const int Sp = (S + 127) / 128 * 128;
     char *base = (char *)ws;
     size_t off = 0;
@@ -861,8 +888,7 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
         _Float16 *kh = (_Float16 *)take(2 * (size_t)d.NH * Sp * d.QD);
         _Float16 *kl = (_Float16 *)take(2 * (size_t)d.NH * Sp * d.QD);
         _Float16 *vt = (_Float16 *)take(2 * (size_t)d.NH * d.DV * Sp);
-        uint16_t *oh = (uint16_t *)take(2 * (size_t)S * d.HO);
-        uint16_t *ol = (uint16_t *)take(2 * (size_t)S * d.HO);
+        _Float16 *heads = (_Float16 *)take(2 * (size_t)S * d.HO);
         const GemmEpi ep{qh, ql, kh, kl, vt, cs, Sp, d.DN, d.DR, d.DV};
         hipLaunchKernelGGL(k_zero_int, dim3(1), dim3(64), 0, st, flags, 8);
         const int split_blocks = (int)std::min<size_t>(2048, ((size_t)S * d.H / 8 + 255) / 256);
@@ -879,12 +905,13 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
         if ((e = gemm<kEpiKV>(st, lath, latl, nullptr, d.R, wkvb, d.KVB, nullptr, 0, d.R, nullptr, 0, S, d.R,
                               ep)) != hipSuccess)
             return e;
-        FlashArgs fa{qh, ql, kh, kl, vt, oh, ol, S, Sp, d.NH, d.HO, smscale * 1.4426950408889634f};
+        FlashArgs fa{qh, ql, kh, kl, vt, heads, S, Sp, d.NH, d.HO, smscale * 1.4426950408889634f};
         hipLaunchKernelGGL(k_flash_prefill, dim3(Sp / kFQ * d.NH), dim3(256), 0, st, fa);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        // attention outputs are never bf16-exact: the lo pass always runs (no flag)
-        if ((e = gemm<kEpiPlain>(st, oh, ol, nullptr, d.HO, wo, d.H, nullptr, 0, d.HO, out, d.H, S, d.HO, ep)) !=
-            hipSuccess)
+        // out = heads . o_proj^T in fp16 (heads rounded once, o_proj converted exactly)
+        if (!wo16) return hipErrorInvalidValue;
+        if ((e = gemm<kEpiPlain, true>(st, (const uint16_t *)heads, nullptr, nullptr, d.HO, (const uint16_t *)wo16,
+                                       d.H, nullptr, 0, d.HO, out, d.H, S, d.HO, ep)) != hipSuccess)
             return e;
         return hipSuccess;
     }

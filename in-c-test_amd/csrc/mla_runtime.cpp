@@ -116,6 +116,8 @@ struct WeightEntry {
     size_t bytes = 0;
     uint64_t digest = 0;
     void *dev = nullptr;
+    void *dev16 = nullptr;  // fp16 copy (prefill o_proj), valid when f16_ok
+    bool f16_ok = false;
     int pins = 0;
 };
 
@@ -284,11 +286,35 @@ int dev_weight(const uint16_t *host, size_t elems, const uint16_t **out) {
         }
     }
     if (!e.dev) HIP_TRY(hipMalloc(&e.dev, bytes));
+    if (e.dev16 && e.bytes != bytes) {
+        HIP_TRY(hipFree(e.dev16));
+        e.dev16 = nullptr;
+    }
     e.bytes = bytes;
+    e.f16_ok = false;
     HIP_TRY(hipMemcpy(e.dev, host, bytes, hipMemcpyHostToDevice));
     e.digest = sample_digest(host, bytes);
     c.weights[host] = e;
     *out = (const uint16_t *)e.dev;
+    return 0;
+}
+
+// fp16 copy of a weight array (converted on the device from its bf16 copy, stream-ordered).
+int dev_weight_f16(const uint16_t *host, size_t elems, const _Float16 **out) {
+    Ctx &c = ctx();
+    const uint16_t *d16;
+    if (dev_weight(host, elems, &d16) != 0) return -1;
+    WeightEntry &e = c.weights[host];
+    if (!e.f16_ok) {
+        if (c.capturing) {
+            set_err("fp16 weight conversion during graph capture");
+            return -1;
+        }
+        if (!e.dev16) HIP_TRY(hipMalloc(&e.dev16, e.bytes));
+        HIP_TRY(launch_bf16_to_f16(c.stream, (_Float16 *)e.dev16, d16, elems));
+        e.f16_ok = true;
+    }
+    *out = (const _Float16 *)e.dev16;
     return 0;
 }
 
@@ -907,8 +933,10 @@ int prefill_device(float *d_out, const float *d_x, int S, const KvlMlaConfig *cf
         }
         if (dev_reserve(c.scores, bytes) != 0) return -1;
     }
+    const _Float16 *wo16 = nullptr;
+    if (prefill_mfma_shape(d) && dev_weight_f16(w->o_proj, (size_t)d.H * d.HO, &wo16) != 0) return -1;
     HIP_TRY(launch_prefill_all(c.stream, d, S, cfg->rms_eps, d_x, d_out, dw.q, dw.kva, dw.norm, dw.kvb,
-                               dw.o, cs, c.scores.p));
+                               dw.o, wo16, cs, c.scores.p));
     return 0;
 }
 
@@ -1262,6 +1290,7 @@ int kvl_mla_release_weights(const KvlMlaBF16 *w) {
         if (it->second.pins > 0) it->second.pins -= 1;
         if (it->second.pins == 0) {
             (void)hipFree(it->second.dev);
+            if (it->second.dev16) (void)hipFree(it->second.dev16);
             c.weights.erase(it);
         }
     }
