@@ -219,7 +219,7 @@ def main():
                    "bytes_per_step": step_bytes, "mode": "eager" if graph is None else "hip-graph"},
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
         "roofline": roofline,
-        "stages_ms_per_launch": {k: round(v["ms_per_launch"], 5) for k, v in stages.items()},
+        "stages_ms_per_launch": {k: round(v["ms_per_launch"], 5) for k, v in stages.items() if v["launches"]},
     }
 
     # ---- parity spot check + CPU baseline on layer 0 -------------------------------------

@@ -30,42 +30,37 @@ struct GemvArgs {
     int ldy, ldx, B, out0, out1, in, acc;
 };
 
-// 32 output rows per block (two 16-row MFMA tiles); wave w of 8 owns the k-eighth
-// [w*in/8, (w+1)*in/8). The weight tiles are the MFMA A operand (exact bf16), the batch of
-// activations the B operand as a hi/lo bf16 pair, so every product is exact and the
-// accumulation is fp32. All weight and activation loads of a wave are issued before the
-// first MFMA (the kernel is latency-bound at decode batch sizes). Up to 16 sequences per
-// block column (blockIdx.y). Requires in % 256 == 0 and 16-byte aligned rows.
-constexpr int kGvKb = 8;  // k-blocks of 32 per wave and pass
+constexpr int kGvKb = 8;  // k-blocks of 32 per wave and pass (at most)
 
-__global__ __launch_bounds__(512) void k_gemv_mfma(GemvArgs a) {
-    __shared__ v4f red[7][2][64];
+// 16 output rows per block (one 16-row MFMA tile); wave w of WAVES owns the k range
+// [w*in/WAVES, (w+1)*in/WAVES). Many small blocks keep every CU busy and many loads in
+// flight (the kernel is latency-bound at decode batch sizes). The weight rows are the MFMA
+// A operand (exact bf16), the batch of activations the B operand as a hi/lo bf16 pair, so
+// every product is exact and the accumulation is fp32. Up to 16 sequences per block column
+// (blockIdx.y). Requires in % (32 * WAVES) == 0 and 16-byte aligned rows.
+template <int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void k_gemv_mfma(GemvArgs a) {
+    __shared__ v4f red[WAVES][64];
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
     const int out = a.out0 + a.out1;
-    const int row0 = blockIdx.x * 32;
-    const uint16_t *wrow[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int row = row0 + 16 * t + n;
-        wrow[t] = row < a.out0 ? a.W0 + (size_t)row * a.in
-                  : row < out  ? a.W1 + (size_t)(row - a.out0) * a.in
-                               : nullptr;
-    }
+    const int row = blockIdx.x * 16 + n;
+    const uint16_t *wrow = row < a.out0 ? a.W0 + (size_t)row * a.in
+                           : row < out  ? a.W1 + (size_t)(row - a.out0) * a.in
+                                        : nullptr;
     const int b = blockIdx.y * 16 + n;
     const float *xrow = b < a.B ? a.X + (size_t)b * a.ldx : nullptr;
-    const int kw = a.in >> 3;
+    const int kw = a.in / WAVES;
     const int kbeg = w * kw;
-    v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
     for (int k0 = 0; k0 < kw; k0 += 32 * kGvKb) {
         const int nkb = min(kGvKb, (kw - k0) >> 5);
-        v4i wa[2][kGvKb];
+        v4i wa[kGvKb];
         v4f xa[kGvKb], xb[kGvKb];
 #pragma unroll
         for (int kb = 0; kb < kGvKb; ++kb) {
             if (kb < nkb) {
                 const int k = kbeg + k0 + kb * 32 + g * 8;
-#pragma unroll
-                for (int t = 0; t < 2; ++t) wa[t][kb] = wrow[t] ? *(const v4i *)(wrow[t] + k) : v4i{0, 0, 0, 0};
+                wa[kb] = wrow ? *(const v4i *)(wrow + k) : v4i{0, 0, 0, 0};
                 xa[kb] = xrow ? *(const v4f *)(xrow + k) : v4f{0.f, 0.f, 0.f, 0.f};
                 xb[kb] = xrow ? *(const v4f *)(xrow + k + 4) : v4f{0.f, 0.f, 0.f, 0.f};
             }
@@ -75,33 +70,24 @@ __global__ __launch_bounds__(512) void k_gemv_mfma(GemvArgs a) {
             if (kb < nkb) {
                 v8bf hi, lo;
                 split8(xa[kb], xb[kb], hi, lo);
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    const v8bf wv = __builtin_bit_cast(v8bf, wa[t][kb]);
-                    acc[t] = mfma_bf16(wv, hi, acc[t]);
-                    acc[t] = mfma_bf16(wv, lo, acc[t]);
-                }
+                const v8bf wv = __builtin_bit_cast(v8bf, wa[kb]);
+                acc = mfma_bf16(wv, hi, acc);
+                acc = mfma_bf16(wv, lo, acc);
             }
         }
     }
-    if (w > 0) {
-        red[w - 1][0][l] = acc[0];
-        red[w - 1][1][l] = acc[1];
-    }
+    red[w][l] = acc;
     __syncthreads();
     if (w == 0 && b < a.B) {
+        v4f s = red[0][l];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            v4f s = acc[t];
+        for (int q = 1; q < WAVES; ++q) s += red[q][l];
 #pragma unroll
-            for (int q = 0; q < 7; ++q) s += red[q][t][l];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = row0 + 16 * t + 4 * g + i;
-                if (r < out) {
-                    float *yp = a.Y + (size_t)b * a.ldy + r;
-                    *yp = a.acc ? *yp + s[i] : s[i];
-                }
+        for (int i = 0; i < 4; ++i) {
+            const int r = blockIdx.x * 16 + 4 * g + i;
+            if (r < out) {
+                float *yp = a.Y + (size_t)b * a.ldy + r;
+                *yp = a.acc ? *yp + s[i] : s[i];
             }
         }
     }
@@ -136,8 +122,9 @@ hipError_t launch_gemv(hipStream_t st, float *Y, int ldy, const float *X, int ld
     const bool aligned = (in % 256) == 0 && (ldx % 4) == 0 && ((uintptr_t)X % 16) == 0 &&
                          ((uintptr_t)W0 % 16) == 0 && (!W1 || ((uintptr_t)W1 % 16) == 0);
     if (aligned) {
-        dim3 grid((out + 31) / 32, (B + 15) / 16);
-        hipLaunchKernelGGL(k_gemv_mfma, grid, dim3(512), 0, st, a);
+        dim3 grid((out + 15) / 16, (B + 15) / 16);
+        if (in % 512 == 0) hipLaunchKernelGGL(k_gemv_mfma<16>, grid, dim3(1024), 0, st, a);
+        else hipLaunchKernelGGL(k_gemv_mfma<8>, grid, dim3(512), 0, st, a);
     } else {
         hipLaunchKernelGGL(k_gemv_generic, dim3((out + 3) / 4), dim3(256), 0, st, a);
     }
@@ -150,9 +137,9 @@ constexpr int kMaxR = 1024;   // kv_lora_rank bound of the device kernels
 constexpr int kMaxDR = 256;   // qk_rope_dim bound
 constexpr int kMaxDN = 512;   // qk_nope_dim bound
 
+// The sequence table and dims are separate kernel arguments (one copy serves the fused
+// append + qprep launch).
 struct AppendArgs {
-    SeqTable t;
-    Dims d;
     const float *y;
     const uint16_t *norm;
     const float2 *cs;
@@ -168,13 +155,13 @@ struct AppendArgs {
 // (absmax/127, inv = 1/scale, roundf, clamp) and the RoPE rotation of
 // src/mla_compressed_q8_state.c:18-32 with host-computed (cos, sin) pairs. The library is
 // compiled with -ffp-contract=off, so each product and sum rounds separately as there.
-__global__ __launch_bounds__(256) void k_append(AppendArgs a) {
+__device__ __forceinline__ void append_body(const SeqTable &t, const Dims &d, const AppendArgs &a, int b) {
     __shared__ float lat[kMaxR];
     __shared__ double redd[256];
     __shared__ float redf[256];
-    const int tid = threadIdx.x, b = blockIdx.x;
-    const SeqDesc &s = a.t.s[a.rows_mode ? 0 : b];
-    const int R = a.d.R, DR = a.d.DR, half = DR / 2, pos = s.pos + (a.rows_mode ? b : 0);
+    const int tid = threadIdx.x;
+    const SeqDesc &s = t.s[a.rows_mode ? 0 : b];
+    const int R = d.R, DR = d.DR, half = DR / 2, pos = s.pos + (a.rows_mode ? b : 0);
     const float *kat = a.y + (size_t)b * a.ldy + a.koff;
 
     if (!a.normed) {
@@ -271,14 +258,14 @@ __global__ __launch_bounds__(256) void k_append(AppendArgs a) {
     }
 }
 
-hipError_t launch_append(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
-                         const float *y, int ldy, int koff, const uint16_t *kv_a_norm,
-                         float eps, const float2 *rope_cs, const DecodeWork &w, bool normed,
-                         int nrows) {
-    if (d.R > kMaxR || d.DR > kMaxDR) return hipErrorInvalidValue;
+__global__ __launch_bounds__(256) void k_append(SeqTable t, Dims d, AppendArgs a) {
+    append_body(t, d, a, blockIdx.x);
+}
+
+static AppendArgs append_args(int fmt, const Dims &d, const float *y, int ldy, int koff,
+                              const uint16_t *kv_a_norm, float eps, const float2 *rope_cs,
+                              const DecodeWork &w, bool normed, int nrows) {
     AppendArgs a;
-    a.t = t;
-    a.d = d;
     a.y = y;
     a.norm = kv_a_norm;
     a.cs = rope_cs;
@@ -293,7 +280,16 @@ hipError_t launch_append(hipStream_t st, int fmt, const SeqTable &t, const Dims 
                                    : 4 * d.NH * (d.QD + d.DV);
     a.eps = eps;
     a.rows_mode = nrows > 0 ? 1 : 0;
-    hipLaunchKernelGGL(k_append, dim3(nrows > 0 ? nrows : t.n), dim3(256), 0, st, a);
+    return a;
+}
+
+hipError_t launch_append(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
+                         const float *y, int ldy, int koff, const uint16_t *kv_a_norm,
+                         float eps, const float2 *rope_cs, const DecodeWork &w, bool normed,
+                         int nrows) {
+    if (d.R > kMaxR || d.DR > kMaxDR) return hipErrorInvalidValue;
+    const AppendArgs a = append_args(fmt, d, y, ldy, koff, kv_a_norm, eps, rope_cs, w, normed, nrows);
+    hipLaunchKernelGGL(k_append, dim3(nrows > 0 ? nrows : t.n), dim3(256), 0, st, t, d, a);
     return hipGetLastError();
 }
 
@@ -378,8 +374,6 @@ hipError_t launch_store_expanded(hipStream_t st, const SeqTable &t, const Dims &
 // ================================================================ query prep ===========
 
 struct QprepArgs {
-    SeqTable t;
-    Dims d;
     const float *y;
     const uint16_t *kv_b;
     const float2 *cs;
@@ -394,13 +388,12 @@ struct QprepArgs {
 // kv_b[h*(DN+DV)+d, r] * q_nope[d] (src/mla_compressed_q8_state.c:206-214), q_rope rotated
 // at the decode position; qf row = [q_lat | q_rope]. Expanded: qf row = [q_nope | q_rope].
 // With `quantize`, q_lat ~= qs * (hi + lo/128) (int8 hi, lo) and q_rope = hi + lo (bf16).
-__global__ __launch_bounds__(256) void k_qprep(QprepArgs a) {
+__device__ __forceinline__ void qprep_body(const SeqTable &t, const Dims &d, const QprepArgs &a, int blk) {
     __shared__ float qn[kMaxDN];
     __shared__ float ql[kMaxR];
     __shared__ float redf[256];
-    const Dims &d = a.d;
-    const int b = blockIdx.x / d.NH, h = blockIdx.x % d.NH, tid = threadIdx.x;
-    const SeqDesc &s = a.t.s[b];
+    const int b = blk / d.NH, h = blk % d.NH, tid = threadIdx.x;
+    const SeqDesc &s = t.s[b];
     const float *qh = a.y + (size_t)b * a.ldy + (size_t)h * d.QD;
     const int half = d.DR / 2;
     for (int i = tid; i < d.DN; i += 256) qn[i] = qh[i];
@@ -521,13 +514,20 @@ __global__ __launch_bounds__(256) void k_qprep(QprepArgs a) {
     if (tid == 0) a.qs[(size_t)b * d.NH + h] = ok ? amax / 127.0f : 0.f;
 }
 
-hipError_t launch_qprep(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
-                        const uint16_t *kv_b, const float2 *rope_cs, const DecodeWork &w,
-                        bool quantize) {
-    if (d.R > kMaxR || d.DN > kMaxDN || d.DR > kMaxDR) return hipErrorInvalidValue;
+__global__ __launch_bounds__(256) void k_qprep(SeqTable t, Dims d, QprepArgs a) {
+    qprep_body(t, d, a, blockIdx.x);
+}
+
+// Blocks [0, na) append the new history rows, the rest prepare the queries: the two stages
+// read different parts of the same projection and are independent.
+__global__ __launch_bounds__(256) void k_append_qprep(SeqTable t, Dims d, AppendArgs aa, QprepArgs qa, int na) {
+    if ((int)blockIdx.x < na) append_body(t, d, aa, blockIdx.x);
+    else qprep_body(t, d, qa, blockIdx.x - na);
+}
+
+static QprepArgs qprep_args(int fmt, const Dims &d, const uint16_t *kv_b, const float2 *rope_cs,
+                            const DecodeWork &w, bool quantize) {
     QprepArgs a;
-    a.t = t;
-    a.d = d;
     a.y = w.y;
     a.kv_b = kv_b;
     a.cs = rope_cs;
@@ -540,7 +540,26 @@ hipError_t launch_qprep(hipStream_t st, int fmt, const SeqTable &t, const Dims &
     a.ldy = d.QO + d.KVO;
     a.fmt = fmt;
     a.quantize = quantize ? 1 : 0;
-    hipLaunchKernelGGL(k_qprep, dim3(t.n * d.NH), dim3(256), 0, st, a);
+    return a;
+}
+
+hipError_t launch_qprep(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
+                        const uint16_t *kv_b, const float2 *rope_cs, const DecodeWork &w,
+                        bool quantize) {
+    if (d.R > kMaxR || d.DN > kMaxDN || d.DR > kMaxDR) return hipErrorInvalidValue;
+    const QprepArgs a = qprep_args(fmt, d, kv_b, rope_cs, w, quantize);
+    hipLaunchKernelGGL(k_qprep, dim3(t.n * d.NH), dim3(256), 0, st, t, d, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_append_qprep(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
+                               const float *y, int ldy, int koff, const uint16_t *kv_a_norm, float eps,
+                               const float2 *rope_cs, const uint16_t *kv_b, const DecodeWork &w,
+                               bool quantize) {
+    if (d.R > kMaxR || d.DN > kMaxDN || d.DR > kMaxDR) return hipErrorInvalidValue;
+    const AppendArgs aa = append_args(fmt, d, y, ldy, koff, kv_a_norm, eps, rope_cs, w, false, 0);
+    const QprepArgs qa = qprep_args(fmt, d, kv_b, rope_cs, w, quantize);
+    hipLaunchKernelGGL(k_append_qprep, dim3(t.n + t.n * d.NH), dim3(256), 0, st, t, d, aa, qa, t.n);
     return hipGetLastError();
 }
 
@@ -1247,11 +1266,93 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
     }
 }
 
+// Compressed formats with R = 512, DV = 128: the same algebra with fewer serial phases.
+// Wave 0 reduces the split maxima and denominators with shuffles (lane i handles splits
+// i, i + 64, ...); thread k of 512 mixes latent column k (all split loads of a group issued
+// together); thread t computes a quarter (128 columns) of W_UV row t / 4, and the four
+// quarters are summed with DPP moves.
+__global__ __launch_bounds__(512) void k_combine_r512(CombineArgs a) {
+    __shared__ float mx[512];
+    __shared__ float wts[kMaxSplits];
+    __shared__ float sinv;
+    const int NH = a.d.NH;
+    const int b = blockIdx.x / NH, h = blockIdx.x % NH, tid = threadIdx.x;
+    const SeqDesc &s = a.t.s[b];
+    const int ns = s.nsplit;
+    const size_t stride = (size_t)NH * (512 + 2);
+    const float *P = a.part + (size_t)s.split0 * stride;
+    if (tid < 64) {
+        float m = -INFINITY;
+        for (int i = tid; i < ns; i += 64) m = fmaxf(m, P[i * stride + (size_t)NH * 512 + h]);
+        m = wave_max(m);
+        float den = 0.f;
+        for (int i = tid; i < ns; i += 64) {
+            const float e = __expf(P[i * stride + (size_t)NH * 512 + h] - m);
+            wts[i] = e;
+            den = fmaf(P[i * stride + (size_t)NH * 512 + NH + h], e, den);
+        }
+        den = wave_sum(den);
+        if (tid == 0) sinv = 1.0f / den;
+    }
+    __syncthreads();
+    const float *Pg = P + (size_t)h * 512 + tid;
+    float v0 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f;
+    int i = 0;
+    for (; i + 8 <= ns; i += 8) {
+        float p[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) p[q] = Pg[(size_t)(i + q) * stride];
+        v0 = fmaf(p[0], wts[i], v0);
+        v1 = fmaf(p[1], wts[i + 1], v1);
+        v2 = fmaf(p[2], wts[i + 2], v2);
+        v3 = fmaf(p[3], wts[i + 3], v3);
+        v0 = fmaf(p[4], wts[i + 4], v0);
+        v1 = fmaf(p[5], wts[i + 5], v1);
+        v2 = fmaf(p[6], wts[i + 6], v2);
+        v3 = fmaf(p[7], wts[i + 7], v3);
+    }
+    for (; i < ns; ++i) v0 = fmaf(Pg[(size_t)i * stride], wts[i], v0);
+    const float v = ((v0 + v1) + (v2 + v3)) * sinv;
+    a.mix[((size_t)b * NH + h) * 512 + tid] = v;
+    mx[tid] = v;
+    __syncthreads();
+    // W_UV row dd = tid / 4, columns 128 q .. 128 q + 127 (16 x 16 B)
+    const int dd = tid >> 2, q = tid & 3;
+    const uint16_t *row = a.kv_b + ((size_t)h * (a.d.DN + 128) + a.d.DN + dd) * 512 + 128 * q;
+    const float *mh = mx + 128 * q;
+    v4i wv[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) wv[c] = *(const v4i *)(row + 8 * c);
+    float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+        const v4f m0 = *(const v4f *)(mh + 8 * c);
+        const v4f m1 = *(const v4f *)(mh + 8 * c + 4);
+        const uint32_t u0 = (uint32_t)wv[c][0], u1 = (uint32_t)wv[c][1];
+        const uint32_t u2 = (uint32_t)wv[c][2], u3 = (uint32_t)wv[c][3];
+        acc0 = fmaf(__uint_as_float(u0 << 16), m0.x, acc0);
+        acc1 = fmaf(__uint_as_float(u0 & 0xffff0000u), m0.y, acc1);
+        acc0 = fmaf(__uint_as_float(u1 << 16), m0.z, acc0);
+        acc1 = fmaf(__uint_as_float(u1 & 0xffff0000u), m0.w, acc1);
+        acc0 = fmaf(__uint_as_float(u2 << 16), m1.x, acc0);
+        acc1 = fmaf(__uint_as_float(u2 & 0xffff0000u), m1.y, acc1);
+        acc0 = fmaf(__uint_as_float(u3 << 16), m1.z, acc0);
+        acc1 = fmaf(__uint_as_float(u3 & 0xffff0000u), m1.w, acc1);
+    }
+    float acc = acc0 + acc1;
+    acc += dpp_f32<0xB1>(acc);  // quad_perm [1,0,3,2]
+    acc += dpp_f32<0x4E>(acc);  // quad_perm [2,3,0,1]
+    if (q == 0) a.ho[(size_t)b * a.d.HO + (size_t)h * 128 + dd] = acc;
+}
+
 hipError_t launch_combine(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
                           const uint16_t *kv_b, const DecodeWork &w) {
     if (d.R > kMaxR) return hipErrorInvalidValue;
     CombineArgs a{t, d, w.part, kv_b, w.mix, w.ho, fmt};
-    hipLaunchKernelGGL(k_combine, dim3(t.n * d.NH), dim3(256), 0, st, a);
+    if (fmt != kFmtExp && d.R == 512 && d.DV == 128)
+        hipLaunchKernelGGL(k_combine_r512, dim3(t.n * d.NH), dim3(512), 0, st, a);
+    else
+        hipLaunchKernelGGL(k_combine, dim3(t.n * d.NH), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

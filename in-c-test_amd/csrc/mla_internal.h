@@ -98,6 +98,11 @@ hipError_t launch_store_expanded(hipStream_t st, const SeqTable &t, const Dims &
 hipError_t launch_qprep(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
                         const uint16_t *kv_b, const float2 *rope_cs, const DecodeWork &w,
                         bool quantize);
+// launch_append (one row per sequence) and launch_qprep as one launch.
+hipError_t launch_append_qprep(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
+                               const float *y, int ldy, int koff, const uint16_t *kv_a_norm, float eps,
+                               const float2 *rope_cs, const uint16_t *kv_b, const DecodeWork &w,
+                               bool quantize);
 
 // Split-K attention over the history; writes partials (acc | m | l) per split.
 // kind: 0 = generic VALU (any dims, one split per problem), 1 = fp32 MFMA (Kimi dims),

@@ -655,17 +655,22 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
         StageTimer tm(0);
         HIP_TRY(launch_gemv(st, w.y, ldy, d_x, d.H, B, dw.q, d.QO, dw.kva, d.KVO, d.H, false));
     }
-    {
-        StageTimer tm(1);
-        HIP_TRY(launch_append(st, fmt, t, d, w.y, ldy, d.QO, dw.norm, eps, cs, w, false, 0));
-        if (fmt == kFmtExp) {
+    if (fmt == kFmtExp) {
+        {
+            StageTimer tm(1);
+            HIP_TRY(launch_append(st, fmt, t, d, w.y, ldy, d.QO, dw.norm, eps, cs, w, false, 0));
             HIP_TRY(launch_gemv(st, w.kv, d.KVB, w.latent, d.R, B, dw.kvb, d.KVB, nullptr, 0, d.R, false));
             HIP_TRY(launch_store_expanded(st, t, d, w));
         }
-    }
-    {
-        StageTimer tm(2);
-        HIP_TRY(launch_qprep(st, fmt, t, d, dw.kvb, cs, w, kind == kAttnQ8Mfma));
+        {
+            StageTimer tm(2);
+            HIP_TRY(launch_qprep(st, fmt, t, d, dw.kvb, cs, w, false));
+        }
+    } else {
+        // append and query preparation in one launch (timed as stage 1)
+        StageTimer tm(1);
+        HIP_TRY(launch_append_qprep(st, fmt, t, d, w.y, ldy, d.QO, dw.norm, eps, cs, dw.kvb, w,
+                                    kind == kAttnQ8Mfma));
     }
     {
         StageTimer tm(3);

@@ -56,7 +56,9 @@ EXT_API = {
     "mla_compressed_state_pull": (C.c_int, [abi.CS, C.c_int, C.c_int]),
 }
 
-STAGES = ("gemv_in", "append", "qprep", "attention", "combine", "gemv_out")
+# stage 1 is the fused append + query preparation of the compressed formats (the expanded
+# format times them as stages 1 and 2)
+STAGES = ("gemv_in", "append_qprep", "qprep", "attention", "combine", "gemv_out")
 RESIDUAL = 1
 NO_ADVANCE = 2
 

@@ -97,7 +97,8 @@ int kvl_mla_graph_destroy(void *graph_exec);
 
 /* Measurement helpers. kvl_mla_timing_enable(1) brackets every decode-step kernel with HIP
  * events on kvl_mla_stream() (not during graph capture); kvl_mla_timing_read() sums the
- * durations (ms) and launch counts of the six stages (gemv_in, append, qprep, attention,
+ * durations (ms) and launch counts of the six stages (gemv_in, append [+ qprep: one launch
+ * for the compressed formats], qprep [expanded format], attention,
  * combine, gemv_out) since the last read. Events: record on the library stream, elapsed
  * time between two recorded events (waits for the second). kvl_mla_copy_kernel: a plain
  * 16-byte vector copy kernel (bytes % 16 == 0), for calibrating memory counters. */
