@@ -396,6 +396,15 @@ __device__ __forceinline__ void qprep_body(const SeqTable &t, const Dims &d, con
     const SeqDesc &s = t.s[b];
     const float *qh = a.y + (size_t)b * a.ldy + (size_t)h * d.QD;
     const int half = d.DR / 2;
+    // Kimi shapes: the W_UK rows of this wave (lane l: latent columns 8l .. 8l+7 of rows
+    // 32w .. 32w+31) do not depend on q, so they are requested before q is.
+    const bool fast = a.fmt != kFmtExp && d.R == 512 && d.DN == 128;
+    v4i wpre[32];
+    if (fast) {
+        const uint16_t *wuk = a.kv_b + (size_t)h * (d.DN + d.DV) * d.R + (size_t)(tid >> 6) * 32 * 512 + 8 * (tid & 63);
+#pragma unroll
+        for (int q = 0; q < 32; ++q) wpre[q] = *(const v4i *)(wuk + (size_t)q * 512);
+    }
     for (int i = tid; i < d.DN; i += 256) qn[i] = qh[i];
     __syncthreads();
     const bool exp = a.fmt == kFmtExp;
@@ -411,7 +420,19 @@ __device__ __forceinline__ void qprep_body(const SeqTable &t, const Dims &d, con
             __shared__ v4f part[4][64][2];
             const int w = tid >> 6, l = tid & 63, kq = d.DN >> 2;
             float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            for (int k0 = 0; k0 < kq; k0 += 8) {
+            if (fast) {
+#pragma unroll
+                for (int q = 0; q < 32; ++q) {
+                    const float qv = qn[w * 32 + q];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t u = (uint32_t)wpre[q][e];
+                        acc[2 * e] = fmaf(__uint_as_float(u << 16), qv, acc[2 * e]);
+                        acc[2 * e + 1] = fmaf(__uint_as_float(u & 0xffff0000u), qv, acc[2 * e + 1]);
+                    }
+                }
+            }
+            for (int k0 = 0; k0 < (fast ? 0 : kq); k0 += 8) {
                 v4i wv[8];
 #pragma unroll
                 for (int q = 0; q < 8; ++q)
@@ -1267,10 +1288,11 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
 }
 
 // Compressed formats with R = 512, DV = 128: the same algebra with fewer serial phases.
-// Wave 0 reduces the split maxima and denominators with shuffles (lane i handles splits
-// i, i + 64, ...); thread k of 512 mixes latent column k (all split loads of a group issued
-// together); thread t computes a quarter (128 columns) of W_UV row t / 4, and the four
-// quarters are summed with DPP moves.
+// Every thread first issues the loads that do not depend on the split weights (its W_UV
+// quarter row and the first partials of its latent column); meanwhile wave 0 reduces the
+// split maxima and denominators with shuffles (lane i handles splits i, i + 64, ...).
+// Thread k of 512 then mixes latent column k; thread t computes a quarter (128 columns) of
+// W_UV row t / 4, and the four quarters are summed with DPP moves.
 __global__ __launch_bounds__(512) void k_combine_r512(CombineArgs a) {
     __shared__ float mx[512];
     __shared__ float wts[kMaxSplits];
@@ -1281,6 +1303,17 @@ __global__ __launch_bounds__(512) void k_combine_r512(CombineArgs a) {
     const int ns = s.nsplit;
     const size_t stride = (size_t)NH * (512 + 2);
     const float *P = a.part + (size_t)s.split0 * stride;
+    // loads independent of the split weights
+    const int dd = tid >> 2, q = tid & 3;
+    const uint16_t *row = a.kv_b + ((size_t)h * (a.d.DN + 128) + a.d.DN + dd) * 512 + 128 * q;
+    v4i wv[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) wv[c] = *(const v4i *)(row + 8 * c);
+    const float *Pg = P + (size_t)h * 512 + tid;
+    constexpr int kPre = 16;
+    float pre[kPre];
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) pre[i] = i < ns ? Pg[(size_t)i * stride] : 0.f;
     if (tid < 64) {
         float m = -INFINITY;
         for (int i = tid; i < ns; i += 64) m = fmaxf(m, P[i * stride + (size_t)NH * 512 + h]);
@@ -1295,9 +1328,15 @@ __global__ __launch_bounds__(512) void k_combine_r512(CombineArgs a) {
         if (tid == 0) sinv = 1.0f / den;
     }
     __syncthreads();
-    const float *Pg = P + (size_t)h * 512 + tid;
     float v0 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f;
-    int i = 0;
+#pragma unroll
+    for (int i = 0; i < kPre; i += 4) {
+        if (i < ns) v0 = fmaf(pre[i], wts[i], v0);
+        if (i + 1 < ns) v1 = fmaf(pre[i + 1], wts[i + 1], v1);
+        if (i + 2 < ns) v2 = fmaf(pre[i + 2], wts[i + 2], v2);
+        if (i + 3 < ns) v3 = fmaf(pre[i + 3], wts[i + 3], v3);
+    }
+    int i = kPre;
     for (; i + 8 <= ns; i += 8) {
         float p[8];
 #pragma unroll
@@ -1316,13 +1355,8 @@ __global__ __launch_bounds__(512) void k_combine_r512(CombineArgs a) {
     a.mix[((size_t)b * NH + h) * 512 + tid] = v;
     mx[tid] = v;
     __syncthreads();
-    // W_UV row dd = tid / 4, columns 128 q .. 128 q + 127 (16 x 16 B)
-    const int dd = tid >> 2, q = tid & 3;
-    const uint16_t *row = a.kv_b + ((size_t)h * (a.d.DN + 128) + a.d.DN + dd) * 512 + 128 * q;
+    // W_UV row dd = tid / 4, columns 128 q .. 128 q + 127 (loaded above)
     const float *mh = mx + 128 * q;
-    v4i wv[16];
-#pragma unroll
-    for (int c = 0; c < 16; ++c) wv[c] = *(const v4i *)(row + 8 * c);
     float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
