@@ -79,6 +79,21 @@ def omp_threads():
         return int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
 
 
+def traffic_bytes(batch, context):
+    """HBM bytes per attention launch measured by rocprofv3 (FETCH_SIZE and WRITE_SIZE passes,
+    scaled by a copy kernel of known size) for this workload, from the committed profile;
+    None for other workloads."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "k_attn_q8_mfma_traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("workload") != {"batch": batch, "context": context}:
+        return None
+    return t.get("hbm_bytes_per_launch")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -204,7 +219,7 @@ def main():
     attn = stages["attention"]
     attn_gbs = hist_bytes / (attn["ms_per_launch"] * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_bytes(B, CTX),
                 "kernel": "k_attn_q8_mfma", "algorithmic_bytes_per_launch": hist_bytes,
                 "avg_launch_ms": round(attn["ms_per_launch"], 5)}
 
