@@ -842,9 +842,12 @@ constexpr int kQ8RopeB = kQ8Ch * 128;               // bf16 RoPE keys of a chunk
 constexpr int kQ8ChunkB = kQ8CodeB + kQ8RopeB;
 constexpr int kQ8Ws = 80;                           // LDS bytes per quantised-weight row
 constexpr int kQ8SclOff = kQ8Ring * kQ8ChunkB;      // scales of the whole split
-constexpr int kQ8WqOff = kQ8SclOff + 4 * kQ8MaxSplitRows;
-constexpr int kQ8MlOff = kQ8WqOff + 2 * 16 * kQ8Ws;
-constexpr int kQ8SmemB = kQ8MlOff + 3 * 4 * 16 * 4;
+constexpr int kQ8WqB = 2 * 16 * kQ8Ws;              // quantised weights of a chunk (hi, lo)
+constexpr int kQ8WqOff = kQ8SclOff + 4 * kQ8MaxSplitRows;  // two buffers, by chunk parity
+constexpr int kQ8MlOff = kQ8WqOff + 2 * kQ8WqB;    // chunk maxima [2][4 waves][16], sums, smax
+constexpr int kQ8QOff = kQ8MlOff + 4 * 4 * 16 * 4;  // query operands of the sequence
+constexpr int kQ8QB = 2 * 16 * 512 + 2 * 16 * 128 + 256;  // int8 hi, lo; bf16 rope hi, lo; scales
+constexpr int kQ8SmemB = kQ8QOff + kQ8QB;
 
 // Slot swizzle of the code rows: physical 16-byte slot = logical slot ^ q8_swz(row).
 __device__ __forceinline__ int q8_swz(int row) { return (row & 7) ^ (((row >> 4) & 1) << 2); }
@@ -859,8 +862,9 @@ __device__ __forceinline__ v2i lds_read_tr8(const uint8_t *p) {
 __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t smem[kQ8SmemB];
     int8_t *wq = (int8_t *)(smem + kQ8WqOff);  // [hi, lo][16 heads][kQ8Ws]
-    float *mloc = (float *)(smem + kQ8MlOff);  // [4 waves][16]
-    float *lsum = mloc + 64;                   // [4 waves][16]
+    float *mloc = (float *)(smem + kQ8MlOff);  // [2 parities][4 waves][16]
+    float *lsum = mloc + 128;                  // [4 waves][16]
+    float *smx = mloc + 192;                   // [4 waves]
     const uint32_t sbase = lds_addr(smem);
     const float *sclv = (const float *)(smem + kQ8SclOff);  // scales of the split's rows
     const int tid = threadIdx.x, l = tid & 63, n = l & 15, g = l >> 4;
@@ -874,22 +878,32 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
     const float *gscl = (const float *)s.b;
     const uint16_t *grope = (const uint16_t *)s.c;
 
-    const size_t bh = (size_t)b * 16 + n;
-    v4i qh[8], ql[8];
+    // Query operands of sequence b come through LDS DMA like the history: every global load
+    // of the kernel is then an asm DMA, and the prologue waits for the first chunk only
+    // (a compiler-visible load would make the compiler wait for every DMA issued before it).
+    // LDS rows of 512 (int8) / 128 (bf16) bytes, 16-byte slots XOR-swizzled by the head so
+    // that the 16 lanes of a lane group (16 heads) hit distinct banks.
+    const uint8_t *sq = smem + kQ8QOff;  // [hi, lo][16][512] int8, [hi, lo][16][64] bf16, qs[16]
+    {
+        const uint32_t qd = sbase + (uint32_t)kQ8QOff;
+        const int8_t *gqh = a.qhi + (size_t)b * 16 * 512, *gql = a.qlo + (size_t)b * 16 * 512;
 #pragma unroll
-    for (int kb = 0; kb < 8; ++kb) {
-        qh[kb] = *(const v4i *)(a.qhi + bh * 512 + 64 * kb + 16 * g);
-        ql[kb] = *(const v4i *)(a.qlo + bh * 512 + 64 * kb + 16 * g);
+        for (int k = 0; k < 2; ++k) {  // 16 KB of int8 hi/lo: 16 instructions, 4 per wave
+            const int p = (w * 2 + k) * 64 + l, head = p >> 5, slot = (p & 31) ^ (head & 31);
+            dma_b128(gqh + head * 512 + 16 * slot, qd + (uint32_t)((w * 2 + k) * 1024));
+            dma_b128(gql + head * 512 + 16 * slot, qd + (uint32_t)(8192 + (w * 2 + k) * 1024));
+        }
+        {  // 4 KB of bf16 rope hi/lo: 4 instructions, one per wave
+            const int p = (w & 1) * 64 + l, head = p >> 3, slot = (p & 7) ^ (head & 7);
+            const uint16_t *src = (w < 2 ? a.qrhi : a.qrlo) + (size_t)b * 16 * 64;
+            dma_b128((const uint8_t *)(src + head * 64) + 16 * slot,
+                     qd + (uint32_t)(16384 + (w >> 1) * 2048 + (w & 1) * 1024));
+        }
+        if (w == 0) dma_b32(a.qs + (size_t)b * 16 + min(l, 15), qd + (uint32_t)(20480));
     }
+    v4i qh[8], ql[8];      // read from LDS once the prologue's loads have landed
     v8bf qrh[2], qrl[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-        qrh[kb] = *(const v8bf *)(a.qrhi + bh * 64 + 32 * kb + 8 * g);
-        qrl[kb] = *(const v8bf *)(a.qrlo + bh * 64 + 32 * kb + 8 * g);
-    }
     float qsd[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) qsd[i] = a.qs[(size_t)b * 16 + 4 * g + i] * a.smscale;
 
     float m_run[4], l_lane[4];
 #pragma unroll
@@ -948,10 +962,10 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
             }
         }
     };
-    // this wave's DMA instructions per chunk: 10
+    // this wave's DMA instructions per chunk: 10; at chunk c's wait, chunk c+1 (issued at
+    // chunk c-1) may still be in flight
     auto wait_chunk = [&](int later) {
-        if (later >= 2) wait_vmcnt<20>();
-        else if (later == 1) wait_vmcnt<10>();
+        if (later >= 1) wait_vmcnt<10>();
         else wait_vmcnt<0>();
     };
 
@@ -974,11 +988,15 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
     auto chunk = [&](auto slot_tag, int c) {
         constexpr int slot = decltype(slot_tag)::value;
         const uint8_t *buf = smem + slot * kQ8ChunkB;
-        if (c + 2 < nch) issue(c + 2);  // ring slot of chunk c-1, released at its end barrier
-        wait_chunk(min(2, nch - 1 - c));
+        // chunk c landed (this wave's part; all waves' after the barrier), and every wave is
+        // past chunk c-1: its ring slot takes chunk c+2. The chunk maxima and quantised
+        // weights alternate between two buffers, so no barrier is needed at the chunk's end.
+        wait_chunk(min(1, nch - 1 - c));
         lds_barrier();
+        if (c + 2 < nch) issue(c + 2);
         const int base = r0 + c * kQ8Ch;
-        float *ml = mloc + 64 * 0;
+        float *ml = mloc + 64 * (c & 1);
+        int8_t *wqc = wq + (c & 1) * kQ8WqB;
 
         v4i ih = {0, 0, 0, 0}, il = {0, 0, 0, 0};
         v4f fr = {0.f, 0.f, 0.f, 0.f};
@@ -1025,8 +1043,8 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
             const float v = p * sj * wscale;
             const float hi = fminf(rintf(v), 127.f);
             const float lo = rintf((v - hi) * 128.0f);
-            wq[hh * kQ8Ws + rowl] = (int8_t)hi;
-            wq[16 * kQ8Ws + hh * kQ8Ws + rowl] = (int8_t)lo;
+            wqc[hh * kQ8Ws + rowl] = (int8_t)hi;
+            wqc[16 * kQ8Ws + hh * kQ8Ws + rowl] = (int8_t)lo;
         }
         if (__any(moved)) {
 #pragma unroll
@@ -1040,8 +1058,8 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
         }
         lds_barrier();
 
-        const v4i wh = *(const v4i *)(wq + wq_off);
-        const v4i wl = *(const v4i *)(wq + 16 * kQ8Ws + wq_off);
+        const v4i wh = *(const v4i *)(wqc + wq_off);
+        const v4i wl = *(const v4i *)(wqc + 16 * kQ8Ws + wq_off);
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             const v2i b0 = lds_read_tr8(buf + tr_off[t][0]);
@@ -1050,7 +1068,6 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
             ahi[t] = mfma_i8(wh, bt, ahi[t]);
             alo[t] = mfma_i8(wl, bt, alo[t]);
         }
-        lds_barrier();  // ring slot, mloc and wq free for the next chunk
     };
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
@@ -1063,32 +1080,32 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
     }
     issue(0);
     if (nch > 1) issue(1);
-    // Settle every load issued so far (query operands, scales, first chunks): the empty
-    // asm consumes each operand, so the compiler waits for them here and never inside the
-    // loop, where a vmcnt wait would also drain the chunk DMA ring.
+    // query operands, scales and chunk 0 have landed once at most chunk 1 is in flight
+    wait_chunk(min(1, nch - 1));
+    lds_barrier();
 #pragma unroll
     for (int kb = 0; kb < 8; ++kb) {
-        asm volatile("" : "+v"(qh[kb]));
-        asm volatile("" : "+v"(ql[kb]));
+        const int o = n * 512 + 16 * ((4 * kb + g) ^ n);
+        qh[kb] = *(const v4i *)(sq + o);
+        ql[kb] = *(const v4i *)(sq + 8192 + o);
     }
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-        asm volatile("" : "+v"(qrh[kb]));
-        asm volatile("" : "+v"(qrl[kb]));
+        const int o = 16384 + n * 128 + 16 * ((4 * kb + g) ^ (n & 7));
+        qrh[kb] = *(const v8bf *)(sq + o);
+        qrl[kb] = *(const v8bf *)(sq + 2048 + o);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(qsd[i]));
-    wait_vmcnt<0>();
-    lds_barrier();
+    for (int i = 0; i < 4; ++i) qsd[i] = ((const float *)(sq + 20480))[4 * g + i] * a.smscale;
     // largest row scale of the split: the common bound of the quantised weights
     float smax;
     {
         float m = 0.f;
         for (int r = tid; r < r1 - r0; r += 256) m = fmaxf(m, sclv[r]);
         m = wave_max(m);
-        if (l == 0) mloc[128 + w] = m;
+        if (l == 0) smx[w] = m;
         lds_barrier();
-        smax = fmaxf(fmaxf(mloc[128], mloc[129]), fmaxf(mloc[130], mloc[131]));
+        smax = fmaxf(fmaxf(smx[0], smx[1]), fmaxf(smx[2], smx[3]));
     }
     // p_j <= 2 relative to the reference max (see the lazy max below)
     wscale = smax > 0.f ? 127.0f / (2.0f * smax) : 0.f;
