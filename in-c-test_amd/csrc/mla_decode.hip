@@ -113,6 +113,192 @@ __global__ __launch_bounds__(256) void k_gemv_generic(GemvArgs a) {
     }
 }
 
+// ---- decode projections -----------------------------------------------------------------
+// Both kernels below feed the activations to the MFMA as 16 columns = bf16 hi (columns 0-7)
+// and bf16 lo (columns 8-15) of 8 sequences: one MFMA per row tile and k-block carries both
+// halves (the products of bf16 operands are exact in fp32), and the two columns of a sequence
+// are added at the end (lanes l and l ^ 8). NG groups of 8 sequences per block, blockIdx.z
+// selects the 16-sequence slice; each sequence's result is the same whatever the batch.
+struct GemvSplitArgs {
+    float *Y;            // k-split: partial q at Y + q * pstride; pre-split: the output
+    const float *X;      // k-split: fp32 activations [B, ldx]
+    const uint16_t *XS;  // pre-split: bf16 planes [2][B][in], plane 0 = hi, plane 1 = lo
+    const uint16_t *W0;
+    const uint16_t *W1;
+    size_t pstride;
+    int ldy, ldx, B, out0, out1, in, acc;
+};
+
+// Y + kq * pstride [b, o] = sum over k in [kq in/kGemvKs, (kq+1) in/kGemvKs) of W[o, k] X[b, k].
+// Block: 64 output rows (4 MFMA row tiles) x one k quarter; 16 waves, each KPW 32-wide
+// k-blocks for all four tiles, so every activation value a wave converts serves four MFMAs.
+// Splitting k keeps the weight bytes per block at 64 KB while each block reads only a quarter
+// of the activations (a 16-row block over the full k range would read all of them). The
+// consumer adds the kGemvKs partials in kq order. Requires in = kGemvKs * 16 * 32 * KPW.
+template <int NG, int KPW>
+__global__ __launch_bounds__(1024) void k_gemv_ksplit(GemvSplitArgs a) {
+    __shared__ v4f red[16][4 * NG][64];
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
+    const int out = a.out0 + a.out1, kq = blockIdx.y, row0 = blockIdx.x * 64, part = n >> 3;
+    const uint16_t *wr[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int row = min(row0 + 16 * t + n, out - 1);  // rows past the end are never stored
+        wr[t] = row < a.out0 ? a.W0 + (size_t)row * a.in : a.W1 + (size_t)(row - a.out0) * a.in;
+    }
+    const int bz = 16 * blockIdx.z;
+    const float *xr[NG];
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) xr[gi] = a.X + (size_t)min(bz + 8 * gi + (n & 7), a.B - 1) * a.ldx;
+    v4f acc[4][NG];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) acc[t][gi] = v4f{0.f, 0.f, 0.f, 0.f};
+    const int kbase = kq * (16 * 32 * KPW) + w * (32 * KPW) + g * 8;
+    v4i wa[KPW][4];
+    v4f xa[KPW][NG], xb[KPW][NG];
+#pragma unroll
+    for (int kb = 0; kb < KPW; ++kb) {
+        const int k = kbase + 32 * kb;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) wa[kb][t] = *(const v4i *)(wr[t] + k);
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+            xa[kb][gi] = *(const v4f *)(xr[gi] + k);
+            xb[kb][gi] = *(const v4f *)(xr[gi] + k + 4);
+        }
+    }
+#pragma unroll
+    for (int kb = 0; kb < KPW; ++kb)
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+            const v8bf xv = split8_part(xa[kb][gi], xb[kb][gi], part);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[t][gi] = mfma_bf16(__builtin_bit_cast(v8bf, wa[kb][t]), xv, acc[t][gi]);
+        }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) red[w][t * NG + gi][l] = acc[t][gi];
+    __syncthreads();
+    if (w >= 4) return;
+    // wave t sums row tile t over the 16 waves in order
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) {
+        v4f s = red[0][w * NG + gi][l];
+#pragma unroll
+        for (int q = 1; q < 16; ++q) s += red[q][w * NG + gi][l];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[i] += dpp_f32<0x128>(s[i]);  // row_ror:8 = lane ^ 8
+        const int b = bz + 8 * gi + n;
+        if (n < 8 && b < a.B) {
+            float *y = a.Y + (size_t)kq * a.pstride + (size_t)b * a.ldy;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = row0 + 16 * w + 4 * g + i;
+                if (r < out) y[r] = s[i];
+            }
+        }
+    }
+}
+
+// Y[b, o] (+)= sum_k W[o, k] (hi + lo)[b, k] with the activations already split into bf16
+// planes by their producer: 16 output rows per block, 16 waves splitting k, one 16-byte
+// activation load and one MFMA per k-block and sequence group. Requires in = 16 * 32 * KPW.
+template <int NG, int KPW>
+__global__ __launch_bounds__(1024) void k_gemv_xs(GemvSplitArgs a) {
+    __shared__ v4f red[16][NG][64];
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
+    const int out = a.out0, part = n >> 3;
+    const uint16_t *wrow = a.W0 + (size_t)min((int)blockIdx.x * 16 + n, out - 1) * a.in;
+    const int bz = 16 * blockIdx.z;
+    const uint16_t *xr[NG];
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi)
+        xr[gi] = a.XS + ((size_t)part * a.B + min(bz + 8 * gi + (n & 7), a.B - 1)) * a.in;
+    const int kbase = w * (32 * KPW) + g * 8;
+    v4i wa[KPW], xv[KPW][NG];
+#pragma unroll
+    for (int kb = 0; kb < KPW; ++kb) {
+        wa[kb] = *(const v4i *)(wrow + kbase + 32 * kb);
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) xv[kb][gi] = *(const v4i *)(xr[gi] + kbase + 32 * kb);
+    }
+    v4f acc[NG];
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) acc[gi] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < KPW; ++kb)
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi)
+            acc[gi] = mfma_bf16(__builtin_bit_cast(v8bf, wa[kb]), __builtin_bit_cast(v8bf, xv[kb][gi]), acc[gi]);
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) red[w][gi][l] = acc[gi];
+    __syncthreads();
+    if (w != 0) return;
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) {
+        v4f s = red[0][gi][l];
+#pragma unroll
+        for (int q = 1; q < 16; ++q) s += red[q][gi][l];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[i] += dpp_f32<0x128>(s[i]);
+        const int b = bz + 8 * gi + n;
+        if (n < 8 && b < a.B) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = blockIdx.x * 16 + 4 * g + i;
+                if (r < out) {
+                    float *yp = a.Y + (size_t)b * a.ldy + r;
+                    *yp = a.acc ? *yp + s[i] : s[i];
+                }
+            }
+        }
+    }
+}
+
+bool gemv_ksplit_ok(int in, int ldx) { return (in == 2048 || in == 4096) && ldx % 4 == 0; }
+
+hipError_t launch_gemv_ksplit(hipStream_t st, float *Y, size_t pstride, int ldy, const float *X,
+                              int ldx, int B, const uint16_t *W0, int out0, const uint16_t *W1,
+                              int out1, int in) {
+    if (!gemv_ksplit_ok(in, ldx) || B < 1 || ((uintptr_t)X % 16) != 0 || ((uintptr_t)W0 % 16) != 0 ||
+        (W1 && ((uintptr_t)W1 % 16) != 0) || out0 + out1 <= 0 || (B + 15) / 16 > 65535)
+        return hipErrorInvalidValue;
+    GemvSplitArgs a{Y, X, nullptr, W0, W1, pstride, ldy, ldx, B, out0, out1, in, 0};
+    const dim3 grid((out0 + out1 + 63) / 64, kGemvKs, (B + 15) / 16);
+    const bool two = B > 8;
+    if (in == 2048) {
+        if (two) hipLaunchKernelGGL((k_gemv_ksplit<2, 1>), grid, dim3(1024), 0, st, a);
+        else hipLaunchKernelGGL((k_gemv_ksplit<1, 1>), grid, dim3(1024), 0, st, a);
+    } else {
+        if (two) hipLaunchKernelGGL((k_gemv_ksplit<2, 2>), grid, dim3(1024), 0, st, a);
+        else hipLaunchKernelGGL((k_gemv_ksplit<1, 2>), grid, dim3(1024), 0, st, a);
+    }
+    return hipGetLastError();
+}
+
+bool gemv_xs_ok(int in) { return in == 2048 || in == 4096; }
+
+hipError_t launch_gemv_xs(hipStream_t st, float *Y, int ldy, const uint16_t *XS, int B,
+                          const uint16_t *W, int out, int in, bool accumulate) {
+    if (!gemv_xs_ok(in) || B < 1 || ((uintptr_t)XS % 16) != 0 || ((uintptr_t)W % 16) != 0 || out <= 0 ||
+        (B + 15) / 16 > 65535)
+        return hipErrorInvalidValue;
+    GemvSplitArgs a{Y, nullptr, XS, W, nullptr, 0, ldy, 0, B, out, 0, in, accumulate ? 1 : 0};
+    const dim3 grid((out + 15) / 16, 1, (B + 15) / 16);
+    const bool two = B > 8;
+    if (in == 2048) {
+        if (two) hipLaunchKernelGGL((k_gemv_xs<2, 4>), grid, dim3(1024), 0, st, a);
+        else hipLaunchKernelGGL((k_gemv_xs<1, 4>), grid, dim3(1024), 0, st, a);
+    } else {
+        if (two) hipLaunchKernelGGL((k_gemv_xs<2, 8>), grid, dim3(1024), 0, st, a);
+        else hipLaunchKernelGGL((k_gemv_xs<1, 8>), grid, dim3(1024), 0, st, a);
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_gemv(hipStream_t st, float *Y, int ldy, const float *X, int ldx, int B,
                        const uint16_t *W0, int out0, const uint16_t *W1, int out1, int in,
                        bool accumulate) {
@@ -140,14 +326,30 @@ constexpr int kMaxDN = 512;   // qk_nope_dim bound
 // The sequence table and dims are separate kernel arguments (one copy serves the fused
 // append + qprep launch).
 struct AppendArgs {
-    const float *y;
+    const float *y;  // projection rows: np partials pstride apart, summed in order
     const uint16_t *norm;
     const float2 *cs;
     uint8_t *rows;
     float *latent;
-    int ldy, koff, fmt, normed, row_bytes, rows_mode;
+    size_t pstride;
+    int ldy, koff, np, fmt, normed, row_bytes, rows_mode;
     float eps;
 };
+
+// Value of a projection output stored as np partials (np = 1 or kGemvKs) pstride floats
+// apart, added in partial order. The kGemvKs loads are issued together.
+__device__ __forceinline__ float sum_parts(const float *p, int np, size_t pstride) {
+    if (np == kGemvKs) {
+        float v[kGemvKs];
+#pragma unroll
+        for (int q = 0; q < kGemvKs; ++q) v[q] = p[(size_t)q * pstride];
+        float s = v[0];
+#pragma unroll
+        for (int q = 1; q < kGemvKs; ++q) s += v[q];
+        return s;
+    }
+    return p[0];
+}
 
 // One block per sequence (rows_mode = 0) or, with rows_mode = 1, one block per row of the
 // single sequence t.s[0]: block i appends row t.s[0].pos + i from input row i. Reproduces src/ops.c:76-83 (RMSNorm: double sum of squares,
@@ -157,12 +359,27 @@ struct AppendArgs {
 // compiled with -ffp-contract=off, so each product and sum rounds separately as there.
 __device__ __forceinline__ void append_body(const SeqTable &t, const Dims &d, const AppendArgs &a, int b) {
     __shared__ float lat[kMaxR];
+    __shared__ float kat[kMaxR + kMaxDR];  // projection row: RMSNorm input | RoPE input
     __shared__ double redd[256];
     __shared__ float redf[256];
     const int tid = threadIdx.x;
     const SeqDesc &s = t.s[a.rows_mode ? 0 : b];
     const int R = d.R, DR = d.DR, half = DR / 2, pos = s.pos + (a.rows_mode ? b : 0);
-    const float *kat = a.y + (size_t)b * a.ldy + a.koff;
+    const int nk = R + DR;
+    const float *ky = a.y + (size_t)b * a.ldy + a.koff;
+    // All global reads first, so that one memory round trip covers them: the projection row
+    // (partials summed), the norm weights of this thread's first two columns, its RoPE pair.
+    float kv[3], nw[2];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) kv[j] = sum_parts(ky + min(tid + 256 * j, nk - 1), a.np, a.pstride);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) nw[j] = a.normed ? 0.f : bf16_to_f32(a.norm[min(tid + 256 * j, R - 1)]);
+    const float2 csv = half > 0 ? a.cs[(size_t)pos * half + min(tid, half - 1)] : float2{0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+        if (tid + 256 * j < nk) kat[tid + 256 * j] = kv[j];
+    for (int r = tid + 768; r < nk; r += 256) kat[r] = sum_parts(ky + r, a.np, a.pstride);  // R + DR > 768
+    __syncthreads();
 
     if (!a.normed) {
         double ss = 0.0;
@@ -178,9 +395,9 @@ __device__ __forceinline__ void append_body(const SeqTable &t, const Dims &d, co
         }
         const float mean_sq = (float)(redd[0] / (double)R);
         const float inv = 1.0f / sqrtf(mean_sq + a.eps);
-        for (int r = tid; r < R; r += 256) {
+        for (int r = tid, j = 0; r < R; r += 256, ++j) {
             const float t = kat[r] * inv;
-            lat[r] = t * bf16_to_f32(a.norm[r]);
+            lat[r] = t * (j < 2 ? nw[j] : bf16_to_f32(a.norm[r]));
         }
     } else {
         for (int r = tid; r < R; r += 256) lat[r] = kat[r];
@@ -230,8 +447,9 @@ __device__ __forceinline__ void append_body(const SeqTable &t, const Dims &d, co
         for (int r = tid; r < R; r += 256) a.latent[(size_t)b * R + r] = lat[r];
     }
 
-    for (int i = tid; i < half; i += 256) {
-        const float2 cs = a.cs[(size_t)pos * half + i];
+    if (tid < half) {  // half <= kMaxDR / 2 < 256
+        const int i = tid;
+        const float2 cs = csv;
         const float ev = kat[R + 2 * i], od = kat[R + 2 * i + 1];
         const float ec = ev * cs.x, os = od * cs.y, oc = od * cs.x, es = ev * cs.y;
         const float d0 = ec - os, d1 = oc + es;
@@ -263,10 +481,12 @@ __global__ __launch_bounds__(256) void k_append(SeqTable t, Dims d, AppendArgs a
 }
 
 static AppendArgs append_args(int fmt, const Dims &d, const float *y, int ldy, int koff,
-                              const uint16_t *kv_a_norm, float eps, const float2 *rope_cs,
-                              const DecodeWork &w, bool normed, int nrows) {
+                              int ynp, size_t ypstride, const uint16_t *kv_a_norm, float eps,
+                              const float2 *rope_cs, const DecodeWork &w, bool normed, int nrows) {
     AppendArgs a;
     a.y = y;
+    a.np = ynp > 1 ? ynp : 1;
+    a.pstride = ypstride;
     a.norm = kv_a_norm;
     a.cs = rope_cs;
     a.rows = w.rows;
@@ -284,11 +504,12 @@ static AppendArgs append_args(int fmt, const Dims &d, const float *y, int ldy, i
 }
 
 hipError_t launch_append(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
-                         const float *y, int ldy, int koff, const uint16_t *kv_a_norm,
-                         float eps, const float2 *rope_cs, const DecodeWork &w, bool normed,
-                         int nrows) {
-    if (d.R > kMaxR || d.DR > kMaxDR) return hipErrorInvalidValue;
-    const AppendArgs a = append_args(fmt, d, y, ldy, koff, kv_a_norm, eps, rope_cs, w, normed, nrows);
+                         const float *y, int ldy, int koff, int ynp, size_t ypstride,
+                         const uint16_t *kv_a_norm, float eps, const float2 *rope_cs,
+                         const DecodeWork &w, bool normed, int nrows) {
+    if (d.R > kMaxR || d.DR > kMaxDR || (ynp != 1 && ynp != kGemvKs)) return hipErrorInvalidValue;
+    const AppendArgs a = append_args(fmt, d, y, ldy, koff, ynp, ypstride, kv_a_norm, eps, rope_cs, w,
+                                     normed, nrows);
     hipLaunchKernelGGL(k_append, dim3(nrows > 0 ? nrows : t.n), dim3(256), 0, st, t, d, a);
     return hipGetLastError();
 }
@@ -374,14 +595,15 @@ hipError_t launch_store_expanded(hipStream_t st, const SeqTable &t, const Dims &
 // ================================================================ query prep ===========
 
 struct QprepArgs {
-    const float *y;
+    const float *y;  // projection rows: np partials pstride apart, summed in order
     const uint16_t *kv_b;
     const float2 *cs;
     float *qf;
     int8_t *qhi, *qlo;
     float *qs;
     uint16_t *qrhi, *qrlo;
-    int ldy, fmt, quantize;
+    size_t pstride;
+    int ldy, np, fmt, quantize;
 };
 
 // One block per (sequence, head). Compressed formats: q_lat[r] = sum_d
@@ -390,12 +612,13 @@ struct QprepArgs {
 // With `quantize`, q_lat ~= qs * (hi + lo/128) (int8 hi, lo) and q_rope = hi + lo (bf16).
 __device__ __forceinline__ void qprep_body(const SeqTable &t, const Dims &d, const QprepArgs &a, int blk) {
     __shared__ float qn[kMaxDN];
+    __shared__ float qr[kMaxDR];  // RoPE input of the head
     __shared__ float ql[kMaxR];
     __shared__ float redf[256];
     const int b = blk / d.NH, h = blk % d.NH, tid = threadIdx.x;
     const SeqDesc &s = t.s[b];
     const float *qh = a.y + (size_t)b * a.ldy + (size_t)h * d.QD;
-    const int half = d.DR / 2;
+    const int half = d.DR / 2, nq = d.DN + d.DR;
     // Kimi shapes: the W_UK rows of this wave (lane l: latent columns 8l .. 8l+7 of rows
     // 32w .. 32w+31) do not depend on q, so they are requested before q is.
     const bool fast = a.fmt != kFmtExp && d.R == 512 && d.DN == 128;
@@ -405,7 +628,18 @@ __device__ __forceinline__ void qprep_body(const SeqTable &t, const Dims &d, con
 #pragma unroll
         for (int q = 0; q < 32; ++q) wpre[q] = *(const v4i *)(wuk + (size_t)q * 512);
     }
-    for (int i = tid; i < d.DN; i += 256) qn[i] = qh[i];
+    // the query head (partials summed) and this thread's RoPE pair, in one round trip
+    {
+        const float v = sum_parts(qh + min(tid, nq - 1), a.np, a.pstride);
+        if (tid < d.DN) qn[tid] = v;
+        else if (tid < nq) qr[tid - d.DN] = v;
+        for (int i = tid + 256; i < nq; i += 256) {  // DN + DR > 256
+            const float u = sum_parts(qh + i, a.np, a.pstride);
+            if (i < d.DN) qn[i] = u;
+            else qr[i - d.DN] = u;
+        }
+    }
+    const float2 csv = half > 0 ? a.cs[(size_t)s.pos * half + min(tid, half - 1)] : float2{0.f, 0.f};
     __syncthreads();
     const bool exp = a.fmt == kFmtExp;
     const int qstride = exp ? d.QD : d.R + d.DR;
@@ -491,9 +725,10 @@ __device__ __forceinline__ void qprep_body(const SeqTable &t, const Dims &d, con
             }
         }
     }
-    for (int i = tid; i < half; i += 256) {
-        const float2 cs = a.cs[(size_t)s.pos * half + i];
-        const float ev = qh[d.DN + 2 * i], od = qh[d.DN + 2 * i + 1];
+    if (tid < half) {  // half <= kMaxDR / 2 < 256
+        const int i = tid;
+        const float2 cs = csv;
+        const float ev = qr[2 * i], od = qr[2 * i + 1];
         const float ec = ev * cs.x, os = od * cs.y, oc = od * cs.x, es = ev * cs.y;
         const float r0 = ec - os, r1 = oc + es;
         qrow[roff + i] = r0;
@@ -559,6 +794,8 @@ static QprepArgs qprep_args(int fmt, const Dims &d, const uint16_t *kv_b, const 
     a.qrhi = w.qrhi;
     a.qrlo = w.qrlo;
     a.ldy = d.QO + d.KVO;
+    a.np = w.ynp > 1 ? w.ynp : 1;
+    a.pstride = w.ypstride;
     a.fmt = fmt;
     a.quantize = quantize ? 1 : 0;
     return a;
@@ -574,11 +811,13 @@ hipError_t launch_qprep(hipStream_t st, int fmt, const SeqTable &t, const Dims &
 }
 
 hipError_t launch_append_qprep(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
-                               const float *y, int ldy, int koff, const uint16_t *kv_a_norm, float eps,
-                               const float2 *rope_cs, const uint16_t *kv_b, const DecodeWork &w,
-                               bool quantize) {
-    if (d.R > kMaxR || d.DN > kMaxDN || d.DR > kMaxDR) return hipErrorInvalidValue;
-    const AppendArgs aa = append_args(fmt, d, y, ldy, koff, kv_a_norm, eps, rope_cs, w, false, 0);
+                               const float *y, int ldy, int koff, int ynp, size_t ypstride,
+                               const uint16_t *kv_a_norm, float eps, const float2 *rope_cs,
+                               const uint16_t *kv_b, const DecodeWork &w, bool quantize) {
+    if (d.R > kMaxR || d.DN > kMaxDN || d.DR > kMaxDR || (ynp != 1 && ynp != kGemvKs))
+        return hipErrorInvalidValue;
+    const AppendArgs aa = append_args(fmt, d, y, ldy, koff, ynp, ypstride, kv_a_norm, eps, rope_cs, w,
+                                      false, 0);
     const QprepArgs qa = qprep_args(fmt, d, kv_b, rope_cs, w, quantize);
     hipLaunchKernelGGL(k_append_qprep, dim3(t.n + t.n * d.NH), dim3(256), 0, st, t, d, aa, qa, t.n);
     return hipGetLastError();
@@ -1185,8 +1424,11 @@ struct CombineArgs {
     const uint16_t *kv_b;
     float *mix;
     float *ho;
+    uint16_t *hos;
     int fmt;
 };
+
+bool combine_writes_hos(int fmt, const Dims &d) { return fmt != kFmtExp && d.R == 512 && d.DV == 128; }
 
 // One block per (sequence, head). m* = max_s m_s, denom = sum_s l_s e^(m_s - m*),
 // mix = sum_s acc_s e^(m_s - m*) / denom; then (compressed formats)
@@ -1304,42 +1546,50 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
     }
 }
 
-// Compressed formats with R = 512, DV = 128: the same algebra with fewer serial phases.
-// Every thread first issues the loads that do not depend on the split weights (its W_UV
-// quarter row and the first partials of its latent column); meanwhile wave 0 reduces the
-// split maxima and denominators with shuffles (lane i handles splits i, i + 64, ...).
-// Thread k of 512 then mixes latent column k; thread t computes a quarter (128 columns) of
-// W_UV row t / 4, and the four quarters are summed with DPP moves.
+// Compressed formats with R = 512, DV = 128: the same algebra in fewer serial phases, over
+// 2 blocks per (sequence, head): block half computes the whole mix (thread k: latent column k)
+// and W_UV rows [64 half, 64 half + 64) of the head output. Wave 0 requests the split maxima
+// and denominators before anything else, so its wait covers one round trip; the W_UV slice
+// (thread t: row t / 8, columns 64 (t % 8) .. + 63) and the first 32 partials of each column
+// are requested meanwhile and consumed after the barrier. The head output is also written as
+// bf16 hi | lo planes (w.hos), the operand format of launch_gemv_xs.
+constexpr int kCombPre = 32;
 __global__ __launch_bounds__(512) void k_combine_r512(CombineArgs a) {
     __shared__ float mx[512];
     __shared__ float wts[kMaxSplits];
     __shared__ float sinv;
-    const int NH = a.d.NH;
-    const int b = blockIdx.x / NH, h = blockIdx.x % NH, tid = threadIdx.x;
+    const int NH = a.d.NH, tid = threadIdx.x;
+    const int half = blockIdx.x & 1, bh = blockIdx.x >> 1, b = bh / NH, h = bh % NH;
     const SeqDesc &s = a.t.s[b];
     const int ns = s.nsplit;
     const size_t stride = (size_t)NH * (512 + 2);
     const float *P = a.part + (size_t)s.split0 * stride;
-    // loads independent of the split weights
-    const int dd = tid >> 2, q = tid & 3;
-    const uint16_t *row = a.kv_b + ((size_t)h * (a.d.DN + 128) + a.d.DN + dd) * 512 + 128 * q;
-    v4i wv[16];
+    const float *Pm = P + (size_t)NH * 512 + h;  // split i: m at Pm[i * stride], l at + NH
+    const int i0 = min(tid, ns - 1);
+    const float m0 = Pm[(size_t)i0 * stride], l0 = Pm[(size_t)i0 * stride + NH];
+    const int dd = 64 * half + (tid >> 3), q = tid & 7;
+    const uint16_t *row = a.kv_b + ((size_t)h * (a.d.DN + 128) + a.d.DN + dd) * 512 + 64 * q;
+    v4i wv[8];
 #pragma unroll
-    for (int c = 0; c < 16; ++c) wv[c] = *(const v4i *)(row + 8 * c);
+    for (int c = 0; c < 8; ++c) wv[c] = *(const v4i *)(row + 8 * c);
     const float *Pg = P + (size_t)h * 512 + tid;
-    constexpr int kPre = 16;
-    float pre[kPre];
+    float pre[kCombPre];
 #pragma unroll
-    for (int i = 0; i < kPre; ++i) pre[i] = i < ns ? Pg[(size_t)i * stride] : 0.f;
+    for (int i = 0; i < kCombPre; ++i) pre[i] = Pg[(size_t)min(i, ns - 1) * stride];
     if (tid < 64) {
-        float m = -INFINITY;
-        for (int i = tid; i < ns; i += 64) m = fmaxf(m, P[i * stride + (size_t)NH * 512 + h]);
+        float m = tid < ns ? m0 : -INFINITY;
+        for (int i = tid + 64; i < ns; i += 64) m = fmaxf(m, Pm[(size_t)i * stride]);
         m = wave_max(m);
         float den = 0.f;
-        for (int i = tid; i < ns; i += 64) {
-            const float e = __expf(P[i * stride + (size_t)NH * 512 + h] - m);
+        if (tid < ns) {
+            const float e = __expf(m0 - m);
+            wts[tid] = e;
+            den = l0 * e;
+        }
+        for (int i = tid + 64; i < ns; i += 64) {
+            const float e = __expf(Pm[(size_t)i * stride] - m);
             wts[i] = e;
-            den = fmaf(P[i * stride + (size_t)NH * 512 + NH + h], e, den);
+            den = fmaf(Pm[(size_t)i * stride + NH], e, den);
         }
         den = wave_sum(den);
         if (tid == 0) sinv = 1.0f / den;
@@ -1347,17 +1597,17 @@ __global__ __launch_bounds__(512) void k_combine_r512(CombineArgs a) {
     __syncthreads();
     float v0 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f;
 #pragma unroll
-    for (int i = 0; i < kPre; i += 4) {
+    for (int i = 0; i < kCombPre; i += 4) {
         if (i < ns) v0 = fmaf(pre[i], wts[i], v0);
         if (i + 1 < ns) v1 = fmaf(pre[i + 1], wts[i + 1], v1);
         if (i + 2 < ns) v2 = fmaf(pre[i + 2], wts[i + 2], v2);
         if (i + 3 < ns) v3 = fmaf(pre[i + 3], wts[i + 3], v3);
     }
-    int i = kPre;
+    int i = kCombPre;
     for (; i + 8 <= ns; i += 8) {
         float p[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) p[q] = Pg[(size_t)(i + q) * stride];
+        for (int u = 0; u < 8; ++u) p[u] = Pg[(size_t)(i + u) * stride];
         v0 = fmaf(p[0], wts[i], v0);
         v1 = fmaf(p[1], wts[i + 1], v1);
         v2 = fmaf(p[2], wts[i + 2], v2);
@@ -1369,39 +1619,46 @@ __global__ __launch_bounds__(512) void k_combine_r512(CombineArgs a) {
     }
     for (; i < ns; ++i) v0 = fmaf(Pg[(size_t)i * stride], wts[i], v0);
     const float v = ((v0 + v1) + (v2 + v3)) * sinv;
-    a.mix[((size_t)b * NH + h) * 512 + tid] = v;
+    if (half == 0) a.mix[((size_t)b * NH + h) * 512 + tid] = v;
     mx[tid] = v;
     __syncthreads();
-    // W_UV row dd = tid / 4, columns 128 q .. 128 q + 127 (loaded above)
-    const float *mh = mx + 128 * q;
+    const float *mh = mx + 64 * q;
     float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
-    for (int c = 0; c < 16; ++c) {
-        const v4f m0 = *(const v4f *)(mh + 8 * c);
-        const v4f m1 = *(const v4f *)(mh + 8 * c + 4);
+    for (int c = 0; c < 8; ++c) {
+        const v4f m0v = *(const v4f *)(mh + 8 * c);
+        const v4f m1v = *(const v4f *)(mh + 8 * c + 4);
         const uint32_t u0 = (uint32_t)wv[c][0], u1 = (uint32_t)wv[c][1];
         const uint32_t u2 = (uint32_t)wv[c][2], u3 = (uint32_t)wv[c][3];
-        acc0 = fmaf(__uint_as_float(u0 << 16), m0.x, acc0);
-        acc1 = fmaf(__uint_as_float(u0 & 0xffff0000u), m0.y, acc1);
-        acc0 = fmaf(__uint_as_float(u1 << 16), m0.z, acc0);
-        acc1 = fmaf(__uint_as_float(u1 & 0xffff0000u), m0.w, acc1);
-        acc0 = fmaf(__uint_as_float(u2 << 16), m1.x, acc0);
-        acc1 = fmaf(__uint_as_float(u2 & 0xffff0000u), m1.y, acc1);
-        acc0 = fmaf(__uint_as_float(u3 << 16), m1.z, acc0);
-        acc1 = fmaf(__uint_as_float(u3 & 0xffff0000u), m1.w, acc1);
+        acc0 = fmaf(__uint_as_float(u0 << 16), m0v.x, acc0);
+        acc1 = fmaf(__uint_as_float(u0 & 0xffff0000u), m0v.y, acc1);
+        acc0 = fmaf(__uint_as_float(u1 << 16), m0v.z, acc0);
+        acc1 = fmaf(__uint_as_float(u1 & 0xffff0000u), m0v.w, acc1);
+        acc0 = fmaf(__uint_as_float(u2 << 16), m1v.x, acc0);
+        acc1 = fmaf(__uint_as_float(u2 & 0xffff0000u), m1v.y, acc1);
+        acc0 = fmaf(__uint_as_float(u3 << 16), m1v.z, acc0);
+        acc1 = fmaf(__uint_as_float(u3 & 0xffff0000u), m1v.w, acc1);
     }
     float acc = acc0 + acc1;
-    acc += dpp_f32<0xB1>(acc);  // quad_perm [1,0,3,2]
-    acc += dpp_f32<0x4E>(acc);  // quad_perm [2,3,0,1]
-    if (q == 0) a.ho[(size_t)b * a.d.HO + (size_t)h * 128 + dd] = acc;
+    acc += dpp_f32<0xB1>(acc);   // quad_perm [1,0,3,2]: lanes t ^ 1
+    acc += dpp_f32<0x4E>(acc);   // quad_perm [2,3,0,1]: lanes t ^ 2
+    acc += dpp_f32<0x12C>(acc);  // row_ror:12 (lane i reads lane i + 4 of its row): t % 8 == 0 completes
+    if (q == 0) {
+        const size_t o = (size_t)b * a.d.HO + (size_t)h * 128 + dd;
+        a.ho[o] = acc;
+        uint16_t hi, lo;
+        split_bf16(acc, hi, lo);
+        a.hos[o] = hi;
+        a.hos[(size_t)a.t.n * a.d.HO + o] = lo;
+    }
 }
 
 hipError_t launch_combine(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
                           const uint16_t *kv_b, const DecodeWork &w) {
     if (d.R > kMaxR) return hipErrorInvalidValue;
-    CombineArgs a{t, d, w.part, kv_b, w.mix, w.ho, fmt};
-    if (fmt != kFmtExp && d.R == 512 && d.DV == 128)
-        hipLaunchKernelGGL(k_combine_r512, dim3(t.n * d.NH), dim3(512), 0, st, a);
+    CombineArgs a{t, d, w.part, kv_b, w.mix, w.ho, w.hos, fmt};
+    if (combine_writes_hos(fmt, d))
+        hipLaunchKernelGGL(k_combine_r512, dim3(2 * t.n * d.NH), dim3(512), 0, st, a);
     else
         hipLaunchKernelGGL(k_combine, dim3(t.n * d.NH), dim3(256), 0, st, a);
     return hipGetLastError();

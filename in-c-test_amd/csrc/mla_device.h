@@ -54,6 +54,25 @@ __device__ __forceinline__ void split8(const v4f &x0, const v4f &x1, v8bf &hi, v
     lo = __builtin_bit_cast(v8bf, lv);
 }
 
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+
+// One half of the split x ~= hi + lo of 8 fp32 values as a bf16x8 MFMA operand: part 0 the hi
+// halves, part 1 the lo halves (both round to nearest even, v_cvt_pk_bf16_f32). Finite inputs.
+__device__ __forceinline__ v8bf split8_part(const v4f &x0, const v4f &x1, int part) {
+    const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    v4i o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const v2f p = {x[2 * j], x[2 * j + 1]};
+        const uint32_t hu = __builtin_bit_cast(uint32_t, __builtin_convertvector(p, v2bf));
+        const v2f r = {x[2 * j] - __uint_as_float(hu << 16), x[2 * j + 1] - __uint_as_float(hu & 0xffff0000u)};
+        const uint32_t lu = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, v2bf));
+        o[j] = (int)(part ? lu : hu);
+    }
+    return __builtin_bit_cast(v8bf, o);
+}
+
 __device__ __forceinline__ v4f mfma_bf16(const v8bf &a, const v8bf &b, const v4f &c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }

@@ -48,7 +48,9 @@ struct SeqTable {
 // Device workspace of one decode launch group (all pointers device memory).
 struct DecodeWork {
     float *x;        // [B,H]      input hidden states
-    float *y;        // [B,QO+KVO] q_proj | kv_a outputs
+    float *y;        // [ynp][B,QO+KVO] q_proj | kv_a outputs: ynp partials ypstride apart
+    int ynp;         //            (their sum is the projection)
+    size_t ypstride;
     float *qf;       // [B,NH,QS]  per-head score-space query (fp32)
     int8_t *qhi;     // [B,NH,R]   Q8 fast path: int8 query, high part
     int8_t *qlo;     // [B,NH,R]   Q8 fast path: int8 query, low part (x1/128)
@@ -61,6 +63,7 @@ struct DecodeWork {
     float *scores;   // generic path: [P, G, Lmax] score scratch
     float *mix;      // [B*NH, DVm] normalised attention mix
     float *ho;       // [B,HO]     per-head outputs
+    uint16_t *hos;   // [2][B,HO]  the same as bf16 hi | lo planes (compressed formats, R = 512)
     float *out;      // [B,H]      layer output
     uint8_t *rows;   // [B,row bytes] copy of the appended history rows (host write-back)
 };
@@ -73,16 +76,34 @@ hipError_t launch_gemv(hipStream_t st, float *Y, int ldy, const float *X, int ld
                        const uint16_t *W0, int out0, const uint16_t *W1, int out1, int in,
                        bool accumulate);
 
+// Decode projection with the k range split over kGemvKs blocks: partial q of Y[b, o] at
+// Y[q * pstride + b * ldy + o]; the consumer adds the partials in q order. Shapes accepted
+// when gemv_ksplit_ok (in = 2048 or 4096; X and W 16-byte aligned), any B; otherwise
+// hipErrorInvalidValue. A sequence's result does not depend on B or its place in the batch,
+// so history rows appended by decode equal those the state prefill writes.
+constexpr int kGemvKs = 4;
+bool gemv_ksplit_ok(int in, int ldx);
+hipError_t launch_gemv_ksplit(hipStream_t st, float *Y, size_t pstride, int ldy, const float *X,
+                              int ldx, int B, const uint16_t *W0, int out0, const uint16_t *W1,
+                              int out1, int in);
+// Y[b, o] (+)= sum_k W[o, k] x[b, k] with x given as bf16 planes XS[2][B][in] (hi, lo), as
+// launch_combine writes them (DecodeWork::hos). Shapes when gemv_xs_ok (in = 2048 or 4096),
+// any B.
+bool gemv_xs_ok(int in);
+hipError_t launch_gemv_xs(hipStream_t st, float *Y, int ldy, const uint16_t *XS, int B,
+                          const uint16_t *W, int out, int in, bool accumulate);
+
 // RMSNorm of katmp[b] (= y + koff) -> latent row; RoPE of katmp[b][R:] at s.pos. Writes the
 // row into the history at row s.pos (fmt Q8/F32) or, for kFmtExp, the normalised latent
 // into w.latent and the rotated key into the tail of w.rows. A copy of the stored row goes
 // to w.rows for host write-back. rope_cs: [npos, DR/2] (cos, sin) pairs.
 // nrows > 0: rows mode, nrows rows of the single sequence t.s[0] starting at t.s[0].pos,
 // input row i at y + i*ldy, staged row i at w.rows + i*row_bytes.
+// y holds ynp (1 or kGemvKs) partials ypstride floats apart; their in-order sum is the input.
 hipError_t launch_append(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
-                         const float *y, int ldy, int koff, const uint16_t *kv_a_norm,
-                         float eps, const float2 *rope_cs, const DecodeWork &w, bool normed,
-                         int nrows);
+                         const float *y, int ldy, int koff, int ynp, size_t ypstride,
+                         const uint16_t *kv_a_norm, float eps, const float2 *rope_cs,
+                         const DecodeWork &w, bool normed, int nrows);
 
 // y[i] = RMSNorm(x[i]) * w for `rows` rows of length n (src/ops.c:76-83).
 hipError_t launch_rmsnorm(hipStream_t st, float *y, const float *x, const uint16_t *w, int n,
@@ -92,7 +113,8 @@ hipError_t launch_rmsnorm(hipStream_t st, float *y, const float *x, const uint16
 hipError_t launch_store_expanded(hipStream_t st, const SeqTable &t, const Dims &d,
                                  const DecodeWork &w);
 
-// Query preparation: absorbed q_lat = W_UK^T q_nope and RoPE(q_rope) per head (fmt Q8/F32),
+// Query preparation from w.y (w.ynp partials, w.ypstride apart): absorbed
+// q_lat = W_UK^T q_nope and RoPE(q_rope) per head (fmt Q8/F32),
 // or [q_nope | RoPE(q_rope)] (kFmtExp). quantize=true also builds the int8/bf16 split
 // operands of the Q8 MFMA attention kernel.
 hipError_t launch_qprep(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
@@ -100,9 +122,9 @@ hipError_t launch_qprep(hipStream_t st, int fmt, const SeqTable &t, const Dims &
                         bool quantize);
 // launch_append (one row per sequence) and launch_qprep as one launch.
 hipError_t launch_append_qprep(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
-                               const float *y, int ldy, int koff, const uint16_t *kv_a_norm, float eps,
-                               const float2 *rope_cs, const uint16_t *kv_b, const DecodeWork &w,
-                               bool quantize);
+                               const float *y, int ldy, int koff, int ynp, size_t ypstride,
+                               const uint16_t *kv_a_norm, float eps, const float2 *rope_cs,
+                               const uint16_t *kv_b, const DecodeWork &w, bool quantize);
 
 // Split-K attention over the history; writes partials (acc | m | l) per split.
 // kind: 0 = generic VALU (any dims, one split per problem), 1 = fp32 MFMA (Kimi dims),
@@ -114,6 +136,8 @@ hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t
 
 // Normalise the split partials into mix[(b*G + g), DVm] and, for the compressed formats,
 // apply W_UV: ho[b, h*DV + d] = sum_r kv_b[h*(DN+DV) + DN + d, r] * mix[b*NH + h, r].
+// When combine_writes_hos(fmt, d), ho is also written to w.hos as bf16 hi | lo planes.
+bool combine_writes_hos(int fmt, const Dims &d);
 hipError_t launch_combine(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
                           const uint16_t *kv_b, const DecodeWork &w);
 

@@ -524,7 +524,9 @@ int decode_work(const Dims &d, int B, int row_bytes, DecodeWork &w) {
     const size_t qs = (size_t)std::max(d.R + d.DR, d.QD);
     auto carve = [&](char *base, Layout &L) {
         w.x = L.take<float>(base, (size_t)B * d.H);
-        w.y = L.take<float>(base, (size_t)B * (d.QO + d.KVO));
+        w.y = L.take<float>(base, (size_t)kGemvKs * B * (d.QO + d.KVO));  // room for the partials
+        w.ynp = 1;
+        w.ypstride = 0;
         w.qf = L.take<float>(base, (size_t)B * d.NH * qs);
         w.qhi = L.take<int8_t>(base, (size_t)B * d.NH * d.R);
         w.qlo = L.take<int8_t>(base, (size_t)B * d.NH * d.R);
@@ -535,6 +537,7 @@ int decode_work(const Dims &d, int B, int row_bytes, DecodeWork &w) {
         w.kv = L.take<float>(base, (size_t)B * d.KVB);
         w.mix = L.take<float>(base, (size_t)B * d.NH * std::max(d.R, d.DV));
         w.ho = L.take<float>(base, (size_t)B * d.HO);
+        w.hos = L.take<uint16_t>(base, (size_t)2 * B * d.HO);
         w.out = L.take<float>(base, (size_t)B * d.H);
         w.rows = L.take<uint8_t>(base, (size_t)B * row_bytes);
     };
@@ -652,13 +655,29 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
 
     const int ldy = d.QO + d.KVO;
     {
+        // q_proj | kv_a: k split over kGemvKs blocks where the shape allows (the consumers
+        // add the partials), else one pass
         StageTimer tm(0);
-        HIP_TRY(launch_gemv(st, w.y, ldy, d_x, d.H, B, dw.q, d.QO, dw.kva, d.KVO, d.H, false));
+        if (gemv_ksplit_ok(d.H, d.H)) {
+            if (((uintptr_t)d_x % 16) != 0) {  // the kernel reads 16-byte vectors
+                HIP_TRY(hipMemcpyAsync(w.x, d_x, (size_t)B * d.H * sizeof(float), hipMemcpyDeviceToDevice, st));
+                d_x = w.x;
+            }
+            w.ynp = kGemvKs;
+            w.ypstride = (size_t)B * ldy;
+            HIP_TRY(launch_gemv_ksplit(st, w.y, w.ypstride, ldy, d_x, d.H, B, dw.q, d.QO, dw.kva,
+                                       d.KVO, d.H));
+        } else {
+            w.ynp = 1;
+            w.ypstride = 0;
+            HIP_TRY(launch_gemv(st, w.y, ldy, d_x, d.H, B, dw.q, d.QO, dw.kva, d.KVO, d.H, false));
+        }
     }
     if (fmt == kFmtExp) {
         {
             StageTimer tm(1);
-            HIP_TRY(launch_append(st, fmt, t, d, w.y, ldy, d.QO, dw.norm, eps, cs, w, false, 0));
+            HIP_TRY(launch_append(st, fmt, t, d, w.y, ldy, d.QO, w.ynp, w.ypstride, dw.norm, eps, cs,
+                                  w, false, 0));
             HIP_TRY(launch_gemv(st, w.kv, d.KVB, w.latent, d.R, B, dw.kvb, d.KVB, nullptr, 0, d.R, false));
             HIP_TRY(launch_store_expanded(st, t, d, w));
         }
@@ -669,7 +688,7 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
     } else {
         // append and query preparation in one launch (timed as stage 1)
         StageTimer tm(1);
-        HIP_TRY(launch_append_qprep(st, fmt, t, d, w.y, ldy, d.QO, dw.norm, eps, cs, dw.kvb, w,
+        HIP_TRY(launch_append_qprep(st, fmt, t, d, w.y, ldy, d.QO, w.ynp, w.ypstride, dw.norm, eps, cs, dw.kvb, w,
                                     kind == kAttnQ8Mfma));
     }
     {
@@ -681,8 +700,12 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
         HIP_TRY(launch_combine(st, fmt, t, d, dw.kvb, w));
     }
     {
+        // o_proj: from the bf16 hi | lo planes of the head outputs when combine wrote them
         StageTimer tm(5);
-        HIP_TRY(launch_gemv(st, d_out, d.H, w.ho, d.HO, B, dw.o, d.H, nullptr, 0, d.HO, residual));
+        if (combine_writes_hos(fmt, d) && gemv_xs_ok(d.HO))
+            HIP_TRY(launch_gemv_xs(st, d_out, d.H, w.hos, B, dw.o, d.H, d.HO, residual));
+        else
+            HIP_TRY(launch_gemv(st, d_out, d.H, w.ho, d.HO, B, dw.o, d.H, nullptr, 0, d.HO, residual));
     }
     return 0;
 }
@@ -878,22 +901,31 @@ int state_prefill(const float *x, int seq_len, const KvlMlaConfig *cfg, const Kv
     const int chunk = 4096;
     for (int t0 = 0; t0 < seq_len; t0 += chunk) {
         const int n = std::min(chunk, seq_len - t0);
+        // kv_a with the decode path's arithmetic (k-split partials where the decode uses them),
+        // so that these rows equal the rows a decode of the same tokens appends
+        const bool ks = gemv_ksplit_ok(H, H);
+        const int np = ks ? kGemvKs : 1;
         Layout L;
         L.take<float>(nullptr, (size_t)n * H);
-        L.take<float>(nullptr, (size_t)n * d.KVO);
+        L.take<float>(nullptr, (size_t)np * n * d.KVO);
         L.take<uint8_t>(nullptr, (size_t)n * rb);
         if (dev_reserve(c.prefill, L.off) != 0) return -1;
         Layout L2;
         char *base = (char *)c.prefill.p;
         float *dx = L2.take<float>(base, (size_t)n * H);
-        float *dy = L2.take<float>(base, (size_t)n * d.KVO);
+        float *dy = L2.take<float>(base, (size_t)np * n * d.KVO);
         uint8_t *drows = L2.take<uint8_t>(base, (size_t)n * rb);
         HIP_TRY(hipMemcpyAsync(dx, x + (size_t)t0 * H, (size_t)n * H * sizeof(float),
                                hipMemcpyHostToDevice, c.stream));
-        for (int b0 = 0; b0 < n; b0 += 16 * 65535) {
-            const int nb = std::min(n - b0, 16 * 65535);
-            HIP_TRY(launch_gemv(c.stream, dy + (size_t)b0 * d.KVO, d.KVO, dx + (size_t)b0 * H, H, nb,
-                                kva, d.KVO, nullptr, 0, H, false));
+        if (ks) {
+            HIP_TRY(launch_gemv_ksplit(c.stream, dy, (size_t)n * d.KVO, d.KVO, dx, H, n, kva, d.KVO,
+                                       nullptr, 0, H));
+        } else {
+            for (int b0 = 0; b0 < n; b0 += 16 * 65535) {
+                const int nb = std::min(n - b0, 16 * 65535);
+                HIP_TRY(launch_gemv(c.stream, dy + (size_t)b0 * d.KVO, d.KVO, dx + (size_t)b0 * H, H, nb,
+                                    kva, d.KVO, nullptr, 0, H, false));
+            }
         }
         SeqTable t;
         memset(&t, 0, sizeof t);
@@ -904,7 +936,8 @@ int state_prefill(const float *x, int seq_len, const KvlMlaConfig *cfg, const Kv
         t.s[0].pos = t0;
         DecodeWork wk{};
         wk.rows = drows;
-        HIP_TRY(launch_append(c.stream, fmt, t, d, dy, d.KVO, 0, norm, cfg->rms_eps, cs, wk, false, n));
+        HIP_TRY(launch_append(c.stream, fmt, t, d, dy, d.KVO, 0, np, (size_t)n * d.KVO, norm, cfg->rms_eps, cs,
+                              wk, false, n));
         if (pin_reserve(c.pin_out, (size_t)n * rb) != 0) return -1;
         HIP_TRY(hipMemcpyAsync(c.pin_out.p, drows, (size_t)n * rb, hipMemcpyDeviceToHost, c.stream));
         HIP_TRY(hipStreamSynchronize(c.stream));
@@ -1503,8 +1536,8 @@ int kvl_mla_q8_pack_rows(int8_t *codes, float *scales, uint16_t *rope_bf16, cons
         }
         DecodeWork wk{};
         wk.rows = drows + (size_t)g0 * rb;
-        HIP_TRY(launch_append(c.stream, kFmtQ8, t, d, din + (size_t)g0 * KVO, KVO, 0, nullptr, 0.f, cs, wk,
-                              true, 0));
+        HIP_TRY(launch_append(c.stream, kFmtQ8, t, d, din + (size_t)g0 * KVO, KVO, 0, 1, 0, nullptr, 0.f, cs,
+                              wk, true, 0));
     }
     std::vector<uint8_t> hrows((size_t)n * rb);
     HIP_TRY(hipMemcpyAsync(hrows.data(), drows, hrows.size(), hipMemcpyDeviceToHost, c.stream));
