@@ -609,7 +609,8 @@ struct QprepArgs {
 // One block per (sequence, head). Compressed formats: q_lat[r] = sum_d
 // kv_b[h*(DN+DV)+d, r] * q_nope[d] (src/mla_compressed_q8_state.c:206-214), q_rope rotated
 // at the decode position; qf row = [q_lat | q_rope]. Expanded: qf row = [q_nope | q_rope].
-// With `quantize`, q_lat ~= qs * (hi + lo/128) (int8 hi, lo) and q_rope = hi + lo (bf16).
+// With `quantize`, q_lat ~= qs * (hi + lo/254) (int8 hi, lo) and q_rope / sqrt(QD) = hi + lo
+// (bf16).
 __device__ __forceinline__ void qprep_body(const SeqTable &t, const Dims &d, const QprepArgs &a, int blk) {
     __shared__ float qn[kMaxDN];
     __shared__ float qr[kMaxDR];  // RoPE input of the head
@@ -734,12 +735,14 @@ __device__ __forceinline__ void qprep_body(const SeqTable &t, const Dims &d, con
         qrow[roff + i] = r0;
         qrow[roff + half + i] = r1;
         if (a.quantize) {
+            // the bf16 hi/lo operands of the Q8 attention carry the softmax scale 1/sqrt(QD)
             uint16_t hi, lo;
             const size_t o = ((size_t)b * d.NH + h) * d.DR;
-            split_bf16(r0, hi, lo);
+            const float qsc = 1.0f / sqrtf((float)d.QD);
+            split_bf16(r0 * qsc, hi, lo);
             a.qrhi[o + i] = hi;
             a.qrlo[o + i] = lo;
-            split_bf16(r1, hi, lo);
+            split_bf16(r1 * qsc, hi, lo);
             a.qrhi[o + half + i] = hi;
             a.qrlo[o + half + i] = lo;
         }
@@ -762,7 +765,7 @@ __device__ __forceinline__ void qprep_body(const SeqTable &t, const Dims &d, con
         const float v = ql[r] * inv;
         float hi = rintf(v);
         hi = fminf(fmaxf(hi, -127.f), 127.f);
-        float lo = rintf((v - hi) * 128.0f);
+        float lo = rintf((v - hi) * 254.0f);  // |v - hi| <= 1/2: lo spans the int8 range
         lo = fminf(fmaxf(lo, -127.f), 127.f);
         a.qhi[o + r] = (int8_t)hi;
         a.qlo[o + r] = (int8_t)lo;
@@ -1065,15 +1068,19 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
 // Scores (wave w: rows 16w..16w+15): v_mfma_i32_16x16x64_i8 on the raw int8 codes against
 // the int8 hi/lo split of q_lat (exact integer dot products), plus bf16 MFMA on the bf16
 // RoPE keys against the hi/lo bf16 split of q_rope. The row scale factors out of the dot
-// (score_j = s_j * q_lat . c_j + q_rope . k_j). Mix: the weights p_j*s_j (p_j <= 1 after
-// the reference max, s_j <= the split's largest scale) are quantised to int8 hi + lo/128
-// against that scale; ds_read_b64_tr_b8 reads the codes transposed (16 rows of one column
-// per lane), and v_mfma_i32_16x16x64_i8 accumulates the exact integer mix in place across
-// chunks. A head's reference max only moves when a chunk exceeds it by more than ln 2
-// (so p_j <= 2 and the weights are bounded by 2 * largest scale); its integer accumulators
+// (score_j = s_j * q_lat . c_j + q_rope . k_j). Mix: the weights p_j*s_j (p_j <= kQ8Pmax
+// against the lazily moved reference max below, s_j <= the split's largest scale) are
+// quantised to int8 hi + lo/254 against kQ8Pmax * that scale; ds_read_b64_tr_b8 reads the
+// codes transposed (16 rows of one column per lane), and v_mfma_i32_16x16x64_i8 accumulates
+// the exact integer mix in place across chunks. A head's reference max only moves when a
+// chunk exceeds it by more than ln kQ8Pmax (so p_j <= kQ8Pmax); its integer accumulators
 // are then rescaled by alpha = exp(m_old - m_new) (rounded, below 2^-17 of the sums).
+// kQ8Pmax = 4 keeps the weights' resolution of the earlier p_j <= 2, lo/128 scheme while
+// rescales become rare (they cost a pass over the accumulators).
 // Each wave accumulates 128 latent columns.
 constexpr int kQ8Ch = 64;
+constexpr float kQ8Pmax = 4.0f;            // bound of p_j = exp(s_j - reference max)
+constexpr float kQ8LnPmax = 1.3862944f;    // ln kQ8Pmax
 constexpr int kQ8Ring = 3;
 constexpr int kQ8MaxSplitRows = 2048;               // rows of one split (scales table)
 constexpr int kQ8CodeB = kQ8Ch * 512;               // codes of a chunk
@@ -1090,6 +1097,32 @@ constexpr int kQ8SmemB = kQ8QOff + kQ8QB;
 
 // Slot swizzle of the code rows: physical 16-byte slot = logical slot ^ q8_swz(row).
 __device__ __forceinline__ int q8_swz(int row) { return (row & 7) ^ (((row >> 4) & 1) << 2); }
+
+// Maxima over the 16 lanes of each DPP row for four values: one v_max_f32_dpp per step and
+// value (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_ror:4, row_ror:8), the four chains
+// interleaved so that each DPP source was written at least three instructions earlier.
+__device__ __forceinline__ void row16_max4(float &a, float &b, float &c, float &d) {
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_max_f32_dpp %0, %0, %0 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "v_max_f32_dpp %1, %1, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "v_max_f32_dpp %2, %2, %2 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "v_max_f32_dpp %3, %3, %3 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "v_max_f32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+        "v_max_f32_dpp %1, %1, %1 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+        "v_max_f32_dpp %2, %2, %2 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+        "v_max_f32_dpp %3, %3, %3 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+        "v_max_f32_dpp %0, %0, %0 row_ror:4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_max_f32_dpp %1, %1, %1 row_ror:4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_max_f32_dpp %2, %2, %2 row_ror:4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_max_f32_dpp %3, %3, %3 row_ror:4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_max_f32_dpp %0, %0, %0 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_max_f32_dpp %1, %1, %1 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_max_f32_dpp %2, %2, %2 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_max_f32_dpp %3, %3, %3 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1"
+        : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+}
 
 typedef int v2i __attribute__((ext_vector_type(2)));
 // ds_read_b64_tr_b8: within each 16-lane group, destination lane j byte i comes from the
@@ -1210,18 +1243,18 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
 
     // ---- per-lane LDS offsets within a ring slot
     const int rowl = 16 * w + n;  // score row of this lane
-    int sc_off[8], rp_off[2], tr_off[8][2];
+    // slot (4 kb + g) ^ s with s < 8: kb and kb + 2 differ by 8 slots, so two bases serve all kb
+    int sc_base[2], rp_off[2], tr_off[8];
 #pragma unroll
-    for (int kb = 0; kb < 8; ++kb) sc_off[kb] = rowl * 512 + 16 * ((4 * kb + g) ^ q8_swz(rowl));
+    for (int kb = 0; kb < 2; ++kb) sc_base[kb] = rowl * 512 + 16 * ((4 * kb + g) ^ q8_swz(rowl));
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) rp_off[kb] = kQ8CodeB + rowl * 128 + 16 * ((4 * kb + g) ^ (rowl & 7));
+    // rows 16g + (n >> 1) and 16g + 8 + (n >> 1) share the swizzle: the second half is + 4096
 #pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            const int row = 16 * g + 8 * hf + (n >> 1);
-            tr_off[t][hf] = row * 512 + 16 * ((8 * w + t) ^ q8_swz(row)) + 8 * (n & 1);
-        }
+    for (int t = 0; t < 8; ++t) {
+        const int row = 16 * g + (n >> 1);
+        tr_off[t] = row * 512 + 16 * ((8 * w + t) ^ q8_swz(row)) + 8 * (n & 1);
+    }
     const int wq_off = n * kQ8Ws + 16 * g;
 
     auto chunk = [&](auto slot_tag, int c) {
@@ -1241,7 +1274,7 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
         v4f fr = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kb = 0; kb < 8; ++kb) {
-            const v4i bv = *(const v4i *)(buf + sc_off[kb]);
+            const v4i bv = *(const v4i *)(buf + sc_base[kb & 1] + 128 * (kb >> 1));
             ih = mfma_i8(qh[kb], bv, ih);
             il = mfma_i8(ql[kb], bv, il);
         }
@@ -1253,37 +1286,50 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
         }
         const float sj = sclv[c * kQ8Ch + rowl];
         const bool valid = base + rowl < r1;
-        float sc[4], lm[4];
+        float sc[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float dot = fmaf((float)il[i], 0.0078125f, (float)ih[i]);
-            sc[i] = valid ? fmaf(qsd[i] * sj, dot, fr[i] * a.smscale) : -INFINITY;
-            lm[i] = row16_max(sc[i]);
+            // 254 ih + il is exact in int32 (|ih|, |il| <= 512 * 127 * 127, so |254 ih + il|
+            // <= 2.106e9 < 2^31); qsd carries the 1/254
+            const float dot = (float)(ih[i] * 254 + il[i]);
+            const float sv = fmaf(qsd[i] * sj, dot, fr[i]);
+            sc[i] = valid ? sv : -INFINITY;
         }
-        if (n == 0)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) ml[w * 16 + 4 * g + i] = lm[i];
+        float lm[4] = {sc[0], sc[1], sc[2], sc[3]};
+        row16_max4(lm[0], lm[1], lm[2], lm[3]);
+        if (n == 0) *(v4f *)(ml + w * 16 + 4 * g) = v4f{lm[0], lm[1], lm[2], lm[3]};
         lds_barrier();
 
+        // the four waves' chunk maxima of this lane's heads 4g .. 4g+3, all read before the
+        // quantised weights are written (the compiler cannot move reads across those writes)
+        const v4f mw0 = *(const v4f *)(ml + 4 * g), mw1 = *(const v4f *)(ml + 16 + 4 * g);
+        const v4f mw2 = *(const v4f *)(ml + 32 + 4 * g), mw3 = *(const v4f *)(ml + 48 + 4 * g);
+        const float swj = sj * wscale;
         float alpha[4];
+        int qhv[4], qlv[4];
         bool moved = false;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int hh = 4 * g + i;
-            const float cm = fmaxf(fmaxf(ml[hh], ml[16 + hh]), fmaxf(ml[32 + hh], ml[48 + hh]));
-            // lazy reference max: moves only when the chunk max exceeds it by > ln 2
-            const bool mv = cm > m_run[i] + 0.6931472f;
+            const float cm = fmaxf(fmaxf(mw0[i], mw1[i]), fmaxf(mw2[i], mw3[i]));
+            // lazy reference max: moves only when the chunk max exceeds it by > ln kQ8Pmax; the
+            // first finite maximum of a head needs no rescale (nothing is accumulated before it)
+            const bool mv = cm > m_run[i] + kQ8LnPmax;
+            const bool rs = mv && m_run[i] != -INFINITY;
             const float mnew = mv ? cm : m_run[i];
-            alpha[i] = mv ? __expf(m_run[i] - mnew) : 1.0f;
-            moved |= mv;
+            alpha[i] = rs ? __expf(m_run[i] - mnew) : 1.0f;
+            moved |= rs;
             m_run[i] = mnew;
             const float p = __expf(sc[i] - mnew);
             l_lane[i] = fmaf(l_lane[i], alpha[i], p);
-            const float v = p * sj * wscale;
+            const float v = p * swj;
             const float hi = fminf(rintf(v), 127.f);
-            const float lo = rintf((v - hi) * 128.0f);
-            wqc[hh * kQ8Ws + rowl] = (int8_t)hi;
-            wqc[16 * kQ8Ws + hh * kQ8Ws + rowl] = (int8_t)lo;
+            qhv[i] = (int)hi;
+            qlv[i] = (int)rintf((v - hi) * 254.0f);  // |v - hi| <= 1/2: lo spans the int8 range
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            wqc[(4 * g + i) * kQ8Ws + rowl] = (int8_t)qhv[i];
+            wqc[16 * kQ8Ws + (4 * g + i) * kQ8Ws + rowl] = (int8_t)qlv[i];
         }
         if (__any(moved)) {
 #pragma unroll
@@ -1301,8 +1347,8 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
         const v4i wl = *(const v4i *)(wqc + 16 * kQ8Ws + wq_off);
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            const v2i b0 = lds_read_tr8(buf + tr_off[t][0]);
-            const v2i b1 = lds_read_tr8(buf + tr_off[t][1]);
+            const v2i b0 = lds_read_tr8(buf + tr_off[t]);
+            const v2i b1 = lds_read_tr8(buf + tr_off[t] + 4096);
             const v4i bt = {b0.x, b0.y, b1.x, b1.y};
             ahi[t] = mfma_i8(wh, bt, ahi[t]);
             alo[t] = mfma_i8(wl, bt, alo[t]);
@@ -1335,7 +1381,7 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
         qrl[kb] = *(const v8bf *)(sq + 2048 + o);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qsd[i] = ((const float *)(sq + 20480))[4 * g + i] * a.smscale;
+    for (int i = 0; i < 4; ++i) qsd[i] = ((const float *)(sq + 20480))[4 * g + i] * (a.smscale / 254.0f);
     // largest row scale of the split: the common bound of the quantised weights
     float smax;
     {
@@ -1346,9 +1392,9 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
         lds_barrier();
         smax = fmaxf(fmaxf(smx[0], smx[1]), fmaxf(smx[2], smx[3]));
     }
-    // p_j <= 2 relative to the reference max (see the lazy max below)
-    wscale = smax > 0.f ? 127.0f / (2.0f * smax) : 0.f;
-    wfac = 2.0f * smax * (1.0f / (127.0f * 128.0f));
+    // p_j <= kQ8Pmax relative to the reference max (see the lazy max below)
+    wscale = smax > 0.f ? 127.0f / (kQ8Pmax * smax) : 0.f;
+    wfac = kQ8Pmax * smax * (1.0f / (127.0f * 254.0f));
     int c = 0;
     for (; c + 3 <= nch; c += 3) {
         chunk(S0{}, c);
@@ -1370,7 +1416,7 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
         const int r = 128 * w + 16 * t + n;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            P[(4 * g + i) * 512 + r] = wfac * fmaf((float)ahi[t][i], 128.0f, (float)alo[t][i]);
+            P[(4 * g + i) * 512 + r] = wfac * fmaf((float)ahi[t][i], 254.0f, (float)alo[t][i]);
     }
     if (w == 0 && n == 0) {
 #pragma unroll
