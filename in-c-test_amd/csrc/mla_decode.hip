@@ -1137,6 +1137,7 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
     float *mloc = (float *)(smem + kQ8MlOff);  // [2 parities][4 waves][16]
     float *lsum = mloc + 128;                  // [4 waves][16]
     float *smx = mloc + 192;                   // [4 waves]
+    int *oflag = (int *)(mloc + 200);          // [4 waves]: a row exceeds the reference max
     const uint32_t sbase = lds_addr(smem);
     const float *sclv = (const float *)(smem + kQ8SclOff);  // scales of the split's rows
     const int tid = threadIdx.x, l = tid & 63, n = l & 15, g = l >> 4;
@@ -1270,23 +1271,38 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
         float *ml = mloc + 64 * (c & 1);
         int8_t *wqc = wq + (c & 1) * kQ8WqB;
 
+        // this chunk's LDS operands: the score rows of this lane, then the transposed codes
+        // of the mix (independent of the weights, so their latency hides behind the scores)
+        v4i bv[8];
+        v8bf rv[2];
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) bv[kb] = *(const v4i *)(buf + sc_base[kb & 1] + 128 * (kb >> 1));
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) rv[kb] = *(const v8bf *)(buf + rp_off[kb]);
+        v4i bt[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const v2i b0 = lds_read_tr8(buf + tr_off[t]);
+            const v2i b1 = lds_read_tr8(buf + tr_off[t] + 4096);
+            bt[t] = v4i{b0.x, b0.y, b1.x, b1.y};
+        }
         v4i ih = {0, 0, 0, 0}, il = {0, 0, 0, 0};
         v4f fr = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kb = 0; kb < 8; ++kb) {
-            const v4i bv = *(const v4i *)(buf + sc_base[kb & 1] + 128 * (kb >> 1));
-            ih = mfma_i8(qh[kb], bv, ih);
-            il = mfma_i8(ql[kb], bv, il);
+            ih = mfma_i8(qh[kb], bv[kb], ih);
+            il = mfma_i8(ql[kb], bv[kb], il);
         }
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
-            const v8bf bv = *(const v8bf *)(buf + rp_off[kb]);
-            fr = mfma_bf16(qrh[kb], bv, fr);
-            fr = mfma_bf16(qrl[kb], bv, fr);
+            fr = mfma_bf16(qrh[kb], rv[kb], fr);
+            fr = mfma_bf16(qrl[kb], rv[kb], fr);
         }
         const float sj = sclv[c * kQ8Ch + rowl];
         const bool valid = base + rowl < r1;
-        float sc[4];
+        const float swj = sj * wscale;
+        float sc[4], pv[4];
+        bool over = false;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             // 254 ih + il is exact in int32 (|ih|, |il| <= 512 * 127 * 127, so |254 ih + il|
@@ -1294,64 +1310,82 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
             const float dot = (float)(ih[i] * 254 + il[i]);
             const float sv = fmaf(qsd[i] * sj, dot, fr[i]);
             sc[i] = valid ? sv : -INFINITY;
+            // weights against the current reference max; a row above it by more than
+            // ln kQ8Pmax (every valid row of the first chunk, where it is -inf) sends the block
+            // through the exchange below
+            over |= sc[i] > m_run[i] + kQ8LnPmax;
+            pv[i] = __expf(sc[i] - m_run[i]);
         }
-        float lm[4] = {sc[0], sc[1], sc[2], sc[3]};
-        row16_max4(lm[0], lm[1], lm[2], lm[3]);
-        if (n == 0) *(v4f *)(ml + w * 16 + 4 * g) = v4f{lm[0], lm[1], lm[2], lm[3]};
+        auto put_weights = [&]() __attribute__((always_inline)) {
+            int qhv[4], qlv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float v = pv[i] * swj;
+                const float hi = fminf(rintf(v), 127.f);
+                qhv[i] = (int)hi;
+                qlv[i] = (int)rintf((v - hi) * 254.0f);  // |v - hi| <= 1/2: lo spans the int8 range
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                wqc[(4 * g + i) * kQ8Ws + rowl] = (int8_t)qhv[i];
+                wqc[16 * kQ8Ws + (4 * g + i) * kQ8Ws + rowl] = (int8_t)qlv[i];
+            }
+        };
+        put_weights();
+        const bool wover = __any(over);
+        if (l == 0) oflag[w] = wover ? 1 : 0;
         lds_barrier();
-
-        // the four waves' chunk maxima of this lane's heads 4g .. 4g+3, all read before the
-        // quantised weights are written (the compiler cannot move reads across those writes)
-        const v4f mw0 = *(const v4f *)(ml + 4 * g), mw1 = *(const v4f *)(ml + 16 + 4 * g);
-        const v4f mw2 = *(const v4f *)(ml + 32 + 4 * g), mw3 = *(const v4f *)(ml + 48 + 4 * g);
-        const float swj = sj * wscale;
-        float alpha[4];
-        int qhv[4], qlv[4];
-        bool moved = false;
+        // the flags and this lane's weights in one LDS round trip; the weights are read again
+        // after the rare exchange below
+        const v4i fl = *(const v4i *)oflag;
+        v4i wh = *(const v4i *)(wqc + wq_off);
+        v4i wl = *(const v4i *)(wqc + 16 * kQ8Ws + wq_off);
+        if ((fl.x | fl.y | fl.z | fl.w) != 0) {
+            // Some row exceeds the reference max: exchange the four waves' chunk maxima, move
+            // the reference max of the heads concerned, rescale their accumulators and quantise
+            // the chunk's weights again. The first finite maximum of a head needs no rescale
+            // (nothing is accumulated before it).
+            float lm[4] = {sc[0], sc[1], sc[2], sc[3]};
+            row16_max4(lm[0], lm[1], lm[2], lm[3]);
+            if (n == 0) *(v4f *)(ml + w * 16 + 4 * g) = v4f{lm[0], lm[1], lm[2], lm[3]};
+            lds_barrier();
+            const v4f mw0 = *(const v4f *)(ml + 4 * g), mw1 = *(const v4f *)(ml + 16 + 4 * g);
+            const v4f mw2 = *(const v4f *)(ml + 32 + 4 * g), mw3 = *(const v4f *)(ml + 48 + 4 * g);
+            float alpha[4];
+            bool moved = false;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float cm = fmaxf(fmaxf(mw0[i], mw1[i]), fmaxf(mw2[i], mw3[i]));
-            // lazy reference max: moves only when the chunk max exceeds it by > ln kQ8Pmax; the
-            // first finite maximum of a head needs no rescale (nothing is accumulated before it)
-            const bool mv = cm > m_run[i] + kQ8LnPmax;
-            const bool rs = mv && m_run[i] != -INFINITY;
-            const float mnew = mv ? cm : m_run[i];
-            alpha[i] = rs ? __expf(m_run[i] - mnew) : 1.0f;
-            moved |= rs;
-            m_run[i] = mnew;
-            const float p = __expf(sc[i] - mnew);
-            l_lane[i] = fmaf(l_lane[i], alpha[i], p);
-            const float v = p * swj;
-            const float hi = fminf(rintf(v), 127.f);
-            qhv[i] = (int)hi;
-            qlv[i] = (int)rintf((v - hi) * 254.0f);  // |v - hi| <= 1/2: lo spans the int8 range
+            for (int i = 0; i < 4; ++i) {
+                const float cm = fmaxf(fmaxf(mw0[i], mw1[i]), fmaxf(mw2[i], mw3[i]));
+                const bool mv = cm > m_run[i] + kQ8LnPmax;
+                const bool rs = mv && m_run[i] != -INFINITY;
+                const float mnew = mv ? cm : m_run[i];
+                alpha[i] = rs ? __expf(m_run[i] - mnew) : 1.0f;
+                moved |= rs;
+                m_run[i] = mnew;
+                pv[i] = __expf(sc[i] - mnew);
+                l_lane[i] *= alpha[i];
+            }
+            put_weights();
+            if (__any(moved)) {
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (alpha[i] != 1.0f) {
+                            ahi[t][i] = (int)rintf((float)ahi[t][i] * alpha[i]);
+                            alo[t][i] = (int)rintf((float)alo[t][i] * alpha[i]);
+                        }
+            }
+            lds_barrier();
+            wh = *(const v4i *)(wqc + wq_off);
+            wl = *(const v4i *)(wqc + 16 * kQ8Ws + wq_off);
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            wqc[(4 * g + i) * kQ8Ws + rowl] = (int8_t)qhv[i];
-            wqc[16 * kQ8Ws + (4 * g + i) * kQ8Ws + rowl] = (int8_t)qlv[i];
-        }
-        if (__any(moved)) {
-#pragma unroll
-            for (int t = 0; t < 8; ++t)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (alpha[i] != 1.0f) {
-                        ahi[t][i] = (int)rintf((float)ahi[t][i] * alpha[i]);
-                        alo[t][i] = (int)rintf((float)alo[t][i] * alpha[i]);
-                    }
-        }
-        lds_barrier();
-
-        const v4i wh = *(const v4i *)(wqc + wq_off);
-        const v4i wl = *(const v4i *)(wqc + 16 * kQ8Ws + wq_off);
+        for (int i = 0; i < 4; ++i) l_lane[i] += pv[i];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            const v2i b0 = lds_read_tr8(buf + tr_off[t]);
-            const v2i b1 = lds_read_tr8(buf + tr_off[t] + 4096);
-            const v4i bt = {b0.x, b0.y, b1.x, b1.y};
-            ahi[t] = mfma_i8(wh, bt, ahi[t]);
-            alo[t] = mfma_i8(wl, bt, alo[t]);
+            ahi[t] = mfma_i8(wh, bt[t], ahi[t]);
+            alo[t] = mfma_i8(wl, bt[t], alo[t]);
         }
     };
     using S0 = std::integral_constant<int, 0>;
@@ -1382,6 +1416,12 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) qsd[i] = ((const float *)(sq + 20480))[4 * g + i] * (a.smscale / 254.0f);
+    // the query operands are only MFMA sources, which read AGPRs as well: keeping them there
+    // leaves the VGPRs to the chunk loop
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) asm volatile("" : "+a"(qh[kb]), "+a"(ql[kb]));
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) asm volatile("" : "+a"(qrh[kb]), "+a"(qrl[kb]));
     // largest row scale of the split: the common bound of the quantised weights
     float smax;
     {
