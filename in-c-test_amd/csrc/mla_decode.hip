@@ -360,8 +360,8 @@ __device__ __forceinline__ float sum_parts(const float *p, int np, size_t pstrid
 __device__ __forceinline__ void append_body(const SeqTable &t, const Dims &d, const AppendArgs &a, int b) {
     __shared__ float lat[kMaxR];
     __shared__ float kat[kMaxR + kMaxDR];  // projection row: RMSNorm input | RoPE input
-    __shared__ double redd[256];
-    __shared__ float redf[256];
+    __shared__ double redd[4];
+    __shared__ float redf[4];
     const int tid = threadIdx.x;
     const SeqDesc &s = t.s[a.rows_mode ? 0 : b];
     const int R = d.R, DR = d.DR, half = DR / 2, pos = s.pos + (a.rows_mode ? b : 0);
@@ -387,13 +387,7 @@ __device__ __forceinline__ void append_body(const SeqTable &t, const Dims &d, co
             const double v = (double)kat[r];
             ss += v * v;
         }
-        redd[tid] = ss;
-        __syncthreads();
-        for (int o = 128; o > 0; o >>= 1) {
-            if (tid < o) redd[tid] += redd[tid + o];
-            __syncthreads();
-        }
-        const float mean_sq = (float)(redd[0] / (double)R);
+        const float mean_sq = (float)(block256_sum_f64(ss, redd) / (double)R);
         const float inv = 1.0f / sqrtf(mean_sq + a.eps);
         for (int r = tid, j = 0; r < R; r += 256, ++j) {
             const float t = kat[r] * inv;
@@ -408,16 +402,10 @@ __device__ __forceinline__ void append_body(const SeqTable &t, const Dims &d, co
     if (a.fmt == kFmtQ8) {
         float m = 0.f;
         for (int r = tid; r < R; r += 256) m = fmaxf(m, fabsf(lat[r]));
-        redf[tid] = m;
-        __syncthreads();
-        for (int o = 128; o > 0; o >>= 1) {
-            if (tid < o) redf[tid] = fmaxf(redf[tid], redf[tid + o]);
-            __syncthreads();
-        }
         // fmaxf drops NaN operands: a NaN latent must still select the zero row, as the
         // reference's sequential `a > amax` scan followed by isfinite() does for Inf; NaN
         // never compares greater there, so it is simply skipped -- identical to fmaxf.
-        const float amax = redf[0];
+        const float amax = block256_max(m, redf);
         int8_t *codes = (int8_t *)s.a + (size_t)pos * R;
         const bool zero = !(amax > 0.0f) || !isfinite(amax);
         const float scale = zero ? 1.0f : amax / 127.0f;
@@ -615,7 +603,7 @@ __device__ __forceinline__ void qprep_body(const SeqTable &t, const Dims &d, con
     __shared__ float qn[kMaxDN];
     __shared__ float qr[kMaxDR];  // RoPE input of the head
     __shared__ float ql[kMaxR];
-    __shared__ float redf[256];
+    __shared__ float redf[4];
     const int b = blk / d.NH, h = blk % d.NH, tid = threadIdx.x;
     const SeqDesc &s = t.s[b];
     const float *qh = a.y + (size_t)b * a.ldy + (size_t)h * d.QD;
@@ -751,13 +739,7 @@ __device__ __forceinline__ void qprep_body(const SeqTable &t, const Dims &d, con
     __syncthreads();
     float m = 0.f;
     for (int r = tid; r < d.R; r += 256) m = fmaxf(m, fabsf(ql[r]));
-    redf[tid] = m;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (tid < o) redf[tid] = fmaxf(redf[tid], redf[tid + o]);
-        __syncthreads();
-    }
-    const float amax = redf[0];
+    const float amax = block256_max(m, redf);
     const bool ok = amax > 0.f && isfinite(amax);
     const float inv = ok ? 127.0f / amax : 0.f;
     const size_t o = ((size_t)b * d.NH + h) * d.R;
