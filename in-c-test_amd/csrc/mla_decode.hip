@@ -279,6 +279,116 @@ hipError_t launch_gemv_ksplit(hipStream_t st, float *Y, size_t pstride, int ldy,
     return hipGetLastError();
 }
 
+// The k_gemv_ksplit partials for many tokens at once (prefill, state prefill), bit for bit.
+// For output (row o, token t) and quarter kq, k_gemv_ksplit lets wave j = 0..15 form
+// r_j = MFMA chain over its KPW 32-wide k-blocks (accumulator starting at 0), separately for
+// the bf16 hi and lo halves of x (a column of an MFMA result depends only on that column),
+// sums r_0 .. r_15 in order, then adds the hi and lo sums. Here one wave walks j = 0..15
+// itself with the same operand layout (W rows as A, k slot 8 g + i), so every partial
+// coincides. The activations come as bf16 planes from k_split, which rounds as split8_part
+// does for finite values. Block: 64 rows x 128 tokens x one k quarter, wave w taking tokens
+// 32 w .. 32 w + 31 (two 16-token tiles) for all four row tiles.
+struct KvaTokArgs {
+    float *Y;                  // partial kq at Y + kq * pstride, [S, ldy]
+    const uint16_t *XH, *XL;   // [S, in] bf16 hi / lo planes
+    const uint16_t *W;         // [out, in]
+    size_t pstride;
+    int ldy, S, out, in;
+};
+
+template <int KPW>
+__global__ __launch_bounds__(256) void k_kva_tok(KvaTokArgs a) {
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
+    const int kq = blockIdx.y, row0 = blockIdx.x * 64, tok0 = blockIdx.z * 128 + 32 * w;
+    const uint16_t *wr[4], *xh[2], *xl[2];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) wr[t] = a.W + (size_t)min(row0 + 16 * t + n, a.out - 1) * a.in;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const size_t tok = (size_t)min(tok0 + 16 * u + n, a.S - 1);
+        xh[u] = a.XH + tok * a.in;
+        xl[u] = a.XL + tok * a.in;
+    }
+    const int kbase = kq * (16 * 32 * KPW) + g * 8;
+    v4f sh[4][2], sl[4][2];
+    v4i wa[KPW][4], ha[KPW][2], la[KPW][2];
+    auto load = [&](int j) {
+#pragma unroll
+        for (int kb = 0; kb < KPW; ++kb) {
+            const int k = kbase + j * (32 * KPW) + 32 * kb;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) wa[kb][t] = *(const v4i *)(wr[t] + k);
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                ha[kb][u] = *(const v4i *)(xh[u] + k);
+                la[kb][u] = *(const v4i *)(xl[u] + k);
+            }
+        }
+    };
+    load(0);
+#pragma unroll 2
+    for (int j = 0; j < 16; ++j) {
+        v4f rh[4][2], rl[4][2];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                rh[t][u] = v4f{0.f, 0.f, 0.f, 0.f};
+                rl[t][u] = v4f{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+        for (int kb = 0; kb < KPW; ++kb)
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const v8bf wv = __builtin_bit_cast(v8bf, wa[kb][t]);
+                    rh[t][u] = mfma_bf16(wv, __builtin_bit_cast(v8bf, ha[kb][u]), rh[t][u]);
+                    rl[t][u] = mfma_bf16(wv, __builtin_bit_cast(v8bf, la[kb][u]), rl[t][u]);
+                }
+        if (j + 1 < 16) load(j + 1);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                sh[t][u] = j == 0 ? rh[t][u] : sh[t][u] + rh[t][u];
+                sl[t][u] = j == 0 ? rl[t][u] : sl[t][u] + rl[t][u];
+            }
+    }
+    float *y = a.Y + (size_t)kq * a.pstride;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int tok = tok0 + 16 * u + n;
+        if (tok >= a.S) continue;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const v4f p = sh[t][u] + sl[t][u];
+            const int r = row0 + 16 * t + 4 * g;
+            float *yp = y + (size_t)tok * a.ldy + r;
+            if (r + 3 < a.out && (a.ldy & 3) == 0) {
+                *(v4f *)yp = p;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (r + i < a.out) yp[i] = p[i];
+            }
+        }
+    }
+}
+
+hipError_t launch_kva_tok(hipStream_t st, float *Y, size_t pstride, int ldy, const uint16_t *XH,
+                          const uint16_t *XL, int S, const uint16_t *W, int out, int in) {
+    if (!gemv_ksplit_ok(in, in) || S < 1 || out <= 0 || ldy < out || (S + 127) / 128 > 65535 ||
+        ((uintptr_t)XH % 16) != 0 || ((uintptr_t)XL % 16) != 0 || ((uintptr_t)W % 16) != 0 ||
+        ((uintptr_t)Y % 16) != 0 || pstride % 4 != 0)
+        return hipErrorInvalidValue;
+    KvaTokArgs a{Y, XH, XL, W, pstride, ldy, S, out, in};
+    const dim3 grid((out + 63) / 64, kGemvKs, (S + 127) / 128);
+    if (in == 2048) hipLaunchKernelGGL((k_kva_tok<1>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((k_kva_tok<2>), grid, dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
 bool gemv_xs_ok(int in) { return in == 2048 || in == 4096; }
 
 hipError_t launch_gemv_xs(hipStream_t st, float *Y, int ldy, const uint16_t *XS, int B,

@@ -86,6 +86,11 @@ bool gemv_ksplit_ok(int in, int ldx);
 hipError_t launch_gemv_ksplit(hipStream_t st, float *Y, size_t pstride, int ldy, const float *X,
                               int ldx, int B, const uint16_t *W0, int out0, const uint16_t *W1,
                               int out1, int in);
+// The same kGemvKs partials (bit for bit) for S tokens given as bf16 planes XH, XL [S, in]
+// (k_split's rounding), tiled over 128 tokens so a weight tile serves many of them: the
+// prefill's kv_a projection and the state prefill. Shapes as launch_gemv_ksplit.
+hipError_t launch_kva_tok(hipStream_t st, float *Y, size_t pstride, int ldy, const uint16_t *XH,
+                          const uint16_t *XL, int S, const uint16_t *W, int out, int in);
 // Y[b, o] (+)= sum_k W[o, k] x[b, k] with x given as bf16 planes XS[2][B][in] (hi, lo), as
 // launch_combine writes them (DecodeWork::hos). Shapes when gemv_xs_ok (in = 2048 or 4096),
 // any B.
@@ -156,12 +161,27 @@ size_t prefill_bytes(const Dims &d, int S);
 // prefill_bytes(d, S) bytes, rope_cs table covering positions [0, S).
 // wo16: o_proj converted to fp16 (launch_bf16_to_f16), used by the MFMA route (the attention
 // output enters the o_proj GEMM as fp16).
+// kva (optional): receives where the kv_a projection of the S tokens lies in ws when it was
+// computed with the decode arithmetic (launch_kva_tok partials), so a state fill can reuse
+// it; kva->y is null otherwise. Valid until ws is reused.
+struct PrefillKva {
+    const float *y;
+    int ldy, np;
+    size_t pstride;
+};
 hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, const float *x,
                               float *out, const uint16_t *wq, const uint16_t *wkva,
                               const uint16_t *wnorm, const uint16_t *wkvb, const uint16_t *wo,
-                              const _Float16 *wo16, const float2 *rope_cs, void *ws);
+                              const _Float16 *wo16, const float2 *rope_cs, void *ws,
+                              PrefillKva *kva = nullptr);
+// True when the prefill's kv_a projection uses the decode arithmetic (launch_kva_tok).
+bool prefill_kva_exact(const Dims &d);
 // True when the prefill of these dims takes the MFMA route (needs the fp16 o_proj copy).
 bool prefill_mfma_shape(const Dims &d);
+// src [rows, cols] fp32 -> bf16 hi, lo planes (x = hi + lo to ~16 bits, both round to nearest
+// even). cols % 8 == 0, 16-byte aligned rows.
+hipError_t launch_split(hipStream_t st, const float *src, int ld_src, uint16_t *hi, uint16_t *lo,
+                        int ld_dst, int rows, int cols);
 // dst[i] = (fp16) bf16 src[i]: exact for |x| >= 2^-17 (bf16 has 8 significant bits).
 hipError_t launch_bf16_to_f16(hipStream_t st, _Float16 *dst, const uint16_t *src, size_t n);
 

@@ -42,7 +42,7 @@ __global__ __launch_bounds__(256) void k_split(const float *src, int ld_src, uin
         any |= ((lv.x | lv.y | lv.z | lv.w) & 0x7fff7fff) != 0;
     }
     // one atomic per block at most, and none once the flag is seen raised
-    if (__syncthreads_or(any) && threadIdx.x == 0 &&
+    if (flag && __syncthreads_or(any) && threadIdx.x == 0 &&
         __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0)
         atomicOr(flag, 1);
 }
@@ -407,7 +407,8 @@ struct KvaPackArgs {
     const float2 *cs;
     uint16_t *lath, *latl;
     _Float16 *qh, *ql, *kh, *kl, *vt;
-    int S, Sp, NH, ldy, R, DN, DR, DV;
+    size_t pstride;  // np partials of y, pstride floats apart, summed in order
+    int np, S, Sp, NH, ldy, R, DN, DR, DV;
     float eps;
 };
 
@@ -430,9 +431,14 @@ __global__ __launch_bounds__(256) void k_kva_pack(KvaPackArgs a) {
         return;
     }
     const float *kat = a.y + (size_t)t * a.ldy;
+    auto kv = [&](int r) {
+        float v = kat[r];
+        for (int q = 1; q < a.np; ++q) v += kat[(size_t)q * a.pstride + r];
+        return v;
+    };
     double ss = 0.0;
     for (int r = l; r < R; r += 64) {
-        const double v = (double)kat[r];
+        const double v = (double)kv(r);
         ss += v * v;
     }
 #pragma unroll
@@ -440,7 +446,7 @@ __global__ __launch_bounds__(256) void k_kva_pack(KvaPackArgs a) {
     const float mean_sq = (float)(ss / (double)R);
     const float inv = 1.0f / sqrtf(mean_sq + a.eps);
     for (int r = l; r < R; r += 64) {
-        const float v = kat[r] * inv;
+        const float v = kv(r) * inv;
         const float y = v * bf16_to_f32(a.norm[r]);
         uint16_t hh, ll;
         split_bf16(y, hh, ll);
@@ -449,7 +455,7 @@ __global__ __launch_bounds__(256) void k_kva_pack(KvaPackArgs a) {
     }
     for (int i = l; i < half; i += 64) {
         const float2 cs = a.cs[(size_t)t * half + i];
-        const float ev = kat[R + 2 * i], od = kat[R + 2 * i + 1];
+        const float ev = kv(R + 2 * i), od = kv(R + 2 * i + 1);
         const float ec = ev * cs.x, os = od * cs.y, oc = od * cs.x, es = ev * cs.y;
         _Float16 h0, l0, h1, l1;
         split_f16(ec - os, h0, l0);
@@ -820,6 +826,17 @@ __global__ __launch_bounds__(256) void k_bf16_to_f16(_Float16 *dst, const uint16
         dst[i] = (_Float16)bf16_to_f32(src[i]);
 }
 
+hipError_t launch_split(hipStream_t st, const float *src, int ld_src, uint16_t *hi, uint16_t *lo,
+                        int ld_dst, int rows, int cols) {
+    if (rows < 1 || cols < 8 || cols % 8 || ld_src % 4 || ld_dst % 8 || ld_src < cols || ld_dst < cols ||
+        ((uintptr_t)src % 16) || ((uintptr_t)hi % 16) || ((uintptr_t)lo % 16))
+        return hipErrorInvalidValue;
+    const int blocks = (int)std::min<size_t>(2048, ((size_t)rows * cols / 8 + 255) / 256);
+    hipLaunchKernelGGL(k_split, dim3(blocks), dim3(256), 0, st, src, ld_src, hi, lo, ld_dst, rows, cols,
+                       nullptr);
+    return hipGetLastError();
+}
+
 hipError_t launch_bf16_to_f16(hipStream_t st, _Float16 *dst, const uint16_t *src, size_t n) {
     const int blocks = (int)std::min<size_t>(4096, (n + 255) / 256);
     hipLaunchKernelGGL(k_bf16_to_f16, dim3(blocks), dim3(256), 0, st, dst, src, n);
@@ -831,6 +848,8 @@ bool prefill_mfma_shape(const Dims &d) {
            d.DN % 8 == 0;
 }
 
+bool prefill_kva_exact(const Dims &d) { return prefill_mfma_shape(d) && gemv_ksplit_ok(d.H, d.H); }
+
 size_t prefill_bytes(const Dims &d, int S) {
     const size_t Sp = (size_t)(S + 127) / 128 * 128;
     size_t b = 0;
@@ -839,7 +858,7 @@ size_t prefill_bytes(const Dims &d, int S) {
         add(4 * 8);                              // flags
         add(2 * (size_t)S * d.H);                // x hi
         add(2 * (size_t)S * d.H);                // x lo
-        add(4 * (size_t)S * d.KVO);              // kv_a projection
+        add(4 * (size_t)S * d.KVO * (prefill_kva_exact(d) ? kGemvKs : 1));  // kv_a projection
         add(2 * (size_t)S * d.R);                // latent hi
         add(2 * (size_t)S * d.R);                // latent lo
         add(2 * (size_t)d.NH * Sp * d.QD);       // q hi (fp16)
@@ -863,8 +882,9 @@ size_t prefill_bytes(const Dims &d, int S) {
 hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, const float *x,
                               float *out, const uint16_t *wq, const uint16_t *wkva,
                               const uint16_t *wnorm, const uint16_t *wkvb, const uint16_t *wo,
-                              const _Float16 *wo16, const float2 *cs, void *ws) {
+                              const _Float16 *wo16, const float2 *cs, void *ws, PrefillKva *kva) {
     const int Sp = (S + 127) / 128 * 128;
+    if (kva) *kva = PrefillKva{nullptr, 0, 0, 0};
     char *base = (char *)ws;
     size_t off = 0;
     auto take = [&](size_t n) {
@@ -880,7 +900,9 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
         int *flags = (int *)take(4 * 8);
         uint16_t *xh = (uint16_t *)take(2 * (size_t)S * d.H);
         uint16_t *xl = (uint16_t *)take(2 * (size_t)S * d.H);
-        float *ykva = (float *)take(4 * (size_t)S * d.KVO);
+        const bool exact = prefill_kva_exact(d);
+        const int np = exact ? kGemvKs : 1;
+        float *ykva = (float *)take(4 * (size_t)S * d.KVO * np);
         uint16_t *lath = (uint16_t *)take(2 * (size_t)S * d.R);
         uint16_t *latl = (uint16_t *)take(2 * (size_t)S * d.R);
         _Float16 *qh = (_Float16 *)take(2 * (size_t)d.NH * Sp * d.QD);
@@ -894,11 +916,22 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
         const int split_blocks = (int)std::min<size_t>(2048, ((size_t)S * d.H / 8 + 255) / 256);
         hipLaunchKernelGGL(k_split, dim3(split_blocks), dim3(256), 0, st, x, d.H, xh, xl, d.H, S, d.H, flags + 0);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        // q (-> Q hi/lo, rotated) | kv_a (-> ykva)
-        if ((e = gemm<kEpiQ>(st, xh, xl, flags + 0, d.H, wq, d.QO, wkva, d.KVO, d.H, ykva, d.KVO, S, d.H,
-                             ep)) != hipSuccess)
+        // q (-> Q hi/lo, rotated) | kv_a (-> ykva); with the decode's k-split arithmetic for
+        // kv_a where the decode uses it, so the state rows of these tokens can come from it
+        if (exact) {
+            if ((e = gemm<kEpiQ>(st, xh, xl, flags + 0, d.H, wq, d.QO, nullptr, 0, d.H, nullptr, 0, S, d.H,
+                                 ep)) != hipSuccess)
+                return e;
+            if ((e = launch_kva_tok(st, ykva, (size_t)S * d.KVO, d.KVO, xh, xl, S, wkva, d.KVO, d.H)) !=
+                hipSuccess)
+                return e;
+            if (kva) *kva = PrefillKva{ykva, d.KVO, np, (size_t)S * d.KVO};
+        } else if ((e = gemm<kEpiQ>(st, xh, xl, flags + 0, d.H, wq, d.QO, wkva, d.KVO, d.H, ykva, d.KVO, S,
+                                    d.H, ep)) != hipSuccess) {
             return e;
-        KvaPackArgs ka{ykva, wnorm, cs, lath, latl, qh, ql, kh, kl, vt, S, Sp, d.NH, d.KVO, d.R, d.DN, d.DR, d.DV, eps};
+        }
+        KvaPackArgs ka{ykva, wnorm, cs, lath, latl, qh, ql, kh, kl, vt, (size_t)S * d.KVO, np,
+                       S, Sp, d.NH, d.KVO, d.R, d.DN, d.DR, d.DV, eps};
         hipLaunchKernelGGL(k_kva_pack, dim3((Sp + 3) / 4), dim3(256), 0, st, ka);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // kv_b (-> K nope part, V^T hi/lo)

@@ -144,7 +144,7 @@ struct Ctx {
     std::unordered_map<const void *, WeightEntry> weights;
     std::unordered_map<const void *, Mirror> mirrors;
     std::unordered_map<uint64_t, RopeTable> ropes;  // key: theta bits << 16 | DR
-    DevBuf work, part, scores, prefill;
+    DevBuf work, part, scores, prefill, fill, fillx;
     PinBuf pin_in, pin_out;
     bool capturing = false;
     // per-stage event timing of decode steps (kvl_mla_timing_*)
@@ -863,11 +863,22 @@ int decode_device(float *d_out, const float *d_x, int B, const KvlMlaConfig *cfg
     return 0;
 }
 
-// State prefill-fill (src/mla_compressed_state.c:52-84, src/mla_compressed_q8_state.c:
-// 129-159): kv_a GEMV of every token, then the append kernel in rows mode.
+// What a state fill needs on the device: dims, the kv_a weight and norm, the RoPE table, the
+// state's device mirror.
+struct FillCtx {
+    Dims d{};
+    int fmt = 0;
+    float eps = 0.f;
+    const uint16_t *kva = nullptr, *norm = nullptr;
+    const float2 *cs = nullptr;
+    Mirror *m = nullptr;
+};
+
+// Checks of src/mla_compressed_state.c:52-66 / src/mla_compressed_q8_state.c:129-140 (empty
+// state, seq_len within capacity, matching dims) and the device set-up of a fill.
 template <class S>
-int state_prefill(const float *x, int seq_len, const KvlMlaConfig *cfg, const KvlMlaBF16 *w, S *s) {
-    if (!x || !cfg || !w || !s || !w->kv_a_proj || !w->kv_a_norm || seq_len <= 0 || s->len != 0 ||
+int fill_begin(int seq_len, const KvlMlaConfig *cfg, const KvlMlaBF16 *w, S *s, FillCtx &f) {
+    if (!cfg || !w || !s || !w->kv_a_proj || !w->kv_a_norm || seq_len <= 0 || s->len != 0 ||
         seq_len > s->capacity || !state_dims_ok(s, cfg)) {
         set_err("invalid arguments");
         return -1;
@@ -882,76 +893,114 @@ int state_prefill(const float *x, int seq_len, const KvlMlaConfig *cfg, const Kv
         return -1;
     }
     if (ensure_ready() != 0) return -1;
+    f.fmt = fmt_of<S>();
+    f.eps = cfg->rms_eps;
+    f.d.H = H;
+    f.d.R = R;
+    f.d.DR = DR;
+    f.d.KVO = R + DR;
+    f.d.NH = 1;
+    if (dev_weight(w->kv_a_proj, (size_t)f.d.KVO * H, &f.kva) != 0) return -1;
+    if (dev_weight(w->kv_a_norm, (size_t)R, &f.norm) != 0) return -1;
+    if (mirror_get(s, view_of(s), &f.m) != 0) return -1;
+    if (rope_table(cfg->rope_theta, DR, seq_len, &f.cs) != 0) return -1;
+    return 0;
+}
+
+// Rows [t0, t0 + n) of the state from the kv_a projection of those tokens on the device (np
+// partials pstride floats apart, token i at y + i * ldy): the append kernel in rows mode
+// (RMSNorm, RoPE, the state's row format) writes the device mirror and stages the rows in
+// c.fill; with host_rows they are also copied into the host arrays (synchronous).
+template <class S>
+int fill_rows(S *s, const FillCtx &f, const float *y, int ldy, int np, size_t pstride, int t0, int n,
+              bool host_rows) {
     Ctx &c = ctx();
-    const int fmt = fmt_of<S>();
-    Dims d{};
-    d.H = H;
-    d.R = R;
-    d.DR = DR;
-    d.KVO = R + DR;
-    d.NH = 1;
-    const uint16_t *kva = nullptr, *norm = nullptr;
-    if (dev_weight(w->kv_a_proj, (size_t)d.KVO * H, &kva) != 0) return -1;
-    if (dev_weight(w->kv_a_norm, (size_t)R, &norm) != 0) return -1;
-    Mirror *m = nullptr;
-    if (mirror_get(s, view_of(s), &m) != 0) return -1;
-    const float2 *cs = nullptr;
-    if (rope_table(cfg->rope_theta, DR, seq_len, &cs) != 0) return -1;
-    const size_t rb = row_bytes_of(fmt, R, DR, 0);
-    const int chunk = 4096;
+    const size_t rb = row_bytes_of(f.fmt, f.d.R, f.d.DR, 0);
+    if (dev_reserve(c.fill, (size_t)n * rb) != 0) return -1;
+    uint8_t *drows = (uint8_t *)c.fill.p;
+    SeqTable t;
+    memset(&t, 0, sizeof t);
+    t.n = 1;
+    t.s[0].a = f.m->a;
+    t.s[0].b = f.m->b;
+    t.s[0].c = f.m->c;
+    t.s[0].pos = t0;
+    DecodeWork wk{};
+    wk.rows = drows;
+    HIP_TRY(launch_append(c.stream, f.fmt, t, f.d, y, ldy, 0, np, pstride, f.norm, f.eps, f.cs, wk, false, n));
+    if (!host_rows) return 0;
+    if (pin_reserve(c.pin_out, (size_t)n * rb) != 0) return -1;
+    HIP_TRY(hipMemcpyAsync(c.pin_out.p, drows, (size_t)n * rb, hipMemcpyDeviceToHost, c.stream));
+    HIP_TRY(hipStreamSynchronize(c.stream));
+    const HostView v = view_of(s);
+    for (int i = 0; i < n; ++i) write_back_rows(f.fmt, v, t0 + i, (const uint8_t *)c.pin_out.p + (size_t)i * rb);
+    return 0;
+}
+
+// kv_a of n tokens from device x [n, H] with the decode path's arithmetic -- the k-split
+// partials (launch_kva_tok over the bf16 planes of x) where the decode uses them, else the
+// plain GEMV -- so the rows equal those a decode of the same tokens appends; then fill_rows.
+// ws: fill_x_bytes(d, n) bytes of device memory, 256-byte aligned.
+size_t fill_x_bytes(const Dims &d, int n) {
+    const bool ks = gemv_ksplit_ok(d.H, d.H);
+    Layout L;
+    L.take<uint16_t>(nullptr, ks ? 2 * (size_t)n * d.H : 0);
+    L.take<float>(nullptr, (size_t)(ks ? kGemvKs : 1) * n * d.KVO);
+    return L.off;
+}
+
+template <class S>
+int fill_from_x(S *s, const FillCtx &f, const float *dx, void *ws, int t0, int n, bool host_rows) {
+    Ctx &c = ctx();
+    const Dims &d = f.d;
+    const bool ks = gemv_ksplit_ok(d.H, d.H);
+    const int np = ks ? kGemvKs : 1;
+    Layout L;
+    uint16_t *xs = L.take<uint16_t>((char *)ws, ks ? 2 * (size_t)n * d.H : 0);
+    float *dy = L.take<float>((char *)ws, (size_t)np * n * d.KVO);
+    if (ks) {
+        uint16_t *xl = xs + (size_t)n * d.H;
+        HIP_TRY(launch_split(c.stream, dx, d.H, xs, xl, d.H, n, d.H));
+        HIP_TRY(launch_kva_tok(c.stream, dy, (size_t)n * d.KVO, d.KVO, xs, xl, n, f.kva, d.KVO, d.H));
+    } else {
+        for (int b0 = 0; b0 < n; b0 += 16 * 65535) {
+            const int nb = std::min(n - b0, 16 * 65535);
+            HIP_TRY(launch_gemv(c.stream, dy + (size_t)b0 * d.KVO, d.KVO, dx + (size_t)b0 * d.H, d.H, nb, f.kva,
+                                d.KVO, nullptr, 0, d.H, false));
+        }
+    }
+    return fill_rows(s, f, dy, d.KVO, np, (size_t)n * d.KVO, t0, n, host_rows);
+}
+
+// State prefill-fill (src/mla_compressed_state.c:52-84, src/mla_compressed_q8_state.c:
+// 129-159): kv_a of every token, then the append kernel in rows mode, in chunks of 4096 tokens.
+template <class S>
+int state_prefill(const float *x, int seq_len, const KvlMlaConfig *cfg, const KvlMlaBF16 *w, S *s) {
+    FillCtx f;
+    if (!x) {
+        set_err("invalid arguments");
+        return -1;
+    }
+    if (fill_begin(seq_len, cfg, w, s, f) != 0) return -1;
+    Ctx &c = ctx();
+    const int H = f.d.H, chunk = 4096;
     for (int t0 = 0; t0 < seq_len; t0 += chunk) {
         const int n = std::min(chunk, seq_len - t0);
-        // kv_a with the decode path's arithmetic (k-split partials where the decode uses them),
-        // so that these rows equal the rows a decode of the same tokens appends
-        const bool ks = gemv_ksplit_ok(H, H);
-        const int np = ks ? kGemvKs : 1;
-        Layout L;
-        L.take<float>(nullptr, (size_t)n * H);
-        L.take<float>(nullptr, (size_t)np * n * d.KVO);
-        L.take<uint8_t>(nullptr, (size_t)n * rb);
-        if (dev_reserve(c.prefill, L.off) != 0) return -1;
-        Layout L2;
-        char *base = (char *)c.prefill.p;
-        float *dx = L2.take<float>(base, (size_t)n * H);
-        float *dy = L2.take<float>(base, (size_t)np * n * d.KVO);
-        uint8_t *drows = L2.take<uint8_t>(base, (size_t)n * rb);
-        HIP_TRY(hipMemcpyAsync(dx, x + (size_t)t0 * H, (size_t)n * H * sizeof(float),
-                               hipMemcpyHostToDevice, c.stream));
-        if (ks) {
-            HIP_TRY(launch_gemv_ksplit(c.stream, dy, (size_t)n * d.KVO, d.KVO, dx, H, n, kva, d.KVO,
-                                       nullptr, 0, H));
-        } else {
-            for (int b0 = 0; b0 < n; b0 += 16 * 65535) {
-                const int nb = std::min(n - b0, 16 * 65535);
-                HIP_TRY(launch_gemv(c.stream, dy + (size_t)b0 * d.KVO, d.KVO, dx + (size_t)b0 * H, H, nb,
-                                    kva, d.KVO, nullptr, 0, H, false));
-            }
-        }
-        SeqTable t;
-        memset(&t, 0, sizeof t);
-        t.n = 1;
-        t.s[0].a = m->a;
-        t.s[0].b = m->b;
-        t.s[0].c = m->c;
-        t.s[0].pos = t0;
-        DecodeWork wk{};
-        wk.rows = drows;
-        HIP_TRY(launch_append(c.stream, fmt, t, d, dy, d.KVO, 0, np, (size_t)n * d.KVO, norm, cfg->rms_eps, cs,
-                              wk, false, n));
-        if (pin_reserve(c.pin_out, (size_t)n * rb) != 0) return -1;
-        HIP_TRY(hipMemcpyAsync(c.pin_out.p, drows, (size_t)n * rb, hipMemcpyDeviceToHost, c.stream));
-        HIP_TRY(hipStreamSynchronize(c.stream));
-        const HostView v = view_of(s);
-        for (int i = 0; i < n; ++i)
-            write_back_rows(fmt, v, t0 + i, (const uint8_t *)c.pin_out.p + (size_t)i * rb);
+        const size_t xb = ((size_t)n * H * sizeof(float) + 255) & ~(size_t)255;
+        if (dev_reserve(c.prefill, xb + fill_x_bytes(f.d, n)) != 0) return -1;
+        float *dx = (float *)c.prefill.p;
+        HIP_TRY(hipMemcpyAsync(dx, x + (size_t)t0 * H, (size_t)n * H * sizeof(float), hipMemcpyHostToDevice,
+                               c.stream));
+        if (fill_from_x(s, f, dx, (char *)c.prefill.p + xb, t0, n, true) != 0) return -1;
     }
     s->len = seq_len;
-    m->synced = seq_len;
+    f.m->synced = seq_len;
     return 0;
 }
 
 // Causal prefill (src/mla_prefill_streaming.c:78-206). d_x/d_out device buffers.
-int prefill_device(float *d_out, const float *d_x, int S, const KvlMlaConfig *cfg, const KvlMlaBF16 *w) {
+int prefill_device(float *d_out, const float *d_x, int S, const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                   PrefillKva *kva = nullptr) {
     Dims d;
     if (!d_out || !d_x || S <= 0 || !weights_ok(w) || !dims_of(cfg, d)) {
         set_err("invalid arguments");
@@ -974,7 +1023,64 @@ int prefill_device(float *d_out, const float *d_x, int S, const KvlMlaConfig *cf
     const _Float16 *wo16 = nullptr;
     if (prefill_mfma_shape(d) && dev_weight_f16(w->o_proj, (size_t)d.H * d.HO, &wo16) != 0) return -1;
     HIP_TRY(launch_prefill_all(c.stream, d, S, cfg->rms_eps, d_x, d_out, dw.q, dw.kva, dw.norm, dw.kvb,
-                               dw.o, wo16, cs, c.scores.p));
+                               dw.o, wo16, cs, c.scores.p, kva));
+    return 0;
+}
+
+// Causal prefill of seq_len tokens plus the fill of state rows [0, seq_len) from the same x
+// (src/generate.c:208-210 calls kvl_mla_prefill_bf16 and then the state prefill on the same
+// x). Results equal those two calls; the kv_a projection is computed once where the prefill
+// computes it with the decode arithmetic (PrefillKva), else the fill computes its own from
+// d_x. Device x and out; host_rows as in fill_rows.
+template <class S>
+int prefill_state_device(float *d_out, const float *d_x, int seq_len, const KvlMlaConfig *cfg,
+                         const KvlMlaBF16 *w, S *s, bool host_rows) {
+    FillCtx f;
+    if (!d_out || !d_x) {
+        set_err("invalid arguments");
+        return -1;
+    }
+    if (ctx().capturing) {
+        set_err("prefill with state fill during graph capture");
+        return -1;
+    }
+    if (fill_begin(seq_len, cfg, w, s, f) != 0) return -1;
+    PrefillKva kv{};
+    if (prefill_device(d_out, d_x, seq_len, cfg, w, &kv) != 0) return -1;
+    if (kv.y) {
+        if (fill_rows(s, f, kv.y, kv.ldy, kv.np, kv.pstride, 0, seq_len, host_rows) != 0) return -1;
+    } else {
+        Ctx &c = ctx();
+        const int chunk = 4096;
+        if (dev_reserve(c.fillx, fill_x_bytes(f.d, std::min(chunk, seq_len))) != 0) return -1;
+        for (int t0 = 0; t0 < seq_len; t0 += chunk) {
+            const int n = std::min(chunk, seq_len - t0);
+            if (fill_from_x(s, f, d_x + (size_t)t0 * f.d.H, c.fillx.p, t0, n, host_rows) != 0) return -1;
+        }
+    }
+    s->len = seq_len;
+    f.m->synced = seq_len;
+    return 0;
+}
+
+template <class S>
+int prefill_state(float *out, const float *x, int seq_len, const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                  S *s) {
+    if (!out || !x || seq_len <= 0 || !cfg || cfg->hidden_size <= 0) {
+        set_err("invalid arguments");
+        return -1;
+    }
+    if (ensure_ready() != 0) return -1;
+    Ctx &c = ctx();
+    const size_t io = (size_t)seq_len * cfg->hidden_size * sizeof(float);
+    const size_t io_al = (io + 255) & ~(size_t)255;
+    if (dev_reserve(c.prefill, 2 * io_al) != 0) return -1;
+    float *dx = (float *)c.prefill.p;
+    float *dout = (float *)((char *)c.prefill.p + io_al);
+    HIP_TRY(hipMemcpyAsync(dx, x, io, hipMemcpyHostToDevice, c.stream));
+    if (prefill_state_device(dout, dx, seq_len, cfg, w, s, true) != 0) return -1;
+    HIP_TRY(hipMemcpyAsync(out, dout, io, hipMemcpyDeviceToHost, c.stream));
+    HIP_TRY(hipStreamSynchronize(c.stream));
     return 0;
 }
 
@@ -1078,6 +1184,33 @@ int kvl_mla_prefill_device(float *d_out, const float *d_x, int seq_len, const Kv
                            const KvlMlaBF16 *w) {
     Guard guard;
     return prefill_device(d_out, d_x, seq_len, cfg, w);
+}
+
+int kvl_mla_prefill_compressed_state_bf16(float *out, const float *x, int seq_len, const KvlMlaConfig *cfg,
+                                          const KvlMlaBF16 *w, KvlMlaCompressedState *state) {
+    Guard guard;
+    return prefill_state(out, x, seq_len, cfg, w, state);
+}
+
+int kvl_mla_prefill_compressed_q8_state_bf16(float *out, const float *x, int seq_len,
+                                             const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                             KvlMlaCompressedQ8State *state) {
+    Guard guard;
+    return prefill_state(out, x, seq_len, cfg, w, state);
+}
+
+int kvl_mla_prefill_compressed_state_device(float *d_out, const float *d_x, int seq_len,
+                                            const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                            KvlMlaCompressedState *state) {
+    Guard guard;
+    return prefill_state_device(d_out, d_x, seq_len, cfg, w, state, false);
+}
+
+int kvl_mla_prefill_compressed_q8_state_device(float *d_out, const float *d_x, int seq_len,
+                                               const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                               KvlMlaCompressedQ8State *state) {
+    Guard guard;
+    return prefill_state_device(d_out, d_x, seq_len, cfg, w, state, false);
 }
 
 // ---- include/kvl/mla_state.h (expanded state) ------------------------------------------

@@ -32,6 +32,12 @@ EXT_API = {
     "mla_decode_compressed_batch_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, abi.CFG,
                                                      abi.W, CSP, C.c_uint]),
     "mla_prefill_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, abi.CFG, abi.W]),
+    "mla_prefill_compressed_state_bf16": (C.c_int, [abi.f32p, abi.f32p, C.c_int, abi.CFG, abi.W, abi.CS]),
+    "mla_prefill_compressed_q8_state_bf16": (C.c_int, [abi.f32p, abi.f32p, C.c_int, abi.CFG, abi.W, abi.QS]),
+    "mla_prefill_compressed_state_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, abi.CFG, abi.W,
+                                                      abi.CS]),
+    "mla_prefill_compressed_q8_state_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, abi.CFG, abi.W,
+                                                         abi.QS]),
     "mla_stream": (C.c_void_p, []),
     "mla_synchronize": (C.c_int, []),
     "mla_device_alloc": (C.c_void_p, [C.c_size_t]),

@@ -82,6 +82,29 @@ int kvl_mla_decode_compressed_batch_device(float *d_out, const float *d_x, int b
 int kvl_mla_prefill_device(float *d_out, const float *d_x, int seq_len, const KvlMlaConfig *cfg,
                            const KvlMlaBF16 *w);
 
+/* Prefill with the state fill of the same tokens, as src/generate.c:208-210 sequences them:
+ * out and the state (rows [0, seq_len), len = seq_len) equal, bit for bit, what
+ * kvl_mla_prefill_bf16(out, x, ...) followed by kvl_mla_compressed[_q8]_state_prefill_bf16(x,
+ * ...) produce, with the same argument checks (state empty, seq_len <= capacity). One upload of
+ * x; the state rows come from the kv_a projection the prefill computes anyway (where its
+ * shapes let it use the decode's arithmetic, e.g. hidden 2048 or 4096; otherwise the fill
+ * computes its own from the uploaded x). Synchronous; host rows written. */
+int kvl_mla_prefill_compressed_state_bf16(float *out, const float *x, int seq_len,
+                                          const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                          KvlMlaCompressedState *state);
+int kvl_mla_prefill_compressed_q8_state_bf16(float *out, const float *x, int seq_len,
+                                             const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                             KvlMlaCompressedQ8State *state);
+/* The same over device buffers (d_x, d_out [seq_len, hidden] fp32), stream-ordered on
+ * kvl_mla_stream(): the rows stay on the device (host rows are written only by *_pull); len is
+ * set to seq_len. Not capturable (the fill may grow its workspace). */
+int kvl_mla_prefill_compressed_state_device(float *d_out, const float *d_x, int seq_len,
+                                            const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                            KvlMlaCompressedState *state);
+int kvl_mla_prefill_compressed_q8_state_device(float *d_out, const float *d_x, int seq_len,
+                                               const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                               KvlMlaCompressedQ8State *state);
+
 /* The library's HIP stream (hipStream_t) and helpers for callers without a HIP binding. */
 void *kvl_mla_stream(void);
 int kvl_mla_synchronize(void);
