@@ -298,6 +298,23 @@ def main():
                              "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4),
                              "algorithmic_gflop": round(flops / 1e9, 3)}
         log(f"[bench] prefill S={S}: {pms:.3f} ms, {tf:.1f} TFLOP/s")
+        # the same prefill filling a Q8 state of the S tokens on the way (one call)
+        qs = abi.KvlMlaCompressedQ8State()
+        lib.check(L.kvl_mla_compressed_q8_state_init(C.byref(qs), C.byref(cfg), S), "state init")
+        fms = []
+        for rep in range(4):
+            L.kvl_mla_compressed_q8_state_reset(C.byref(qs))
+            lib.check(L.kvl_mla_synchronize(), "sync")
+            f0 = L.kvl_mla_event_record()
+            lib.check(L.kvl_mla_prefill_compressed_q8_state_device(d_po, d_px, S, C.byref(cfg), C.byref(wstructs[0]),
+                                                                   C.byref(qs)), "prefill + state fill")
+            f1 = L.kvl_mla_event_record()
+            if rep:
+                fms.append(L.kvl_mla_event_elapsed_ms(f0, f1))
+        fm = float(np.median(fms))
+        result["prefill"]["with_q8_state_fill_ms"] = round(fm, 4)
+        log(f"[bench] prefill + Q8 state fill S={S}: {fm:.3f} ms")
+        L.kvl_mla_compressed_q8_state_free(C.byref(qs))
         L.kvl_mla_device_free(d_px)
         L.kvl_mla_device_free(d_po)
 

@@ -287,7 +287,8 @@ hipError_t launch_gemv_ksplit(hipStream_t st, float *Y, size_t pstride, int ldy,
 // itself with the same operand layout (W rows as A, k slot 8 g + i), so every partial
 // coincides. The activations come as bf16 planes from k_split, which rounds as split8_part
 // does for finite values. Block: 64 rows x 128 tokens x one k quarter, wave w taking tokens
-// 32 w .. 32 w + 31 (two 16-token tiles) for all four row tiles.
+// 32 w .. 32 w + 31 (two 16-token tiles) for all four row tiles. Used for in = 4096 (KPW 2);
+// in = 2048 takes the LDS-tiled k_kva_gemm below.
 struct KvaTokArgs {
     float *Y;                  // partial kq at Y + kq * pstride, [S, ldy]
     const uint16_t *XH, *XL;   // [S, in] bf16 hi / lo planes
@@ -376,6 +377,123 @@ __global__ __launch_bounds__(256) void k_kva_tok(KvaTokArgs a) {
     }
 }
 
+// The same partials for in = 2048 (one 32-wide k-block per k_gemv_ksplit wave) as a tiled
+// GEMM: x hi, x lo and W stream through a 3-stage LDS ring by DMA (16-byte slot s of a 64-byte
+// row r stored at s ^ ((r >> 1) & 3), so the 8 rows of one ds_read_b128 phase hit distinct
+// banks). Block: 128 tokens x 192 rows x one k quarter, 6 waves of 64 tokens x 64 rows (4 x 4
+// MFMA tiles); per 32-wide k step each tile takes one MFMA from a zero accumulator for the hi
+// and one for the lo half, added to the running sums in k order (the sums of k_gemv_ksplit's
+// waves 0..15). Tiles are numbered row block fastest, then quarter, then token block, and XCD
+// b % 8 takes a contiguous eighth of them, so the row blocks sharing a token block's
+// activations run under one L2.
+constexpr int kKvgNT = 2, kKvgNR = 3;  // waves along tokens, along rows
+constexpr int kKvgBT = 64 * kKvgNT, kKvgBR = 64 * kKvgNR;
+
+__global__ __launch_bounds__(64 * kKvgNT * kKvgNR) void k_kva_gemm(KvaTokArgs a) {
+    constexpr int NWV = kKvgNT * kKvgNR, NT = 64 * NWV, BT = kKvgBT, BR = kKvgBR;
+    constexpr int ROWB = 64, XPL = BT * ROWB, STAGE = 2 * XPL + BR * ROWB;
+    constexpr int SLOTS = STAGE / 16, NI = (SLOTS + NT - 1) / NT, NMIN = SLOTS / NT;
+    static_assert(SLOTS % 64 == 0, "the ring is filled by whole waves");
+    __shared__ __attribute__((aligned(16))) uint8_t smem[3 * STAGE];
+    const uint32_t sbase = lds_addr(smem);
+    const int tid = threadIdx.x, l = tid & 63, n = l & 15, g = l >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wt = w % kKvgNT, wr = w / kKvgNT;
+    const int nrb = (a.out + BR - 1) / BR, ntb = (a.S + BT - 1) / BT, nt = nrb * kGemvKs * ntb;
+    int tile = blockIdx.x;
+    if (nt % 8 == 0) tile = (tile & 7) * (nt / 8) + (tile >> 3);
+    const int rb = tile % nrb, kq = (tile / nrb) % kGemvKs, tb = tile / nrb / kGemvKs;
+    const int row0 = rb * BR, tok0 = tb * BT;
+    auto swz = [](int row) { return (row >> 1) & 3; };
+    // DMA: wave w's instruction i fills slots (i * NWV + w) * 64 .. + 63 of a stage: x hi rows,
+    // x lo rows, then W rows, 4 slots each. Rows past the end are clamped (never stored).
+    const uint8_t *src[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int p = min((i * NWV + w) * 64 + l, SLOTS - 1);
+        const int xrow = (p % (BT * 4)) / 4, wrow = (p - 2 * BT * 4) / 4;
+        const uint16_t *rp;
+        int s;
+        if (p < 2 * BT * 4) {
+            rp = (p < BT * 4 ? a.XH : a.XL) + (size_t)min(tok0 + xrow, a.S - 1) * a.in;
+            s = (p & 3) ^ swz(xrow);
+        } else {
+            rp = a.W + (size_t)min(row0 + wrow, a.out - 1) * a.in;
+            s = (p & 3) ^ swz(wrow);
+        }
+        src[i] = (const uint8_t *)(rp + kq * 512 + 8 * s);
+    }
+    auto issue = [&](int j) __attribute__((always_inline)) {
+        const uint32_t dst = sbase + (j % 3) * STAGE + (uint32_t)w * 1024;
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+            if (i < NMIN || (i * NWV + w) * 64 < SLOTS) dma_b128(src[i] + (size_t)j * 64, dst + i * (NWV * 1024));
+    };
+    int fx[4], fw[4];  // fragment offsets: row 16 u + n of the wave's tile, logical slot g
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int row = 64 * wt + 16 * u + n;
+        fx[u] = row * ROWB + 16 * (g ^ swz(row));
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int row = 64 * wr + 16 * t + n;
+        fw[t] = 2 * XPL + row * ROWB + 16 * (g ^ swz(row));
+    }
+    v4f sh[4][4], sl[4][4];
+    issue(0);
+    issue(1);
+    auto step = [&](int j) __attribute__((always_inline)) {
+        // stage j has landed when only stage j + 1 may still be in flight (a wave issues NMIN
+        // or NMIN + 1 copies per stage; waiting for NMIN is exact or conservative)
+        if (j + 1 < 16) wait_vmcnt<NMIN>();
+        else wait_vmcnt<0>();
+        lds_barrier();  // also: every wave is done with stage j - 1, refilled next
+        if (j + 2 < 16) issue(j + 2);
+        const uint8_t *st = smem + (j % 3) * STAGE;
+        v8bf xh[4], xl[4], wv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            xh[u] = *(const v8bf *)(st + fx[u]);
+            xl[u] = *(const v8bf *)(st + XPL + fx[u]);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) wv[t] = *(const v8bf *)(st + fw[t]);
+        const v4f z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const v4f rh = mfma_bf16(wv[t], xh[u], z);
+                const v4f rl = mfma_bf16(wv[t], xl[u], z);
+                sh[t][u] = j == 0 ? rh : sh[t][u] + rh;
+                sl[t][u] = j == 0 ? rl : sl[t][u] + rl;
+            }
+    };
+    step(0);
+#pragma nounroll
+    for (int j = 1; j < 16; ++j) step(j);
+    float *y = a.Y + (size_t)kq * a.pstride;
+    const bool vec = (a.ldy & 3) == 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int tok = tok0 + 64 * wt + 16 * u + n;
+        if (tok >= a.S) continue;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const v4f p = sh[t][u] + sl[t][u];  // lane (g, n): rows 4 g .. 4 g + 3, token n
+            const int r = row0 + 64 * wr + 16 * t + 4 * g;
+            float *yp = y + (size_t)tok * a.ldy + r;
+            if (vec && r + 3 < a.out) {
+                *(v4f *)yp = p;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (r + i < a.out) yp[i] = p[i];
+            }
+        }
+    }
+}
+
 hipError_t launch_kva_tok(hipStream_t st, float *Y, size_t pstride, int ldy, const uint16_t *XH,
                           const uint16_t *XL, int S, const uint16_t *W, int out, int in) {
     if (!gemv_ksplit_ok(in, in) || S < 1 || out <= 0 || ldy < out || (S + 127) / 128 > 65535 ||
@@ -383,9 +501,14 @@ hipError_t launch_kva_tok(hipStream_t st, float *Y, size_t pstride, int ldy, con
         ((uintptr_t)Y % 16) != 0 || pstride % 4 != 0)
         return hipErrorInvalidValue;
     KvaTokArgs a{Y, XH, XL, W, pstride, ldy, S, out, in};
-    const dim3 grid((out + 63) / 64, kGemvKs, (S + 127) / 128);
-    if (in == 2048) hipLaunchKernelGGL((k_kva_tok<1>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((k_kva_tok<2>), grid, dim3(256), 0, st, a);
+    if (in == 2048) {
+        const size_t tiles = (size_t)((out + kKvgBR - 1) / kKvgBR) * kGemvKs * ((S + kKvgBT - 1) / kKvgBT);
+        if (tiles > 0x7fffffff) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(k_kva_gemm, dim3((unsigned)tiles), dim3(64 * kKvgNT * kKvgNR), 0, st, a);
+    } else {
+        const dim3 grid((out + 63) / 64, kGemvKs, (S + 127) / 128);
+        hipLaunchKernelGGL((k_kva_tok<2>), grid, dim3(256), 0, st, a);
+    }
     return hipGetLastError();
 }
 

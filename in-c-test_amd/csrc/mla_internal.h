@@ -161,9 +161,10 @@ size_t prefill_bytes(const Dims &d, int S);
 // prefill_bytes(d, S) bytes, rope_cs table covering positions [0, S).
 // wo16: o_proj converted to fp16 (launch_bf16_to_f16), used by the MFMA route (the attention
 // output enters the o_proj GEMM as fp16).
-// kva (optional): receives where the kv_a projection of the S tokens lies in ws when it was
-// computed with the decode arithmetic (launch_kva_tok partials), so a state fill can reuse
-// it; kva->y is null otherwise. Valid until ws is reused.
+// kva (optional): asks for the kv_a projection of the S tokens in the decode arithmetic
+// (launch_kva_tok partials, where prefill_kva_exact) so a state fill can reuse it; receives
+// its place in ws, or kva->y = null when these dims do not allow it. Valid until ws is reused.
+// Without kva the projection is part of the q GEMM (another summation order).
 struct PrefillKva {
     const float *y;
     int ldy, np;
@@ -174,7 +175,7 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
                               const uint16_t *wnorm, const uint16_t *wkvb, const uint16_t *wo,
                               const _Float16 *wo16, const float2 *rope_cs, void *ws,
                               PrefillKva *kva = nullptr);
-// True when the prefill's kv_a projection uses the decode arithmetic (launch_kva_tok).
+// True when a prefill of these dims can give its kv_a projection in the decode arithmetic.
 bool prefill_kva_exact(const Dims &d);
 // True when the prefill of these dims takes the MFMA route (needs the fp16 o_proj copy).
 bool prefill_mfma_shape(const Dims &d);

@@ -318,8 +318,9 @@ __global__ __launch_bounds__(512) void k_gemm16(GemmArgs a, GemmEpi e) {
     }
 }
 
-// C = A . [B0; B1]^T with N0 + N1 output columns (N1 = 0: a single weight matrix). The
-// 256 x 256 tile is used when it still gives one tile per CU, else 256 x 128.
+// C = A . [B0; B1]^T with N0 + N1 output columns (N1 = 0: a single weight matrix). One block
+// per CU: the 256 x 256 tile is used unless 256 x 128 tiles (half the work each) need fewer
+// than twice as many rounds over the 256 CUs.
 template <int EPI, bool F16 = false>
 static hipError_t gemm(hipStream_t st, const uint16_t *Ah, const uint16_t *Al, const int *flag,
                        int lda, const uint16_t *B0, int N0, const uint16_t *B1, int N1, int ldb,
@@ -328,12 +329,13 @@ static hipError_t gemm(hipStream_t st, const uint16_t *Ah, const uint16_t *Al, c
     const int tm = (M + kGBm - 1) / kGBm;
     const int t256 = tm * ((N0 + 255) / 256 + (N1 + 255) / 256);
     const int t128 = tm * ((N0 + 127) / 128 + (N1 + 127) / 128);
+    const bool big = 2 * ((t256 + 255) / 256) <= (t128 + 255) / 256;
     if (Al) {
-        if (t256 >= 224) hipLaunchKernelGGL((k_gemm16<256, EPI, F16, true>), dim3(t256), dim3(512), 0, st, a, e);
+        if (big) hipLaunchKernelGGL((k_gemm16<256, EPI, F16, true>), dim3(t256), dim3(512), 0, st, a, e);
         else hipLaunchKernelGGL((k_gemm16<128, EPI, F16, true>), dim3(t128), dim3(512), 0, st, a, e);
     } else {
         if (K % 64) return hipErrorInvalidValue;
-        if (t256 >= 224) hipLaunchKernelGGL((k_gemm16<256, EPI, F16, false>), dim3(t256), dim3(512), 0, st, a, e);
+        if (big) hipLaunchKernelGGL((k_gemm16<256, EPI, F16, false>), dim3(t256), dim3(512), 0, st, a, e);
         else hipLaunchKernelGGL((k_gemm16<128, EPI, F16, false>), dim3(t128), dim3(512), 0, st, a, e);
     }
     return hipGetLastError();
@@ -900,7 +902,7 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
         int *flags = (int *)take(4 * 8);
         uint16_t *xh = (uint16_t *)take(2 * (size_t)S * d.H);
         uint16_t *xl = (uint16_t *)take(2 * (size_t)S * d.H);
-        const bool exact = prefill_kva_exact(d);
+        const bool exact = kva && prefill_kva_exact(d);
         const int np = exact ? kGemvKs : 1;
         float *ykva = (float *)take(4 * (size_t)S * d.KVO * np);
         uint16_t *lath = (uint16_t *)take(2 * (size_t)S * d.R);
@@ -916,8 +918,9 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
         const int split_blocks = (int)std::min<size_t>(2048, ((size_t)S * d.H / 8 + 255) / 256);
         hipLaunchKernelGGL(k_split, dim3(split_blocks), dim3(256), 0, st, x, d.H, xh, xl, d.H, S, d.H, flags + 0);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        // q (-> Q hi/lo, rotated) | kv_a (-> ykva); with the decode's k-split arithmetic for
-        // kv_a where the decode uses it, so the state rows of these tokens can come from it
+        // q (-> Q hi/lo, rotated) | kv_a (-> ykva). When the caller fills a state from this
+        // kv_a, it is computed with the decode's k-split arithmetic (launch_kva_tok) so those
+        // rows equal the rows a decode appends; otherwise it rides along in the q GEMM.
         if (exact) {
             if ((e = gemm<kEpiQ>(st, xh, xl, flags + 0, d.H, wq, d.QO, nullptr, 0, d.H, nullptr, 0, S, d.H,
                                  ep)) != hipSuccess)

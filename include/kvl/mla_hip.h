@@ -82,13 +82,15 @@ int kvl_mla_decode_compressed_batch_device(float *d_out, const float *d_x, int b
 int kvl_mla_prefill_device(float *d_out, const float *d_x, int seq_len, const KvlMlaConfig *cfg,
                            const KvlMlaBF16 *w);
 
-/* Prefill with the state fill of the same tokens, as src/generate.c:208-210 sequences them:
- * out and the state (rows [0, seq_len), len = seq_len) equal, bit for bit, what
- * kvl_mla_prefill_bf16(out, x, ...) followed by kvl_mla_compressed[_q8]_state_prefill_bf16(x,
- * ...) produce, with the same argument checks (state empty, seq_len <= capacity). One upload of
- * x; the state rows come from the kv_a projection the prefill computes anyway (where its
- * shapes let it use the decode's arithmetic, e.g. hidden 2048 or 4096; otherwise the fill
- * computes its own from the uploaded x). Synchronous; host rows written. */
+/* Prefill with the state fill of the same tokens, as src/generate.c:208-210 sequences them
+ * (kvl_mla_prefill_bf16(out, x, ...), then kvl_mla_compressed[_q8]_state_prefill_bf16(x, ...)),
+ * with the same argument checks (state empty, seq_len <= capacity). The state (rows
+ * [0, seq_len), len = seq_len) equals the state prefill's bit for bit. One upload of x; where
+ * the shapes allow it (hidden 2048 or 4096 on the MFMA route) the prefill computes its kv_a
+ * projection in the decode's summation order and both its attention and the state rows use
+ * that one projection, so out equals kvl_mla_prefill_bf16's up to the rounding of kv_a
+ * (kvl_mla_prefill_bf16 sums it inside its q GEMM); otherwise out is bit-identical and the
+ * fill computes its own kv_a from the uploaded x. Synchronous; host rows written. */
 int kvl_mla_prefill_compressed_state_bf16(float *out, const float *x, int seq_len,
                                           const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
                                           KvlMlaCompressedState *state);

@@ -73,8 +73,10 @@ CASES = [("stream", STREAM, 37, 0.2, False), ("kimi", KIMI, 130, 0.02, False), (
 @pytest.mark.parametrize("name,dims,S,std,bf16_x", CASES, ids=[f"{c[0]}-{c[2]}" for c in CASES])
 @pytest.mark.parametrize("kind", ["f32", "q8"])
 def test_fused_equals_prefill_then_state_prefill(name, dims, S, std, bf16_x, kind):
-    """Bit-identical to the two calls: the generic route (stream-probe shapes, the fill computes
-    its own kv_a) and the Kimi-VL MFMA route (kv_a shared), S not a multiple of the tiles."""
+    """State bit-identical to the state prefill's. Generic route (stream-probe shapes, the fill
+    computes its own kv_a): output bit-identical too. Kimi-VL MFMA route (one kv_a for the
+    attention and the state, in the decode's summation order): output within the rounding of
+    kv_a of the plain prefill's. S not a multiple of the tiles."""
     print(f"[fused] {kind} {name} S={S}", flush=True)
     cfg = inputs.config(**dims)
     layer = inputs.make_layer(cfg, 0xF0 + S, std=std)
@@ -83,7 +85,11 @@ def test_fused_equals_prefill_then_state_prefill(name, dims, S, std, bf16_x, kin
     oa, sa = separate(kind, cfg, w, x, S + 3)
     ob, sb = fused(kind, cfg, w, x, S + 3)
     assert sa.len == sb.len == S
-    np.testing.assert_array_equal(ob, oa)
+    if name == "stream":
+        np.testing.assert_array_equal(ob, oa)
+    else:
+        print(f"[fused]   vs plain prefill max|d|/max|ref| = {rel_err(ob, oa):.3e}", flush=True)
+        assert rel_err(ob, oa) <= 1e-4
     assert_snap_equal(snapshot(kind, sb, cfg), snapshot(kind, sa, cfg))
     free_state(G, kind, sa)
     free_state(G, kind, sb)
