@@ -105,6 +105,7 @@ def main():
     ap.add_argument("--prefill-tokens", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-block", action="store_true", help="skip the block-verify leg")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain copy kernel of MIB MiB (memory-counter calibration)")
@@ -274,6 +275,44 @@ def main():
         result["parity"] = {"layer0_max_rel_err_vs_cpu": float(max(errs)), "tolerance": 2e-3,
                             "sequences": n_done}
         log(f"[bench] cpu baseline {result['cpu_baseline']['value']} GB/s ({kind}), parity {max(errs):.2e}")
+
+    # ---- block verify: 8 draft tokens of one sequence over the 32K Q8 history of layer 0 ----
+    # (host API both ways: one block call against 8 single-token decodes; equal bit for bit)
+    if not args.no_block:
+        T = 8
+        bst = abi.KvlMlaCompressedQ8State()
+        lib.check(L.kvl_mla_compressed_q8_state_init(C.byref(bst), C.byref(cfg), CTX + T), "block state init")
+        lib.check(L.kvl_mla_compressed_q8_state_fill_synthetic(C.byref(bst), 0, CTX, 0xB5), "block state fill")
+        xb = np.ascontiguousarray(inputs.hidden(cfg, 0xB5, T, tag="block_x"))
+        o_blk, o_ser = np.zeros_like(xb), np.zeros_like(xb)
+        fp = lambda a: a.ctypes.data_as(abi.f32p)  # noqa: E731
+
+        def serial():
+            for t in range(T):
+                lib.check(L.kvl_mla_decode_compressed_q8_bf16(fp(o_ser[t]), fp(xb[t]), CTX + t, C.byref(cfg),
+                                                              C.byref(wstructs[0]), C.byref(bst)), "serial decode")
+            lib.check(L.kvl_mla_compressed_q8_state_truncate(C.byref(bst), CTX), "truncate")
+
+        def block():
+            lib.check(L.kvl_mla_decode_compressed_q8_block_bf16(fp(o_blk), fp(xb), T, CTX, C.byref(cfg),
+                                                                C.byref(wstructs[0]), C.byref(bst)), "block decode")
+            lib.check(L.kvl_mla_compressed_q8_state_truncate(C.byref(bst), CTX), "truncate")
+
+        times = {}
+        for name, fn in (("serial", serial), ("block", block)):
+            fn()
+            reps = 5
+            ts = time.perf_counter()
+            for _ in range(reps):
+                fn()
+            times[name] = (time.perf_counter() - ts) * 1e3 / reps
+        same = bool(np.array_equal(o_blk, o_ser))
+        result["block_verify"] = {"tokens": T, "context": CTX, "block_ms": round(times["block"], 3),
+                                  "serial_ms": round(times["serial"], 3), "bit_identical": same,
+                                  "api": "host buffers, synchronous"}
+        log(f"[bench] block verify {T} tokens @{CTX}: block {times['block']:.3f} ms, "
+            f"serial {times['serial']:.3f} ms, identical {same}")
+        L.kvl_mla_compressed_q8_state_free(C.byref(bst))
 
     # ---- causal prefill, 4096 tokens -----------------------------------------------------
     if not args.no_prefill:

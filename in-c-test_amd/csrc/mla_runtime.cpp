@@ -578,9 +578,27 @@ struct SeqIn {
 // One decode step for a group of B <= kMaxBatch sequences whose mirrors are synced.
 // d_x: device input rows [B,H]; d_out: device output rows [B,H]. Rows appended on the device
 // at each pos; staged copies in w.rows.
+// Balanced split-K plan of the MFMA attention kernels: about wg_per_cu workgroups per CU in
+// total, shared among the sequences of a launch in proportion to their lengths (len of
+// total_rows); rows per split a multiple of the kernel's chunk (rounded down), at least four
+// chunks, at most 1024 rows for Q8 (every split < 2048 rows). The last split of a sequence
+// takes the remainder: nsplit = max(1, len / rows).
+long split_rows(int kind, long len, long total_rows, int ncu) {
+    const int chunk = kind == kAttnQ8Mfma ? 64 : 16;
+    const int wg_per_cu = kind == kAttnQ8Mfma ? 1 : 3;
+    const double target = (double)wg_per_cu * ncu;
+    const long want = std::max(1L, std::lround(target * (double)len / (double)total_rows));
+    long r = len / (want * chunk) * chunk;
+    r = std::max<long>(r, 4L * chunk);
+    if (kind == kAttnQ8Mfma) r = std::min<long>(r, 1024L);
+    return r;
+}
+
+// solo: every sequence gets the plan it would get alone in the launch, so its result does
+// not depend on the other members (block decode).
 int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeights &dw,
                  const SeqIn *seqs, int B, const float *d_x, float *d_out, bool residual,
-                 DecodeWork &w) {
+                 DecodeWork &w, bool solo = false) {
     Ctx &c = ctx();
     hipStream_t st = c.stream;
     int maxpos = 0;
@@ -605,7 +623,7 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
         total_rows += s.len;
         lmax = std::max(lmax, s.len);
     }
-    // split-K plan: about two workgroups per CU, rows per split a multiple of the chunk
+    // split-K plan (split_rows)
     int rps = 0, total_splits = 0;
     if (kind == kAttnGeneric) {
         for (int i = 0; i < B; ++i) {
@@ -614,18 +632,9 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
         }
         total_splits = fmt == kFmtExp ? B * d.NH : B;
     } else {
-        // Balanced split-K: about wg_per_cu workgroups per CU in total, shared among the
-        // sequences in proportion to their lengths; rows per split a multiple of the
-        // kernel's chunk (rounded down), the last split of a sequence takes the remainder.
-        const int chunk = kind == kAttnQ8Mfma ? 64 : 16;
-        const int wg_per_cu = kind == kAttnQ8Mfma ? 1 : 3;
-        const double target = (double)wg_per_cu * c.ncu;
         for (int i = 0; i < B; ++i) {
             SeqDesc &s = t.s[i];
-            const long want = std::max(1L, std::lround(target * (double)s.len / (double)total_rows));
-            long r = (long)s.len / (want * chunk) * chunk;
-            r = std::max<long>(r, 4L * chunk);
-            if (kind == kAttnQ8Mfma) r = std::min<long>(r, 1024L);  // every split < 2048 rows
+            const long r = split_rows(kind, s.len, solo ? s.len : total_rows, c.ncu);
             s.rps = (int)r;
             s.split0 = total_splits;
             s.nsplit = std::max(1, (int)(s.len / r));
@@ -810,6 +819,73 @@ int decode_host(float *out, const float *x, const int *positions, int B, const K
             s->len = pos + 1;
             seqs[i].m->synced = s->len;
         }
+    }
+    return 0;
+}
+
+// Block decode of `count` tokens of one sequence (src/mla_compressed_state.c:163-184 loops the
+// single-token decode). Here the tokens run through the batched path as members that share the
+// state: member t sits at position start + t and gets the split plan a lone decode at that
+// position gets. Each stage computes a member exactly as a lone decode computes its token (the
+// projections, the append, the attention splits, the combine and o_proj depend only on that
+// member's inputs and rows), and a group's rows are all appended before its attention reads
+// them (member t reads rows [0, start + t]). Outputs and rows therefore equal the serial
+// loop's bit for bit; the launches and the history reads of a group are shared.
+template <class S>
+int decode_block(float *out, const float *x, int count, int start, const KvlMlaConfig *cfg,
+                 const KvlMlaBF16 *w, S *state) {
+    Dims d;
+    if (!out || !x || !cfg || !w || !state || count <= 0 || start != state->len || start < 0 ||
+        count > state->capacity - start) {
+        set_err("invalid arguments");
+        return -1;
+    }
+    if (!weights_ok(w) || !dims_of(cfg, d) || !state_dims_ok(state, cfg)) {
+        set_err("invalid config, weights or state dims");
+        return -1;
+    }
+    if (!dims_supported(d)) return -1;
+    if (ensure_ready() != 0) return -1;
+    Ctx &c = ctx();
+    const int fmt = fmt_of<S>();
+    DevWeights dw;
+    if (dev_weights(w, d, dw) != 0) return -1;
+    const size_t rb = row_bytes_of(fmt, d.R, d.DR, 0);
+    Mirror *m = nullptr;
+    if (mirror_get(state, view_of(state), &m) != 0) return -1;
+    const int kind = !kimi_attn(d) ? kAttnGeneric : fmt == kFmtQ8 ? kAttnQ8Mfma : kAttnF32Mfma;
+    for (int t0 = 0; t0 < count;) {
+        // members of this group: at most kMaxBatch, and their lone plans within 2048 splits
+        int n = 0;
+        long splits = 0;
+        while (t0 + n < count && n < kMaxBatch) {
+            const long len = (long)start + t0 + n + 1;
+            const long ns = kind == kAttnGeneric ? 1 : std::max(1L, len / split_rows(kind, len, len, c.ncu));
+            if (n > 0 && splits + ns > 2048) break;
+            splits += ns;
+            ++n;
+        }
+        DecodeWork wk;
+        if (decode_work(d, n, (int)rb, wk) != 0) return -1;
+        SeqIn seqs[kMaxBatch];
+        for (int i = 0; i < n; ++i) seqs[i] = {m, start + t0 + i};
+        const size_t xin = (size_t)n * d.H * sizeof(float);
+        if (pin_reserve(c.pin_in, xin) != 0 || pin_reserve(c.pin_out, xin + (size_t)n * rb) != 0) return -1;
+        memcpy(c.pin_in.p, x + (size_t)t0 * d.H, xin);
+        HIP_TRY(hipMemcpyAsync(wk.x, c.pin_in.p, xin, hipMemcpyHostToDevice, c.stream));
+        if (decode_group(fmt, d, cfg->rms_eps, cfg->rope_theta, dw, seqs, n, wk.x, wk.out, false, wk, true) != 0)
+            return -1;
+        HIP_TRY(hipMemcpyAsync(c.pin_out.p, wk.out, xin, hipMemcpyDeviceToHost, c.stream));
+        HIP_TRY(hipMemcpyAsync((char *)c.pin_out.p + xin, wk.rows, (size_t)n * rb, hipMemcpyDeviceToHost,
+                               c.stream));
+        HIP_TRY(hipStreamSynchronize(c.stream));
+        memcpy(out + (size_t)t0 * d.H, c.pin_out.p, xin);
+        const HostView v = view_of(state);
+        for (int i = 0; i < n; ++i)
+            write_back_rows(fmt, v, start + t0 + i, (const uint8_t *)c.pin_out.p + xin + (size_t)i * rb);
+        state->len = start + t0 + n;
+        m->synced = state->len;
+        t0 += n;
     }
     return 0;
 }
@@ -1342,17 +1418,14 @@ int kvl_mla_decode_compressed_block_bf16(float *out, const float *x, int count, 
                                          const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
                                          KvlMlaCompressedState *state) {
     Guard guard;
-    if (!out || !x || !cfg || !w || !state || count <= 0 || start_position != state->len ||
-        start_position < 0 || count > state->capacity - start_position)
-        return -1;
-    const int H = cfg->hidden_size;
-    if (H <= 0) return -1;
-    for (int t = 0; t < count; ++t) {
-        KvlMlaCompressedState *st[1] = {state};
-        const int pos = start_position + t;
-        if (decode_host(out + (size_t)t * H, x + (size_t)t * H, &pos, 1, cfg, w, st) != 0) return -1;
-    }
-    return 0;
+    return decode_block(out, x, count, start_position, cfg, w, state);
+}
+
+int kvl_mla_decode_compressed_q8_block_bf16(float *out, const float *x, int count, int start_position,
+                                            const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                            KvlMlaCompressedQ8State *state) {
+    Guard guard;
+    return decode_block(out, x, count, start_position, cfg, w, state);
 }
 
 // ---- include/kvl/mla_compressed_q8_state.h ----------------------------------------------

@@ -27,6 +27,8 @@ EXT_API = {
                                                    abi.CFG, abi.W, CSP]),
     "mla_decode_compressed_q8_batch_bf16": (C.c_int, [abi.f32p, abi.f32p, C.POINTER(C.c_int),
                                                       C.c_int, abi.CFG, abi.W, QSP]),
+    "mla_decode_compressed_q8_block_bf16": (C.c_int, [abi.f32p, abi.f32p, C.c_int, C.c_int, abi.CFG, abi.W,
+                                                      abi.QS]),
     "mla_decode_compressed_q8_batch_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, abi.CFG,
                                                         abi.W, QSP, C.c_uint]),
     "mla_decode_compressed_batch_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, abi.CFG,

@@ -39,7 +39,9 @@ int kvl_mla_decode_compressed_bf16(float *out, const float *x, int position,
                                    KvlMlaCompressedState *state);
 
 /* include/kvl/mla_compressed_state.h:40-46 (src/mla_compressed_state.c:163-184).
- * Serial per-token decode of `count` tokens; every token takes the single-token path. */
+ * Decode of `count` tokens of one sequence, equal bit for bit to `count` single-token decodes
+ * (the reference loops them): the tokens run as one batch whose members share the state, each
+ * computed as a lone decode at its position would be. */
 int kvl_mla_decode_compressed_block_bf16(float *out, const float *x, int count,
                                          int start_position, const KvlMlaConfig *cfg,
                                          const KvlMlaBF16 *w, KvlMlaCompressedState *state);

@@ -59,6 +59,15 @@ int kvl_mla_decode_compressed_q8_batch_bf16(float *out, const float *x, const in
                                             const KvlMlaBF16 *w,
                                             KvlMlaCompressedQ8State *const *states);
 
+/* Block decode over the Q8 history, the counterpart of kvl_mla_decode_compressed_block_bf16
+ * (which the reference defines for the FP32 state only, src/mla_compressed_state.c:163-184):
+ * count tokens at positions start_position .. start_position + count - 1 (start_position must
+ * equal len). Outputs and appended rows equal those of count single-token decodes bit for bit;
+ * the tokens share launches and history reads. */
+int kvl_mla_decode_compressed_q8_block_bf16(float *out, const float *x, int count,
+                                            int start_position, const KvlMlaConfig *cfg,
+                                            const KvlMlaBF16 *w, KvlMlaCompressedQ8State *state);
+
 /* Flags of the device-pointer variants. */
 #define KVL_MLA_RESIDUAL 1u   /* out += attention(x) instead of out = attention(x)      */
 #define KVL_MLA_NO_ADVANCE 2u /* append at position len but leave len (and host rows)  */
