@@ -144,7 +144,7 @@ struct Ctx {
     std::unordered_map<const void *, WeightEntry> weights;
     std::unordered_map<const void *, Mirror> mirrors;
     std::unordered_map<uint64_t, RopeTable> ropes;  // key: theta bits << 16 | DR
-    DevBuf work, part, scores, prefill, fill, fillx;
+    DevBuf work, part, scores, prefill, fill, fillx, layer;
     PinBuf pin_in, pin_out;
     bool capturing = false;
     // per-stage event timing of decode steps (kvl_mla_timing_*)
@@ -820,6 +820,47 @@ int decode_host(float *out, const float *x, const int *positions, int B, const K
             seqs[i].m->synced = s->len;
         }
     }
+    return 0;
+}
+
+template <class S>
+int decode_device(float *d_out, const float *d_x, int B, const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                  S *const *states, unsigned flags);
+
+// The attention half of a decoder layer (src/generate.c:34-67, attention_token) for a batch,
+// stream-ordered over device buffers: n1 = RMSNorm(h, input_norm) (src/ops.c:76-83 rounding),
+// h += attention(n1) with each sequence's row appended, n2 = RMSNorm(h, post_attn_norm) for
+// the MLP. The residual add is the o_proj kernel's accumulate: h + o, as the reference's
+// r1[i] = x[i] + attn[i].
+template <class S>
+int attention_layer_device(float *d_h, float *d_n2, int B, const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                           const uint16_t *input_norm, const uint16_t *post_norm, S *const *states,
+                           unsigned flags) {
+    if (!d_h || !d_n2 || d_n2 == d_h || B <= 0 || !cfg || !input_norm || !post_norm || cfg->hidden_size <= 0) {
+        set_err("invalid arguments");
+        return -1;
+    }
+    if (flags & ~(unsigned)KVL_MLA_NO_ADVANCE) {
+        set_err("unsupported flags (the residual add is implied)");
+        return -1;
+    }
+    if (ensure_ready() != 0) return -1;
+    Ctx &c = ctx();
+    const int H = cfg->hidden_size;
+    const uint16_t *din = nullptr, *dpost = nullptr;
+    if (dev_weight(input_norm, (size_t)H, &din) != 0 || dev_weight(post_norm, (size_t)H, &dpost) != 0) return -1;
+    const size_t need = (size_t)B * H * sizeof(float);
+    if (c.layer.bytes < need) {
+        if (c.capturing) {
+            set_err("layer workspace growth during graph capture");
+            return -1;
+        }
+        if (dev_reserve(c.layer, need) != 0) return -1;
+    }
+    float *n1 = (float *)c.layer.p;
+    HIP_TRY(launch_rmsnorm(c.stream, n1, d_h, din, H, B, cfg->rms_eps));
+    if (decode_device(d_h, n1, B, cfg, w, states, flags | KVL_MLA_RESIDUAL) != 0) return -1;
+    HIP_TRY(launch_rmsnorm(c.stream, d_n2, d_h, dpost, H, B, cfg->rms_eps));
     return 0;
 }
 
@@ -1588,6 +1629,22 @@ int kvl_mla_decode_compressed_batch_device(float *d_out, const float *d_x, int b
                                            KvlMlaCompressedState *const *states, unsigned flags) {
     Guard guard;
     return decode_device(d_out, d_x, batch, cfg, w, states, flags);
+}
+
+int kvl_mla_attention_layer_q8_device(float *d_h, float *d_n2, int batch, const KvlMlaConfig *cfg,
+                                      const KvlMlaBF16 *w, const uint16_t *input_norm,
+                                      const uint16_t *post_attn_norm,
+                                      KvlMlaCompressedQ8State *const *states, unsigned flags) {
+    Guard guard;
+    return attention_layer_device(d_h, d_n2, batch, cfg, w, input_norm, post_attn_norm, states, flags);
+}
+
+int kvl_mla_attention_layer_device(float *d_h, float *d_n2, int batch, const KvlMlaConfig *cfg,
+                                   const KvlMlaBF16 *w, const uint16_t *input_norm,
+                                   const uint16_t *post_attn_norm, KvlMlaCompressedState *const *states,
+                                   unsigned flags) {
+    Guard guard;
+    return attention_layer_device(d_h, d_n2, batch, cfg, w, input_norm, post_attn_norm, states, flags);
 }
 
 void *kvl_mla_stream(void) {

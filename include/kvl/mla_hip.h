@@ -86,6 +86,24 @@ int kvl_mla_decode_compressed_batch_device(float *d_out, const float *d_x, int b
                                            KvlMlaCompressedState *const *states,
                                            unsigned flags);
 
+/* The attention half of a decoder layer, as src/generate.c:34-67 (attention_token) computes it
+ * for one token, for a batch over device buffers:
+ *   n1 = RMSNorm(h, input_norm); h += attention(n1) (appending each sequence's row);
+ *   n2 = RMSNorm(h, post_attn_norm).
+ * d_h [batch, hidden] is the residual stream (in/out), d_n2 [batch, hidden] receives the MLP
+ * input (must not alias d_h). The norms round as kvl_rmsnorm_bf16; the residual add is
+ * h[i] + attn[i] in fp32 as the reference's. input_norm / post_attn_norm: bf16 [hidden] host
+ * arrays (cached on the device like the weights). flags: 0 or KVL_MLA_NO_ADVANCE. Capturable
+ * once warm, like the decode variants. */
+int kvl_mla_attention_layer_q8_device(float *d_h, float *d_n2, int batch, const KvlMlaConfig *cfg,
+                                      const KvlMlaBF16 *w, const uint16_t *input_norm,
+                                      const uint16_t *post_attn_norm,
+                                      KvlMlaCompressedQ8State *const *states, unsigned flags);
+int kvl_mla_attention_layer_device(float *d_h, float *d_n2, int batch, const KvlMlaConfig *cfg,
+                                   const KvlMlaBF16 *w, const uint16_t *input_norm,
+                                   const uint16_t *post_attn_norm, KvlMlaCompressedState *const *states,
+                                   unsigned flags);
+
 /* Stream-ordered causal prefill over device buffers (d_x, d_out [seq_len, hidden] fp32);
  * same arithmetic as kvl_mla_prefill_bf16. */
 int kvl_mla_prefill_device(float *d_out, const float *d_x, int seq_len, const KvlMlaConfig *cfg,
