@@ -60,6 +60,23 @@ def test_prefill_sharp_attention(q_std):
     assert rel_err(a, b) <= TOL, rel_err(a, b)
 
 
+def test_prefill_repeats_bit_for_bit():
+    """Same inputs, same output: every stage (including the library GEMM of o_proj) picks its
+    kernels deterministically and sums in a fixed order."""
+    cfg = inputs.config(**inputs.KIMI)
+    layer = inputs.make_layer(cfg, 0xC9)
+    w = layer.struct()
+    S = 700
+    x = inputs.hidden(cfg, 0xC9, S)
+    outs = []
+    for _ in range(3):
+        o = np.zeros((S, cfg.hidden_size), np.float32)
+        lib.check(L.kvl_mla_prefill_bf16(f32(o), f32(x), S, C.byref(cfg), C.byref(w)), "prefill")
+        outs.append(o)
+    np.testing.assert_array_equal(outs[0], outs[1])
+    np.testing.assert_array_equal(outs[0], outs[2])
+
+
 def test_prefill_rejects_bad_arguments():
     cfg = inputs.config(**inputs.KIMI)
     layer = inputs.make_layer(inputs.config(**STREAM), 1)
