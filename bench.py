@@ -317,26 +317,35 @@ def main():
     # ---- causal prefill, 4096 tokens -----------------------------------------------------
     if not args.no_prefill:
         S = args.prefill_tokens
-        xs = np.ascontiguousarray(inputs.bf16_bits_to_f32(inputs.f32_to_bf16_bits(
-            np.random.default_rng(0xC3).standard_normal((S, H), dtype=np.float32))))
-        d_px = L.kvl_mla_device_alloc(xs.nbytes)
-        d_po = L.kvl_mla_device_alloc(xs.nbytes)
-        lib.check(L.kvl_mla_copy_to_device(d_px, xs.ctypes.data, xs.nbytes), "h2d")
-        for _ in range(2):
-            lib.check(L.kvl_mla_prefill_device(d_po, d_px, S, C.byref(cfg), C.byref(wstructs[0])), "prefill")
-        lib.check(L.kvl_mla_synchronize(), "sync")
-        reps = 5
-        p0 = L.kvl_mla_event_record()
-        for _ in range(reps):
-            lib.check(L.kvl_mla_prefill_device(d_po, d_px, S, C.byref(cfg), C.byref(wstructs[0])), "prefill")
-        p1 = L.kvl_mla_event_record()
-        pms = L.kvl_mla_event_elapsed_ms(p0, p1) / reps
+        # x as the layer sees it: fp32 RMSNorm outputs (full mantissa), so the q|kv_a GEMM runs
+        # its hi and lo passes; also timed with bf16-representable x, where the lo pass is skipped
+        x32 = np.random.default_rng(0xC3).standard_normal((S, H), dtype=np.float32)
+        xbf = np.ascontiguousarray(inputs.bf16_bits_to_f32(inputs.f32_to_bf16_bits(x32)))
+        d_px = L.kvl_mla_device_alloc(x32.nbytes)
+        d_po = L.kvl_mla_device_alloc(x32.nbytes)
+
+        def time_prefill(xs):
+            lib.check(L.kvl_mla_copy_to_device(d_px, xs.ctypes.data, xs.nbytes), "h2d")
+            for _ in range(2):
+                lib.check(L.kvl_mla_prefill_device(d_po, d_px, S, C.byref(cfg), C.byref(wstructs[0])), "prefill")
+            lib.check(L.kvl_mla_synchronize(), "sync")
+            reps = 5
+            p0 = L.kvl_mla_event_record()
+            for _ in range(reps):
+                lib.check(L.kvl_mla_prefill_device(d_po, d_px, S, C.byref(cfg), C.byref(wstructs[0])), "prefill")
+            p1 = L.kvl_mla_event_record()
+            return L.kvl_mla_event_elapsed_ms(p0, p1) / reps
+
+        pms_bf = time_prefill(xbf)
+        pms = time_prefill(np.ascontiguousarray(x32))
         flops = prefill_flops(S, cfg)
         tf = flops / (pms * 1e-3) / 1e12
         result["prefill"] = {"tokens": S, "ms": round(pms, 4), "tflops": round(tf, 2),
                              "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4),
-                             "algorithmic_gflop": round(flops / 1e9, 3)}
-        log(f"[bench] prefill S={S}: {pms:.3f} ms, {tf:.1f} TFLOP/s")
+                             "algorithmic_gflop": round(flops / 1e9, 3), "x": "fp32 N(0,1)",
+                             "bf16_x_ms": round(pms_bf, 4),
+                             "bf16_x_tflops": round(flops / (pms_bf * 1e-3) / 1e12, 2)}
+        log(f"[bench] prefill S={S}: {pms:.3f} ms, {tf:.1f} TFLOP/s (fp32 x); {pms_bf:.3f} ms with bf16 x")
         # the same prefill filling a Q8 state of the S tokens on the way (one call)
         qs = abi.KvlMlaCompressedQ8State()
         lib.check(L.kvl_mla_compressed_q8_state_init(C.byref(qs), C.byref(cfg), S), "state init")

@@ -1,7 +1,7 @@
 // HIP kernels of the causal MLA prefill (src/mla_prefill_streaming.c:78-206 of the
 // reference: non-absorbed attention, K/V expanded through kv_b for every token).
 //
-// MFMA route (H, R, QD multiples of 32, DV multiple of 16, DN multiple of 8):
+// MFMA route (H, R and NH * DV multiples of 64, QD = 192, DV = 128, DN multiple of 8):
 //   split     x (fp32) -> bf16 hi + lo operands; a flag records whether any lo is non-zero
 //   gemm      [q | kv_a] = x . W^T           (bf16 MFMA, fp32 accumulate, lo pass skipped
 //                                             when the operand is exactly bf16); epilogue:
@@ -60,26 +60,28 @@ __global__ void k_zero_int(int *p, int n) {
 //
 // Block tile 256 x BN (BN = 256 or 128), eight waves (2 per SIMD) in a WM x WN grid, each
 // owning a (256 / WM) x (BN / WN) quadrant of v_mfma_f32_16x16x32 tiles. Large tiles keep
-// the L2 traffic at 24-32 bytes per clock per CU at the MFMA rate. A hi, A lo and B stream
-// into an LDS ring of 3 stages (2 where 3 do not fit) by global_load_lds_dwordx4 DMA (the
-// later stages in flight while one is computed). With a lo operand possible (LOK) the k step is 32 (64-byte LDS rows, slot s of
-// row r at s ^ ((r >> 1) & 3)); without, the ring has room for a k step of 64 (128-byte
-// rows, slot s at s ^ (r & 7)), twice the MFMAs per barrier. Either swizzle spreads the 8
-// rows one ds_read_b128 phase touches over distinct banks. The lo pass runs when Al is
-// given and either no flag is given or *lo_flag != 0 (the flag is raised by the producer
-// of Al when some lo word is non-zero). Requires K % BK == 0, lda and ldb multiples of 8.
+// the L2 traffic at 24-32 bytes per clock per CU at the MFMA rate. The lo operand, when it
+// is given and needed, is a second pass over k: the k loop runs over [Ah | Al] against
+// [B | B], so each stage is one A and one B tile with a k step of 64, and all stages have
+// the same shape. They stream into an LDS ring of 3 stages (2 where 3 do not fit) by
+// global_load_lds_dwordx4 DMA (the later stages in flight while one is computed); 128-byte
+// rows with slot s at s ^ (r & 7) spread the 8 rows one ds_read_b128 phase touches over
+// distinct banks. Each wave reads all its fragments of a 32-deep k-sub before its MFMAs.
+// The lo pass runs when Al is given and either no flag is given or *lo_flag != 0 (the flag
+// is raised by the producer of Al when some lo word is non-zero). Requires K % 64 == 0, lda
+// and ldb multiples of 8.
 constexpr int kGBm = 256;
 
-template <int BN, bool LOK>
+template <int BN>
 struct GemmShape {
-    static constexpr int BK = LOK ? 32 : 64, RowB = BK * 2, Spr = BK / 8;  // slots per row
+    static constexpr int BK = 64, RowB = BK * 2, Spr = BK / 8;  // 16-byte slots per row
     static constexpr int WM = BN == 256 ? 2 : 4, WN = 8 / WM;
     static constexpr int TM = kGBm / WM / 16, TN = BN / WN / 16;  // 16x16 tiles per wave
     static constexpr int ATile = kGBm * RowB, BTile = BN * RowB;
-    static constexpr int Stage = (LOK ? 2 : 1) * ATile + BTile;
+    static constexpr int Stage = ATile + BTile;
     static constexpr int Stages = (160 * 1024) / Stage >= 3 ? 3 : 2;  // ring depth that fits
     static constexpr int Smem = Stages * Stage;
-    __device__ static int swz(int row) { return LOK ? (row >> 1) & 3 : row & 7; }
+    __device__ static int swz(int row) { return row & 7; }
 };
 
 struct GemmArgs {
@@ -112,9 +114,9 @@ __device__ __forceinline__ v4f mfma16(const v8bf &a, const v8bf &b, const v4f &c
     else return mfma_bf16(a, b, c);
 }
 
-template <int BN, int EPI, bool F16, bool LOK>
+template <int BN, int EPI, bool F16>
 __global__ __launch_bounds__(512) void k_gemm16(GemmArgs a, GemmEpi e) {
-    using Sh = GemmShape<BN, LOK>;
+    using Sh = GemmShape<BN>;
     constexpr int BK = Sh::BK, RowB = Sh::RowB, Spr = Sh::Spr;
     constexpr int TM = Sh::TM, TN = Sh::TN;
     __shared__ __attribute__((aligned(16))) uint8_t smem[Sh::Smem];
@@ -136,7 +138,7 @@ __global__ __launch_bounds__(512) void k_gemm16(GemmArgs a, GemmEpi e) {
     const int nb0 = seg1 ? (nt - tn0) * BN : nt * BN;  // first row of B in this tile
     const int c0 = seg1 ? N0 + nb0 : nb0;              // first column of C
     const int m0 = mt * kGBm;
-    const bool use_lo = LOK && a.Al && (!a.lo_flag || *a.lo_flag);
+    const bool use_lo = a.Al && (!a.lo_flag || *a.lo_flag);
 
     // DMA: thread (w, l), instruction i fills slot (8i + w) * 64 + l of a tile: row p / Spr,
     // physical slot p % Spr holding logical slot (p % Spr) ^ swz(row). Rows past the end of A
@@ -154,19 +156,18 @@ __global__ __launch_bounds__(512) void k_gemm16(GemmArgs a, GemmEpi e) {
         boff[i] = (uint32_t)(min(nb0 + row, Nseg - 1) - nb0) * ldb * 2 + 16 * s;
     }
     const uint8_t *gah = (const uint8_t *)(a.Ah + (size_t)m0 * lda);
-    const uint8_t *gal = a.Al ? (const uint8_t *)(a.Al + (size_t)m0 * lda) : nullptr;
+    const uint8_t *gal = use_lo ? (const uint8_t *)(a.Al + (size_t)m0 * lda) : gah;
     const uint8_t *gb = (const uint8_t *)(B + (size_t)nb0 * ldb);
+    const int nk = K / BK, nkt = use_lo ? 2 * nk : nk;  // k steps of the hi pass, of all passes
     auto issue = [&](int kt, int stage) __attribute__((always_inline)) {
         const uint32_t dst = sbase + stage * Sh::Stage + (uint32_t)w * 1024;
-        const size_t ko = (size_t)kt * BK * 2;
+        const bool lo = kt >= nk;
+        const uint8_t *ga = lo ? gal : gah;
+        const size_t ko = (size_t)(lo ? kt - nk : kt) * BK * 2;
 #pragma unroll
-        for (int i = 0; i < NA; ++i) dma_b128(gah + ko + aoff[i], dst + i * 8192);
-        if (use_lo) {
+        for (int i = 0; i < NA; ++i) dma_b128(ga + ko + aoff[i], dst + i * 8192);
 #pragma unroll
-            for (int i = 0; i < NA; ++i) dma_b128(gal + ko + aoff[i], dst + Sh::ATile + i * 8192);
-        }
-#pragma unroll
-        for (int i = 0; i < NB; ++i) dma_b128(gb + ko + boff[i], dst + (LOK ? 2 : 1) * Sh::ATile + i * 8192);
+        for (int i = 0; i < NB; ++i) dma_b128(gb + ko + boff[i], dst + Sh::ATile + i * 8192);
     };
     // fragment rows 16 * tile + n (n & 7 = row & 7), logical slot 4 ks + g of k-sub ks
     int frd[BK / 32];
@@ -180,42 +181,29 @@ __global__ __launch_bounds__(512) void k_gemm16(GemmArgs a, GemmEpi e) {
         for (int j = 0; j < TN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
     constexpr int NS = Sh::Stages;
-    const int nk = K / BK;
 #pragma unroll
     for (int q = 0; q < NS - 1; ++q)
-        if (q < nk) issue(q, q);
-    for (int kt = 0; kt < nk; ++kt) {
-        // stage kt has landed when at most min(NS - 2, nk - 1 - kt) later stages are in flight
-        if (NS == 3 && kt + 1 < nk) {
-            if (use_lo) wait_vmcnt<2 * NA + NB>();
-            else wait_vmcnt<NA + NB>();
-        } else {
-            wait_vmcnt<0>();
-        }
+        if (q < nkt) issue(q, q);
+    for (int kt = 0; kt < nkt; ++kt) {
+        // stage kt has landed when at most min(NS - 2, nkt - 1 - kt) later stages are in flight
+        if (NS == 3 && kt + 1 < nkt) wait_vmcnt<NA + NB>();
+        else wait_vmcnt<0>();
         lds_barrier();  // also: every wave is done with stage kt - 1, whose slot is refilled next
-        if (kt + NS - 1 < nk) issue(kt + NS - 1, (kt + NS - 1) % NS);
+        if (kt + NS - 1 < nkt) issue(kt + NS - 1, (kt + NS - 1) % NS);
         const uint8_t *st = smem + (kt % NS) * Sh::Stage;
 #pragma unroll
         for (int ks = 0; ks < BK / 32; ++ks) {
             const uint8_t *sa = st + wm * (TM * 16) * RowB + frd[ks];
-            const uint8_t *sb = st + (LOK ? 2 : 1) * Sh::ATile + wn * (TN * 16) * RowB + frd[ks];
-            v8bf bo[TN];
+            const uint8_t *sb = st + Sh::ATile + wn * (TN * 16) * RowB + frd[ks];
+            v8bf bo[TN], ao[TM];
 #pragma unroll
             for (int j = 0; j < TN; ++j) bo[j] = *(const v8bf *)(sb + j * 16 * RowB);
 #pragma unroll
-            for (int i = 0; i < TM; ++i) {
-                const v8bf ah = *(const v8bf *)(sa + i * 16 * RowB);
+            for (int i = 0; i < TM; ++i) ao[i] = *(const v8bf *)(sa + i * 16 * RowB);
 #pragma unroll
-                for (int j = 0; j < TN; ++j) acc[i][j] = mfma16<F16>(ah, bo[j], acc[i][j]);
-            }
-            if (use_lo) {
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int i = 0; i < TM; ++i) {
-                    const v8bf al = *(const v8bf *)(sa + Sh::ATile + i * 16 * RowB);
-#pragma unroll
-                    for (int j = 0; j < TN; ++j) acc[i][j] = mfma16<F16>(al, bo[j], acc[i][j]);
-                }
-            }
+                for (int j = 0; j < TN; ++j) acc[i][j] = mfma16<F16>(ao[i], bo[j], acc[i][j]);
         }
     }
     // Epilogue. D layout: lane (g, n) of tile (i, j) holds rows 4g + r, column n. Row-major
@@ -330,14 +318,9 @@ static hipError_t gemm(hipStream_t st, const uint16_t *Ah, const uint16_t *Al, c
     const int t256 = tm * ((N0 + 255) / 256 + (N1 + 255) / 256);
     const int t128 = tm * ((N0 + 127) / 128 + (N1 + 127) / 128);
     const bool big = 2 * ((t256 + 255) / 256) <= (t128 + 255) / 256;
-    if (Al) {
-        if (big) hipLaunchKernelGGL((k_gemm16<256, EPI, F16, true>), dim3(t256), dim3(512), 0, st, a, e);
-        else hipLaunchKernelGGL((k_gemm16<128, EPI, F16, true>), dim3(t128), dim3(512), 0, st, a, e);
-    } else {
-        if (K % 64) return hipErrorInvalidValue;
-        if (big) hipLaunchKernelGGL((k_gemm16<256, EPI, F16, false>), dim3(t256), dim3(512), 0, st, a, e);
-        else hipLaunchKernelGGL((k_gemm16<128, EPI, F16, false>), dim3(t128), dim3(512), 0, st, a, e);
-    }
+    if (K % 64) return hipErrorInvalidValue;
+    if (big) hipLaunchKernelGGL((k_gemm16<256, EPI, F16>), dim3(t256), dim3(512), 0, st, a, e);
+    else hipLaunchKernelGGL((k_gemm16<128, EPI, F16>), dim3(t128), dim3(512), 0, st, a, e);
     return hipGetLastError();
 }
 
@@ -846,7 +829,7 @@ hipError_t launch_bf16_to_f16(hipStream_t st, _Float16 *dst, const uint16_t *src
 }
 
 bool prefill_mfma_shape(const Dims &d) {
-    return d.H % 32 == 0 && d.R % 32 == 0 && d.QD == 192 && d.DV == 128 && d.HO % 32 == 0 &&
+    return d.H % 64 == 0 && d.R % 64 == 0 && d.QD == 192 && d.DV == 128 && d.HO % 64 == 0 &&
            d.DN % 8 == 0;
 }
 
