@@ -41,10 +41,12 @@ __global__ __launch_bounds__(256) void k_split(const float *src, int ld_src, uin
         const v4i lv = __builtin_bit_cast(v4i, l);
         any |= ((lv.x | lv.y | lv.z | lv.w) & 0x7fff7fff) != 0;
     }
-    // one atomic per block at most, and none once the flag is seen raised
-    if (flag && __syncthreads_or(any) && threadIdx.x == 0 &&
-        __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0)
-        atomicOr(flag, 1);
+    // Blocks with a non-zero lo word store 1. Every writer stores the same value and the reader
+    // is a later kernel, so a workgroup-scope store (cached in the XCD's L2, written back at
+    // the kernel's end) suffices; device-coherent stores or atomics to one address from every
+    // block serialise at memory (measured 13-65 us for 2048 blocks). The flag starts at 0.
+    if (flag && __syncthreads_or(any) && threadIdx.x == 0)
+        __hip_atomic_store(flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 __global__ void k_zero_int(int *p, int n) {
@@ -207,17 +209,18 @@ __global__ __launch_bounds__(512) void k_gemm16(GemmArgs a, GemmEpi e) {
         }
     }
     // Epilogue. D layout: lane (g, n) of tile (i, j) holds rows 4g + r, column n. Row-major
-    // outputs go through a per-wave LDS buffer (16 rows x 64 columns per tile row i) so that
-    // each lane ends up with 16 consecutive columns of one row: wide stores, and the rope
-    // pairs (2p, 2p+1) in one lane. The V^T part of kEpiKV wants 4 consecutive tokens per
-    // lane, which the D layout already gives.
+    // outputs go through a per-wave LDS buffer (16 rows x 64 columns per tile row i): lane l
+    // then takes columns 4 (l % 16) .. + 3 of rows l / 16 + 4 q, q = 0..3, so the 16 lanes of a
+    // row write its 64 columns as one contiguous run (scattered 16-byte pieces per lane cost
+    // ~10 us more per launch at these sizes), and the rope pairs (2p, 2p+1) sit in one lane.
+    // The V^T part of kEpiKV wants 4 consecutive tokens per lane, which the D layout gives.
     const int QD = e.DN + e.DR, KH = e.DN + e.DV, half = e.DR / 2;
     static_assert(TN == 4, "the staged epilogue assumes 64 columns per wave");
     lds_barrier();  // every wave is done with the ring
     float *ep = (float *)smem + w * (16 * 68);
     const int cw = wn * 64;                      // wave's first column within the tile
     const bool vt_wave = EPI == kEpiKV && ((nb0 + cw) % KH) >= e.DN;
-    const int rr = l >> 2, cc = (l & 3) * 16;    // staged row / first column of this lane
+    const int rr = l >> 4, cc = (l & 15) * 4;    // staged row (+ 4 q) / first column of this lane
     const int nl0 = nb0 + cw + cc;               // segment column of v[0]
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -246,61 +249,67 @@ __global__ __launch_bounds__(512) void k_gemm16(GemmArgs a, GemmEpi e) {
         for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) ep[(4 * g + r) * 68 + 16 * j + n] = acc[i][j][r];
-        float v[16];
+        v4f vq[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) vq[q] = *(const v4f *)(ep + (rr + 4 * q) * 68 + cc);
+        if (nl0 >= Nseg) continue;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const v4f x = *(const v4f *)(ep + rr * 68 + cc + 4 * q);
-            v[4 * q] = x.x;
-            v[4 * q + 1] = x.y;
-            v[4 * q + 2] = x.z;
-            v[4 * q + 3] = x.w;
-        }
-        const int t = rbase + rr;
-        if (t >= M || nl0 >= Nseg) continue;
-        if (EPI == kEpiPlain || (EPI == kEpiQ && seg1)) {
-            float *dst = EPI == kEpiPlain ? a.C + (size_t)t * a.ldc + c0 + cw + cc : a.C + (size_t)t * a.ldc + nl0;
+            const int t = rbase + rr + 4 * q;
+            if (t >= M) continue;
+            const float v[4] = {vq[q].x, vq[q].y, vq[q].z, vq[q].w};
+            if (EPI == kEpiPlain || (EPI == kEpiQ && seg1)) {
+                float *dst = EPI == kEpiPlain ? a.C + (size_t)t * a.ldc + c0 + cw + cc : a.C + (size_t)t * a.ldc + nl0;
+                *(v4f *)dst = vq[q];
+            } else if (EPI == kEpiQ) {
+                const int h = nl0 / QD, k0 = nl0 % QD;
+                const size_t o = ((size_t)h * e.Sp + t) * QD;
+                if (k0 < e.DN) {
+                    v4h hi, lo;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) *(v4f *)(dst + 4 * q) = v4f{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-        } else if (EPI == kEpiQ) {
-            const int h = nl0 / QD, k0 = nl0 % QD;
-            const size_t o = ((size_t)h * e.Sp + t) * QD;
-            if (k0 < e.DN) {
+                    for (int u = 0; u < 4; ++u) {
+                        _Float16 hh, ll;
+                        split_f16(v[u], hh, ll);
+                        hi[u] = hh;
+                        lo[u] = ll;
+                    }
+                    *(v4h *)(e.qh + o + k0) = hi;
+                    *(v4h *)(e.ql + o + k0) = lo;
+                } else {
+                    // pairs (ev, od) = (v[2p], v[2p+1]) of rope index i2 + p
+                    const int i2 = (k0 - e.DN) >> 1;
+                    const float2 *cs = e.cs + (size_t)t * half + i2;
+                    v2h h0, l0, h1, l1;
 #pragma unroll
-                for (int q = 0; q < 2; ++q) {
-                    v8h hi, lo;
-                    split8_f16(v + 8 * q, hi, lo);
-                    *(v8h *)(e.qh + o + k0 + 8 * q) = hi;
-                    *(v8h *)(e.ql + o + k0 + 8 * q) = lo;
+                    for (int p = 0; p < 2; ++p) {
+                        const float2 c = cs[p];
+                        const float ev = v[2 * p], od = v[2 * p + 1];
+                        _Float16 hh, ll;
+                        split_f16(ev * c.x - od * c.y, hh, ll);
+                        h0[p] = hh;
+                        l0[p] = ll;
+                        split_f16(od * c.x + ev * c.y, hh, ll);
+                        h1[p] = hh;
+                        l1[p] = ll;
+                    }
+                    *(v2h *)(e.qh + o + e.DN + i2) = h0;
+                    *(v2h *)(e.ql + o + e.DN + i2) = l0;
+                    *(v2h *)(e.qh + o + e.DN + half + i2) = h1;
+                    *(v2h *)(e.ql + o + e.DN + half + i2) = l1;
                 }
-            } else {
-                // pairs (ev, od) = (v[2p], v[2p+1]) of rope index i2 = (k0 - DN) / 2 + p
-                const int i2 = (k0 - e.DN) >> 1;
-                const float2 *cs = e.cs + (size_t)t * half + i2;
-                float r0[8], r1[8];
+            } else {  // kEpiKV, k_nope columns
+                const int h = nl0 / KH, k0 = nl0 % KH;
+                const size_t o = ((size_t)h * e.Sp + t) * QD + k0;
+                v4h hi, lo;
 #pragma unroll
-                for (int p = 0; p < 8; ++p) {
-                    const float2 c = cs[p];
-                    const float ev = v[2 * p], od = v[2 * p + 1];
-                    r0[p] = ev * c.x - od * c.y;
-                    r1[p] = od * c.x + ev * c.y;
+                for (int u = 0; u < 4; ++u) {
+                    _Float16 hh, ll;
+                    split_f16(v[u], hh, ll);
+                    hi[u] = hh;
+                    lo[u] = ll;
                 }
-                v8h hi, lo;
-                split8_f16(r0, hi, lo);
-                *(v8h *)(e.qh + o + e.DN + i2) = hi;
-                *(v8h *)(e.ql + o + e.DN + i2) = lo;
-                split8_f16(r1, hi, lo);
-                *(v8h *)(e.qh + o + e.DN + half + i2) = hi;
-                *(v8h *)(e.ql + o + e.DN + half + i2) = lo;
-            }
-        } else {  // kEpiKV, k_nope columns
-            const int h = nl0 / KH, k0 = nl0 % KH;
-            const size_t o = ((size_t)h * e.Sp + t) * QD + k0;
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                v8h hi, lo;
-                split8_f16(v + 8 * q, hi, lo);
-                *(v8h *)(e.kh + o + 8 * q) = hi;
-                *(v8h *)(e.kl + o + 8 * q) = lo;
+                *(v4h *)(e.kh + o) = hi;
+                *(v4h *)(e.kl + o) = lo;
             }
         }
     }
