@@ -330,6 +330,64 @@ def test_batched_ragged_decode(kind):
         freeg(C.byref(s))
 
 
+def test_config2_ragged_64_sequences_bf16_cache():
+    """64 sequences, context lengths uniform in [512, 32768] (seeded), each with its own
+    bf16-representable latent cache (FP32 state, device-generated), one query each, through
+    the batched entry point. Every sequence against a lone GPU decode of the same token (the
+    batch only changes the split boundaries), and 6 of them (shortest, longest, 4 others)
+    against the oracle on the pulled rows."""
+    cfg, layer, _ = model(KIMI, 0xC8)
+    w = layer.struct()
+    lib.check(L.kvl_mla_bind_weights(C.byref(cfg), C.byref(w)), "bind")
+    rng = np.random.default_rng(0xC8)
+    lens = rng.integers(512, 32769, size=64)
+    B, H = len(lens), cfg.hidden_size
+    print(f"[config2] 64 sequences, {int(lens.sum())} rows", flush=True)
+    xb = np.ascontiguousarray(inputs.hidden(cfg, 0xC8, B, tag="query"))
+
+    def make_states():
+        sts = []
+        for i, n in enumerate(lens):
+            st = abi.KvlMlaCompressedState()
+            assert G.mla_compressed_state_init(C.byref(st), C.byref(cfg), int(n) + 1) == 0
+            lib.check(L.kvl_mla_compressed_state_fill_synthetic(C.byref(st), 0, int(n), 0xC80 + i), "fill")
+            sts.append(st)
+        return sts
+
+    batch_states = make_states()
+    arr = (C.POINTER(abi.KvlMlaCompressedState) * B)(*[C.pointer(s) for s in batch_states])
+    pos = np.ascontiguousarray(lens, dtype=np.int32)
+    out = np.zeros((B, H), np.float32)
+    lib.check(L.kvl_mla_decode_compressed_batch_bf16(f32(out), f32(xb), pos.ctypes.data_as(C.POINTER(C.c_int)), B,
+                                                     C.byref(cfg), C.byref(w), arr), "batched decode")
+    assert all(s.len == n + 1 for s, n in zip(batch_states, lens))
+    for s in batch_states:
+        G.mla_compressed_state_free(C.byref(s))
+    print("[config2]   batch done; lone decodes", flush=True)
+    lone_states = make_states()
+    lone = np.zeros_like(out)
+    for i, st in enumerate(lone_states):
+        lib.check(L.kvl_mla_decode_compressed_bf16(f32(lone[i]), f32(xb[i]), int(lens[i]), C.byref(cfg), C.byref(w),
+                                                   C.byref(st)), f"lone decode {i}")
+    worst = max(rel_err(out[i], lone[i]) for i in range(B))
+    print(f"[config2]   batch vs lone max rel err {worst:.3e}", flush=True)
+    assert worst <= 1e-4
+    picks = sorted({int(np.argmin(lens)), int(np.argmax(lens)), 5, 17, 33, 50})
+    for i in picks:
+        st = lone_states[i]
+        n = int(lens[i])
+        lib.check(L.kvl_mla_compressed_state_pull(C.byref(st), 0, n), "pull")
+        st.len = n  # the oracle appends the same token at position n
+        ref = np.zeros(H, np.float32)
+        assert O.mla_decode_compressed_bf16(f32(ref), f32(xb[i]), n, C.byref(cfg), C.byref(w), C.byref(st)) == 0
+        e = rel_err(out[i], ref)
+        print(f"[config2]   sequence {i} ({n} rows) vs oracle {e:.3e}", flush=True)
+        assert e <= TOL, (i, n, e)
+    for s in lone_states:
+        G.mla_compressed_state_free(C.byref(s))
+    L.kvl_mla_release_weights(C.byref(w))
+
+
 def test_synthetic_history_matches_host_mirror():
     cfg = inputs.config(**KIMI)
     st = abi.KvlMlaCompressedQ8State()
