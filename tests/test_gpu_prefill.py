@@ -60,6 +60,31 @@ def test_prefill_sharp_attention(q_std):
     assert rel_err(a, b) <= TOL, rel_err(a, b)
 
 
+def test_prefill_4096_prefix_and_oracle_1024():
+    """The 4096-token prefill workload (bf16 inputs, theta 50000): rows [0, 1024) of the
+    4096-token prefill equal the 1024-token prefill (causality: row t sees tokens <= t, and each
+    stage computes a token independently of the sequence length; the only difference allowed
+    is the rounding of the o_proj library GEMM, whose kernel choice depends on the token count),
+    and the 1024-token prefill matches the oracle's streaming prefill."""
+    cfg = inputs.config(**inputs.KIMI)
+    layer = inputs.make_layer(cfg, 0xCA)
+    w = layer.struct()
+    x = inputs.hidden(cfg, 0xCA, 4096, bf16_exact=True)
+    full = np.zeros((4096, cfg.hidden_size), np.float32)
+    part = np.zeros((1024, cfg.hidden_size), np.float32)
+    lib.check(L.kvl_mla_prefill_bf16(f32(full), f32(x), 4096, C.byref(cfg), C.byref(w)), "prefill 4096")
+    xp = np.ascontiguousarray(x[:1024])
+    lib.check(L.kvl_mla_prefill_bf16(f32(part), f32(xp), 1024, C.byref(cfg), C.byref(w)), "prefill 1024")
+    e_prefix = rel_err(full[:1024], part)
+    print(f"[prefill] 4096 rows [0,1024) vs 1024-token prefill {e_prefix:.3e}", flush=True)
+    assert np.all(np.isfinite(full)) and e_prefix <= 1e-5
+    ref = np.zeros_like(part)
+    assert ORC.orc_mla_prefill_streaming(f32(ref), f32(xp), 1024, C.byref(cfg), C.byref(w)) == 0
+    e = rel_err(part, ref)
+    print(f"[prefill] 1024 tokens vs oracle {e:.3e}", flush=True)
+    assert e <= TOL
+
+
 def test_prefill_repeats_bit_for_bit():
     """Same inputs, same output: every stage (including the library GEMM of o_proj) picks its
     kernels deterministically and sums in a fixed order."""
