@@ -175,18 +175,20 @@ __device__ __forceinline__ double block256_sum_f64(double v, double *red4) {
 __device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)p; }
 
 // Asynchronous global -> LDS copies: lane l's bytes land at lds_base + l * size. lds_base
-// must be wave-uniform. M0 is saved and restored around the instruction.
+// must be wave-uniform. M0 is saved and restored around the instruction. GFX9 needs one
+// wait state between an SALU write of M0 and a global load with LDS = 1 that reads it; the
+// compiler inserts it for its own code but not inside an asm statement, hence the s_nop.
 __device__ __forceinline__ void dma_b128(const void *gptr, uint32_t lds_base) {
     lds_base = __builtin_amdgcn_readfirstlane(lds_base);
     uint32_t saved;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
                  : "=&s"(saved)
                  : "s"(lds_base), "v"(gptr)
                  : "memory");
 }
 __device__ __forceinline__ void dma_b32(const void *gptr, uint32_t lds_base) {
     uint32_t saved;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dword %2, off\n\ts_mov_b32 m0, %0"
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %2, off\n\ts_mov_b32 m0, %0"
                  : "=&s"(saved)
                  : "s"(lds_base), "v"(gptr)
                  : "memory");
