@@ -149,6 +149,7 @@ struct Ctx {
     bool capturing = false;
     // per-stage event timing of decode steps (kvl_mla_timing_*)
     bool timing = false;
+    bool timing_graph = false;  // also record into a graph being captured (event-record nodes)
     std::vector<hipEvent_t> ev_pool;
     std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> ev_used;
 };
@@ -190,21 +191,23 @@ hipEvent_t ev_get() {
     return e;
 }
 
-// Brackets one launch of stage `st` with events when timing is on (never during capture).
+// Brackets one launch of stage `st` with events when timing is on (during capture only in
+// timing mode 2, as event-record nodes of the graph).
 struct StageTimer {
     int stage;
     hipEvent_t a = nullptr, b = nullptr;
     explicit StageTimer(int s) : stage(s) {
         Ctx &c = ctx();
-        if (!c.timing || c.capturing) return;
+        if (!c.timing || (c.capturing && !c.timing_graph)) return;
         a = ev_get();
         b = ev_get();
-        if (a && b) (void)hipEventRecord(a, c.stream);
+        // inside a capture, only an external record becomes a timestamped node of the graph
+        if (a && b) (void)hipEventRecordWithFlags(a, c.stream, c.capturing ? hipEventRecordExternal : 0);
     }
     ~StageTimer() {
         Ctx &c = ctx();
         if (!a || !b) return;
-        (void)hipEventRecord(b, c.stream);
+        (void)hipEventRecordWithFlags(b, c.stream, c.capturing ? hipEventRecordExternal : 0);
         c.ev_used.push_back({stage, {a, b}});
     }
 };
@@ -1817,7 +1820,9 @@ int kvl_mla_q8_pack_rows(int8_t *codes, float *scales, uint16_t *rope_bf16, cons
 int kvl_mla_timing_enable(int on) {
     Guard guard;
     if (ensure_ready() != 0) return -1;
+    if (on < 0 || on > 2) return -1;
     ctx().timing = on != 0;
+    ctx().timing_graph = on == 2;
     return 0;
 }
 

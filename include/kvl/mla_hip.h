@@ -148,7 +148,10 @@ int kvl_mla_graph_launch(void *graph_exec);
 int kvl_mla_graph_destroy(void *graph_exec);
 
 /* Measurement helpers. kvl_mla_timing_enable(1) brackets every decode-step kernel with HIP
- * events on kvl_mla_stream() (not during graph capture); kvl_mla_timing_read() sums the
+ * events on kvl_mla_stream() (not during graph capture); kvl_mla_timing_enable(2) also
+ * records the events into a graph being captured (event-record nodes: each replay of that
+ * graph overwrites their timestamps, so read once after the last replay, then destroy the
+ * graph before timing anything else). kvl_mla_timing_read() sums the
  * durations (ms) and launch counts of the six stages (gemv_in, append [+ qprep: one launch
  * for the compressed formats], qprep [expanded format], attention,
  * combine, gemv_out) since the last read. Events: record on the library stream, elapsed
