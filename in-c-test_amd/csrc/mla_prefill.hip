@@ -425,6 +425,62 @@ __global__ __launch_bounds__(256) void k_kva_pack(KvaPackArgs a) {
         return;
     }
     const float *kat = a.y + (size_t)t * a.ldy;
+    if (R == 512 && a.DR == 64 && (a.DN & 7) == 0 && (a.ldy & 3) == 0 && (a.pstride & 3) == 0) {
+        // lane l: latent columns 8l .. 8l+7 (16-byte loads and stores); the rotated RoPE key
+        // goes through LDS so that each head's 128-byte hi and lo rows are written by 8 lanes
+        // of 16 bytes, four heads per store instruction
+        __shared__ __attribute__((aligned(16))) _Float16 rp[4][2][64];
+        const int w = threadIdx.x >> 6;
+        float v[8];
+        {
+            v4f p0 = *(const v4f *)(kat + 8 * l), p1 = *(const v4f *)(kat + 8 * l + 4);
+            for (int q = 1; q < a.np; ++q) {
+                p0 += *(const v4f *)(kat + (size_t)q * a.pstride + 8 * l);
+                p1 += *(const v4f *)(kat + (size_t)q * a.pstride + 8 * l + 4);
+            }
+            v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w;
+            v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
+        }
+        double ss = 0.0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += (double)v[e] * (double)v[e];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        const float inv = 1.0f / sqrtf((float)(ss / (double)R) + a.eps);
+        const v4i nw = *(const v4i *)(a.norm + 8 * l);
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const uint32_t u = (uint32_t)nw[e >> 1];
+            uint16_t h0, l0, h1, l1;
+            split_bf16((v[e] * inv) * __uint_as_float(u << 16), h0, l0);
+            split_bf16((v[e + 1] * inv) * __uint_as_float(u & 0xffff0000u), h1, l1);
+            hw[e >> 1] = pack2(h0, h1);
+            lw[e >> 1] = pack2(l0, l1);
+        }
+        *(v4i *)(a.lath + (size_t)t * R + 8 * l) = v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]};
+        *(v4i *)(a.latl + (size_t)t * R + 8 * l) = v4i{(int)lw[0], (int)lw[1], (int)lw[2], (int)lw[3]};
+        if (l < 32) {
+            const float2 cs = a.cs[(size_t)t * 32 + l];
+            float ev = kat[R + 2 * l], od = kat[R + 2 * l + 1];
+            for (int q = 1; q < a.np; ++q) {
+                ev += kat[(size_t)q * a.pstride + R + 2 * l];
+                od += kat[(size_t)q * a.pstride + R + 2 * l + 1];
+            }
+            const float ec = ev * cs.x, os = od * cs.y, oc = od * cs.x, es = ev * cs.y;
+            split_f16(ec - os, rp[w][0][l], rp[w][1][l]);
+            split_f16(oc + es, rp[w][0][32 + l], rp[w][1][32 + l]);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int part = (l >> 3) & 1, c = l & 7;
+        const v4i rv = *(const v4i *)&rp[w][part][8 * c];
+        _Float16 *dst = part ? a.kl : a.kh;
+        for (int h = l >> 4; h < a.NH; h += 4)
+            *(v4i *)(dst + ((size_t)h * a.Sp + t) * QD + a.DN + 8 * c) = rv;
+        return;
+    }
     auto kv = [&](int r) {
         float v = kat[r];
         for (int q = 1; q < a.np; ++q) v += kat[(size_t)q * a.pstride + r];
