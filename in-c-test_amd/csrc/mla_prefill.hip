@@ -29,17 +29,20 @@ __global__ __launch_bounds__(256) void k_split(const float *src, int ld_src, uin
                                                uint16_t *lo, int ld_dst, int rows, int cols,
                                                int *flag) {
     const int c8 = cols / 8;
-    const size_t n = (size_t)rows * c8;
     int any = 0;
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
-        const size_t r = i / c8, c = (i % c8) * 8;
-        const v4f x0 = *(const v4f *)(src + r * ld_src + c), x1 = *(const v4f *)(src + r * ld_src + c + 4);
-        v8bf h, l;
-        split8(x0, x1, h, l);
-        *(v8bf *)(hi + r * ld_dst + c) = h;
-        *(v8bf *)(lo + r * ld_dst + c) = l;
-        const v4i lv = __builtin_bit_cast(v4i, l);
-        any |= ((lv.x | lv.y | lv.z | lv.w) & 0x7fff7fff) != 0;
+    // rows over blocks, 8-column groups over threads (no index division in the loop)
+    for (int r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float *s = src + (size_t)r * ld_src;
+        uint16_t *hr = hi + (size_t)r * ld_dst, *lr = lo + (size_t)r * ld_dst;
+        for (int c = 8 * threadIdx.x; c < 8 * c8; c += 8 * 256) {
+            const v4f x0 = *(const v4f *)(s + c), x1 = *(const v4f *)(s + c + 4);
+            v8bf h, l;
+            split8(x0, x1, h, l);
+            *(v8bf *)(hr + c) = h;
+            *(v8bf *)(lr + c) = l;
+            const v4i lv = __builtin_bit_cast(v4i, l);
+            any |= ((lv.x | lv.y | lv.z | lv.w) & 0x7fff7fff) != 0;
+        }
     }
     // Blocks with a non-zero lo word store 1. Every writer stores the same value and the reader
     // is a later kernel, so a workgroup-scope store (cached in the XCD's L2, written back at
@@ -881,7 +884,7 @@ hipError_t launch_split(hipStream_t st, const float *src, int ld_src, uint16_t *
     if (rows < 1 || cols < 8 || cols % 8 || ld_src % 4 || ld_dst % 8 || ld_src < cols || ld_dst < cols ||
         ((uintptr_t)src % 16) || ((uintptr_t)hi % 16) || ((uintptr_t)lo % 16))
         return hipErrorInvalidValue;
-    const int blocks = (int)std::min<size_t>(2048, ((size_t)rows * cols / 8 + 255) / 256);
+    const int blocks = std::min(2048, rows);  // k_split loops over rows by block
     hipLaunchKernelGGL(k_split, dim3(blocks), dim3(256), 0, st, src, ld_src, hi, lo, ld_dst, rows, cols,
                        nullptr);
     return hipGetLastError();
@@ -963,7 +966,7 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
         _Float16 *heads = (_Float16 *)take(2 * (size_t)S * d.HO);
         const GemmEpi ep{qh, ql, kh, kl, vt, cs, Sp, d.DN, d.DR, d.DV};
         hipLaunchKernelGGL(k_zero_int, dim3(1), dim3(64), 0, st, flags, 8);
-        const int split_blocks = (int)std::min<size_t>(2048, ((size_t)S * d.H / 8 + 255) / 256);
+        const int split_blocks = std::min(2048, S);
         hipLaunchKernelGGL(k_split, dim3(split_blocks), dim3(256), 0, st, x, d.H, xh, xl, d.H, S, d.H, flags + 0);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // q (-> Q hi/lo, rotated) | kv_a (-> ykva). When the caller fills a state from this
