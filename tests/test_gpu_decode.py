@@ -464,3 +464,63 @@ def test_device_api_and_graph_replay_match_host_api():
     for st in states:
         G.mla_compressed_q8_state_free(C.byref(st))
     L.kvl_mla_release_weights(C.byref(w))
+
+
+def test_stage_events_inside_a_graph():
+    """Timing mode 2 records the stage events into a captured graph: after replays, every
+    stage of the decode has one positive duration per launch, the graph's output equals the
+    eager call's, and the durations add up to less than the replay's own time."""
+    cfg, layer, _ = model(KIMI, 0xD3)
+    w = layer.struct()
+    lib.check(L.kvl_mla_bind_weights(C.byref(cfg), C.byref(w)), "bind")
+    B, n = 2, 3000
+    states = []
+    for i in range(B):
+        st = abi.KvlMlaCompressedQ8State()
+        assert G.mla_compressed_q8_state_init(C.byref(st), C.byref(cfg), n + 4) == 0
+        lib.check(L.kvl_mla_compressed_q8_state_fill_synthetic(C.byref(st), 0, n, 90 + i), "fill")
+        states.append(st)
+    xb = np.ascontiguousarray(inputs.hidden(cfg, 0xD3, B, tag="q"))
+    arr = (C.POINTER(abi.KvlMlaCompressedQ8State) * B)(*[C.pointer(s) for s in states])
+    nbytes = xb.nbytes
+    dx, dout = L.kvl_mla_device_alloc(nbytes), L.kvl_mla_device_alloc(nbytes)
+    assert dx and dout
+    lib.check(L.kvl_mla_copy_to_device(dx, xb.ctypes.data, nbytes), "h2d")
+    lib.check(L.kvl_mla_decode_compressed_q8_batch_device(dout, dx, B, C.byref(cfg), C.byref(w), arr,
+                                                          lib.NO_ADVANCE), "eager decode")
+    eager = np.zeros_like(xb)
+    lib.check(L.kvl_mla_copy_to_host(eager.ctypes.data, dout, nbytes), "d2h")
+    ms, cnt = (C.c_double * 6)(), (C.c_int * 6)()
+    lib.check(L.kvl_mla_timing_read(ms, cnt), "clear records")
+    lib.check(L.kvl_mla_timing_enable(2), "timing mode 2")
+    lib.check(L.kvl_mla_capture_begin(), "capture begin")
+    rc = L.kvl_mla_decode_compressed_q8_batch_device(dout, dx, B, C.byref(cfg), C.byref(w), arr, lib.NO_ADVANCE)
+    ge = C.c_void_p()
+    lib.check(L.kvl_mla_capture_end(C.byref(ge)), "capture end")
+    lib.check(L.kvl_mla_timing_enable(0), "timing off")
+    lib.check(rc, "captured decode")
+    for _ in range(3):
+        lib.check(L.kvl_mla_graph_launch(ge), "graph launch")
+    e0 = L.kvl_mla_event_record()
+    lib.check(L.kvl_mla_graph_launch(ge), "graph launch")
+    e1 = L.kvl_mla_event_record()
+    lib.check(L.kvl_mla_synchronize(), "sync")
+    replay_ms = L.kvl_mla_event_elapsed_ms(e0, e1)
+    L.kvl_mla_event_destroy(e0)
+    L.kvl_mla_event_destroy(e1)
+    lib.check(L.kvl_mla_timing_read(ms, cnt), "timing read")
+    lib.check(L.kvl_mla_graph_destroy(ge), "graph destroy")
+    got = np.zeros_like(xb)
+    lib.check(L.kvl_mla_copy_to_host(got.ctypes.data, dout, nbytes), "d2h")
+    np.testing.assert_array_equal(got, eager)
+    stages = {name: (ms[i], cnt[i]) for i, name in enumerate(lib.STAGES)}
+    print(f"[timing] graph replay {replay_ms:.4f} ms, stages {stages}", flush=True)
+    for name in ("gemv_in", "append_qprep", "attention", "combine", "gemv_out"):
+        t, c = stages[name]
+        assert c == 1 and t > 0.0, (name, t, c)
+    assert sum(t for t, _ in stages.values()) <= replay_ms * 1.001
+    L.kvl_mla_device_free(dx)
+    L.kvl_mla_device_free(dout)
+    for st in states:
+        G.mla_compressed_q8_state_free(C.byref(st))
+    L.kvl_mla_release_weights(C.byref(w))
