@@ -41,20 +41,6 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def layer_weights(cfg, seed):
-    """bf16(N(0, 0.02)) matrices and bf16(1 + N(0, 0.02)) kv_a_norm from PCG64(seed)."""
-    rng = np.random.default_rng(seed)
-    H, NH = cfg.hidden_size, cfg.num_heads
-    DN, DR, DV, R = cfg.qk_nope_dim, cfg.qk_rope_dim, cfg.v_head_dim, cfg.kv_lora_rank
-
-    def mat(shape, mean=0.0):
-        return inputs.f32_to_bf16_bits(rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)
-                                       + np.float32(mean))
-    return inputs.Layer(q_proj=mat((NH * (DN + DR), H)), kv_a_proj=mat((R + DR, H)),
-                        kv_a_norm=mat((R,), 1.0), kv_b_proj=mat((NH * (DN + DV), R)),
-                        o_proj=mat((H, NH * DV)))
-
-
 def weight_bytes(cfg):
     H, NH = cfg.hidden_size, cfg.num_heads
     DN, DR, DV, R = cfg.qk_nope_dim, cfg.qk_rope_dim, cfg.v_head_dim, cfg.kv_lora_rank
@@ -125,7 +111,7 @@ def main():
     t_setup = time.time()
     layers, wstructs = [], []
     for li in range(NL):
-        lw = layer_weights(cfg, 0xC4 + li)
+        lw = inputs.fast_layer(cfg, 0xC4 + li)
         layers.append(lw)
         ws = lw.struct()
         wstructs.append(ws)
@@ -139,8 +125,8 @@ def main():
             st = abi.KvlMlaCompressedQ8State()
             if L.kvl_mla_compressed_q8_state_init(C.byref(st), C.byref(cfg), CTX + 1) != 0:
                 raise RuntimeError("state init failed")
-            seed = (0xC4 << 16) ^ (li << 8) ^ b
-            lib.check(L.kvl_mla_compressed_q8_state_fill_synthetic(C.byref(st), 0, CTX, seed), "fill")
+            lib.check(L.kvl_mla_compressed_q8_state_fill_synthetic(C.byref(st), 0, CTX, inputs.stack_seed(li, b)),
+                      "fill")
             row.append(st)
         states.append(row)
         arrays.append((Q8P * B)(*[C.pointer(s) for s in row]))

@@ -1285,13 +1285,15 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
 // RoPE keys against the hi/lo bf16 split of q_rope. The row scale factors out of the dot
 // (score_j = s_j * q_lat . c_j + q_rope . k_j). Mix: the weights p_j*s_j (p_j <= kQ8Pmax
 // against the lazily moved reference max below, s_j <= the split's largest scale) are
-// quantised to int8 hi + lo/254 against kQ8Pmax * that scale; ds_read_b64_tr_b8 reads the
-// codes transposed (16 rows of one column per lane), and v_mfma_i32_16x16x64_i8 accumulates
-// the exact integer mix in place across chunks. A head's reference max only moves when a
-// chunk exceeds it by more than ln kQ8Pmax (so p_j <= kQ8Pmax); its integer accumulators
-// are then rescaled by alpha = exp(m_old - m_new) (rounded, below 2^-17 of the sums).
-// kQ8Pmax = 4 keeps the weights' resolution of the earlier p_j <= 2, lo/128 scheme while
-// rescales become rare (they cost a pass over the accumulators).
+// quantised to three int8 levels hi + lo/254 + lo2/254^2 against kQ8Pmax * that scale (23
+// bits below the bound: a row whose scale is far below the split's largest -- an all-zero
+// latent stored with scale 1, or a flat row beside a one-hot-like one -- keeps the precision
+// of its own weight); ds_read_b64_tr_b8 reads the codes transposed (16 rows of one column per
+// lane), and v_mfma_i32_16x16x64_i8 accumulates the exact integer mix of each level in place
+// across chunks. A head's reference max only moves when a chunk exceeds it by more than
+// ln kQ8Pmax (so p_j <= kQ8Pmax); its integer accumulators are then rescaled by
+// alpha = exp(m_old - m_new) in double, each level's rounding remainder carried into the
+// next one. kQ8Pmax = 4 makes rescales rare (they cost a pass over the accumulators).
 // Each wave accumulates 128 latent columns.
 constexpr int kQ8Ch = 64;
 constexpr float kQ8Pmax = 4.0f;            // bound of p_j = exp(s_j - reference max)
@@ -1303,7 +1305,7 @@ constexpr int kQ8RopeB = kQ8Ch * 128;               // bf16 RoPE keys of a chunk
 constexpr int kQ8ChunkB = kQ8CodeB + kQ8RopeB;
 constexpr int kQ8Ws = 80;                           // LDS bytes per quantised-weight row
 constexpr int kQ8SclOff = kQ8Ring * kQ8ChunkB;      // scales of the whole split
-constexpr int kQ8WqB = 2 * 16 * kQ8Ws;              // quantised weights of a chunk (hi, lo)
+constexpr int kQ8WqB = 3 * 16 * kQ8Ws;              // quantised weights of a chunk (hi, lo, lo2)
 constexpr int kQ8WqOff = kQ8SclOff + 4 * kQ8MaxSplitRows;  // two buffers, by chunk parity
 constexpr int kQ8MlOff = kQ8WqOff + 2 * kQ8WqB;    // chunk maxima [2][4 waves][16], sums, smax
 constexpr int kQ8QOff = kQ8MlOff + 4 * 4 * 16 * 4;  // query operands of the sequence
@@ -1399,11 +1401,12 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
         m_run[i] = -INFINITY;
         l_lane[i] = 0.f;
     }
-    v4i ahi[8], alo[8];
+    v4i ahi[8], alo[8], alo2[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
         ahi[t] = v4i{0, 0, 0, 0};
         alo[t] = v4i{0, 0, 0, 0};
+        alo2[t] = v4i{0, 0, 0, 0};
     }
 
     float wscale = 0.f, wfac = 0.f;  // weight quantisation scale, set once the scales are in
@@ -1532,18 +1535,23 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
             pv[i] = __expf(sc[i] - m_run[i]);
         }
         auto put_weights = [&]() __attribute__((always_inline)) {
-            int qhv[4], qlv[4];
+            int qhv[4], qlv[4], q2v[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float v = pv[i] * swj;
                 const float hi = fminf(rintf(v), 127.f);
+                // v - hi is exact (|v - hi| <= 1/2): lo and lo2 span the int8 range
+                const float r1 = (v - hi) * 254.0f;
+                const float lo = rintf(r1);
                 qhv[i] = (int)hi;
-                qlv[i] = (int)rintf((v - hi) * 254.0f);  // |v - hi| <= 1/2: lo spans the int8 range
+                qlv[i] = (int)lo;
+                q2v[i] = (int)rintf((r1 - lo) * 254.0f);
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 wqc[(4 * g + i) * kQ8Ws + rowl] = (int8_t)qhv[i];
                 wqc[16 * kQ8Ws + (4 * g + i) * kQ8Ws + rowl] = (int8_t)qlv[i];
+                wqc[32 * kQ8Ws + (4 * g + i) * kQ8Ws + rowl] = (int8_t)q2v[i];
             }
         };
         put_weights();
@@ -1555,6 +1563,7 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
         const v4i fl = *(const v4i *)oflag;
         v4i wh = *(const v4i *)(wqc + wq_off);
         v4i wl = *(const v4i *)(wqc + 16 * kQ8Ws + wq_off);
+        v4i wl2 = *(const v4i *)(wqc + 32 * kQ8Ws + wq_off);
         if ((fl.x | fl.y | fl.z | fl.w) != 0) {
             // Some row exceeds the reference max: exchange the four waves' chunk maxima, move
             // the reference max of the heads concerned, rescale their accumulators and quantise
@@ -1582,18 +1591,26 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
             }
             put_weights();
             if (__any(moved)) {
+                // (254^2 hi + 254 lo + lo2) * alpha, level by level in double (the products are
+                // exact), each level's rounding remainder carried into the next
 #pragma unroll
                 for (int t = 0; t < 8; ++t)
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
                         if (alpha[i] != 1.0f) {
-                            ahi[t][i] = (int)rintf((float)ahi[t][i] * alpha[i]);
-                            alo[t][i] = (int)rintf((float)alo[t][i] * alpha[i]);
+                            const double al = (double)alpha[i];
+                            const double h = (double)ahi[t][i] * al, hr = rint(h);
+                            const double o = (h - hr) * 254.0 + (double)alo[t][i] * al, orr = rint(o);
+                            const double o2 = (o - orr) * 254.0 + (double)alo2[t][i] * al;
+                            ahi[t][i] = (int)hr;
+                            alo[t][i] = (int)orr;
+                            alo2[t][i] = (int)rint(o2);
                         }
             }
             lds_barrier();
             wh = *(const v4i *)(wqc + wq_off);
             wl = *(const v4i *)(wqc + 16 * kQ8Ws + wq_off);
+            wl2 = *(const v4i *)(wqc + 32 * kQ8Ws + wq_off);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) l_lane[i] += pv[i];
@@ -1601,6 +1618,7 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
         for (int t = 0; t < 8; ++t) {
             ahi[t] = mfma_i8(wh, bt[t], ahi[t]);
             alo[t] = mfma_i8(wl, bt[t], alo[t]);
+            alo2[t] = mfma_i8(wl2, bt[t], alo2[t]);
         }
     };
     using S0 = std::integral_constant<int, 0>;
@@ -1649,7 +1667,7 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
     }
     // p_j <= kQ8Pmax relative to the reference max (see the lazy max below)
     wscale = smax > 0.f ? 127.0f / (kQ8Pmax * smax) : 0.f;
-    wfac = kQ8Pmax * smax * (1.0f / (127.0f * 254.0f));
+    wfac = kQ8Pmax * smax * (1.0f / (127.0f * 254.0f * 254.0f));
     int c = 0;
     for (; c + 3 <= nch; c += 3) {
         chunk(S0{}, c);
@@ -1671,7 +1689,8 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
         const int r = 128 * w + 16 * t + n;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            P[(4 * g + i) * 512 + r] = wfac * fmaf((float)ahi[t][i], 254.0f, (float)alo[t][i]);
+            P[(4 * g + i) * 512 + r] =
+                wfac * fmaf((float)ahi[t][i], 64516.0f, fmaf((float)alo[t][i], 254.0f, (float)alo2[t][i]));
     }
     if (w == 0 && n == 0) {
 #pragma unroll

@@ -179,10 +179,6 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
 bool prefill_kva_exact(const Dims &d);
 // True when the prefill of these dims takes the MFMA route (needs the fp16 o_proj copy).
 bool prefill_mfma_shape(const Dims &d);
-// C[M, N] (ldc) = A[M, K] (lda) . W[N, K]^T (ldw), fp16 operands, fp32 accumulate and output,
-// through hipBLASLt (mla_blas.cpp); hipErrorNotSupported when the library has no kernel for it.
-hipError_t lt_gemm_f16(hipStream_t st, float *C, int ldc, const _Float16 *A, int lda, const _Float16 *W,
-                       int ldw, int M, int N, int K);
 // src [rows, cols] fp32 -> bf16 hi, lo planes (x = hi + lo to ~16 bits, both round to nearest
 // even). cols % 8 == 0, 16-byte aligned rows.
 hipError_t launch_split(hipStream_t st, const float *src, int ld_src, uint16_t *hi, uint16_t *lo,

@@ -995,14 +995,10 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
         FlashArgs fa{qh, ql, kh, kl, vt, heads, S, Sp, d.NH, d.HO, smscale * 1.4426950408889634f};
         hipLaunchKernelGGL(k_flash_prefill, dim3(Sp / kFQ * d.NH), dim3(256), 0, st, fa);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        // out = heads . o_proj^T in fp16 (heads rounded once, o_proj converted exactly): a plain
-        // GEMM with no epilogue, by hipBLASLt where it has a kernel for the shape
+        // out = heads . o_proj^T in fp16 (heads rounded once, o_proj converted exactly)
         if (!wo16) return hipErrorInvalidValue;
-        e = lt_gemm_f16(st, out, d.H, heads, d.HO, wo16, d.HO, S, d.H, d.HO);
-        if (e == hipErrorNotSupported)
-            e = gemm<kEpiPlain, true>(st, (const uint16_t *)heads, nullptr, nullptr, d.HO, (const uint16_t *)wo16, d.H,
-                                      nullptr, 0, d.HO, out, d.H, S, d.HO, ep);
-        return e;
+        return gemm<kEpiPlain, true>(st, (const uint16_t *)heads, nullptr, nullptr, d.HO, (const uint16_t *)wo16, d.H,
+                                     nullptr, 0, d.HO, out, d.H, S, d.HO, ep);
     }
     float *y = (float *)take(4 * (size_t)S * ldy);
     float *latf = (float *)take(4 * (size_t)S * d.R);

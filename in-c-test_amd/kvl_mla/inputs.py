@@ -107,6 +107,25 @@ def make_layer(cfg, seed, std=0.02, q_std=None):
                  o_proj=normal_bf16(seed, "o_proj", (H, NH * DV), std=std))
 
 
+def fast_layer(cfg, seed):
+    """Random-init layer drawn with numpy's PCG64 (fast enough for 27-layer stacks):
+    bf16(N(0, 0.02)) matrices and bf16(1 + N(0, 0.02)) kv_a_norm, in a fixed draw order."""
+    rng = np.random.default_rng(seed)
+    H, NH = cfg.hidden_size, cfg.num_heads
+    DN, DR, DV, R = cfg.qk_nope_dim, cfg.qk_rope_dim, cfg.v_head_dim, cfg.kv_lora_rank
+
+    def mat(shape, mean=0.0):
+        return f32_to_bf16_bits(rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)
+                                + np.float32(mean))
+    return Layer(q_proj=mat((NH * (DN + DR), H)), kv_a_proj=mat((R + DR, H)), kv_a_norm=mat((R,), 1.0),
+                 kv_b_proj=mat((NH * (DN + DV), R)), o_proj=mat((H, NH * DV)))
+
+
+def stack_seed(layer, seq):
+    """Seed of the synthetic Q8 history of (layer, sequence) in the 27-layer stack workload."""
+    return (0xC4 << 16) ^ (layer << 8) ^ seq
+
+
 def hidden(cfg, seed, n, bf16_exact=False, tag="x"):
     """[n, hidden] float32 hidden states ~ N(0,1); optionally BF16-representable."""
     x = normal_f32(seed, tag, (n, cfg.hidden_size))

@@ -610,16 +610,32 @@ static double dot_f64(const float *a, const float *b, int n) {
 }
 
 /* src/mla_prefill_streaming.c:78-206 */
-int orc_mla_prefill_streaming(float *out, const float *x, int seq_len, const KvlMlaConfig *cfg,
-                              const KvlMlaBF16 *w) {
+/* Query rows of the streaming prefill: all S rows (rows == NULL; out [S, H], heads written to
+ * out as the reference does when HO == H), or the listed rows only (out [nrows, H]: row i of
+ * out is query row rows[i]). A listed row takes exactly the arithmetic of the full form (its
+ * kv_a, keys and values of every j <= t, its query, scores, softmax and o_proj), so it equals
+ * that row of the full prefill bit for bit. */
+static int prefill_streaming_rows(float *out, const float *x, int seq_len, const int *rows,
+                                  int nrows, const KvlMlaConfig *cfg, const KvlMlaBF16 *w) {
     Dims d;
     if (!out || !x || !cfg || !weights_ok(w) || seq_len <= 0 || dims_of(cfg, &d) != 0) return -1;
-    const int S = seq_len, KHV = d.DN + d.DV;
+    int S = seq_len;
+    const int KHV = d.DN + d.DV;
+    const int NQ = rows ? nrows : S;
+    if (rows) {
+        if (nrows <= 0) return -1;
+        int last = 0;
+        for (int i = 0; i < nrows; ++i) {
+            if (rows[i] < 0 || rows[i] >= seq_len) return -1;
+            if (rows[i] > last) last = rows[i];
+        }
+        S = last + 1; /* rows past the last query row are never attended */
+    }
     int workers = 1;
 #ifdef _OPENMP
     workers = omp_get_max_threads();
     if (workers < 1) workers = 1;
-    if (workers > S) workers = S;
+    if (workers > NQ) workers = NQ;
 #endif
     float *lat = (float *)malloc((size_t)S * d.R * sizeof(float));
     float *rope = (float *)malloc((size_t)S * d.DR * sizeof(float));
@@ -632,7 +648,7 @@ int orc_mla_prefill_streaming(float *out, const float *x, int seq_len, const Kvl
     float *katmp = (float *)malloc((size_t)d.KVO * sizeof(float));
     float *kvtmp = (float *)malloc((size_t)KHV * sizeof(float));
     float *htmp = (float *)malloc((size_t)d.HO * sizeof(float));
-    float *heads = d.HO == d.H ? out : (float *)malloc((size_t)S * d.HO * sizeof(float));
+    float *heads = (d.HO == d.H && !rows) ? out : (float *)malloc((size_t)NQ * d.HO * sizeof(float));
     int rc = -1;
     if (!lat || !rope || !knope || !vals || !sc_all || !q_all || !qr_all || !acc_all || !katmp ||
         !kvtmp || !htmp || !heads)
@@ -652,11 +668,12 @@ int orc_mla_prefill_streaming(float *out, const float *x, int seq_len, const Kvl
             memcpy(vals + (size_t)j * d.DV, kvtmp + d.DN, (size_t)d.DV * sizeof(float));
         }
         const uint16_t *qh = w->q_proj + (size_t)h * d.QD * d.H;
-        int t;
+        int i;
 #ifdef _OPENMP
-#pragma omp parallel for schedule(dynamic, 8) if (S >= 128) num_threads(workers)
+#pragma omp parallel for schedule(dynamic, 8) if (NQ >= 128 || rows) num_threads(workers)
 #endif
-        for (t = 0; t < S; ++t) {
+        for (i = 0; i < NQ; ++i) {
+            const int t = rows ? rows[i] : i;
             int tid = 0;
 #ifdef _OPENMP
             tid = omp_get_thread_num();
@@ -688,11 +705,11 @@ int orc_mla_prefill_streaming(float *out, const float *x, int seq_len, const Kvl
                     acc[k] = acc[k] + pv;
                 }
             }
-            float *ho = heads + (size_t)t * d.HO + (size_t)h * d.DV;
+            float *ho = heads + (size_t)i * d.HO + (size_t)h * d.DV;
             for (int k = 0; k < d.DV; ++k) ho[k] = (float)acc[k];
         }
     }
-    for (int t = 0; t < S; ++t) {
+    for (int t = 0; t < NQ; ++t) {
         memcpy(htmp, heads + (size_t)t * d.HO, (size_t)d.HO * sizeof(float));
         orc_matvec_bf16(out + (size_t)t * d.H, htmp, w->o_proj, d.HO, d.H);
     }
@@ -702,6 +719,16 @@ done:
     free(acc_all); free(katmp); free(kvtmp); free(htmp);
     if (heads != out) free(heads);
     return rc;
+}
+
+int orc_mla_prefill_streaming(float *out, const float *x, int seq_len, const KvlMlaConfig *cfg,
+                              const KvlMlaBF16 *w) {
+    return prefill_streaming_rows(out, x, seq_len, NULL, 0, cfg, w);
+}
+
+int orc_mla_prefill_streaming_rows(float *out, const float *x, int seq_len, const int *rows,
+                                   int nrows, const KvlMlaConfig *cfg, const KvlMlaBF16 *w) {
+    return prefill_streaming_rows(out, x, seq_len, rows, nrows, cfg, w);
 }
 
 /* src/ops.c:105-192: every token's Q, K=[k_nope|rope] and V materialised for all heads, then

@@ -101,6 +101,10 @@ int orc_mla_prefill_streaming(float *out, const float *x, int seq_len, const Kvl
                               const KvlMlaBF16 *w);
 int orc_mla_prefill_materialized(float *out, const float *x, int seq_len, const KvlMlaConfig *cfg,
                                  const KvlMlaBF16 *w);
+/* Selected query rows of the streaming prefill (out [nrows, H], row i = query row rows[i]),
+ * each bit-identical to that row of orc_mla_prefill_streaming: a checker for long prefills. */
+int orc_mla_prefill_streaming_rows(float *out, const float *x, int seq_len, const int *rows,
+                                   int nrows, const KvlMlaConfig *cfg, const KvlMlaBF16 *w);
 
 #ifdef __cplusplus
 }

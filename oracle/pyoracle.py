@@ -34,6 +34,8 @@ _EXTRA = {
                                  C.c_int, C.c_float, C.c_int, C.c_float]),
     "mla_prefill_streaming": (C.c_int, [abi.f32p, abi.f32p, C.c_int, abi.CFG, abi.W]),
     "mla_prefill_materialized": (C.c_int, [abi.f32p, abi.f32p, C.c_int, abi.CFG, abi.W]),
+    "mla_prefill_streaming_rows": (C.c_int, [abi.f32p, abi.f32p, C.c_int, C.POINTER(C.c_int), C.c_int,
+                                             abi.CFG, abi.W]),
 }
 
 _cache = {}

@@ -91,3 +91,35 @@ def test_synth_normal_moments_and_determinism():
     assert abs(float(v.mean())) < 0.01 and abs(float(v.std()) - 1.0) < 0.01
     assert np.max(np.abs(v)) <= 2.0 * np.sqrt(3.0)
     np.testing.assert_array_equal(v[1000:1010], inputs.synth_normal(0xC4, np.arange(1000, 1010)))
+
+
+def test_host_helpers_match_reference_formulas():
+    """The library's host-only exports, called through the C ABI (no HIP call is made):
+    kvl_bf16_to_f32 over every BF16 word is the word shifted into the high half
+    (src/ops.c:12-17); the *_state_bytes of the three state kinds are sizeof(struct) plus
+    capacity x the per-row bytes of the reference layouts (src/mla_state.c:57-64,
+    src/mla_compressed_state.c:47-50, src/mla_compressed_q8_state.c:104-109), and 0 for a
+    freed state."""
+    L = lib.load()
+    words = np.arange(65536, dtype=np.uint32)
+    got = np.array([L.kvl_bf16_to_f32(int(u)) for u in words], dtype=np.float32)
+    want = words << np.uint32(16)
+    # ctypes returns the float as a Python float (a double): signalling NaNs come back quieted,
+    # so NaN words are checked as NaN with the same sign, every other word bit for bit
+    nan = np.isnan(want.view(np.float32))
+    np.testing.assert_array_equal(got.view(np.uint32)[~nan], want[~nan])
+    assert np.isnan(got[nan]).all()
+    np.testing.assert_array_equal(np.signbit(got[nan]), np.signbit(want.view(np.float32)[nan]))
+    for d, cap in ((dict(inputs.KIMI), 33), (dict(inputs.KIMI, num_heads=4, kv_lora_rank=96, qk_rope_dim=16), 7)):
+        cfg = inputs.config(**d)
+        R, DR, NH = cfg.kv_lora_rank, cfg.qk_rope_dim, cfg.num_heads
+        QD, DV = cfg.qk_nope_dim + cfg.qk_rope_dim, cfg.v_head_dim
+        cases = ((abi.KvlMlaCompressedQ8State, "compressed_q8_state", R + 4 + 2 * DR),
+                 (abi.KvlMlaCompressedState, "compressed_state", 4 * (R + DR)),
+                 (abi.KvlMlaState, "state", 4 * NH * (QD + DV)))
+        for T, name, per_row in cases:
+            st = T()
+            assert getattr(L, f"kvl_mla_{name}_init")(C.byref(st), C.byref(cfg), cap) == 0
+            assert getattr(L, f"kvl_mla_{name}_bytes")(C.byref(st)) == C.sizeof(T) + cap * per_row, name
+            getattr(L, f"kvl_mla_{name}_free")(C.byref(st))
+            assert getattr(L, f"kvl_mla_{name}_bytes")(C.byref(st)) == 0, name

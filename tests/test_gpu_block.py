@@ -8,13 +8,16 @@ import ctypes as C
 import numpy as np
 import pytest
 
-from helpers import f32, rel_err, snapshot
+import pyoracle
+from helpers import Api, f32, rel_err, snapshot
 from kvl_mla import abi, inputs, lib
 
 pytestmark = pytest.mark.gpu
 
 L = lib.load()
+O = Api(pyoracle.load_oracle(), "orc_")
 KIMI = dict(inputs.KIMI)
+TOL = 2e-3
 
 KINDS = {
     "f32": (abi.KvlMlaCompressedState, "compressed_state", L.kvl_mla_decode_compressed_bf16,
@@ -60,6 +63,37 @@ def test_block_equals_serial_long_history(kind, P, count):
     for k in a:  # the appended rows (the history below P lives on the device only)
         np.testing.assert_array_equal(a[k][P:], b[k][P:], err_msg=k)
     assert rel_err(got, want) == 0.0
+    # the oracle on the same history: its block decode for the FP32 state
+    # (src/mla_compressed_state.c:163-184), its serial decodes for the Q8 state
+    lib.check(getattr(L, f"kvl_mla_{name}_pull")(C.byref(blk), 0, P), "pull")
+    ref_st = KINDS[kind][0]()
+    assert getattr(O, f"mla_{name}_init")(C.byref(ref_st), C.byref(cfg), P + count) == 0
+    fields = ({"codes": "latent_q8", "scale": "latent_scale", "rope": "rope_bf16"} if kind == "q8"
+              else {"latent": "latent", "rope": "rope"})
+    for k, v in snapshot(kind, blk, cfg).items():
+        n = v[:P].size
+        np.ctypeslib.as_array(getattr(ref_st, fields[k]), (n,))[:] = v[:P].ravel()
+    ref_st.len = P
+    ref = np.zeros_like(want)
+    if kind == "f32":
+        assert O.mla_decode_compressed_block_bf16(f32(ref), f32(x), count, P, C.byref(cfg), C.byref(w),
+                                                  C.byref(ref_st)) == 0
+    else:
+        for t in range(count):
+            assert O.mla_decode_compressed_q8_bf16(f32(ref[t]), f32(np.ascontiguousarray(x[t])), P + t, C.byref(cfg),
+                                                   C.byref(w), C.byref(ref_st)) == 0
+    e = rel_err(got, ref)
+    print(f"[block]   vs oracle max|d|/max|ref| = {e:.3e}", flush=True)
+    assert e <= TOL, e
+    sa, so = snapshot(kind, blk, cfg), snapshot(kind, ref_st, cfg)
+    if kind == "q8":  # appended rows: kv_a sums in another order, so codes may differ by one step
+        dc = np.abs(sa["codes"][P:].astype(int) - so["codes"][P:].astype(int))
+        assert dc.max() <= 1 and dc.mean() < 0.01, (dc.max(), dc.mean())
+        np.testing.assert_allclose(sa["scale"][P:], so["scale"][P:], rtol=1e-5)
+    else:
+        for k in sa:
+            assert rel_err(sa[k][P:], so[k][P:]) < 1e-4, k
+    getattr(O, f"mla_{name}_free")(C.byref(ref_st))
     for st in (ser, blk):
         getattr(L, f"kvl_mla_{name}_free")(C.byref(st))
     L.kvl_mla_release_weights(C.byref(w))

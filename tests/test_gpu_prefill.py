@@ -60,34 +60,40 @@ def test_prefill_sharp_attention(q_std):
     assert rel_err(a, b) <= TOL, rel_err(a, b)
 
 
-def test_prefill_4096_prefix_and_oracle_1024():
-    """The 4096-token prefill workload (bf16 inputs, theta 50000): rows [0, 1024) of the
-    4096-token prefill equal the 1024-token prefill (causality: row t sees tokens <= t, and each
-    stage computes a token independently of the sequence length; the only difference allowed
-    is the rounding of the o_proj library GEMM, whose kernel choice depends on the token count),
-    and the 1024-token prefill matches the oracle's streaming prefill."""
+def test_prefill_4096_vs_oracle_every_query_tile():
+    """The 4096-token prefill workload (bf16 inputs from seeded N(0,1) hidden states, theta
+    50000) against the oracle's streaming prefill (src/mla_prefill_streaming.c:78-206) on a
+    fixed sample of query rows: one row in every 128-query tile of the attention kernel (at a
+    different offset in each tile), the first and the last two rows. Then a size-independent
+    property over all rows: rows [0, 1024) equal the 1024-token prefill bit for bit (row t sees
+    tokens <= t, and every stage computes a token independently of the sequence length)."""
     cfg = inputs.config(**inputs.KIMI)
     layer = inputs.make_layer(cfg, 0xCA)
     w = layer.struct()
-    x = inputs.hidden(cfg, 0xCA, 4096, bf16_exact=True)
-    full = np.zeros((4096, cfg.hidden_size), np.float32)
+    S = 4096
+    x = inputs.hidden(cfg, 0xCA, S, bf16_exact=True)
+    full = np.zeros((S, cfg.hidden_size), np.float32)
+    lib.check(L.kvl_mla_prefill_bf16(f32(full), f32(x), S, C.byref(cfg), C.byref(w)), "prefill 4096")
+    assert np.all(np.isfinite(full))
+    rows = sorted({0, S - 2, S - 1} | {128 * i + (53 * i + 17) % 128 for i in range(S // 128)})
+    idx = np.ascontiguousarray(rows, dtype=np.int32)
+    ref = np.zeros((len(rows), cfg.hidden_size), np.float32)
+    assert ORC.orc_mla_prefill_streaming_rows(f32(ref), f32(x), S, idx.ctypes.data_as(C.POINTER(C.c_int)),
+                                              len(rows), C.byref(cfg), C.byref(w)) == 0
+    e = rel_err(full[idx], ref)
+    worst = max((rel_err(full[t], ref[i]), t) for i, t in enumerate(rows))
+    print(f"[prefill] 4096 tokens, {len(rows)} sampled rows vs oracle {e:.3e} (worst single row {worst[0]:.3e} "
+          f"at {worst[1]})", flush=True)
+    assert e <= TOL
     part = np.zeros((1024, cfg.hidden_size), np.float32)
-    lib.check(L.kvl_mla_prefill_bf16(f32(full), f32(x), 4096, C.byref(cfg), C.byref(w)), "prefill 4096")
     xp = np.ascontiguousarray(x[:1024])
     lib.check(L.kvl_mla_prefill_bf16(f32(part), f32(xp), 1024, C.byref(cfg), C.byref(w)), "prefill 1024")
-    e_prefix = rel_err(full[:1024], part)
-    print(f"[prefill] 4096 rows [0,1024) vs 1024-token prefill {e_prefix:.3e}", flush=True)
-    assert np.all(np.isfinite(full)) and e_prefix <= 1e-5
-    ref = np.zeros_like(part)
-    assert ORC.orc_mla_prefill_streaming(f32(ref), f32(xp), 1024, C.byref(cfg), C.byref(w)) == 0
-    e = rel_err(part, ref)
-    print(f"[prefill] 1024 tokens vs oracle {e:.3e}", flush=True)
-    assert e <= TOL
+    np.testing.assert_array_equal(full[:1024], part)
 
 
 def test_prefill_repeats_bit_for_bit():
-    """Same inputs, same output: every stage (including the library GEMM of o_proj) picks its
-    kernels deterministically and sums in a fixed order."""
+    """Same inputs, same output: every stage picks its kernels deterministically and sums in a
+    fixed order."""
     cfg = inputs.config(**inputs.KIMI)
     layer = inputs.make_layer(cfg, 0xC9)
     w = layer.struct()

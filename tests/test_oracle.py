@@ -424,3 +424,26 @@ def test_position_zero_decode_closed_form():
     lat0 = snap["latent"][0].astype(np.float64)
     ho = np.concatenate([Wb[h, 8:] @ lat0 for h in range(4)])
     np.testing.assert_allclose(out[0], f(layer.o_proj) @ ho, rtol=0, atol=1e-6)
+
+
+@pytest.mark.parametrize("name,dims,std,S,rows", [
+    ("stream", STREAM, 0.2, 64, [0, 1, 31, 63]),
+    ("lab", LAB, 0.05, 33, [32, 0, 17]),
+    ("kimi", inputs.KIMI, 0.02, 24, [0, 5, 23])], ids=["stream", "lab", "kimi"])
+def test_prefill_rows_equal_full_prefill(name, dims, std, S, rows):
+    """orc_mla_prefill_streaming_rows (the checker of long GPU prefills) reproduces the listed
+    rows of the full streaming prefill -- itself bit-exact with the reference build -- bit for
+    bit, in any row order; rows past the sequence are rejected."""
+    cfg, layer, x = model(dims, 23, std=std, n=S, xstd=0.25)
+    w = layer.struct()
+    H = cfg.hidden_size
+    full = np.zeros((S, H), np.float32)
+    assert ORC.orc_mla_prefill_streaming(f32(full), f32(x), S, C.byref(cfg), C.byref(w)) == 0
+    idx = np.ascontiguousarray(rows, dtype=np.int32)
+    part = np.zeros((len(rows), H), np.float32)
+    ip = idx.ctypes.data_as(C.POINTER(C.c_int))
+    assert ORC.orc_mla_prefill_streaming_rows(f32(part), f32(x), S, ip, len(rows), C.byref(cfg), C.byref(w)) == 0
+    np.testing.assert_array_equal(part.view(np.uint32), full[idx].view(np.uint32))
+    bad = np.ascontiguousarray([0, S], dtype=np.int32)
+    assert ORC.orc_mla_prefill_streaming_rows(f32(part), f32(x), S, bad.ctypes.data_as(C.POINTER(C.c_int)), 2,
+                                              C.byref(cfg), C.byref(w)) == -1
