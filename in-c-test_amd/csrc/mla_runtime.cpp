@@ -37,7 +37,19 @@
 
 using namespace kvl;
 
+// Device scratch of the no-allocation decode entry point
+// (kvl_mla_decode_compressed_q8_batch_device_noalloc): the decode workspace of up to
+// kNoAllocMaxBatch sequences followed by the split-K partials. Every GPU the library runs on
+// holds its own copy for the life of the process. Host code never uses the array's name as a
+// device address: its address on each device comes from hipGetSymbolAddress at set-up.
+constexpr size_t kNoAllocScratchBytes = (size_t)24 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
 namespace {
+
+constexpr int kNoAllocMaxBatch = 16;
+constexpr int kMaxDevices = 64;
+void *g_scratch[kMaxDevices];  // device address of `scratch` per device (null: not resolved)
 
 thread_local std::string g_err;
 
@@ -171,6 +183,15 @@ int ensure_ready() {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
         set_err("libkvl_mla is built for gfx950; device %d is %s", dev, prop.gcnArchName);
         return -1;
+    }
+    if (dev < 0 || dev >= kMaxDevices) {
+        set_err("device index %d out of range", dev);
+        return -1;
+    }
+    if (!g_scratch[dev]) {
+        void *p = nullptr;
+        HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        g_scratch[dev] = p;
     }
     HIP_TRY(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
     c.device = dev;
@@ -340,14 +361,30 @@ bool weights_ok(const KvlMlaBF16 *w) {
 
 // ---------------------------------------------------------------- RoPE table ------------
 
+uint64_t rope_key(float theta, int DR) {
+    uint32_t tb;
+    memcpy(&tb, &theta, sizeof tb);
+    return ((uint64_t)tb << 16) | (uint64_t)DR;
+}
+
+// The existing table when it covers positions [0, need_pos), without growing it.
+int rope_lookup(float theta, int DR, int need_pos, const float2 **out) {
+    Ctx &c = ctx();
+    auto it = c.ropes.find(rope_key(theta, DR));
+    if (it == c.ropes.end() || it->second.npos < need_pos) {
+        set_err("the RoPE table does not cover position %d yet (a decode at that position or later "
+                "through an allocating entry point builds it)", need_pos - 1);
+        return -1;
+    }
+    *out = it->second.dev;
+    return 0;
+}
+
 // (cos, sin) of pos * theta^(-2i/DR) computed exactly as src/mla_compressed_q8_state.c:22-25:
 // double pow/cos/sin, rounded to float. The device kernels only apply the rotation.
 int rope_table(float theta, int DR, int need_pos, const float2 **out) {
     Ctx &c = ctx();
-    uint32_t tb;
-    memcpy(&tb, &theta, sizeof tb);
-    const uint64_t key = ((uint64_t)tb << 16) | (uint64_t)DR;
-    RopeTable &t = c.ropes[key];
+    RopeTable &t = c.ropes[rope_key(theta, DR)];
     if (need_pos > t.npos) {
         if (c.capturing) {
             set_err("RoPE table growth during graph capture");
@@ -521,9 +558,9 @@ struct Layout {
     }
 };
 
-// Carves DecodeWork for a group of B sequences out of the workspace buffer.
-int decode_work(const Dims &d, int B, int row_bytes, DecodeWork &w) {
-    Ctx &c = ctx();
+// Carves DecodeWork for a group of B sequences out of `base` (nullptr: sizing only); returns
+// the bytes it spans.
+size_t decode_work_at(const Dims &d, int B, int row_bytes, char *base, DecodeWork &w) {
     const size_t qs = (size_t)std::max(d.R + d.DR, d.QD);
     auto carve = [&](char *base, Layout &L) {
         w.x = L.take<float>(base, (size_t)B * d.H);
@@ -544,17 +581,24 @@ int decode_work(const Dims &d, int B, int row_bytes, DecodeWork &w) {
         w.out = L.take<float>(base, (size_t)B * d.H);
         w.rows = L.take<uint8_t>(base, (size_t)B * row_bytes);
     };
-    Layout probe;
-    carve(nullptr, probe);
-    if (c.work.bytes < probe.off) {
+    Layout L;
+    carve(base, L);
+    w.part = nullptr;
+    return (L.off + 255) & ~(size_t)255;
+}
+
+// DecodeWork for a group of B sequences in the library's workspace buffer (grown on demand).
+int decode_work(const Dims &d, int B, int row_bytes, DecodeWork &w) {
+    Ctx &c = ctx();
+    const size_t need = decode_work_at(d, B, row_bytes, nullptr, w);
+    if (c.work.bytes < need) {
         if (c.capturing) {
             set_err("workspace growth during graph capture");
             return -1;
         }
-        if (dev_reserve(c.work, probe.off) != 0) return -1;
+        if (dev_reserve(c.work, need) != 0) return -1;
     }
-    Layout L;
-    carve((char *)c.work.p, L);
+    decode_work_at(d, B, row_bytes, (char *)c.work.p, w);
     return 0;
 }
 
@@ -599,15 +643,18 @@ long split_rows(int kind, long len, long total_rows, int ncu) {
 
 // solo: every sequence gets the plan it would get alone in the launch, so its result does
 // not depend on the other members (block decode).
+// part_cap > 0: w.part is a caller-provided buffer of part_cap bytes for the split partials and
+// nothing is allocated (the RoPE table must already cover the positions).
 int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeights &dw,
                  const SeqIn *seqs, int B, const float *d_x, float *d_out, bool residual,
-                 DecodeWork &w, bool solo = false) {
+                 DecodeWork &w, bool solo = false, size_t part_cap = 0) {
     Ctx &c = ctx();
     hipStream_t st = c.stream;
     int maxpos = 0;
     for (int i = 0; i < B; ++i) maxpos = std::max(maxpos, seqs[i].pos);
     const float2 *cs = nullptr;
-    if (rope_table(theta, d.DR, maxpos + 1, &cs) != 0) return -1;
+    if ((part_cap ? rope_lookup(theta, d.DR, maxpos + 1, &cs) : rope_table(theta, d.DR, maxpos + 1, &cs)) != 0)
+        return -1;
 
     const bool kimi = kimi_attn(d) && fmt != kFmtExp;
     const int kind = !kimi ? kAttnGeneric : fmt == kFmtQ8 ? kAttnQ8Mfma : kAttnF32Mfma;
@@ -651,7 +698,16 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
     }
     const int G = fmt == kFmtExp ? 1 : d.NH;
     const int DVm = fmt == kFmtExp ? d.DV : d.R;
-    if (reserve_part((size_t)total_splits * G * (DVm + 2) * sizeof(float), &w.part) != 0) return -1;
+    const size_t part_bytes = (size_t)total_splits * G * (DVm + 2) * sizeof(float);
+    if (part_cap) {
+        if (part_bytes > part_cap || kind == kAttnGeneric) {
+            set_err("the split plan needs %zu bytes of partials; the fixed scratch holds %zu (%d splits)",
+                    part_bytes, part_cap, total_splits);
+            return -1;
+        }
+    } else if (reserve_part(part_bytes, &w.part) != 0) {
+        return -1;
+    }
     if (kind == kAttnGeneric) {
         const int P = fmt == kFmtExp ? B * d.NH : B;
         const size_t bytes = (size_t)P * G * lmax * sizeof(float);
@@ -980,6 +1036,93 @@ int decode_device(float *d_out, const float *d_x, int B, const KvlMlaConfig *cfg
         }
     }
     (void)c;
+    return 0;
+}
+
+// Decode of decode_device's arithmetic (Q8 histories, the MFMA route) that allocates nothing:
+// the workspace and the partials live in the device array `scratch`; the weights must be bound,
+// every state's device copy must exist and hold its rows [0, len), and the RoPE table must
+// cover the positions. Rows appended at len stay on the device; len advances unless
+// KVL_MLA_NO_ADVANCE. Two calls on one GPU share the array, so calls that overlap in time on
+// that GPU (graph launches on other streams) race.
+int decode_q8_noalloc(float *d_out, const float *d_x, int B, const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                      KvlMlaCompressedQ8State *const *states, unsigned flags) {
+    Dims d;
+    if (!d_out || !d_x || B <= 0 || !states || !weights_ok(w) || !dims_of(cfg, d)) {
+        set_err("invalid arguments");
+        return -1;
+    }
+    if (B > kNoAllocMaxBatch) {
+        set_err("batch %d exceeds the %d sequences of the fixed scratch", B, kNoAllocMaxBatch);
+        return -1;
+    }
+    if (flags & ~(unsigned)(KVL_MLA_RESIDUAL | KVL_MLA_NO_ADVANCE)) {
+        set_err("unsupported flags");
+        return -1;
+    }
+    if (!kimi_attn(d) || !dims_supported(d)) {
+        set_err("dims outside the MFMA route (16 heads, kv_lora_rank 512, qk_rope_dim 64)");
+        return -1;
+    }
+    if (ensure_ready() != 0) return -1;
+    Ctx &c = ctx();
+    int dev = -1;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev != c.device || !g_scratch[dev]) {
+        set_err("current device %d is not the library's device %d", dev, c.device);
+        return -1;
+    }
+    DevWeights dw;
+    const uint16_t **slot[5] = {&dw.q, &dw.kva, &dw.norm, &dw.kvb, &dw.o};
+    const uint16_t *host[5] = {w->q_proj, w->kv_a_proj, w->kv_a_norm, w->kv_b_proj, w->o_proj};
+    const size_t elems[5] = {(size_t)d.QO * d.H, (size_t)d.KVO * d.H, (size_t)d.R, (size_t)d.KVB * d.R,
+                             (size_t)d.H * d.HO};
+    for (int k = 0; k < 5; ++k) {
+        auto it = c.weights.find(host[k]);
+        if (it == c.weights.end() || it->second.pins <= 0 || it->second.bytes != elems[k] * sizeof(uint16_t)) {
+            set_err("weights must be bound (kvl_mla_bind_weights) before a no-allocation call");
+            return -1;
+        }
+        *slot[k] = (const uint16_t *)it->second.dev;
+    }
+    SeqIn seqs[kNoAllocMaxBatch];
+    for (int i = 0; i < B; ++i) {
+        KvlMlaCompressedQ8State *s = states[i];
+        if (!s || s->len < 0 || s->len >= s->capacity || !state_dims_ok(s, cfg)) {
+            set_err("sequence %d: capacity/dims check failed", i);
+            return -1;
+        }
+        const HostView v = view_of(s);
+        auto it = c.mirrors.find(s);
+        if (it == c.mirrors.end() || it->second.fmt != v.fmt || it->second.ha != v.ha || it->second.hb != v.hb ||
+            it->second.hc != v.hc || it->second.capacity != v.capacity || it->second.d0 != v.d0 ||
+            it->second.d1 != v.d1 || it->second.synced < s->len) {
+            set_err("sequence %d: the state's rows [0, len) are not on the device (an allocating call or "
+                    "*_fill_synthetic puts them there)", i);
+            return -1;
+        }
+        seqs[i] = {&it->second, s->len};
+    }
+    DecodeWork wk;
+    const size_t rb = row_bytes_of(kFmtQ8, d.R, d.DR, 0);
+    const size_t wbytes = decode_work_at(d, B, (int)rb, nullptr, wk);
+    if (wbytes >= kNoAllocScratchBytes) {
+        set_err("the decode workspace (%zu bytes) exceeds the fixed scratch (%zu bytes)", wbytes,
+                kNoAllocScratchBytes);
+        return -1;
+    }
+    char *base = (char *)g_scratch[dev];
+    decode_work_at(d, B, (int)rb, base, wk);
+    wk.part = (float *)(base + wbytes);
+    if (decode_group(kFmtQ8, d, cfg->rms_eps, cfg->rope_theta, dw, seqs, B, d_x, d_out,
+                     (flags & KVL_MLA_RESIDUAL) != 0, wk, false, kNoAllocScratchBytes - wbytes) != 0)
+        return -1;
+    if (!(flags & KVL_MLA_NO_ADVANCE)) {
+        for (int i = 0; i < B; ++i) {
+            states[i]->len += 1;
+            seqs[i].m->synced = states[i]->len;
+        }
+    }
     return 0;
 }
 
@@ -1625,6 +1768,13 @@ int kvl_mla_decode_compressed_q8_batch_device(float *d_out, const float *d_x, in
                                               KvlMlaCompressedQ8State *const *states, unsigned flags) {
     Guard guard;
     return decode_device(d_out, d_x, batch, cfg, w, states, flags);
+}
+
+int kvl_mla_decode_compressed_q8_batch_device_noalloc(float *d_out, const float *d_x, int batch,
+                                                      const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                                      KvlMlaCompressedQ8State *const *states, unsigned flags) {
+    Guard guard;
+    return decode_q8_noalloc(d_out, d_x, batch, cfg, w, states, flags);
 }
 
 int kvl_mla_decode_compressed_batch_device(float *d_out, const float *d_x, int batch,

@@ -33,6 +33,8 @@ EXT_API = {
                                                         abi.W, QSP, C.c_uint]),
     "mla_decode_compressed_batch_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, abi.CFG,
                                                      abi.W, CSP, C.c_uint]),
+    "mla_decode_compressed_q8_batch_device_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, abi.CFG,
+                                                                abi.W, QSP, C.c_uint]),
     "mla_attention_layer_q8_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, abi.CFG, abi.W, abi.u16p,
                                                  abi.u16p, QSP, C.c_uint]),
     "mla_attention_layer_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, abi.CFG, abi.W, abi.u16p,

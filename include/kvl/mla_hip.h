@@ -86,6 +86,23 @@ int kvl_mla_decode_compressed_batch_device(float *d_out, const float *d_x, int b
                                            KvlMlaCompressedState *const *states,
                                            unsigned flags);
 
+/* No counterpart in the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc). The same computation and
+ * results, bit for bit, as kvl_mla_decode_compressed_q8_batch_device, but every buffer beyond
+ * the inputs, outputs, bound weights and state copies (the decode workspace and the split-K
+ * partials) lives in one fixed device array of 24 MiB per GPU, and the call makes no
+ * hipMalloc / hipFree. Limits, each rejected with -1 and a message: batch <= 16; the dims of
+ * the MFMA route (16 heads, kv_lora_rank 512, qk_rope_dim 64); a split plan whose partials fit
+ * the array (about 21 MiB, i.e. ~650 splits: e.g. 16 x 40K or 8 x 80K rows); weights bound;
+ * each state's rows [0, len) already on the device (an allocating call or *_fill_synthetic
+ * put them there); the RoPE table already covering the positions (an allocating decode at the
+ * same or a later position built it). All calls on one GPU share the array: calls that overlap
+ * in time on that GPU (a captured graph launched on another stream while a call runs) race. */
+int kvl_mla_decode_compressed_q8_batch_device_noalloc(float *d_out, const float *d_x, int batch,
+                                                      const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                                      KvlMlaCompressedQ8State *const *states,
+                                                      unsigned flags);
+
 /* The attention half of a decoder layer, as src/generate.c:34-67 (attention_token) computes it
  * for one token, for a batch over device buffers:
  *   n1 = RMSNorm(h, input_norm); h += attention(n1) (appending each sequence's row);
