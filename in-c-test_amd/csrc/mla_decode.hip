@@ -1275,42 +1275,57 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
 }
 
 // ---- int8 MFMA path (Q8 history, NH=16, R=512, DR=64) ---------------------------------
-// One workgroup (4 waves) per CU streams its split in chunks of 64 rows through a ring of
-// three LDS chunk buffers (41 KB each) filled by global_load_lds_dwordx4 DMA: while chunk c
-// is computed, chunks c+1 and c+2 are in flight, and no VGPRs stage the stream. The 16-byte
-// slots of each LDS row are XOR-swizzled so that the row reads of the score and the
-// transposing column reads of the mix are free of bank conflicts.
-// Scores (wave w: rows 16w..16w+15): v_mfma_i32_16x16x64_i8 on the raw int8 codes against
-// the int8 hi/lo split of q_lat (exact integer dot products), plus bf16 MFMA on the bf16
-// RoPE keys against the hi/lo bf16 split of q_rope. The row scale factors out of the dot
-// (score_j = s_j * q_lat . c_j + q_rope . k_j). Mix: the weights p_j*s_j (p_j <= kQ8Pmax
-// against the lazily moved reference max below, s_j <= the split's largest scale) are
-// quantised to three int8 levels hi + lo/254 + lo2/254^2 against kQ8Pmax * that scale (23
-// bits below the bound: a row whose scale is far below the split's largest -- an all-zero
-// latent stored with scale 1, or a flat row beside a one-hot-like one -- keeps the precision
-// of its own weight); ds_read_b64_tr_b8 reads the codes transposed (16 rows of one column per
-// lane), and v_mfma_i32_16x16x64_i8 accumulates the exact integer mix of each level in place
-// across chunks. A head's reference max only moves when a chunk exceeds it by more than
-// ln kQ8Pmax (so p_j <= kQ8Pmax); its integer accumulators are then rescaled by
-// alpha = exp(m_old - m_new) in double, each level's rounding remainder carried into the
-// next one. kQ8Pmax = 4 makes rescales rare (they cost a pass over the accumulators).
-// Each wave accumulates 128 latent columns.
+// One workgroup of 8 waves (two per SIMD) per CU streams its split-K slice in chunks of 64
+// rows. The waves specialise, and the two roles run one chunk apart:
+//   score waves 0-3 (rows 16w .. 16w+15 of a chunk) take chunk k in step k: scores, softmax,
+//     and the quantised mix weights of their rows into LDS;
+//   mix waves 4-7 (latent columns 128(w-4) .. +127) take chunk k-1 in step k: they issue the
+//     history DMA (global_load_lds_dwordx4 into a ring of four 32 KB code slots: chunk k-1
+//     being mixed, chunk k being scored, chunks k+1 and k+2 in flight) and accumulate the mix.
+// A score wave's softmax and quantisation (VALU) thus overlap the mix wave's MFMAs and DMA on
+// the same SIMD. One barrier per step orders everything in the common case: the weights of
+// chunk k are written before it and read after it, the mix waves have waited for chunk k+1's
+// DMA and finished reading chunk k-1's slot before it.
+// Scores: v_mfma_i32_16x16x64_i8 on the raw int8 codes against the int8 hi/lo split of q_lat
+// (exact integer dot products), plus bf16 MFMA on the bf16 RoPE keys (loaded by the score
+// waves straight into registers, one chunk ahead) against the hi/lo bf16 split of q_rope. The
+// row scale factors out of the dot (score_j = s_j * q_lat . c_j + q_rope . k_j).
+// Mix: the weights p_j*s_j (p_j <= kQ8Pmax against the lazily moved reference max below,
+// s_j <= the split's largest scale) are quantised to three int8 levels hi + lo/254 + lo2/254^2
+// against kQ8Pmax * that scale (23 bits below the bound: a row whose scale is far below the
+// split's largest -- an all-zero latent stored with scale 1, or a flat row beside a
+// one-hot-like one -- keeps the precision of its own weight); ds_read_b64_tr_b8 reads the codes
+// transposed (16 rows of one column per lane), and v_mfma_i32_16x16x64_i8 accumulates the exact
+// integer mix of each level across chunks. A head's reference max only moves when a chunk
+// exceeds it by more than ln kQ8Pmax (so p_j <= kQ8Pmax): the score waves then exchange their
+// chunk maxima (two more barriers, taken by all eight waves on the same LDS flags), requantise
+// the chunk's weights and publish alpha = exp(m_old - m_new); the mix waves rescale their
+// accumulators by alpha (in double, each level's rounding remainder carried into the next)
+// before they add that chunk. kQ8Pmax = 4 makes these exchanges rare after the first chunk.
 constexpr int kQ8Ch = 64;
 constexpr float kQ8Pmax = 4.0f;            // bound of p_j = exp(s_j - reference max)
 constexpr float kQ8LnPmax = 1.3862944f;    // ln kQ8Pmax
-constexpr int kQ8Ring = 3;
-constexpr int kQ8MaxSplitRows = 2048;               // rows of one split (scales table)
+constexpr int kQ8Ring = 4;                          // code slots (chunks k .. k+3)
 constexpr int kQ8CodeB = kQ8Ch * 512;               // codes of a chunk
+constexpr int kQ8RRing = 3;                         // RoPE-key + scale slots (chunks k .. k+2)
 constexpr int kQ8RopeB = kQ8Ch * 128;               // bf16 RoPE keys of a chunk
-constexpr int kQ8ChunkB = kQ8CodeB + kQ8RopeB;
-constexpr int kQ8Ws = 80;                           // LDS bytes per quantised-weight row
-constexpr int kQ8SclOff = kQ8Ring * kQ8ChunkB;      // scales of the whole split
+constexpr int kQ8RSlot = kQ8RopeB + kQ8Ch * 4;      // + the chunk's row scales
+constexpr int kQ8RopeOff = kQ8Ring * kQ8CodeB;
+constexpr int kQ8Ws = 64;                           // LDS bytes per quantised-weight row
 constexpr int kQ8WqB = 3 * 16 * kQ8Ws;              // quantised weights of a chunk (hi, lo, lo2)
-constexpr int kQ8WqOff = kQ8SclOff + 4 * kQ8MaxSplitRows;  // two buffers, by chunk parity
-constexpr int kQ8MlOff = kQ8WqOff + 2 * kQ8WqB;    // chunk maxima [2][4 waves][16], sums, smax
-constexpr int kQ8QOff = kQ8MlOff + 4 * 4 * 16 * 4;  // query operands of the sequence
-constexpr int kQ8QB = 2 * 16 * 512 + 2 * 16 * 128 + 256;  // int8 hi, lo; bf16 rope hi, lo; scales
-constexpr int kQ8SmemB = kQ8QOff + kQ8QB;
+constexpr int kQ8WqOff = kQ8RopeOff + kQ8RRing * kQ8RSlot;  // two weight buffers, by chunk parity
+constexpr int kQ8FlagOff = kQ8WqOff + 2 * kQ8WqB;   // [2][4] int: a row exceeds the reference max
+constexpr int kQ8MlOff = kQ8FlagOff + 2 * 4 * 4;    // [2][4 waves][16] chunk maxima
+constexpr int kQ8AlOff = kQ8MlOff + 2 * 4 * 16 * 4; // [2][16] alpha of a moved reference max
+constexpr int kQ8LsOff = kQ8AlOff + 2 * 16 * 4;     // [4 waves][16] softmax denominators
+constexpr int kQ8SmOff = kQ8LsOff + 4 * 16 * 4;     // [4] largest row scale per score wave
+constexpr int kQ8SmemB = kQ8SmOff + 4 * 4;
+static_assert(kQ8SmemB <= 160 * 1024, "LDS of one CU");
+
+// Position of the quantised weight of (head h, chunk row r) within one level: 16-byte groups
+// of rows XOR-swizzled by the head, so the mix waves' 16-byte reads (one head, 16 rows per lane)
+// spread over the banks.
+__device__ __forceinline__ int q8_wpos(int h, int r) { return h * kQ8Ws + ((((r >> 4) ^ (h >> 1)) & 3) << 4) + (r & 15); }
 
 // Slot swizzle of the code rows: physical 16-byte slot = logical slot ^ q8_swz(row).
 __device__ __forceinline__ int q8_swz(int row) { return (row & 7) ^ (((row >> 4) & 1) << 2); }
@@ -1348,235 +1363,178 @@ __device__ __forceinline__ v2i lds_read_tr8(const uint8_t *p) {
     return __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i *)(p));
 }
 
-__global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t smem[kQ8SmemB];
-    int8_t *wq = (int8_t *)(smem + kQ8WqOff);  // [hi, lo][16 heads][kQ8Ws]
-    float *mloc = (float *)(smem + kQ8MlOff);  // [2 parities][4 waves][16]
-    float *lsum = mloc + 128;                  // [4 waves][16]
-    float *smx = mloc + 192;                   // [4 waves]
-    int *oflag = (int *)(mloc + 200);          // [4 waves]: a row exceeds the reference max
-    const uint32_t sbase = lds_addr(smem);
-    const float *sclv = (const float *)(smem + kQ8SclOff);  // scales of the split's rows
-    const int tid = threadIdx.x, l = tid & 63, n = l & 15, g = l >> 4;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int b = find_seq(a.t, blockIdx.x);
-    const SeqDesc &s = a.t.s[b];
-    const int split = blockIdx.x - s.split0;
-    const int r0 = split * s.rps;
-    const int r1 = split == s.nsplit - 1 ? s.len : r0 + s.rps;  // last split takes the rest
-    const int8_t *gcodes = (const int8_t *)s.a;
-    const float *gscl = (const float *)s.b;
-    const uint16_t *grope = (const uint16_t *)s.c;
-
-    // Query operands of sequence b come through LDS DMA like the history: every global load
-    // of the kernel is then an asm DMA, and the prologue waits for the first chunk only
-    // (a compiler-visible load would make the compiler wait for every DMA issued before it).
-    // LDS rows of 512 (int8) / 128 (bf16) bytes, 16-byte slots XOR-swizzled by the head so
-    // that the 16 lanes of a lane group (16 heads) hit distinct banks.
-    const uint8_t *sq = smem + kQ8QOff;  // [hi, lo][16][512] int8, [hi, lo][16][64] bf16, qs[16]
-    {
-        const uint32_t qd = sbase + (uint32_t)kQ8QOff;
-        const int8_t *gqh = a.qhi + (size_t)b * 16 * 512, *gql = a.qlo + (size_t)b * 16 * 512;
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {  // 16 KB of int8 hi/lo: 16 instructions, 4 per wave
-            const int p = (w * 2 + k) * 64 + l, head = p >> 5, slot = (p & 31) ^ (head & 31);
-            dma_b128(gqh + head * 512 + 16 * slot, qd + (uint32_t)((w * 2 + k) * 1024));
-            dma_b128(gql + head * 512 + 16 * slot, qd + (uint32_t)(8192 + (w * 2 + k) * 1024));
-        }
-        {  // 4 KB of bf16 rope hi/lo: 4 instructions, one per wave
-            const int p = (w & 1) * 64 + l, head = p >> 3, slot = (p & 7) ^ (head & 7);
-            const uint16_t *src = (w < 2 ? a.qrhi : a.qrlo) + (size_t)b * 16 * 64;
-            dma_b128((const uint8_t *)(src + head * 64) + 16 * slot,
-                     qd + (uint32_t)(16384 + (w >> 1) * 2048 + (w & 1) * 1024));
-        }
-        if (w == 0) dma_b32(a.qs + (size_t)b * 16 + min(l, 15), qd + (uint32_t)(20480));
-    }
-    v4i qh[8], ql[8];      // read from LDS once the prologue's loads have landed
-    v8bf qrh[2], qrl[2];
-    float qsd[4];
-
-    float m_run[4], l_lane[4];
+// The three-level quantised weights of this lane's row (rowl) for heads 4g .. 4g+3:
+// v = p * s * wscale in [0, 127] ~= hi + lo/254 + lo2/254^2.
+__device__ __forceinline__ void put_q8_weights(int8_t *wqc, const float *pv, float swj, int g, int rowl) {
+    int qhv[4], qlv[4], q2v[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+        const float v = pv[i] * swj;
+        const float hi = fminf(rintf(v), 127.f);
+        // v - hi is exact (|v - hi| <= 1/2): lo and lo2 span the int8 range
+        const float r1 = (v - hi) * 254.0f;
+        const float lo = rintf(r1);
+        qhv[i] = (int)hi;
+        qlv[i] = (int)lo;
+        q2v[i] = (int)rintf((r1 - lo) * 254.0f);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int o = q8_wpos(4 * g + i, rowl);
+        wqc[o] = (int8_t)qhv[i];
+        wqc[16 * kQ8Ws + o] = (int8_t)qlv[i];
+        wqc[32 * kQ8Ws + o] = (int8_t)q2v[i];
+    }
+}
+
+// s_waitcnt vmcnt(n) for the counts the mix waves use (n wave-uniform).
+__device__ __forceinline__ void wait_vm(int n) {
+    switch (n) {
+    case 0: wait_vmcnt<0>(); break;
+    case 2: wait_vmcnt<2>(); break;
+    case 3: wait_vmcnt<3>(); break;
+    case 8: wait_vmcnt<8>(); break;
+    case 10: wait_vmcnt<10>(); break;
+    case 11: wait_vmcnt<11>(); break;
+    case 16: wait_vmcnt<16>(); break;
+    case 18: wait_vmcnt<18>(); break;
+    case 19: wait_vmcnt<19>(); break;
+    default: wait_vmcnt<0>(); break;
+    }
+}
+
+// The two roles run separate code (their registers do not overlap) with the same sequence of
+// workgroup barriers: two in the prologue (P0: the score waves' query and scale loads are
+// issued before the mix waves' first DMA burst, so they do not queue behind it; P: chunk 0 has
+// landed), per step k = 0 .. nch one (A) plus two more (B, C) when the flags read after A ask
+// for an exchange, and one at the end. Every wave reads the
+// same LDS flags after A, so all eight take the same barriers. Everything the score waves read
+// per chunk (codes, RoPE keys, scales) arrives in LDS by the mix waves' DMA, so their steps
+// never wait on global-memory latency.
+__device__ __forceinline__ void q8_score_role(const AttnArgs &a, uint8_t *smem, int w, int b, int r0, int r1, int nch,
+                                              int sid) {
+    int8_t *wq = (int8_t *)(smem + kQ8WqOff);
+    int *oflag = (int *)(smem + kQ8FlagOff);
+    float *mloc = (float *)(smem + kQ8MlOff);
+    float *abuf = (float *)(smem + kQ8AlOff);
+    float *lsum = (float *)(smem + kQ8LsOff);
+    float *smx = (float *)(smem + kQ8SmOff);
+    const int tid = threadIdx.x, l = tid & 63, n = l & 15, g = l >> 4;
+    const float *gscl = (const float *)a.t.s[b].b;
+    const int rowl = 16 * w + n;  // chunk row of this lane
+    int sc_base[2], rp_off[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        sc_base[kb] = rowl * 512 + 16 * ((4 * kb + g) ^ q8_swz(rowl));
+        rp_off[kb] = rowl * 128 + 16 * ((4 * kb + g) ^ (rowl & 7));
+    }
+    // query operands (A of the score MFMAs: head n, k slice 16g .. 16g+15 of each 64-wide block)
+    // and the split's largest row scale: all loads issued before the first wait
+    v4i qh[8], ql[8];
+    v8bf qrh[2], qrl[2];
+    float qsd[4], m_run[4], l_lane[4];
+    const size_t qo = ((size_t)b * 16 + n) * 512;
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) {
+        qh[kb] = *(const v4i *)(a.qhi + qo + 64 * kb + 16 * g);
+        ql[kb] = *(const v4i *)(a.qlo + qo + 64 * kb + 16 * g);
+    }
+    const size_t ro = ((size_t)b * 16 + n) * 64;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        qrh[kb] = *(const v8bf *)(a.qrhi + ro + 8 * (4 * kb + g));
+        qrl[kb] = *(const v8bf *)(a.qrlo + ro + 8 * (4 * kb + g));
+    }
+    {
+        const int nr = r1 - r0;
+        float sv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sv[i] = tid + 256 * i < nr ? gscl[r0 + tid + 256 * i] : 0.f;
+        lds_barrier();  // P0
+        float m = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, sv[i]);
+        for (int r = tid + 2048; r < nr; r += 256) m = fmaxf(m, gscl[r0 + r]);
+        m = wave_max(m);
+        if (l == 0) smx[w] = m;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        qsd[i] = a.qs[(size_t)b * 16 + 4 * g + i] * (a.smscale / 254.0f);
         m_run[i] = -INFINITY;
         l_lane[i] = 0.f;
     }
-    v4i ahi[8], alo[8], alo2[8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        ahi[t] = v4i{0, 0, 0, 0};
-        alo[t] = v4i{0, 0, 0, 0};
-        alo2[t] = v4i{0, 0, 0, 0};
-    }
+    lds_barrier();  // P: chunk 0 has landed; the split's largest scale is published
+    // largest row scale of the split: the common bound of the quantised weights
+    const float smax = fmaxf(fmaxf(smx[0], smx[1]), fmaxf(smx[2], smx[3]));
+    const float wscale = smax > 0.f ? 127.0f / (kQ8Pmax * smax) : 0.f;
 
-    float wscale = 0.f, wfac = 0.f;  // weight quantisation scale, set once the scales are in
-    const int nch = (r1 - r0 + kQ8Ch - 1) / kQ8Ch;
-    // ---- DMA plan: wave w copies row pairs 8w..8w+7 of the codes and row octets 2w, 2w+1
-    // of the RoPE keys of each chunk. Per-lane global byte offsets relative to the chunk's
-    // first row; rows past the split end (last chunk only) re-read the split's last row
-    // (in bounds) and are masked in the scores. The scales of the whole split are copied
-    // once, together with the first two chunks.
-    int code_off[8], rope_off[2];
+    for (int k = 0; k <= nch; ++k) {
+        const int par = k & 1;
+        int *fl_out = oflag + 4 * par;
+        float *ml = mloc + 64 * par;
+        int8_t *wqc = wq + par * kQ8WqB;  // weights of chunk k
+        float sc[4], pv[4], sj = 0.f;
+        if (k < nch) {
+            const uint8_t *buf = smem + (k % kQ8Ring) * kQ8CodeB;
+            const uint8_t *rbuf = smem + kQ8RopeOff + (k % kQ8RRing) * kQ8RSlot;
+            const int base = r0 + k * kQ8Ch;
+            v4i bv[8];
+            v8bf rv[2];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const int row = 2 * (w * 8 + k) + (l >> 5);
-        code_off[k] = row * 512 + 16 * ((l & 31) ^ q8_swz(row));
-    }
+            for (int kb = 0; kb < 8; ++kb) bv[kb] = *(const v4i *)(buf + sc_base[kb & 1] + 128 * (kb >> 1));
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int row = 8 * (w * 2 + k) + (l >> 3);
-        rope_off[k] = row * 128 + 16 * ((l & 7) ^ (row & 7));
-    }
-    auto issue = [&](int c) {
-        const uint32_t buf = sbase + (uint32_t)((c % kQ8Ring) * kQ8ChunkB);
-        const int rb0 = r0 + c * kQ8Ch;
-        if (rb0 + kQ8Ch <= r1) {
-            const int8_t *gc = gcodes + (size_t)rb0 * 512;
-            const uint8_t *gr = (const uint8_t *)(grope + (size_t)rb0 * 64);
+            for (int kb = 0; kb < 2; ++kb) rv[kb] = *(const v8bf *)(rbuf + rp_off[kb]);
+            sj = ((const float *)(rbuf + kQ8RopeB))[rowl];
+            v4i ih = {0, 0, 0, 0}, il = {0, 0, 0, 0};
+            v4f fr = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int k = 0; k < 8; ++k) dma_b128(gc + code_off[k], buf + (uint32_t)((w * 8 + k) * 1024));
+            for (int kb = 0; kb < 8; ++kb) {
+                ih = mfma_i8(qh[kb], bv[kb], ih);
+                il = mfma_i8(ql[kb], bv[kb], il);
+            }
 #pragma unroll
-            for (int k = 0; k < 2; ++k) dma_b128(gr + rope_off[k], buf + (uint32_t)(kQ8CodeB + (w * 2 + k) * 1024));
+            for (int kb = 0; kb < 2; ++kb) {
+                fr = mfma_bf16(qrh[kb], rv[kb], fr);
+                fr = mfma_bf16(qrl[kb], rv[kb], fr);
+            }
+            const bool valid = base + rowl < r1;
+            bool over = false;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                // 254 ih + il is exact in int32 (|ih|, |il| <= 512 * 127 * 127, so |254 ih + il|
+                // <= 2.106e9 < 2^31); qsd carries the 1/254
+                const float dot = (float)(ih[i] * 254 + il[i]);
+                const float sv = fmaf(qsd[i] * sj, dot, fr[i]);
+                sc[i] = valid ? sv : -INFINITY;
+                // weights against the current reference max; a row above it by more than
+                // ln kQ8Pmax (every valid row of the first chunk, where it is -inf) sends the
+                // block through the exchange below
+                over |= sc[i] > m_run[i] + kQ8LnPmax;
+                pv[i] = __expf(sc[i] - m_run[i]);
+            }
+            put_q8_weights(wqc, pv, sj * wscale, g, rowl);
+            const bool wover = __any(over);
+            if (l == 0) fl_out[w] = wover ? 1 : 0;
         } else {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int row = code_off[k] >> 9;
-                const int gro = min(rb0 + row, r1 - 1);
-                dma_b128(gcodes + (size_t)gro * 512 + (code_off[k] & 511), buf + (uint32_t)((w * 8 + k) * 1024));
-            }
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                const int row = rope_off[k] >> 7;
-                const int gro = min(rb0 + row, r1 - 1);
-                dma_b128((const uint8_t *)(grope + (size_t)gro * 64) + (rope_off[k] & 127),
-                         buf + (uint32_t)(kQ8CodeB + (w * 2 + k) * 1024));
-            }
+            for (int i = 0; i < 4; ++i) sc[i] = pv[i] = 0.f;
+            if (l == 0) fl_out[w] = 0;  // the mix waves' last step: nothing to exchange
         }
-    };
-    // this wave's DMA instructions per chunk: 10; at chunk c's wait, chunk c+1 (issued at
-    // chunk c-1) may still be in flight
-    auto wait_chunk = [&](int later) {
-        if (later >= 1) wait_vmcnt<10>();
-        else wait_vmcnt<0>();
-    };
-
-    // ---- per-lane LDS offsets within a ring slot
-    const int rowl = 16 * w + n;  // score row of this lane
-    // slot (4 kb + g) ^ s with s < 8: kb and kb + 2 differ by 8 slots, so two bases serve all kb
-    int sc_base[2], rp_off[2], tr_off[8];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) sc_base[kb] = rowl * 512 + 16 * ((4 * kb + g) ^ q8_swz(rowl));
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) rp_off[kb] = kQ8CodeB + rowl * 128 + 16 * ((4 * kb + g) ^ (rowl & 7));
-    // rows 16g + (n >> 1) and 16g + 8 + (n >> 1) share the swizzle: the second half is + 4096
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        const int row = 16 * g + (n >> 1);
-        tr_off[t] = row * 512 + 16 * ((8 * w + t) ^ q8_swz(row)) + 8 * (n & 1);
-    }
-    const int wq_off = n * kQ8Ws + 16 * g;
-
-    auto chunk = [&](auto slot_tag, int c) {
-        constexpr int slot = decltype(slot_tag)::value;
-        const uint8_t *buf = smem + slot * kQ8ChunkB;
-        // chunk c landed (this wave's part; all waves' after the barrier), and every wave is
-        // past chunk c-1: its ring slot takes chunk c+2. The chunk maxima and quantised
-        // weights alternate between two buffers, so no barrier is needed at the chunk's end.
-        wait_chunk(min(1, nch - 1 - c));
-        lds_barrier();
-        if (c + 2 < nch) issue(c + 2);
-        const int base = r0 + c * kQ8Ch;
-        float *ml = mloc + 64 * (c & 1);
-        int8_t *wqc = wq + (c & 1) * kQ8WqB;
-
-        // this chunk's LDS operands: the score rows of this lane, then the transposed codes
-        // of the mix (independent of the weights, so their latency hides behind the scores)
-        v4i bv[8];
-        v8bf rv[2];
-#pragma unroll
-        for (int kb = 0; kb < 8; ++kb) bv[kb] = *(const v4i *)(buf + sc_base[kb & 1] + 128 * (kb >> 1));
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) rv[kb] = *(const v8bf *)(buf + rp_off[kb]);
-        v4i bt[8];
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const v2i b0 = lds_read_tr8(buf + tr_off[t]);
-            const v2i b1 = lds_read_tr8(buf + tr_off[t] + 4096);
-            bt[t] = v4i{b0.x, b0.y, b1.x, b1.y};
-        }
-        v4i ih = {0, 0, 0, 0}, il = {0, 0, 0, 0};
-        v4f fr = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kb = 0; kb < 8; ++kb) {
-            ih = mfma_i8(qh[kb], bv[kb], ih);
-            il = mfma_i8(ql[kb], bv[kb], il);
-        }
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            fr = mfma_bf16(qrh[kb], rv[kb], fr);
-            fr = mfma_bf16(qrl[kb], rv[kb], fr);
-        }
-        const float sj = sclv[c * kQ8Ch + rowl];
-        const bool valid = base + rowl < r1;
-        const float swj = sj * wscale;
-        float sc[4], pv[4];
-        bool over = false;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            // 254 ih + il is exact in int32 (|ih|, |il| <= 512 * 127 * 127, so |254 ih + il|
-            // <= 2.106e9 < 2^31); qsd carries the 1/254
-            const float dot = (float)(ih[i] * 254 + il[i]);
-            const float sv = fmaf(qsd[i] * sj, dot, fr[i]);
-            sc[i] = valid ? sv : -INFINITY;
-            // weights against the current reference max; a row above it by more than
-            // ln kQ8Pmax (every valid row of the first chunk, where it is -inf) sends the block
-            // through the exchange below
-            over |= sc[i] > m_run[i] + kQ8LnPmax;
-            pv[i] = __expf(sc[i] - m_run[i]);
-        }
-        auto put_weights = [&]() __attribute__((always_inline)) {
-            int qhv[4], qlv[4], q2v[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float v = pv[i] * swj;
-                const float hi = fminf(rintf(v), 127.f);
-                // v - hi is exact (|v - hi| <= 1/2): lo and lo2 span the int8 range
-                const float r1 = (v - hi) * 254.0f;
-                const float lo = rintf(r1);
-                qhv[i] = (int)hi;
-                qlv[i] = (int)lo;
-                q2v[i] = (int)rintf((r1 - lo) * 254.0f);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                wqc[(4 * g + i) * kQ8Ws + rowl] = (int8_t)qhv[i];
-                wqc[16 * kQ8Ws + (4 * g + i) * kQ8Ws + rowl] = (int8_t)qlv[i];
-                wqc[32 * kQ8Ws + (4 * g + i) * kQ8Ws + rowl] = (int8_t)q2v[i];
-            }
-        };
-        put_weights();
-        const bool wover = __any(over);
-        if (l == 0) oflag[w] = wover ? 1 : 0;
-        lds_barrier();
-        // the flags and this lane's weights in one LDS round trip; the weights are read again
-        // after the rare exchange below
-        const v4i fl = *(const v4i *)oflag;
-        v4i wh = *(const v4i *)(wqc + wq_off);
-        v4i wl = *(const v4i *)(wqc + 16 * kQ8Ws + wq_off);
-        v4i wl2 = *(const v4i *)(wqc + 32 * kQ8Ws + wq_off);
+        lds_barrier();  // A
+        const v4i fl = *(const v4i *)fl_out;
         if ((fl.x | fl.y | fl.z | fl.w) != 0) {
-            // Some row exceeds the reference max: exchange the four waves' chunk maxima, move
-            // the reference max of the heads concerned, rescale their accumulators and quantise
-            // the chunk's weights again. The first finite maximum of a head needs no rescale
-            // (nothing is accumulated before it).
+            // Some row of chunk k exceeds the reference max: exchange the chunk maxima, move the
+            // reference max of the heads concerned, quantise the chunk's weights again and
+            // publish alpha for the mix waves (they rescale before adding chunk k). The first
+            // finite maximum of a head needs no rescale (nothing is accumulated before it).
             float lm[4] = {sc[0], sc[1], sc[2], sc[3]};
             row16_max4(lm[0], lm[1], lm[2], lm[3]);
             if (n == 0) *(v4f *)(ml + w * 16 + 4 * g) = v4f{lm[0], lm[1], lm[2], lm[3]};
-            lds_barrier();
+            lds_barrier();  // B
             const v4f mw0 = *(const v4f *)(ml + 4 * g), mw1 = *(const v4f *)(ml + 16 + 4 * g);
             const v4f mw2 = *(const v4f *)(ml + 32 + 4 * g), mw3 = *(const v4f *)(ml + 48 + 4 * g);
             float alpha[4];
-            bool moved = false;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float cm = fmaxf(fmaxf(mw0[i], mw1[i]), fmaxf(mw2[i], mw3[i]));
@@ -1584,115 +1542,26 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
                 const bool rs = mv && m_run[i] != -INFINITY;
                 const float mnew = mv ? cm : m_run[i];
                 alpha[i] = rs ? __expf(m_run[i] - mnew) : 1.0f;
-                moved |= rs;
                 m_run[i] = mnew;
                 pv[i] = __expf(sc[i] - mnew);
                 l_lane[i] *= alpha[i];
             }
-            put_weights();
-            if (__any(moved)) {
-                // (254^2 hi + 254 lo + lo2) * alpha, level by level in double (the products are
-                // exact), each level's rounding remainder carried into the next
-#pragma unroll
-                for (int t = 0; t < 8; ++t)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        if (alpha[i] != 1.0f) {
-                            const double al = (double)alpha[i];
-                            const double h = (double)ahi[t][i] * al, hr = rint(h);
-                            const double o = (h - hr) * 254.0 + (double)alo[t][i] * al, orr = rint(o);
-                            const double o2 = (o - orr) * 254.0 + (double)alo2[t][i] * al;
-                            ahi[t][i] = (int)hr;
-                            alo[t][i] = (int)orr;
-                            alo2[t][i] = (int)rint(o2);
-                        }
-            }
-            lds_barrier();
-            wh = *(const v4i *)(wqc + wq_off);
-            wl = *(const v4i *)(wqc + 16 * kQ8Ws + wq_off);
-            wl2 = *(const v4i *)(wqc + 32 * kQ8Ws + wq_off);
+            put_q8_weights(wqc, pv, sj * wscale, g, rowl);
+            if (w == 0 && n == 0) *(v4f *)(abuf + 16 * par + 4 * g) = v4f{alpha[0], alpha[1], alpha[2], alpha[3]};
+            lds_barrier();  // C
         }
+        if (k < nch)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) l_lane[i] += pv[i];
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            ahi[t] = mfma_i8(wh, bt[t], ahi[t]);
-            alo[t] = mfma_i8(wl, bt[t], alo[t]);
-            alo2[t] = mfma_i8(wl2, bt[t], alo2[t]);
-        }
-    };
-    using S0 = std::integral_constant<int, 0>;
-    using S1 = std::integral_constant<int, 1>;
-    using S2 = std::integral_constant<int, 2>;
-
-    {
-        const uint32_t sdst = sbase + (uint32_t)kQ8SclOff;
-        for (int q = w; q * 64 < r1 - r0; q += 4)
-            dma_b32(gscl + min(r0 + 64 * q + l, r1 - 1), sdst + (uint32_t)(256 * q));
+            for (int i = 0; i < 4; ++i) l_lane[i] += pv[i];
     }
-    issue(0);
-    if (nch > 1) issue(1);
-    // query operands, scales and chunk 0 have landed once at most chunk 1 is in flight
-    wait_chunk(min(1, nch - 1));
-    lds_barrier();
-#pragma unroll
-    for (int kb = 0; kb < 8; ++kb) {
-        const int o = n * 512 + 16 * ((4 * kb + g) ^ n);
-        qh[kb] = *(const v4i *)(sq + o);
-        ql[kb] = *(const v4i *)(sq + 8192 + o);
-    }
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-        const int o = 16384 + n * 128 + 16 * ((4 * kb + g) ^ (n & 7));
-        qrh[kb] = *(const v8bf *)(sq + o);
-        qrl[kb] = *(const v8bf *)(sq + 2048 + o);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) qsd[i] = ((const float *)(sq + 20480))[4 * g + i] * (a.smscale / 254.0f);
-    // the query operands are only MFMA sources, which read AGPRs as well: keeping them there
-    // leaves the VGPRs to the chunk loop
-#pragma unroll
-    for (int kb = 0; kb < 8; ++kb) asm volatile("" : "+a"(qh[kb]), "+a"(ql[kb]));
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) asm volatile("" : "+a"(qrh[kb]), "+a"(qrl[kb]));
-    // largest row scale of the split: the common bound of the quantised weights
-    float smax;
-    {
-        float m = 0.f;
-        for (int r = tid; r < r1 - r0; r += 256) m = fmaxf(m, sclv[r]);
-        m = wave_max(m);
-        if (l == 0) smx[w] = m;
-        lds_barrier();
-        smax = fmaxf(fmaxf(smx[0], smx[1]), fmaxf(smx[2], smx[3]));
-    }
-    // p_j <= kQ8Pmax relative to the reference max (see the lazy max below)
-    wscale = smax > 0.f ? 127.0f / (kQ8Pmax * smax) : 0.f;
-    wfac = kQ8Pmax * smax * (1.0f / (127.0f * 254.0f * 254.0f));
-    int c = 0;
-    for (; c + 3 <= nch; c += 3) {
-        chunk(S0{}, c);
-        chunk(S1{}, c + 1);
-        chunk(S2{}, c + 2);
-    }
-    if (c < nch) chunk(S0{}, c);
-    if (c + 1 < nch) chunk(S1{}, c + 1);
-
 #pragma unroll
     for (int i = 0; i < 4; ++i) l_lane[i] = row16_sum(l_lane[i]);
     if (n == 0)
 #pragma unroll
         for (int i = 0; i < 4; ++i) lsum[w * 16 + 4 * g + i] = l_lane[i];
-    lds_barrier();
-    float *P = a.part + (size_t)blockIdx.x * 16 * 514;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        const int r = 128 * w + 16 * t + n;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            P[(4 * g + i) * 512 + r] =
-                wfac * fmaf((float)ahi[t][i], 64516.0f, fmaf((float)alo[t][i], 254.0f, (float)alo2[t][i]));
-    }
+    lds_barrier();  // end
     if (w == 0 && n == 0) {
+        float *P = a.part + (size_t)sid * 16 * 514;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int hh = 4 * g + i;
@@ -1700,6 +1569,176 @@ __global__ __launch_bounds__(256) void k_attn_q8_mfma(AttnArgs a) {
             P[8192 + 16 + hh] = (lsum[hh] + lsum[16 + hh]) + (lsum[32 + hh] + lsum[48 + hh]);
         }
     }
+}
+
+__device__ __forceinline__ void q8_mix_role(const AttnArgs &a, uint8_t *smem, int mw, int b, int r0, int r1, int nch,
+                                            int sid) {
+    const int8_t *wq = (const int8_t *)(smem + kQ8WqOff);
+    const int *oflag = (const int *)(smem + kQ8FlagOff);
+    const float *abuf = (const float *)(smem + kQ8AlOff);
+    const float *smx = (const float *)(smem + kQ8SmOff);
+    const uint32_t sbase = lds_addr(smem);
+    const int l = threadIdx.x & 63, n = l & 15, g = l >> 4;
+    const int8_t *gcodes = (const int8_t *)a.t.s[b].a;
+    const float *gscl = (const float *)a.t.s[b].b;
+    const uint16_t *grope = (const uint16_t *)a.t.s[b].c;
+    // DMA plan. Codes: mix wave mw copies row pairs 8mw .. 8mw+7 of a chunk; lane l of
+    // instruction k takes row 2(8mw + k) + (l >> 5), physical slot l & 31 (logical slot
+    // (l & 31) ^ swz). RoPE keys: instruction k of wave mw covers rows 8(2mw + k) .. +7, lane l
+    // row 8(2mw + k) + (l >> 3), physical slot l & 7 (logical (l & 7) ^ (row & 7)). Scales: wave
+    // 0, lane l row l. Rows past the split end (last chunk only) re-read the split's last row
+    // (in bounds); their weights are 0.
+    int code_off[8], rope_row[2], rope_el[2];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int row = 2 * (mw * 8 + k) + (l >> 5);
+        code_off[k] = row * 512 + 16 * ((l & 31) ^ q8_swz(row));
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int row = 8 * (2 * mw + k) + (l >> 3);
+        rope_row[k] = row;
+        rope_el[k] = 8 * ((l & 7) ^ (row & 7));
+    }
+    const int nrope = mw == 0 ? 3 : 2;  // DMA instructions per chunk for keys + scales
+    auto issue_codes = [&](int c) __attribute__((always_inline)) {
+        const uint32_t buf = sbase + (uint32_t)((c % kQ8Ring) * kQ8CodeB);
+        const int rb0 = r0 + c * kQ8Ch;
+        if (rb0 + kQ8Ch <= r1) {
+            const int8_t *gc = gcodes + (size_t)rb0 * 512;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) dma_b128(gc + code_off[k], buf + (uint32_t)((mw * 8 + k) * 1024));
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int row = code_off[k] >> 9;
+                const int gro = min(rb0 + row, r1 - 1);
+                dma_b128(gcodes + (size_t)gro * 512 + (code_off[k] & 511), buf + (uint32_t)((mw * 8 + k) * 1024));
+            }
+        }
+    };
+    auto issue_rope = [&](int c) __attribute__((always_inline)) {
+        const uint32_t buf = sbase + (uint32_t)(kQ8RopeOff + (c % kQ8RRing) * kQ8RSlot);
+        const int rb0 = r0 + c * kQ8Ch;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int gro = min(rb0 + rope_row[k], r1 - 1);
+            dma_b128(grope + (size_t)gro * 64 + rope_el[k], buf + (uint32_t)((2 * mw + k) * 1024));
+        }
+        if (mw == 0) dma_b32(gscl + min(rb0 + l, r1 - 1), buf + (uint32_t)kQ8RopeB);
+    };
+    // transposed reads: rows 16g + (n >> 1) and 16g + 8 + (n >> 1) share the swizzle (+4096)
+    int tr_off[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const int row = 16 * g + (n >> 1);
+        tr_off[t] = row * 512 + 16 * ((8 * mw + t) ^ q8_swz(row)) + 8 * (n & 1);
+    }
+    const int wq_off = n * kQ8Ws + (((g ^ (n >> 1)) & 3) << 4);  // q8_wpos(n, 16 g)
+    v4i ahi[8], alo[8], alo2[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        ahi[t] = v4i{0, 0, 0, 0};
+        alo[t] = v4i{0, 0, 0, 0};
+        alo2[t] = v4i{0, 0, 0, 0};
+    }
+    // prologue: codes of chunks 0 .. 2 and keys of chunks 0, 1 in flight, chunk 0 first; the
+    // issue order codes(c+1) before keys(c) keeps the per-step wait count below uniform
+    lds_barrier();  // P0
+    issue_codes(0);
+    issue_rope(0);
+    if (nch > 1) issue_codes(1);
+    if (nch > 2) issue_codes(2);
+    if (nch > 1) issue_rope(1);
+    wait_vm(nch > 1 ? (nch > 2 ? 16 : 8) + nrope : 0);
+    lds_barrier();  // P
+    const float smax = fmaxf(fmaxf(smx[0], smx[1]), fmaxf(smx[2], smx[3]));
+    bool pend = false;  // a reference max moved in the previous step: rescale before mixing
+    v4i bt[8];          // chunk k-1's codes, transposed (read in step k-1)
+    for (int k = 0; k <= nch; ++k) {
+        const int par = k & 1;
+        // codes of chunk k+3 into the slot of chunk k-1 and keys of chunk k+2 into the slot of
+        // chunk k-1: every wave finished reading both before the previous barrier
+        if (k + 3 < nch) issue_codes(k + 3);
+        if (k + 2 < nch) issue_rope(k + 2);
+        if (k >= 1) {
+            if (pend) {
+                // (254^2 hi + 254 lo + lo2) * alpha, level by level in double (the products are
+                // exact), each level's rounding remainder carried into the next
+                const v4f al4 = *(const v4f *)(abuf + 16 * (par ^ 1) + 4 * g);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (al4[i] == 1.0f) continue;
+                    const double al = (double)al4[i];
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        const double h = (double)ahi[t][i] * al, hr = rint(h);
+                        const double o = (h - hr) * 254.0 + (double)alo[t][i] * al, orr = rint(o);
+                        const double o2 = (o - orr) * 254.0 + (double)alo2[t][i] * al;
+                        ahi[t][i] = (int)hr;
+                        alo[t][i] = (int)orr;
+                        alo2[t][i] = (int)rint(o2);
+                    }
+                }
+            }
+            // chunk k-1 with its weights (written by the score waves in step k-1)
+            const int8_t *wqp = wq + (par ^ 1) * kQ8WqB;
+            const v4i wh = *(const v4i *)(wqp + wq_off);
+            const v4i wl = *(const v4i *)(wqp + 16 * kQ8Ws + wq_off);
+            const v4i wl2 = *(const v4i *)(wqp + 32 * kQ8Ws + wq_off);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                ahi[t] = mfma_i8(wh, bt[t], ahi[t]);
+                alo[t] = mfma_i8(wl, bt[t], alo[t]);
+                alo2[t] = mfma_i8(wl2, bt[t], alo2[t]);
+            }
+        }
+        if (k < nch) {
+            // chunk k (being scored in this step): codes transposed for the next step's mix
+            const uint8_t *buf = smem + (k % kQ8Ring) * kQ8CodeB;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const v2i b0 = lds_read_tr8(buf + tr_off[t]);
+                const v2i b1 = lds_read_tr8(buf + tr_off[t] + 4096);
+                bt[t] = v4i{b0.x, b0.y, b1.x, b1.y};
+            }
+        }
+        // codes and keys of chunk k+1 (scored in the next step) have landed before the barrier:
+        // issued after the keys of chunk k+1 are only the codes of k+3 and the keys of k+2
+        if (k + 1 < nch) wait_vm((k + 3 < nch ? 8 : 0) + (k + 2 < nch ? nrope : 0));
+        lds_barrier();  // A
+        const v4i fl = *(const v4i *)(oflag + 4 * par);
+        pend = (fl.x | fl.y | fl.z | fl.w) != 0;
+        if (pend) {
+            lds_barrier();  // B
+            lds_barrier();  // C
+        }
+    }
+    lds_barrier();  // end
+    float *P = a.part + (size_t)sid * 16 * 514;
+    const float wfac = kQ8Pmax * smax * (1.0f / (127.0f * 254.0f * 254.0f));
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const int r = 128 * mw + 16 * t + n;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            P[(4 * g + i) * 512 + r] =
+                wfac * fmaf((float)ahi[t][i], 64516.0f, fmaf((float)alo[t][i], 254.0f, (float)alo2[t][i]));
+    }
+}
+
+__global__ __launch_bounds__(512) void k_attn_q8_mfma(AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[kQ8SmemB];
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int sid = blockIdx.x;
+    const int b = find_seq(a.t, sid);
+    const SeqDesc &s = a.t.s[b];
+    const int split = sid - s.split0;
+    const int r0 = split * s.rps;
+    const int r1 = split == s.nsplit - 1 ? s.len : r0 + s.rps;  // last split takes the rest
+    const int nch = (r1 - r0 + kQ8Ch - 1) / kQ8Ch;
+    if (w >= 4) q8_mix_role(a, smem, w - 4, b, r0, r1, nch, sid);
+    else q8_score_role(a, smem, w, b, r0, r1, nch, sid);
 }
 
 hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t, const Dims &d,
@@ -1720,7 +1759,7 @@ hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t
     a.lmax = lmax;
     a.smscale = 1.0f / sqrtf((float)d.QD);
     if (kind == kAttnQ8Mfma) {
-        hipLaunchKernelGGL(k_attn_q8_mfma, dim3(total_splits), dim3(256), 0, st, a);
+        hipLaunchKernelGGL(k_attn_q8_mfma, dim3(total_splits), dim3(512), 0, st, a);
     } else if (kind == kAttnF32Mfma) {
         hipLaunchKernelGGL(k_attn_f32_mfma, dim3(total_splits), dim3(256), 0, st, a);
     } else {

@@ -24,10 +24,10 @@ struct Dims {
     int H, NH, DN, DR, DV, R, QD, QO, KVO, KVB, HO;
 };
 
-// One sequence of a batched call. a/b/c are the device arrays of its history
-// (see Fmt), len the number of rows attended (position + 1), pos the row appended
-// by this step. split0/nsplit locate its split-K partials; each split covers rps rows
-// except the last, which takes the remainder.
+// One sequence of a batched call. a/b/c are the device arrays of its history (see Fmt), pos
+// the row appended by this step, len the number of rows attended (pos + 1). split0/nsplit
+// locate its split-K partials; each split covers rps rows except the last, which takes the
+// remainder.
 struct SeqDesc {
     void *a;
     void *b;

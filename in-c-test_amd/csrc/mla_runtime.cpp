@@ -641,6 +641,12 @@ long split_rows(int kind, long len, long total_rows, int ncu) {
     return r;
 }
 
+// Number of splits of a sequence whose attention reads `rows` (>= 1) rows.
+long plan_nsplit(int kind, long rows, long total_rows, int ncu) {
+    if (kind == kAttnGeneric) return 1;
+    return std::max(1L, rows / split_rows(kind, rows, total_rows, ncu));
+}
+
 // solo: every sequence gets the plan it would get alone in the launch, so its result does
 // not depend on the other members (block decode).
 // part_cap > 0: w.part is a caller-provided buffer of part_cap bytes for the split partials and
@@ -684,10 +690,9 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
     } else {
         for (int i = 0; i < B; ++i) {
             SeqDesc &s = t.s[i];
-            const long r = split_rows(kind, s.len, solo ? s.len : total_rows, c.ncu);
-            s.rps = (int)r;
             s.split0 = total_splits;
-            s.nsplit = std::max(1, (int)(s.len / r));
+            s.nsplit = (int)plan_nsplit(kind, s.len, solo ? s.len : total_rows, c.ncu);
+            s.rps = (int)split_rows(kind, s.len, solo ? s.len : total_rows, c.ncu);
             total_splits += s.nsplit;
             rps = std::max(rps, s.rps);
         }
@@ -959,8 +964,8 @@ int decode_block(float *out, const float *x, int count, int start, const KvlMlaC
         int n = 0;
         long splits = 0;
         while (t0 + n < count && n < kMaxBatch) {
-            const long len = (long)start + t0 + n + 1;
-            const long ns = kind == kAttnGeneric ? 1 : std::max(1L, len / split_rows(kind, len, len, c.ncu));
+            const long rows = (long)start + t0 + n + 1;
+            const long ns = plan_nsplit(kind, rows, rows, c.ncu);
             if (n > 0 && splits + ns > 2048) break;
             splits += ns;
             ++n;
