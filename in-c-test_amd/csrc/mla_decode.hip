@@ -1793,7 +1793,6 @@ bool combine_writes_hos(int fmt, const Dims &d) { return fmt != kFmtExp && d.R =
 // mix = sum_s acc_s e^(m_s - m*) / denom; then (compressed formats)
 // ho[d] = sum_r kv_b[h*(DN+DV)+DN+d, r] * mix[r] (src/mla_compressed_q8_state.c:239-247).
 // Split weights are computed once into LDS; the mix loop issues independent loads.
-constexpr int kMaxSplits = 2048;
 
 __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
     __shared__ float mx[kMaxR];

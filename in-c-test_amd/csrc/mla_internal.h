@@ -9,6 +9,9 @@
 
 namespace kvl {
 
+// Split-K partials one sequence may have (the combine kernels stage one weight per split).
+constexpr int kMaxSplits = 2048;
+
 // Sequences handled by one launch group. Per-sequence descriptors travel as kernel
 // arguments (SeqTable, 64 x 48 B), so no per-call descriptor upload is needed.
 constexpr int kMaxBatch = 64;

@@ -816,19 +816,21 @@ __global__ __launch_bounds__(256) void k_gen_epi(GenEpiArgs a) {
 }
 
 // Causal attention, one block per (query t, head h), any dims; scores in global scratch.
+// Queries t0 .. t0 + gridDim.x - 1 (one tile of the sequence: the score scratch holds one row
+// of S scores per (query of the tile, head), so its size stays linear in S).
 struct GenAttnArgs {
     const float *qf, *kv, *krope;
     float *heads, *scr;
-    int S, NH, DN, DR, DV;
+    int S, NH, DN, DR, DV, t0;
     float smscale;
 };
 
 __global__ __launch_bounds__(256) void k_gen_attn(GenAttnArgs a) {
     __shared__ float red[256];
-    const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const int t = a.t0 + blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
     const int QD = a.DN + a.DR, KH = a.DN + a.DV, L = t + 1;
     const float *q = a.qf + ((size_t)t * a.NH + h) * QD;
-    float *sc = a.scr + ((size_t)t * a.NH + h) * a.S;
+    float *sc = a.scr + ((size_t)blockIdx.x * a.NH + h) * a.S;
     for (int j = tid; j < L; j += 256) {
         const float *kj = a.kv + (size_t)j * a.NH * KH + (size_t)h * KH;
         const float *rj = a.krope + (size_t)j * a.DR;
@@ -903,6 +905,14 @@ bool prefill_mfma_shape(const Dims &d) {
 
 bool prefill_kva_exact(const Dims &d) { return prefill_mfma_shape(d) && gemv_ksplit_ok(d.H, d.H); }
 
+// Queries per launch of the generic route's attention: the score scratch (queries x NH x S
+// fp32) stays within 64 MiB, or one query's NH x S when that alone is larger.
+static int gen_query_tile(const Dims &d, int S) {
+    const size_t per_query = (size_t)d.NH * (size_t)S;
+    const size_t cap = (size_t)16 << 20;  // floats
+    return (int)std::max<size_t>(1, std::min<size_t>((size_t)S, cap / per_query));
+}
+
 size_t prefill_bytes(const Dims &d, int S) {
     const size_t Sp = (size_t)(S + 127) / 128 * 128;
     size_t b = 0;
@@ -927,7 +937,7 @@ size_t prefill_bytes(const Dims &d, int S) {
         add(4 * (size_t)S * d.NH * d.QD);
         add(4 * (size_t)S * d.KVB);
         add(4 * (size_t)S * d.HO);
-        add(4 * (size_t)S * d.NH * S);
+        add(4 * (size_t)gen_query_tile(d, S) * d.NH * S);
     }
     return b;
 }
@@ -1006,7 +1016,8 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
     float *qf = (float *)take(4 * (size_t)S * d.NH * d.QD);
     float *kv = (float *)take(4 * (size_t)S * d.KVB);
     float *heads = (float *)take(4 * (size_t)S * d.HO);
-    float *scr = (float *)take(4 * (size_t)S * d.NH * S);
+    const int tq = gen_query_tile(d, S);
+    float *scr = (float *)take(4 * (size_t)tq * d.NH * S);
     if ((e = launch_gemv(st, y, ldy, x, d.H, S, wq, d.QO, wkva, d.KVO, d.H, false)) != hipSuccess) return e;
     KvaEpiArgs ea{y, wnorm, cs, latf, nullptr, nullptr, krope, nullptr, ldy, d.QO, d.R, d.DR, eps};
     hipLaunchKernelGGL(k_kva_epi, dim3(S), dim3(256), 0, st, ea);
@@ -1014,9 +1025,11 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
     hipLaunchKernelGGL(k_gen_epi, dim3(S), dim3(256), 0, st, ga);
     if ((e = launch_gemv(st, kv, d.KVB, latf, d.R, S, wkvb, d.KVB, nullptr, 0, d.R, false)) != hipSuccess)
         return e;
-    GenAttnArgs aa{qf, kv, krope, heads, scr, S, d.NH, d.DN, d.DR, d.DV, smscale};
-    hipLaunchKernelGGL(k_gen_attn, dim3(S, d.NH), dim3(256), 0, st, aa);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    for (int t0 = 0; t0 < S; t0 += tq) {
+        GenAttnArgs aa{qf, kv, krope, heads, scr, S, d.NH, d.DN, d.DR, d.DV, t0, smscale};
+        hipLaunchKernelGGL(k_gen_attn, dim3(std::min(tq, S - t0), d.NH), dim3(256), 0, st, aa);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
     return launch_gemv(st, out, d.H, heads, d.HO, S, wo, d.H, nullptr, 0, d.HO, false);
 }
 

@@ -79,10 +79,13 @@ struct DevBuf {
     size_t bytes = 0;
 };
 
+// hipFree of library-owned device memory (see Ctx::free_gen).
+hipError_t dev_free(void *p);
+
 int dev_reserve(DevBuf &b, size_t bytes) {
     if (bytes <= b.bytes) return 0;
     if (b.p) {
-        hipError_t e = hipFree(b.p);
+        hipError_t e = dev_free(b.p);
         b.p = nullptr;
         b.bytes = 0;
         if (e != hipSuccess) {
@@ -159,6 +162,9 @@ struct Ctx {
     DevBuf work, part, scores, prefill, fill, fillx, layer;
     PinBuf pin_in, pin_out;
     bool capturing = false;
+    // bumped by every release of library-owned device memory: a graph captured before a bump
+    // may hold pointers to freed memory (kvl_mla_graph_launch refuses it)
+    uint64_t free_gen = 0;
     // per-stage event timing of decode steps (kvl_mla_timing_*)
     bool timing = false;
     bool timing_graph = false;  // also record into a graph being captured (event-record nodes)
@@ -171,6 +177,11 @@ constexpr int kStages = 6;  // gemv_in, append, qprep, attention, combine, gemv_
 Ctx &ctx() {
     static Ctx *c = new Ctx();  // never destroyed: device memory is released by the driver
     return *c;
+}
+
+hipError_t dev_free(void *p) {
+    ++ctx().free_gen;
+    return hipFree(p);
 }
 
 int ensure_ready() {
@@ -305,13 +316,13 @@ int dev_weight(const uint16_t *host, size_t elems, const uint16_t **out) {
     if (it != c.weights.end()) {
         e = it->second;
         if (e.bytes != bytes) {
-            HIP_TRY(hipFree(e.dev));
+            HIP_TRY(dev_free(e.dev));
             e.dev = nullptr;
         }
     }
     if (!e.dev) HIP_TRY(hipMalloc(&e.dev, bytes));
     if (e.dev16 && e.bytes != bytes) {
-        HIP_TRY(hipFree(e.dev16));
+        HIP_TRY(dev_free(e.dev16));
         e.dev16 = nullptr;
     }
     e.bytes = bytes;
@@ -401,7 +412,7 @@ int rope_table(float theta, int DR, int need_pos, const float2 **out) {
                 h[(size_t)p * half + i] = make_float2((float)cos(ang), (float)sin(ang));
             }
         }
-        if (t.dev) HIP_TRY(hipFree(t.dev));
+        if (t.dev) HIP_TRY(dev_free(t.dev));
         t.dev = nullptr;
         t.npos = 0;
         HIP_TRY(hipMalloc((void **)&t.dev, h.size() * sizeof(float2)));
@@ -421,9 +432,9 @@ size_t row_bytes_of(int fmt, int d0, int d1, int d2) {
 }
 
 void mirror_free(Mirror &m) {
-    if (m.a) (void)hipFree(m.a);
-    if (m.b) (void)hipFree(m.b);
-    if (m.c) (void)hipFree(m.c);
+    if (m.a) (void)dev_free(m.a);
+    if (m.b) (void)dev_free(m.b);
+    if (m.c) (void)dev_free(m.c);
     m.a = m.b = m.c = nullptr;
 }
 
@@ -622,9 +633,6 @@ struct SeqIn {
     int pos;
 };
 
-// One decode step for a group of B <= kMaxBatch sequences whose mirrors are synced.
-// d_x: device input rows [B,H]; d_out: device output rows [B,H]. Rows appended on the device
-// at each pos; staged copies in w.rows.
 // Balanced split-K plan of the MFMA attention kernels: about wg_per_cu workgroups per CU in
 // total, shared among the sequences of a launch in proportion to their lengths (len of
 // total_rows); rows per split a multiple of the kernel's chunk (rounded down), at least four
@@ -638,6 +646,10 @@ long split_rows(int kind, long len, long total_rows, int ncu) {
     long r = len / (want * chunk) * chunk;
     r = std::max<long>(r, 4L * chunk);
     if (kind == kAttnQ8Mfma) r = std::min<long>(r, 1024L);
+    // at most kMaxSplits splits per sequence (the combine's per-split staging): very long
+    // histories get longer splits
+    const long rmin = (len + kMaxSplits - 1) / kMaxSplits;
+    if (r < rmin) r = (rmin + chunk - 1) / chunk * chunk;
     return r;
 }
 
@@ -647,8 +659,102 @@ long plan_nsplit(int kind, long rows, long total_rows, int ncu) {
     return std::max(1L, rows / split_rows(kind, rows, total_rows, ncu));
 }
 
-// solo: every sequence gets the plan it would get alone in the launch, so its result does
-// not depend on the other members (block decode).
+// Attention plan of a launch group: the per-sequence descriptors with their split-K layout,
+// and the device scratch it needs. solo: every sequence gets the plan it would get alone in
+// the launch, so its result does not depend on the other members (block decode).
+struct GroupPlan {
+    SeqTable t;
+    int kind = 0, rps = 0, total_splits = 0, lmax = 0;
+    size_t part_bytes = 0, scores_bytes = 0;
+};
+
+void plan_group(int fmt, const Dims &d, const SeqIn *seqs, int B, bool solo, GroupPlan &p) {
+    const int ncu = ctx().ncu;
+    const bool kimi = kimi_attn(d) && fmt != kFmtExp;
+    p.kind = !kimi ? kAttnGeneric : fmt == kFmtQ8 ? kAttnQ8Mfma : kAttnF32Mfma;
+    SeqTable &t = p.t;
+    memset(&t, 0, sizeof t);
+    t.n = B;
+    long total_rows = 0;
+    p.lmax = 0;
+    for (int i = 0; i < B; ++i) {
+        SeqDesc &s = t.s[i];
+        s.a = seqs[i].m->a;
+        s.b = seqs[i].m->b;
+        s.c = seqs[i].m->c;
+        s.pos = seqs[i].pos;
+        s.len = seqs[i].pos + 1;
+        total_rows += s.len;
+        p.lmax = std::max(p.lmax, s.len);
+    }
+    p.rps = 0;
+    p.total_splits = 0;
+    if (p.kind == kAttnGeneric) {
+        for (int i = 0; i < B; ++i) {
+            t.s[i].split0 = fmt == kFmtExp ? i * d.NH : i;
+            t.s[i].nsplit = 1;
+        }
+        p.total_splits = fmt == kFmtExp ? B * d.NH : B;
+    } else {
+        for (int i = 0; i < B; ++i) {
+            SeqDesc &s = t.s[i];
+            s.split0 = p.total_splits;
+            s.nsplit = (int)plan_nsplit(p.kind, s.len, solo ? s.len : total_rows, ncu);
+            s.rps = (int)split_rows(p.kind, s.len, solo ? s.len : total_rows, ncu);
+            p.total_splits += s.nsplit;
+            p.rps = std::max(p.rps, s.rps);
+        }
+    }
+    const int G = fmt == kFmtExp ? 1 : d.NH;
+    const int DVm = fmt == kFmtExp ? d.DV : d.R;
+    p.part_bytes = (size_t)p.total_splits * G * (DVm + 2) * sizeof(float);
+    const int P = fmt == kFmtExp ? B * d.NH : B;
+    p.scores_bytes = p.kind == kAttnGeneric ? (size_t)P * G * p.lmax * sizeof(float) : 0;
+}
+
+// Everything the launch groups of a call need, acquired before any group launches, so that a
+// failure (an allocation) leaves every state unchanged: the device copies of all states, the
+// workspace of the largest group, the partials and score scratch of the most demanding group,
+// and the RoPE table up to the largest position.
+template <class S>
+int prepare_groups(int fmt, const Dims &d, float theta, S *const *states, int B, size_t rb,
+                   std::vector<Mirror *> &ms) {
+    Ctx &c = ctx();
+    ms.assign(B, nullptr);
+    int maxpos = 0;
+    for (int i = 0; i < B; ++i) {
+        if (mirror_get(states[i], view_of(states[i]), &ms[i]) != 0) return -1;
+        maxpos = std::max(maxpos, states[i]->len);
+    }
+    const float2 *cs = nullptr;
+    if (rope_table(theta, d.DR, maxpos + 1, &cs) != 0) return -1;
+    DecodeWork wk;
+    if (decode_work(d, std::min(B, kMaxBatch), (int)rb, wk) != 0) return -1;
+    size_t part = 0, scores = 0;
+    for (int g0 = 0; g0 < B; g0 += kMaxBatch) {
+        const int n = std::min(kMaxBatch, B - g0);
+        SeqIn seqs[kMaxBatch];
+        for (int i = 0; i < n; ++i) seqs[i] = {ms[g0 + i], states[g0 + i]->len};
+        GroupPlan gp;
+        plan_group(fmt, d, seqs, n, false, gp);
+        part = std::max(part, gp.part_bytes);
+        scores = std::max(scores, gp.scores_bytes);
+    }
+    float *pp = nullptr;
+    if (reserve_part(part, &pp) != 0) return -1;
+    if (c.scores.bytes < scores) {
+        if (c.capturing) {
+            set_err("score scratch growth during graph capture");
+            return -1;
+        }
+        if (dev_reserve(c.scores, scores) != 0) return -1;
+    }
+    return 0;
+}
+
+// One decode step for a group of B <= kMaxBatch sequences whose mirrors are synced.
+// d_x: device input rows [B,H]; d_out: device output rows [B,H]. Rows appended on the device
+// at each pos; staged copies in w.rows. solo: see plan_group.
 // part_cap > 0: w.part is a caller-provided buffer of part_cap bytes for the split partials and
 // nothing is allocated (the RoPE table must already cover the positions).
 int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeights &dw,
@@ -662,48 +768,11 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
     if ((part_cap ? rope_lookup(theta, d.DR, maxpos + 1, &cs) : rope_table(theta, d.DR, maxpos + 1, &cs)) != 0)
         return -1;
 
-    const bool kimi = kimi_attn(d) && fmt != kFmtExp;
-    const int kind = !kimi ? kAttnGeneric : fmt == kFmtQ8 ? kAttnQ8Mfma : kAttnF32Mfma;
-    SeqTable t;
-    memset(&t, 0, sizeof t);
-    t.n = B;
-    long total_rows = 0;
-    int lmax = 0;
-    for (int i = 0; i < B; ++i) {
-        SeqDesc &s = t.s[i];
-        s.a = seqs[i].m->a;
-        s.b = seqs[i].m->b;
-        s.c = seqs[i].m->c;
-        s.pos = seqs[i].pos;
-        s.len = seqs[i].pos + 1;
-        total_rows += s.len;
-        lmax = std::max(lmax, s.len);
-    }
-    // split-K plan (split_rows)
-    int rps = 0, total_splits = 0;
-    if (kind == kAttnGeneric) {
-        for (int i = 0; i < B; ++i) {
-            t.s[i].split0 = fmt == kFmtExp ? i * d.NH : i;
-            t.s[i].nsplit = 1;
-        }
-        total_splits = fmt == kFmtExp ? B * d.NH : B;
-    } else {
-        for (int i = 0; i < B; ++i) {
-            SeqDesc &s = t.s[i];
-            s.split0 = total_splits;
-            s.nsplit = (int)plan_nsplit(kind, s.len, solo ? s.len : total_rows, c.ncu);
-            s.rps = (int)split_rows(kind, s.len, solo ? s.len : total_rows, c.ncu);
-            total_splits += s.nsplit;
-            rps = std::max(rps, s.rps);
-        }
-        if (total_splits > 2048) {
-            set_err("split plan exceeds 2048 partials");
-            return -1;
-        }
-    }
-    const int G = fmt == kFmtExp ? 1 : d.NH;
-    const int DVm = fmt == kFmtExp ? d.DV : d.R;
-    const size_t part_bytes = (size_t)total_splits * G * (DVm + 2) * sizeof(float);
+    GroupPlan gp;
+    plan_group(fmt, d, seqs, B, solo, gp);
+    SeqTable &t = gp.t;
+    const int kind = gp.kind, rps = gp.rps, total_splits = gp.total_splits, lmax = gp.lmax;
+    const size_t part_bytes = gp.part_bytes;
     if (part_cap) {
         if (part_bytes > part_cap || kind == kAttnGeneric) {
             set_err("the split plan needs %zu bytes of partials; the fixed scratch holds %zu (%d splits)",
@@ -714,8 +783,7 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
         return -1;
     }
     if (kind == kAttnGeneric) {
-        const int P = fmt == kFmtExp ? B * d.NH : B;
-        const size_t bytes = (size_t)P * G * lmax * sizeof(float);
+        const size_t bytes = gp.scores_bytes;
         if (c.scores.bytes < bytes) {
             if (c.capturing) {
                 set_err("score scratch growth during graph capture");
@@ -853,17 +921,17 @@ int decode_host(float *out, const float *x, const int *positions, int B, const K
     if (dev_weights(w, d, dw) != 0) return -1;
     const size_t rb = fmt == kFmtExp ? row_bytes_of(fmt, d.NH, d.QD, d.DV)
                                      : row_bytes_of(fmt, d.R, d.DR, 0);
+    std::vector<Mirror *> ms;
+    if (prepare_groups(fmt, d, cfg->rope_theta, states, B, rb, ms) != 0) return -1;
+    if (pin_reserve(c.pin_in, (size_t)std::min(B, kMaxBatch) * d.H * sizeof(float)) != 0 ||
+        pin_reserve(c.pin_out, (size_t)std::min(B, kMaxBatch) * (d.H * sizeof(float) + rb)) != 0)
+        return -1;
     for (int g0 = 0; g0 < B; g0 += kMaxBatch) {
         const int n = std::min(kMaxBatch, B - g0);
         DecodeWork wk;
         if (decode_work(d, n, (int)rb, wk) != 0) return -1;
         SeqIn seqs[kMaxBatch];
-        for (int i = 0; i < n; ++i) {
-            S *s = states[g0 + i];
-            Mirror *m = nullptr;
-            if (mirror_get(s, view_of(s), &m) != 0) return -1;
-            seqs[i] = {m, s->len};
-        }
+        for (int i = 0; i < n; ++i) seqs[i] = {ms[g0 + i], states[g0 + i]->len};
         const size_t xin = (size_t)n * d.H * sizeof(float);
         const size_t outb = xin + (size_t)n * rb;
         if (pin_reserve(c.pin_in, xin) != 0 || pin_reserve(c.pin_out, outb) != 0) return -1;
@@ -958,18 +1026,9 @@ int decode_block(float *out, const float *x, int count, int start, const KvlMlaC
     const size_t rb = row_bytes_of(fmt, d.R, d.DR, 0);
     Mirror *m = nullptr;
     if (mirror_get(state, view_of(state), &m) != 0) return -1;
-    const int kind = !kimi_attn(d) ? kAttnGeneric : fmt == kFmtQ8 ? kAttnQ8Mfma : kAttnF32Mfma;
     for (int t0 = 0; t0 < count;) {
-        // members of this group: at most kMaxBatch, and their lone plans within 2048 splits
-        int n = 0;
-        long splits = 0;
-        while (t0 + n < count && n < kMaxBatch) {
-            const long rows = (long)start + t0 + n + 1;
-            const long ns = plan_nsplit(kind, rows, rows, c.ncu);
-            if (n > 0 && splits + ns > 2048) break;
-            splits += ns;
-            ++n;
-        }
+        // members of this group: at most kMaxBatch
+        const int n = std::min(kMaxBatch, count - t0);
         DecodeWork wk;
         if (decode_work(d, n, (int)rb, wk) != 0) return -1;
         SeqIn seqs[kMaxBatch];
@@ -1018,17 +1077,14 @@ int decode_device(float *d_out, const float *d_x, int B, const KvlMlaConfig *cfg
     DevWeights dw;
     if (dev_weights(w, d, dw) != 0) return -1;
     const size_t rb = row_bytes_of(fmt, d.R, d.DR, 0);
+    std::vector<Mirror *> ms;
+    if (prepare_groups(fmt, d, cfg->rope_theta, states, B, rb, ms) != 0) return -1;
     for (int g0 = 0; g0 < B; g0 += kMaxBatch) {
         const int n = std::min(kMaxBatch, B - g0);
         DecodeWork wk;
         if (decode_work(d, n, (int)rb, wk) != 0) return -1;
         SeqIn seqs[kMaxBatch];
-        for (int i = 0; i < n; ++i) {
-            S *s = states[g0 + i];
-            Mirror *m = nullptr;
-            if (mirror_get(s, view_of(s), &m) != 0) return -1;
-            seqs[i] = {m, s->len};
-        }
+        for (int i = 0; i < n; ++i) seqs[i] = {ms[g0 + i], states[g0 + i]->len};
         if (decode_group(fmt, d, cfg->rms_eps, cfg->rope_theta, dw, seqs, n, d_x + (size_t)g0 * d.H,
                          d_out + (size_t)g0 * d.H, (flags & KVL_MLA_RESIDUAL) != 0, wk) != 0)
             return -1;
@@ -1351,6 +1407,12 @@ int prefill_state(float *out, const float *x, int seq_len, const KvlMlaConfig *c
     HIP_TRY(hipStreamSynchronize(c.stream));
     return 0;
 }
+
+// A captured graph and the free generation at its capture.
+struct GraphHandle {
+    hipGraphExec_t exec;
+    uint64_t gen;
+};
 
 struct Guard {
     std::lock_guard<std::recursive_mutex> g;
@@ -1725,8 +1787,8 @@ int kvl_mla_release_weights(const KvlMlaBF16 *w) {
         if (it == c.weights.end()) continue;
         if (it->second.pins > 0) it->second.pins -= 1;
         if (it->second.pins == 0) {
-            (void)hipFree(it->second.dev);
-            if (it->second.dev16) (void)hipFree(it->second.dev16);
+            (void)dev_free(it->second.dev);
+            if (it->second.dev16) (void)dev_free(it->second.dev16);
             c.weights.erase(it);
         }
     }
@@ -1874,21 +1936,30 @@ int kvl_mla_capture_end(void **graph_exec) {
         set_err("hipGraphInstantiate: %s", hipGetErrorString(e));
         return -1;
     }
-    *graph_exec = (void *)exec;
+    *graph_exec = (void *)new GraphHandle{exec, c.free_gen};
     return 0;
 }
 
 int kvl_mla_graph_launch(void *graph_exec) {
     Guard guard;
     if (!graph_exec) return -1;
-    HIP_TRY(hipGraphLaunch((hipGraphExec_t)graph_exec, ctx().stream));
+    const GraphHandle *g = (const GraphHandle *)graph_exec;
+    if (g->gen != ctx().free_gen) {
+        set_err("library device memory was released or reallocated after this graph was captured "
+                "(workspace or RoPE table growth, state free/re-init, weight release): capture it again");
+        return -1;
+    }
+    HIP_TRY(hipGraphLaunch(g->exec, ctx().stream));
     return 0;
 }
 
 int kvl_mla_graph_destroy(void *graph_exec) {
     Guard guard;
     if (!graph_exec) return 0;
-    HIP_TRY(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
+    GraphHandle *g = (GraphHandle *)graph_exec;
+    const hipError_t e = hipGraphExecDestroy(g->exec);
+    delete g;
+    HIP_TRY(e);
     return 0;
 }
 

@@ -35,9 +35,11 @@ const char *kvl_mla_last_error(void);
 int kvl_mla_init(void);
 
 /* Uploads the five weight arrays of a layer and pins the device copies under their host
- * addresses, so later calls with the same KvlMlaBF16 skip the content check. Unpinned
- * weights are cached by address, size and a sampled content digest, and re-uploaded when
- * the digest changes. */
+ * addresses, so later calls with the same KvlMlaBF16 skip the content check; release them
+ * before freeing or reusing the host arrays. Unpinned weights are cached by address, size
+ * and a digest of 18 sampled 64-byte windows, and re-uploaded when that digest changes: an
+ * in-place edit outside the sampled windows is not seen, so callers that edit weights in
+ * place bind them or release them after the edit. */
 int kvl_mla_bind_weights(const KvlMlaConfig *cfg, const KvlMlaBF16 *w);
 int kvl_mla_release_weights(const KvlMlaBF16 *w);
 
@@ -158,7 +160,11 @@ void *kvl_mla_device_alloc(size_t bytes);
 int kvl_mla_device_free(void *p);
 int kvl_mla_copy_to_device(void *dst, const void *src, size_t bytes);
 int kvl_mla_copy_to_host(void *dst, const void *src, size_t bytes);
-/* HIP graph capture of the calls made between begin and end on kvl_mla_stream(). */
+/* HIP graph capture of the calls made between begin and end on kvl_mla_stream(). A replay
+ * repeats the captured calls exactly (positions, lengths, buffers). kvl_mla_graph_launch()
+ * returns -1 when library-owned device memory was released or reallocated after the capture
+ * (workspace or RoPE-table growth, a state freed or re-initialised, weights released), since
+ * the graph may point into it; capture again then. */
 int kvl_mla_capture_begin(void);
 int kvl_mla_capture_end(void **graph_exec);
 int kvl_mla_graph_launch(void *graph_exec);
