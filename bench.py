@@ -95,6 +95,8 @@ def main():
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain copy kernel of MIB MiB (memory-counter calibration)")
+    ap.add_argument("--no-ragged", action="store_true", help="skip the 64-sequence ragged decode leg")
+    ap.add_argument("--no-peak", action="store_true", help="skip the measured copy-bandwidth leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the MLA path here runs on a single GPU "
@@ -380,9 +382,121 @@ def main():
         fm = float(np.median(fms))
         result["prefill"]["with_q8_state_fill_ms"] = round(fm, 4)
         log(f"[bench] prefill + Q8 state fill S={S}: {fm:.3f} ms")
+        if not args.no_cpu:
+            # the reference prefill (src/mla_prefill_streaming.c:78-206, built from its sources; the
+            # oracle restatement where that build is absent) on the host cores at two lengths,
+            # extrapolated to S with T(S) = a S + b S^2 (linear projections, causal attention);
+            # the GPU prefill of the same tokens doubles as a parity check
+            import pyoracle
+            from helpers import rel_err
+            ref = pyoracle.load_reference("avx2")
+            pkind = "reference" if ref is not None else "port"
+            pfn = ref.kvl_mla_prefill_bf16 if ref is not None else pyoracle.load_oracle().orc_mla_prefill_streaming
+            samples, perr = {}, []
+            for Sc in (S // 4, S // 2):
+                xc = np.ascontiguousarray(xbf[:Sc])
+                oc = np.zeros((Sc, H), np.float32)
+                og = np.zeros((Sc, H), np.float32)
+                ts = time.perf_counter()
+                if pfn(oc.ctypes.data_as(abi.f32p), xc.ctypes.data_as(abi.f32p), Sc, C.byref(cfg),
+                       C.byref(wstructs[0])) != 0:
+                    raise RuntimeError("CPU prefill failed")
+                samples[Sc] = time.perf_counter() - ts
+                lib.check(L.kvl_mla_prefill_bf16(og.ctypes.data_as(abi.f32p), xc.ctypes.data_as(abi.f32p), Sc,
+                                                 C.byref(cfg), C.byref(wstructs[0])), "prefill parity")
+                perr.append(rel_err(og, oc))
+            (s1, t1), (s2, t2) = sorted(samples.items())
+            bq = max(0.0, (t2 * s1 - t1 * s2) / (s1 * s2 * (s2 - s1)))
+            aq = (t1 - bq * s1 * s1) / s1 if bq > 0 else t2 / s2
+            tS = aq * S + bq * S * S
+            result["prefill"]["cpu_baseline"] = {
+                "value": round(flops / tS / 1e12, 4), "unit": "TFLOP/s", "cores": omp_threads(), "kind": pkind,
+                "sample": f"S={s1} ({t1:.2f} s) and S={s2} ({t2:.2f} s) measured on the same tokens and weights; "
+                          f"S={S} extrapolated with T = aS + bS^2 ({tS:.1f} s)"}
+            result["prefill"]["parity_vs_cpu"] = {"max_rel_err": float(max(perr)), "tokens": [s1, s2],
+                                                  "tolerance": 2e-3}
+            log(f"[bench] prefill CPU baseline ({pkind}): S={s1} {t1:.2f} s, S={s2} {t2:.2f} s -> S={S} "
+                f"{tS:.1f} s; GPU vs CPU {max(perr):.2e}")
         L.kvl_mla_compressed_q8_state_free(C.byref(qs))
         L.kvl_mla_device_free(d_px)
         L.kvl_mla_device_free(d_po)
+
+    # ---- 64 ragged sequences, one decode token each (FP32 state of bf16-representable rows) ---
+    if not args.no_ragged:
+        rng = np.random.default_rng(0xC8)
+        lens = rng.integers(512, 32769, size=64)
+        RB = len(lens)
+        CSP = C.POINTER(abi.KvlMlaCompressedState)
+        rstates = []
+        for i, n in enumerate(lens):
+            st = abi.KvlMlaCompressedState()
+            lib.check(L.kvl_mla_compressed_state_init(C.byref(st), C.byref(cfg), int(n) + 1), "ragged init")
+            lib.check(L.kvl_mla_compressed_state_fill_synthetic(C.byref(st), 0, int(n), 0xC80 + i), "ragged fill")
+            rstates.append(st)
+        rarr = (CSP * RB)(*[C.pointer(s) for s in rstates])
+        xr = np.ascontiguousarray(inputs.hidden(cfg, 0xC8, RB, tag="query"))
+        d_rx = L.kvl_mla_device_alloc(xr.nbytes)
+        d_ro = L.kvl_mla_device_alloc(xr.nbytes)
+        lib.check(L.kvl_mla_copy_to_device(d_rx, xr.ctypes.data, xr.nbytes), "h2d")
+        rdec = L.kvl_mla_decode_compressed_batch_device
+        for _ in range(3):
+            lib.check(rdec(d_ro, d_rx, RB, C.byref(cfg), C.byref(wstructs[0]), rarr, lib.NO_ADVANCE), "ragged")
+        lib.check(L.kvl_mla_synchronize(), "sync")
+        reps = 10
+        r0 = L.kvl_mla_event_record()
+        for _ in range(reps):
+            lib.check(rdec(d_ro, d_rx, RB, C.byref(cfg), C.byref(wstructs[0]), rarr, lib.NO_ADVANCE), "ragged")
+        r1 = L.kvl_mla_event_record()
+        rms = L.kvl_mla_event_elapsed_ms(r0, r1) / reps
+        L.kvl_mla_event_destroy(r0)
+        L.kvl_mla_event_destroy(r1)
+        rbytes = wb + int((lens + 1).sum()) * 4 * (cfg.kv_lora_rank + cfg.qk_rope_dim)
+        rgbs = rbytes / (rms * 1e-3) / 1e9
+        result["ragged_decode"] = {
+            "sequences": RB, "rows": int(lens.sum()), "context": "uniform 512..32768 (seeded)",
+            "state": "fp32 rows (2304 B/row) of bf16-representable latents", "ms": round(rms, 4),
+            "gbs": round(rgbs, 1), "frac_hbm_peak": round(rgbs / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes": rbytes, "api": "device buffers, stream-ordered, eager launches"}
+        log(f"[bench] ragged 64 sequences ({int(lens.sum())} rows): {rms:.4f} ms, {rgbs:.1f} GB/s")
+        L.kvl_mla_device_free(d_rx)
+        L.kvl_mla_device_free(d_ro)
+        for st in rstates:
+            L.kvl_mla_compressed_state_free(C.byref(st))
+
+    # ---- measured memory peak: a plain 16-byte copy kernel over 1 GiB (read + write) -------
+    if not args.no_peak:
+        nb = 1 << 30
+        pa = L.kvl_mla_device_alloc(nb)
+        pb = L.kvl_mla_device_alloc(nb)
+        if pa and pb:
+            for _ in range(3):
+                lib.check(L.kvl_mla_copy_kernel(pb, pa, nb), "copy")
+            lib.check(L.kvl_mla_synchronize(), "sync")
+            c0 = L.kvl_mla_event_record()
+            for _ in range(5):
+                lib.check(L.kvl_mla_copy_kernel(pb, pa, nb), "copy")
+            c1 = L.kvl_mla_event_record()
+            cms = L.kvl_mla_event_elapsed_ms(c0, c1) / 5
+            peak = 2 * nb / (cms * 1e-3) / 1e9
+            for _ in range(3):
+                lib.check(L.kvl_mla_read_kernel(pa, nb), "read")
+            lib.check(L.kvl_mla_synchronize(), "sync")
+            c2 = L.kvl_mla_event_record()
+            for _ in range(5):
+                lib.check(L.kvl_mla_read_kernel(pa, nb), "read")
+            c3 = L.kvl_mla_event_record()
+            rms_ = L.kvl_mla_event_elapsed_ms(c2, c3) / 5
+            rpeak = nb / (rms_ * 1e-3) / 1e9
+            for e in (c0, c1, c2, c3):
+                L.kvl_mla_event_destroy(e)
+            result["measured_peak"] = {"read_gbs": round(rpeak, 1), "copy_gbs_read_plus_write": round(peak, 1),
+                                       "bytes": nb, "nominal_gbs": HBM_PEAK_GBS,
+                                       "attention_frac_of_measured_read": round(roofline["achieved"] / rpeak, 4)}
+            roofline["measured_read_peak"] = round(rpeak, 1)
+            log(f"[bench] measured bandwidth: streaming read {rpeak:.1f} GB/s, copy {peak:.1f} GB/s (read + write)")
+        for q in (pa, pb):
+            if q:
+                L.kvl_mla_device_free(q)
 
     if args.calibrate_copy:
         nb = args.calibrate_copy << 20

@@ -2029,6 +2029,28 @@ __global__ __launch_bounds__(256) void k_copy(v4i *dst, const v4i *src, size_t n
         dst[i] = src[i];
 }
 
+// Streaming read of n 16-byte words, four independent loads in flight per thread, folded by
+// XOR; the fold reaches memory only for one (practically never occurring) pattern, which keeps
+// every load live: a read-bandwidth probe.
+__global__ __launch_bounds__(256) void k_read(const v4i *src, size_t n, v4i *sink) {
+    const size_t stride = (size_t)gridDim.x * 256;
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    v4i acc = {0, 0, 0, 0};
+    for (; i + 3 * stride < n; i += 4 * stride) {
+        const v4i a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
+        acc ^= (a ^ b) ^ (c ^ d);
+    }
+    for (; i < n; i += stride) acc ^= src[i];
+    if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x5a17c3e1) sink[(size_t)blockIdx.x * 256 + threadIdx.x] = acc;
+}
+
+hipError_t launch_read(hipStream_t st, const void *src, size_t bytes, void *sink) {
+    const size_t n = bytes / 16;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_read, dim3(kReadBlocks), dim3(256), 0, st, (const v4i *)src, n, (v4i *)sink);
+    return hipGetLastError();
+}
+
 hipError_t launch_copy(hipStream_t st, void *dst, const void *src, size_t bytes) {
     const size_t n = bytes / 16;
     if (n == 0) return hipSuccess;

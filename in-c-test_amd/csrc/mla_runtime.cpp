@@ -159,7 +159,7 @@ struct Ctx {
     std::unordered_map<const void *, WeightEntry> weights;
     std::unordered_map<const void *, Mirror> mirrors;
     std::unordered_map<uint64_t, RopeTable> ropes;  // key: theta bits << 16 | DR
-    DevBuf work, part, scores, prefill, fill, fillx, layer;
+    DevBuf work, part, scores, prefill, fill, fillx, layer, sink;
     PinBuf pin_in, pin_out;
     bool capturing = false;
     // bumped by every release of library-owned device memory: a graph captured before a bump
@@ -2116,6 +2116,25 @@ int kvl_mla_copy_kernel(void *dst, const void *src, size_t bytes) {
     }
     if (ensure_ready() != 0) return -1;
     HIP_TRY(launch_copy(ctx().stream, dst, src, bytes));
+    return 0;
+}
+
+int kvl_mla_read_kernel(const void *src, size_t bytes) {
+    Guard guard;
+    if (!src || bytes % 16 != 0 || ((uintptr_t)src % 16) != 0) {
+        set_err("invalid arguments (16-byte aligned source, bytes %% 16 == 0)");
+        return -1;
+    }
+    if (ensure_ready() != 0) return -1;
+    Ctx &c = ctx();
+    if (c.sink.bytes < (size_t)kReadBlocks * 256 * 16) {
+        if (c.capturing) {
+            set_err("sink allocation during graph capture");
+            return -1;
+        }
+        if (dev_reserve(c.sink, (size_t)kReadBlocks * 256 * 16) != 0) return -1;
+    }
+    HIP_TRY(launch_read(c.stream, src, bytes, c.sink.p));
     return 0;
 }
 

@@ -186,6 +186,9 @@ void *kvl_mla_event_record(void);
 double kvl_mla_event_elapsed_ms(void *start, void *end);
 int kvl_mla_event_destroy(void *event);
 int kvl_mla_copy_kernel(void *dst, const void *src, size_t bytes);
+/* A streaming read of bytes (% 16 == 0) from a 16-byte aligned device buffer, enqueued on
+ * kvl_mla_stream(): the measured read-bandwidth ceiling beside the nominal HBM peak. */
+int kvl_mla_read_kernel(const void *src, size_t bytes);
 
 /* Quantiser boundary, computed on the GPU: for row i, latent [n, R] (already normalised) ->
  * int8 codes [n, R] + fp32 scale [n]; k_rope_raw [n, DR] (before rotation) -> RoPE at
