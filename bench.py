@@ -421,47 +421,55 @@ def main():
         L.kvl_mla_device_free(d_px)
         L.kvl_mla_device_free(d_po)
 
-    # ---- 64 ragged sequences, one decode token each (FP32 state of bf16-representable rows) ---
+    # ---- 64 ragged sequences, one decode token each: the BF16-latent state (1152 B/row), and
+    # the FP32 state of the same bf16-valued rows (2304 B/row) beside it -------------------------
     if not args.no_ragged:
         rng = np.random.default_rng(0xC8)
         lens = rng.integers(512, 32769, size=64)
         RB = len(lens)
-        CSP = C.POINTER(abi.KvlMlaCompressedState)
-        rstates = []
-        for i, n in enumerate(lens):
-            st = abi.KvlMlaCompressedState()
-            lib.check(L.kvl_mla_compressed_state_init(C.byref(st), C.byref(cfg), int(n) + 1), "ragged init")
-            lib.check(L.kvl_mla_compressed_state_fill_synthetic(C.byref(st), 0, int(n), 0xC80 + i), "ragged fill")
-            rstates.append(st)
-        rarr = (CSP * RB)(*[C.pointer(s) for s in rstates])
         xr = np.ascontiguousarray(inputs.hidden(cfg, 0xC8, RB, tag="query"))
         d_rx = L.kvl_mla_device_alloc(xr.nbytes)
         d_ro = L.kvl_mla_device_alloc(xr.nbytes)
         lib.check(L.kvl_mla_copy_to_device(d_rx, xr.ctypes.data, xr.nbytes), "h2d")
-        rdec = L.kvl_mla_decode_compressed_batch_device
-        for _ in range(3):
-            lib.check(rdec(d_ro, d_rx, RB, C.byref(cfg), C.byref(wstructs[0]), rarr, lib.NO_ADVANCE), "ragged")
-        lib.check(L.kvl_mla_synchronize(), "sync")
-        reps = 10
-        r0 = L.kvl_mla_event_record()
-        for _ in range(reps):
-            lib.check(rdec(d_ro, d_rx, RB, C.byref(cfg), C.byref(wstructs[0]), rarr, lib.NO_ADVANCE), "ragged")
-        r1 = L.kvl_mla_event_record()
-        rms = L.kvl_mla_event_elapsed_ms(r0, r1) / reps
-        L.kvl_mla_event_destroy(r0)
-        L.kvl_mla_event_destroy(r1)
-        rbytes = wb + int((lens + 1).sum()) * 4 * (cfg.kv_lora_rank + cfg.qk_rope_dim)
-        rgbs = rbytes / (rms * 1e-3) / 1e9
-        result["ragged_decode"] = {
-            "sequences": RB, "rows": int(lens.sum()), "context": "uniform 512..32768 (seeded)",
-            "state": "fp32 rows (2304 B/row) of bf16-representable latents", "ms": round(rms, 4),
-            "gbs": round(rgbs, 1), "frac_hbm_peak": round(rgbs / HBM_PEAK_GBS, 4),
-            "algorithmic_bytes": rbytes, "api": "device buffers, stream-ordered, eager launches"}
-        log(f"[bench] ragged 64 sequences ({int(lens.sum())} rows): {rms:.4f} ms, {rgbs:.1f} GB/s")
+        kinds = {
+            "bf16": (abi.KvlMlaCompressedBF16State, "compressed_bf16_state", 2,
+                     L.kvl_mla_decode_compressed_bf16_batch_device, "bf16 rows (1152 B/row)"),
+            "f32": (abi.KvlMlaCompressedState, "compressed_state", 4,
+                    L.kvl_mla_decode_compressed_batch_device, "fp32 rows (2304 B/row) of the same bf16 values"),
+        }
+        for kind, (T, name, eb, rdec, what) in kinds.items():
+            rstates = []
+            for i, n in enumerate(lens):
+                st = T()
+                lib.check(getattr(L, f"kvl_mla_{name}_init")(C.byref(st), C.byref(cfg), int(n) + 1), "ragged init")
+                lib.check(getattr(L, f"kvl_mla_{name}_fill_synthetic")(C.byref(st), 0, int(n), 0xC80 + i),
+                          "ragged fill")
+                rstates.append(st)
+            rarr = (C.POINTER(T) * RB)(*[C.pointer(s) for s in rstates])
+            for _ in range(3):
+                lib.check(rdec(d_ro, d_rx, RB, C.byref(cfg), C.byref(wstructs[0]), rarr, lib.NO_ADVANCE), "ragged")
+            lib.check(L.kvl_mla_synchronize(), "sync")
+            reps = 10
+            r0 = L.kvl_mla_event_record()
+            for _ in range(reps):
+                lib.check(rdec(d_ro, d_rx, RB, C.byref(cfg), C.byref(wstructs[0]), rarr, lib.NO_ADVANCE), "ragged")
+            r1 = L.kvl_mla_event_record()
+            rms = L.kvl_mla_event_elapsed_ms(r0, r1) / reps
+            L.kvl_mla_event_destroy(r0)
+            L.kvl_mla_event_destroy(r1)
+            rbytes = wb + int((lens + 1).sum()) * eb * (cfg.kv_lora_rank + cfg.qk_rope_dim)
+            rgbs = rbytes / (rms * 1e-3) / 1e9
+            entry = {
+                "sequences": RB, "rows": int(lens.sum()), "context": "uniform 512..32768 (seeded)",
+                "state": what, "ms": round(rms, 4), "gbs": round(rgbs, 1),
+                "frac_hbm_peak": round(rgbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": rbytes,
+                "api": "device buffers, stream-ordered, eager launches"}
+            result["ragged_decode" if kind == "bf16" else "ragged_decode_fp32_state"] = entry
+            log(f"[bench] ragged 64 sequences ({int(lens.sum())} rows, {kind} state): {rms:.4f} ms, {rgbs:.1f} GB/s")
+            for st in rstates:
+                getattr(L, f"kvl_mla_{name}_free")(C.byref(st))
         L.kvl_mla_device_free(d_rx)
         L.kvl_mla_device_free(d_ro)
-        for st in rstates:
-            L.kvl_mla_compressed_state_free(C.byref(st))
 
     # ---- measured memory peak: a plain 16-byte copy kernel over 1 GiB (read + write) -------
     if not args.no_peak:

@@ -664,6 +664,13 @@ __device__ __forceinline__ void append_body(const SeqTable &t, const Dims &d, co
             dst[r] = lat[r];
             ((float *)row_out)[r] = lat[r];
         }
+    } else if (a.fmt == kFmtBF16) {
+        uint16_t *dst = (uint16_t *)s.a + (size_t)pos * R;
+        for (int r = tid; r < R; r += 256) {
+            const uint16_t h = f32_to_bf16_rne(lat[r]);
+            dst[r] = h;
+            ((uint16_t *)row_out)[r] = h;
+        }
     } else {
         for (int r = tid; r < R; r += 256) a.latent[(size_t)b * R + r] = lat[r];
     }
@@ -689,6 +696,14 @@ __device__ __forceinline__ void append_body(const SeqTable &t, const Dims &d, co
             float *ro = (float *)row_out + R;
             ro[i] = d0;
             ro[half + i] = d1;
+        } else if (a.fmt == kFmtBF16) {
+            uint16_t *rp = (uint16_t *)s.b + (size_t)pos * DR;
+            const uint16_t h0 = f32_to_bf16_rne(d0), h1 = f32_to_bf16_rne(d1);
+            rp[i] = h0;
+            rp[half + i] = h1;
+            uint16_t *ro = (uint16_t *)row_out + R;
+            ro[i] = h0;
+            ro[half + i] = h1;
         } else {
             float *ro = (float *)row_out;  // expanded: rotated key staged for store_expanded
             ro[i] = d0;
@@ -716,9 +731,10 @@ static AppendArgs append_args(int fmt, const Dims &d, const float *y, int ldy, i
     a.koff = koff;
     a.fmt = fmt;
     a.normed = normed ? 1 : 0;
-    a.row_bytes = fmt == kFmtQ8 ? d.R + 4 + 2 * d.DR
+    a.row_bytes = fmt == kFmtQ8    ? d.R + 4 + 2 * d.DR
                   : fmt == kFmtF32 ? 4 * (d.R + d.DR)
-                                   : 4 * d.NH * (d.QD + d.DV);
+                  : fmt == kFmtBF16 ? 2 * (d.R + d.DR)
+                                    : 4 * d.NH * (d.QD + d.DV);
     a.eps = eps;
     a.rows_mode = nrows > 0 ? 1 : 0;
     return a;
@@ -1075,6 +1091,9 @@ __device__ __forceinline__ float score_elem(const SeqDesc &s, const Dims &d, int
     } else if (FMT == kFmtF32) {
         if (k < d.R) return ((const float *)s.a)[(size_t)j * d.R + k];
         return ((const float *)s.b)[(size_t)j * d.DR + (k - d.R)];
+    } else if (FMT == kFmtBF16) {
+        if (k < d.R) return bf16_to_f32(((const uint16_t *)s.a)[(size_t)j * d.R + k]);
+        return bf16_to_f32(((const uint16_t *)s.b)[(size_t)j * d.DR + (k - d.R)]);
     } else {
         return ((const float *)s.a)[((size_t)j * d.NH + h) * d.QD + k];
     }
@@ -1083,6 +1102,7 @@ template <int FMT>
 __device__ __forceinline__ float value_elem(const SeqDesc &s, const Dims &d, int h, int j, int k) {
     if (FMT == kFmtQ8) return (float)((const int8_t *)s.a)[(size_t)j * d.R + k] * ((const float *)s.b)[j];
     if (FMT == kFmtF32) return ((const float *)s.a)[(size_t)j * d.R + k];
+    if (FMT == kFmtBF16) return bf16_to_f32(((const uint16_t *)s.a)[(size_t)j * d.R + k]);
     return ((const float *)s.b)[((size_t)j * d.NH + h) * d.DV + k];
 }
 
@@ -1274,6 +1294,211 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
     }
 }
 
+// s_waitcnt vmcnt(n) for the counts the DMA pipelines of the attention kernels use (n
+// wave-uniform; any other n waits for everything).
+__device__ __forceinline__ void wait_vm(int n) {
+    switch (n) {
+    case 0: wait_vmcnt<0>(); break;
+    case 2: wait_vmcnt<2>(); break;
+    case 3: wait_vmcnt<3>(); break;
+    case 8: wait_vmcnt<8>(); break;
+    case 9: wait_vmcnt<9>(); break;
+    case 10: wait_vmcnt<10>(); break;
+    case 11: wait_vmcnt<11>(); break;
+    case 16: wait_vmcnt<16>(); break;
+    case 18: wait_vmcnt<18>(); break;
+    case 19: wait_vmcnt<19>(); break;
+    default: wait_vmcnt<0>(); break;
+    }
+}
+
+// ---- bf16 MFMA path (BF16 history, NH=16, R=512, DR=64) -------------------------------
+// One workgroup of four waves per CU streams its split-K slice in chunks of 32 rows (36 KB: 32 KB
+// of latents, 4 KB of RoPE keys) through a ring of four LDS slots filled by
+// global_load_lds_dwordx4: chunk k is computed while chunks k+1 .. k+3 are in flight. The rows
+// are exact bf16 MFMA operands, so only the query side and the softmax weights are split:
+//   scores: M = 16 heads, N = 16 rows, K = 576. Wave w takes rows 16 (w & 1) .. +15 and the
+//     k-blocks 9 (w >> 1) .. +8 of 32 against the bf16 hi | lo split of q * softmax scale (two
+//     v_mfma_f32_16x16x32_bf16 per block); the two k-halves are summed through LDS;
+//   softmax: every wave keeps the online statistics of all 16 heads (the same arithmetic in
+//     each wave); lane group g takes chunk rows 8g .. 8g+7;
+//   mix: wave w owns latent columns 128w .. +127 (M = heads, N = 16 columns, K = the 32 rows),
+//     p split into bf16 hi | lo, the rows read transposed by ds_read_b64_tr_b16, fp32
+//     accumulators rescaled by exp(m_old - m_new) every chunk.
+// The 16-byte slots of a latent row are XOR-swizzled by b16_swz(row), so that the score reads
+// (16 rows, one slot) and the transposed reads (4 rows x 32 bytes per 16 lanes, 8 rows per half
+// wave) spread over the LDS banks.
+constexpr int kB16Ch = 32;
+constexpr int kB16Ring = 4;
+constexpr int kB16LatB = kB16Ch * 1024;            // latents of a chunk
+constexpr int kB16Slot = kB16LatB + kB16Ch * 128;  // + RoPE keys
+constexpr int kB16SpHs = 36;                       // floats per head in a score half: 32 + 4
+constexpr int kB16SpOff = kB16Ring * kB16Slot;     // score halves [2][16 heads][kB16SpHs]
+constexpr int kB16SmemB = kB16SpOff + 2 * 16 * kB16SpHs * 4;
+static_assert(kB16SmemB <= 160 * 1024, "LDS of one CU");
+
+// bits (r3, r2, r1, r0) of a chunk row -> slot XOR (r3, r1, r0, r2): a bijection on 16 rows, and
+// (r3, r1, r0) -> distinct slot pairs for the 8 rows of a transposed half-wave read
+__device__ __forceinline__ int b16_swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1) | (row & 8); }
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16: within each 16-lane group, destination lane i element e is element i & 3
+// of the four addressed by source lane 4e + (i >> 2).
+__device__ __forceinline__ v4s lds_read_tr16(const uint8_t *p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s *)(p));
+}
+
+__global__ __launch_bounds__(256) void k_attn_bf16_mfma(AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[kB16SmemB];
+    const int tid = threadIdx.x, l = tid & 63, n = l & 15, g = l >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int sid = blockIdx.x;
+    const int b = find_seq(a.t, sid);
+    const SeqDesc &s = a.t.s[b];
+    const int split = sid - s.split0;
+    const int r0 = split * s.rps;
+    const int r1 = split == s.nsplit - 1 ? s.len : r0 + s.rps;  // last split takes the rest
+    const int nch = (r1 - r0 + kB16Ch - 1) / kB16Ch;
+    const uint16_t *glat = (const uint16_t *)s.a;
+    const uint16_t *grope = (const uint16_t *)s.b;
+    const uint32_t sbase = lds_addr(smem);
+    float *sp = (float *)(smem + kB16SpOff);
+    const int rb = w & 1, kh = w >> 1;
+
+    // query operands (A of the score MFMAs: head n, k = 32 kb + 8g .. +7), loaded and split
+    // before the first history DMA is issued
+    v8bf qh[9], ql[9];
+    {
+        const float *qrow = a.qf + ((size_t)b * 16 + n) * 576 + 8 * g + 32 * 9 * kh;
+        v4f qv[18];
+#pragma unroll
+        for (int j = 0; j < 9; ++j) {
+            qv[2 * j] = *(const v4f *)(qrow + 32 * j);
+            qv[2 * j + 1] = *(const v4f *)(qrow + 32 * j + 4);
+        }
+#pragma unroll
+        for (int j = 0; j < 9; ++j) {
+            split8(qv[2 * j] * a.smscale, qv[2 * j + 1] * a.smscale, qh[j], ql[j]);
+            // the operands exist before the DMA below is issued: the wait for these loads then
+            // does not count the history loads
+            asm volatile("" ::"v"(qh[j]), "v"(ql[j]));
+        }
+    }
+
+    // DMA per chunk and wave: latent rows 8w .. 8w+7, one 1 KB instruction per row (lane i
+    // writes physical slot i, which holds logical slot i ^ b16_swz(row)); RoPE rows 8w .. 8w+7,
+    // one instruction (lane i: row 8w + (i >> 3), physical slot i & 7 = logical (i & 7) ^
+    // (row & 7)). Rows past the split end (last chunk only) re-read the split's last row (in
+    // bounds); their scores are masked.
+    auto issue = [&](int c) __attribute__((always_inline)) {
+        const uint32_t buf = sbase + (uint32_t)((c % kB16Ring) * kB16Slot);
+        const int rbase = r0 + c * kB16Ch;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int row = 8 * w + k;
+            const int gr = min(rbase + row, r1 - 1);
+            dma_b128(glat + (size_t)gr * 512 + 8 * (l ^ b16_swz(row)), buf + (uint32_t)(row * 1024));
+        }
+        const int row = 8 * w + (l >> 3);
+        const int gr = min(rbase + row, r1 - 1);
+        dma_b128(grope + (size_t)gr * 64 + 8 * ((l & 7) ^ (row & 7)), buf + (uint32_t)(kB16LatB + w * 1024));
+    };
+
+    // score operand offsets (row srow of the chunk, slot 4 kb + g of its latents / RoPE key)
+    const int srow = 16 * rb + n;
+    int bofs[9];
+#pragma unroll
+    for (int j = 0; j < 9; ++j) {
+        const int kb = 9 * kh + j;
+        bofs[j] = kb < 16 ? srow * 1024 + 16 * ((4 * kb + g) ^ b16_swz(srow))
+                          : kB16LatB + srow * 128 + 16 * ((4 * (kb - 16) + g) ^ (srow & 7));
+    }
+    // transposed reads of column block 8w + t: half h covers rows 8g + 4h .. +3 (lane n
+    // addresses row 8g + 4h + (n >> 2), columns 4 (n & 3) .. +3 of the block)
+    int tro[2][8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int row = 8 * g + 4 * h + (n >> 2);
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+            tro[h][t] = row * 1024 + 16 * ((2 * (8 * w + t) + ((n >> 1) & 1)) ^ b16_swz(row)) + 8 * (n & 1);
+    }
+
+    issue(0);
+    if (nch > 1) issue(1);
+    if (nch > 2) issue(2);
+    float m_run = -INFINITY, l_run = 0.f;  // head n
+    v4f acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < nch; ++k) {
+        // this wave's DMA of chunk k has landed (chunks k+1, k+2 may stay in flight)
+        wait_vm(k + 2 < nch ? 18 : (k + 1 < nch ? 9 : 0));
+        lds_barrier();  // chunk k complete; every wave is done with chunk k-1's slot and the scores
+        if (k + 3 < nch) issue(k + 3);
+        const uint8_t *buf = smem + (k % kB16Ring) * kB16Slot;
+        v4f dp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 9; ++j) {
+            const v8bf bv = *(const v8bf *)(buf + bofs[j]);
+            dp = mfma_bf16(qh[j], bv, dp);
+            dp = mfma_bf16(ql[j], bv, dp);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sp[(kh * 16 + 4 * g + i) * kB16SpHs + srow] = dp[i];
+        lds_barrier();  // both k-halves of every score are in LDS
+        const float *s0 = sp + n * kB16SpHs + 8 * g, *s1 = sp + (16 + n) * kB16SpHs + 8 * g;
+        const v4f a0 = *(const v4f *)s0, a1 = *(const v4f *)(s0 + 4);
+        const v4f c0 = *(const v4f *)s1, c1 = *(const v4f *)(s1 + 4);
+        const int nv = r1 - (r0 + k * kB16Ch);  // valid rows of the chunk (>= 1)
+        float sc[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            sc[e] = 8 * g + e < nv ? a0[e] + c0[e] : -INFINITY;
+            sc[e + 4] = 8 * g + e + 4 < nv ? a1[e] + c1[e] : -INFINITY;
+        }
+        float cmax = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+        const float mnew = fmaxf(m_run, cmax);
+        const float alpha = __expf(m_run - mnew);
+        float p[8], psum = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            p[e] = __expf(sc[e] - mnew);
+            psum += p[e];
+        }
+        psum += __shfl_xor(psum, 16);
+        psum += __shfl_xor(psum, 32);
+        l_run = fmaf(l_run, alpha, psum);
+        m_run = mnew;
+        v8bf ph, pl;
+        split8(v4f{p[0], p[1], p[2], p[3]}, v4f{p[4], p[5], p[6], p[7]}, ph, pl);
+        float ad[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ad[i] = __shfl(alpha, 4 * g + i);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const v4s lo4 = lds_read_tr16(buf + tro[0][t]);
+            const v4s hi4 = lds_read_tr16(buf + tro[1][t]);
+            const v8bf bt = __builtin_bit_cast(v8bf, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[t][i] *= ad[i];
+            acc[t] = mfma_bf16(ph, bt, acc[t]);
+            acc[t] = mfma_bf16(pl, bt, acc[t]);
+        }
+    }
+    float *P = a.part + (size_t)sid * 16 * 514;
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) P[(4 * g + i) * 512 + 128 * w + 16 * t + n] = acc[t][i];
+    if (w == 0 && g == 0) {
+        P[8192 + n] = m_run;
+        P[8192 + 16 + n] = l_run;
+    }
+}
+
 // ---- int8 MFMA path (Q8 history, NH=16, R=512, DR=64) ---------------------------------
 // One workgroup of 8 waves (two per SIMD) per CU streams its split-K slice in chunks of 64
 // rows. The waves specialise, and the two roles run one chunk apart:
@@ -1387,21 +1612,6 @@ __device__ __forceinline__ void put_q8_weights(int8_t *wqc, const float *pv, flo
     }
 }
 
-// s_waitcnt vmcnt(n) for the counts the mix waves use (n wave-uniform).
-__device__ __forceinline__ void wait_vm(int n) {
-    switch (n) {
-    case 0: wait_vmcnt<0>(); break;
-    case 2: wait_vmcnt<2>(); break;
-    case 3: wait_vmcnt<3>(); break;
-    case 8: wait_vmcnt<8>(); break;
-    case 10: wait_vmcnt<10>(); break;
-    case 11: wait_vmcnt<11>(); break;
-    case 16: wait_vmcnt<16>(); break;
-    case 18: wait_vmcnt<18>(); break;
-    case 19: wait_vmcnt<19>(); break;
-    default: wait_vmcnt<0>(); break;
-    }
-}
 
 // The two roles run separate code (their registers do not overlap) with the same sequence of
 // workgroup barriers: two in the prologue (P0: the score waves' query and scale loads are
@@ -1762,12 +1972,16 @@ hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t
         hipLaunchKernelGGL(k_attn_q8_mfma, dim3(total_splits), dim3(512), 0, st, a);
     } else if (kind == kAttnF32Mfma) {
         hipLaunchKernelGGL(k_attn_f32_mfma, dim3(total_splits), dim3(256), 0, st, a);
+    } else if (kind == kAttnBF16Mfma) {
+        hipLaunchKernelGGL(k_attn_bf16_mfma, dim3(total_splits), dim3(256), 0, st, a);
     } else {
         const int P = fmt == kFmtExp ? t.n * d.NH : t.n;
         if (fmt == kFmtQ8)
             hipLaunchKernelGGL(k_attn_generic<kFmtQ8>, dim3(P), dim3(256), 0, st, a);
         else if (fmt == kFmtF32)
             hipLaunchKernelGGL(k_attn_generic<kFmtF32>, dim3(P), dim3(256), 0, st, a);
+        else if (fmt == kFmtBF16)
+            hipLaunchKernelGGL(k_attn_generic<kFmtBF16>, dim3(P), dim3(256), 0, st, a);
         else
             hipLaunchKernelGGL(k_attn_generic<kFmtExp>, dim3(P), dim3(256), 0, st, a);
     }
@@ -2068,7 +2282,8 @@ struct FillArgs {
 
 // One wave per row. Element e of global row j draws synth_normal(seed, j*(R+DR) + e).
 // Q8: the R latents go through the history quantiser, the DR RoPE values are rounded to
-// bf16. F32: all values are rounded to bf16 first (bf16-representable fp32 history).
+// bf16. F32: all values are rounded to bf16 first (bf16-representable fp32 history). BF16:
+// the same bf16 values, stored as bf16 (a BF16 and an F32 history of one seed hold equal rows).
 __global__ __launch_bounds__(256) void k_fill_history(FillArgs a) {
     const int wv = (blockIdx.x * blockDim.x + threadIdx.x) >> 6, l = threadIdx.x & 63;
     if (wv >= a.nrows) return;
@@ -2089,6 +2304,11 @@ __global__ __launch_bounds__(256) void k_fill_history(FillArgs a) {
         }
         if (l == 0) ((float *)a.b)[j] = scale;
         uint16_t *rope = (uint16_t *)a.c + (size_t)j * a.DR;
+        for (int e = l; e < a.DR; e += 64) rope[e] = f32_to_bf16_rne(synth_normal(a.seed, base + a.R + e));
+    } else if (a.fmt == kFmtBF16) {
+        uint16_t *lat = (uint16_t *)a.a + (size_t)j * a.R;
+        uint16_t *rope = (uint16_t *)a.b + (size_t)j * a.DR;
+        for (int e = l; e < a.R; e += 64) lat[e] = f32_to_bf16_rne(synth_normal(a.seed, base + e));
         for (int e = l; e < a.DR; e += 64) rope[e] = f32_to_bf16_rne(synth_normal(a.seed, base + a.R + e));
     } else {
         float *lat = (float *)a.a + (size_t)j * a.R;

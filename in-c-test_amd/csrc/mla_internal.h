@@ -21,6 +21,7 @@ enum Fmt : int {
     kFmtQ8 = 0,   // int8 codes [cap,R], fp32 scale [cap], bf16 RoPE key [cap,DR]
     kFmtF32 = 1,  // fp32 latent [cap,R], fp32 RoPE key [cap,DR]
     kFmtExp = 2,  // expanded fp32 keys [cap,NH,QD], values [cap,NH,DV]
+    kFmtBF16 = 3, // bf16 latent [cap,R], bf16 RoPE key [cap,DR]
 };
 
 struct Dims {
@@ -102,7 +103,7 @@ hipError_t launch_gemv_xs(hipStream_t st, float *Y, int ldy, const uint16_t *XS,
                           const uint16_t *W, int out, int in, bool accumulate);
 
 // RMSNorm of katmp[b] (= y + koff) -> latent row; RoPE of katmp[b][R:] at s.pos. Writes the
-// row into the history at row s.pos (fmt Q8/F32) or, for kFmtExp, the normalised latent
+// row into the history at row s.pos (fmt Q8/F32/BF16) or, for kFmtExp, the normalised latent
 // into w.latent and the rotated key into the tail of w.rows. A copy of the stored row goes
 // to w.rows for host write-back. rope_cs: [npos, DR/2] (cos, sin) pairs.
 // nrows > 0: rows mode, nrows rows of the single sequence t.s[0] starting at t.s[0].pos,
@@ -136,8 +137,8 @@ hipError_t launch_append_qprep(hipStream_t st, int fmt, const SeqTable &t, const
 
 // Split-K attention over the history; writes partials (acc | m | l) per split.
 // kind: 0 = generic VALU (any dims, one split per problem), 1 = fp32 MFMA (Kimi dims),
-// 2 = int8 MFMA (Kimi dims, Q8 rows).
-enum AttnKind : int { kAttnGeneric = 0, kAttnF32Mfma = 1, kAttnQ8Mfma = 2 };
+// 2 = int8 MFMA (Kimi dims, Q8 rows), 3 = bf16 MFMA (Kimi dims, BF16 rows).
+enum AttnKind : int { kAttnGeneric = 0, kAttnF32Mfma = 1, kAttnQ8Mfma = 2, kAttnBF16Mfma = 3 };
 hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t, const Dims &d,
                             int rows_per_split, int total_splits, int lmax,
                             const DecodeWork &w);
@@ -149,7 +150,7 @@ bool combine_writes_hos(int fmt, const Dims &d);
 hipError_t launch_combine(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
                           const uint16_t *kv_b, const DecodeWork &w);
 
-// Device-side generator of a synthetic Q8 / F32 history (benchmark and test workloads):
+// Device-side generator of a synthetic Q8 / F32 / BF16 history (benchmark and test workloads):
 // latents ~ Irwin-Hall(4) normal from SplitMix64, quantised with the history quantiser.
 hipError_t launch_fill_history(hipStream_t st, int fmt, void *a, void *b, void *c, int R,
                                int DR, int row0, int nrows, uint64_t seed);

@@ -428,6 +428,7 @@ int rope_table(float theta, int DR, int need_pos, const float2 **out) {
 size_t row_bytes_of(int fmt, int d0, int d1, int d2) {
     if (fmt == kFmtQ8) return (size_t)d0 + 4 + 2 * (size_t)d1;
     if (fmt == kFmtF32) return 4 * ((size_t)d0 + (size_t)d1);
+    if (fmt == kFmtBF16) return 2 * ((size_t)d0 + (size_t)d1);
     return 4 * (size_t)d0 * ((size_t)d1 + (size_t)d2);
 }
 
@@ -468,6 +469,10 @@ HostView view_of(const KvlMlaCompressedState *s) {
     return {kFmtF32, s->latent, s->rope, nullptr, s->capacity, s->len, s->kv_lora_rank,
             s->qk_rope_dim, 0};
 }
+HostView view_of(const KvlMlaCompressedBF16State *s) {
+    return {kFmtBF16, s->latent, s->rope, nullptr, s->capacity, s->len, s->kv_lora_rank,
+            s->qk_rope_dim, 0};
+}
 HostView view_of(const KvlMlaState *s) {
     return {kFmtExp, s->keys, s->values, nullptr, s->capacity, s->len, s->num_heads,
             s->qk_nope_dim + s->qk_rope_dim, s->v_head_dim};
@@ -482,6 +487,10 @@ void comp_bytes(int fmt, int d0, int d1, int d2, size_t &ea, size_t &eb, size_t 
     } else if (fmt == kFmtF32) {
         ea = 4 * (size_t)d0;
         eb = 4 * (size_t)d1;
+        ec = 0;
+    } else if (fmt == kFmtBF16) {
+        ea = 2 * (size_t)d0;
+        eb = 2 * (size_t)d1;
         ec = 0;
     } else {
         ea = 4 * (size_t)d0 * d1;
@@ -639,8 +648,8 @@ struct SeqIn {
 // chunks, at most 1024 rows for Q8 (every split < 2048 rows). The last split of a sequence
 // takes the remainder: nsplit = max(1, len / rows).
 long split_rows(int kind, long len, long total_rows, int ncu) {
-    const int chunk = kind == kAttnQ8Mfma ? 64 : 16;
-    const int wg_per_cu = kind == kAttnQ8Mfma ? 1 : 3;
+    const int chunk = kind == kAttnQ8Mfma ? 64 : kind == kAttnBF16Mfma ? 32 : 16;
+    const int wg_per_cu = kind == kAttnQ8Mfma || kind == kAttnBF16Mfma ? 1 : 3;
     const double target = (double)wg_per_cu * ncu;
     const long want = std::max(1L, std::lround(target * (double)len / (double)total_rows));
     long r = len / (want * chunk) * chunk;
@@ -671,7 +680,7 @@ struct GroupPlan {
 void plan_group(int fmt, const Dims &d, const SeqIn *seqs, int B, bool solo, GroupPlan &p) {
     const int ncu = ctx().ncu;
     const bool kimi = kimi_attn(d) && fmt != kFmtExp;
-    p.kind = !kimi ? kAttnGeneric : fmt == kFmtQ8 ? kAttnQ8Mfma : kAttnF32Mfma;
+    p.kind = !kimi ? kAttnGeneric : fmt == kFmtQ8 ? kAttnQ8Mfma : fmt == kFmtBF16 ? kAttnBF16Mfma : kAttnF32Mfma;
     SeqTable &t = p.t;
     memset(&t, 0, sizeof t);
     t.n = B;
@@ -862,6 +871,10 @@ void write_back_rows(int fmt, const HostView &v, int pos, const uint8_t *row) {
         const int R = v.d0, DR = v.d1;
         memcpy((float *)v.ha + (size_t)pos * R, row, 4 * (size_t)R);
         memcpy((float *)v.hb + (size_t)pos * DR, row + 4 * (size_t)R, 4 * (size_t)DR);
+    } else if (fmt == kFmtBF16) {
+        const int R = v.d0, DR = v.d1;
+        memcpy((uint16_t *)v.ha + (size_t)pos * R, row, 2 * (size_t)R);
+        memcpy((uint16_t *)v.hb + (size_t)pos * DR, row + 2 * (size_t)R, 2 * (size_t)DR);
     } else {
         const size_t nk = (size_t)v.d0 * v.d1, nv = (size_t)v.d0 * v.d2;
         memcpy((float *)v.ha + (size_t)pos * nk, row, 4 * nk);
@@ -882,6 +895,10 @@ bool state_dims_ok(const KvlMlaCompressedState *s, const KvlMlaConfig *cfg) {
     return s->kv_lora_rank == cfg->kv_lora_rank && s->qk_rope_dim == cfg->qk_rope_dim;
 }
 template <>
+bool state_dims_ok(const KvlMlaCompressedBF16State *s, const KvlMlaConfig *cfg) {
+    return s->kv_lora_rank == cfg->kv_lora_rank && s->qk_rope_dim == cfg->qk_rope_dim;
+}
+template <>
 bool state_dims_ok(const KvlMlaState *s, const KvlMlaConfig *cfg) {
     return s->num_heads == cfg->num_heads && s->qk_nope_dim == cfg->qk_nope_dim &&
            s->qk_rope_dim == cfg->qk_rope_dim && s->v_head_dim == cfg->v_head_dim;
@@ -893,6 +910,8 @@ template <>
 int fmt_of<KvlMlaCompressedQ8State>() { return kFmtQ8; }
 template <>
 int fmt_of<KvlMlaCompressedState>() { return kFmtF32; }
+template <>
+int fmt_of<KvlMlaCompressedBF16State>() { return kFmtBF16; }
 template <>
 int fmt_of<KvlMlaState>() { return kFmtExp; }
 
@@ -1682,6 +1701,111 @@ int kvl_mla_decode_compressed_q8_block_bf16(float *out, const float *x, int coun
     return decode_block(out, x, count, start_position, cfg, w, state);
 }
 
+// ---- BF16-latent state (include/kvl/mla_hip.h) -------------------------------------------
+// The FP32 state's life cycle and checks (src/mla_compressed_state.c:24-50) over bf16 arrays.
+
+int kvl_mla_compressed_bf16_state_init(KvlMlaCompressedBF16State *state, const KvlMlaConfig *cfg, int capacity) {
+    Guard guard;
+    if (!state || !cfg || capacity <= 0 || cfg->kv_lora_rank <= 0 || cfg->qk_rope_dim <= 0 ||
+        (cfg->qk_rope_dim & 1)) {
+        set_err("invalid arguments");
+        return -1;
+    }
+    mirror_drop(state);
+    memset(state, 0, sizeof(*state));
+    state->latent = (uint16_t *)calloc((size_t)capacity * cfg->kv_lora_rank, sizeof(uint16_t));
+    state->rope = (uint16_t *)calloc((size_t)capacity * cfg->qk_rope_dim, sizeof(uint16_t));
+    if (!state->latent || !state->rope) {
+        free(state->latent);
+        free(state->rope);
+        memset(state, 0, sizeof(*state));
+        set_err("host allocation of %d rows failed", capacity);
+        return -1;
+    }
+    state->capacity = capacity;
+    state->kv_lora_rank = cfg->kv_lora_rank;
+    state->qk_rope_dim = cfg->qk_rope_dim;
+    return 0;
+}
+
+void kvl_mla_compressed_bf16_state_reset(KvlMlaCompressedBF16State *state) {
+    Guard guard;
+    if (!state) return;
+    state->len = 0;
+    mirror_lower(state, 0);
+}
+
+int kvl_mla_compressed_bf16_state_truncate(KvlMlaCompressedBF16State *state, int new_len) {
+    Guard guard;
+    if (!state || new_len < 0 || new_len > state->len) {
+        set_err("invalid truncate length");
+        return -1;
+    }
+    state->len = new_len;
+    mirror_lower(state, new_len);
+    return 0;
+}
+
+void kvl_mla_compressed_bf16_state_free(KvlMlaCompressedBF16State *state) {
+    Guard guard;
+    if (!state) return;
+    mirror_drop(state);
+    free(state->latent);
+    free(state->rope);
+    memset(state, 0, sizeof(*state));
+}
+
+size_t kvl_mla_compressed_bf16_state_bytes(const KvlMlaCompressedBF16State *state) {
+    if (!state || state->capacity <= 0) return 0;
+    return sizeof(*state) + (size_t)state->capacity *
+                                ((size_t)state->kv_lora_rank + (size_t)state->qk_rope_dim) * sizeof(uint16_t);
+}
+
+int kvl_mla_compressed_bf16_state_sync(KvlMlaCompressedBF16State *state) {
+    Guard guard;
+    if (!state) return -1;
+    mirror_lower(state, 0);
+    return 0;
+}
+
+int kvl_mla_compressed_bf16_state_prefill_bf16(const float *x, int seq_len, const KvlMlaConfig *cfg,
+                                               const KvlMlaBF16 *w, KvlMlaCompressedBF16State *state) {
+    Guard guard;
+    return state_prefill(x, seq_len, cfg, w, state);
+}
+
+int kvl_mla_decode_compressed_bf16_bf16(float *out, const float *x, int position, const KvlMlaConfig *cfg,
+                                        const KvlMlaBF16 *w, KvlMlaCompressedBF16State *state) {
+    Guard guard;
+    KvlMlaCompressedBF16State *st[1] = {state};
+    return decode_host(out, x, &position, 1, cfg, w, st);
+}
+
+int kvl_mla_decode_compressed_bf16_block_bf16(float *out, const float *x, int count, int start_position,
+                                              const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                              KvlMlaCompressedBF16State *state) {
+    Guard guard;
+    return decode_block(out, x, count, start_position, cfg, w, state);
+}
+
+int kvl_mla_decode_compressed_bf16_batch_bf16(float *out, const float *x, const int *positions, int batch,
+                                              const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                              KvlMlaCompressedBF16State *const *states) {
+    Guard guard;
+    if (!positions) {
+        set_err("invalid arguments");
+        return -1;
+    }
+    return decode_host(out, x, positions, batch, cfg, w, states);
+}
+
+int kvl_mla_decode_compressed_bf16_batch_device(float *d_out, const float *d_x, int batch,
+                                                const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                                KvlMlaCompressedBF16State *const *states, unsigned flags) {
+    Guard guard;
+    return decode_device(d_out, d_x, batch, cfg, w, states, flags);
+}
+
 // ---- include/kvl/mla_compressed_q8_state.h ----------------------------------------------
 
 int kvl_mla_compressed_q8_state_init(KvlMlaCompressedQ8State *state, const KvlMlaConfig *cfg,
@@ -2200,6 +2324,20 @@ int kvl_mla_compressed_q8_state_pull(KvlMlaCompressedQ8State *state, int row0, i
 }
 
 int kvl_mla_compressed_state_pull(KvlMlaCompressedState *state, int row0, int nrows) {
+    Guard guard;
+    if (!state) return -1;
+    return pull_rows(state, view_of(state), row0, nrows);
+}
+
+int kvl_mla_compressed_bf16_state_fill_synthetic(KvlMlaCompressedBF16State *state, int row0, int nrows,
+                                                 uint64_t seed) {
+    Guard guard;
+    if (!state) return -1;
+    return fill_synth(state, view_of(state), row0, nrows, seed,
+                      [](const void *k, int len) { ((KvlMlaCompressedBF16State *)k)->len = len; });
+}
+
+int kvl_mla_compressed_bf16_state_pull(KvlMlaCompressedBF16State *state, int row0, int nrows) {
     Guard guard;
     if (!state) return -1;
     return pull_rows(state, view_of(state), row0, nrows);

@@ -42,11 +42,19 @@ class KvlMlaCompressedQ8State(C.Structure):
                 ("rope_bf16", u16p)]
 
 
+class KvlMlaCompressedBF16State(C.Structure):
+    """BF16-latent history of include/kvl/mla_hip.h (an extension: the FP32 state's layout with
+    bf16 rows)."""
+    _fields_ = [("capacity", c_int), ("len", c_int), ("kv_lora_rank", c_int),
+                ("qk_rope_dim", c_int), ("latent", u16p), ("rope", u16p)]
+
+
 CFG = C.POINTER(KvlMlaConfig)
 W = C.POINTER(KvlMlaBF16)
 ST = C.POINTER(KvlMlaState)
 CS = C.POINTER(KvlMlaCompressedState)
 QS = C.POINTER(KvlMlaCompressedQ8State)
+BS = C.POINTER(KvlMlaCompressedBF16State)
 
 # name (without prefix) -> (restype, argtypes)
 REFERENCE_API = {

@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(HERE, "libkvl_mla.so")
 
 QSP = C.POINTER(abi.QS)
 CSP = C.POINTER(abi.CS)
+BSP = C.POINTER(abi.BS)
 
 # include/kvl/mla_hip.h
 EXT_API = {
@@ -69,6 +70,23 @@ EXT_API = {
     "mla_compressed_state_fill_synthetic": (C.c_int, [abi.CS, C.c_int, C.c_int, C.c_uint64]),
     "mla_compressed_q8_state_pull": (C.c_int, [abi.QS, C.c_int, C.c_int]),
     "mla_compressed_state_pull": (C.c_int, [abi.CS, C.c_int, C.c_int]),
+    # BF16-latent state
+    "mla_compressed_bf16_state_init": (C.c_int, [abi.BS, abi.CFG, C.c_int]),
+    "mla_compressed_bf16_state_reset": (None, [abi.BS]),
+    "mla_compressed_bf16_state_truncate": (C.c_int, [abi.BS, C.c_int]),
+    "mla_compressed_bf16_state_free": (None, [abi.BS]),
+    "mla_compressed_bf16_state_bytes": (C.c_size_t, [abi.BS]),
+    "mla_compressed_bf16_state_sync": (C.c_int, [abi.BS]),
+    "mla_compressed_bf16_state_prefill_bf16": (C.c_int, [abi.f32p, C.c_int, abi.CFG, abi.W, abi.BS]),
+    "mla_decode_compressed_bf16_bf16": (C.c_int, [abi.f32p, abi.f32p, C.c_int, abi.CFG, abi.W, abi.BS]),
+    "mla_decode_compressed_bf16_block_bf16": (C.c_int, [abi.f32p, abi.f32p, C.c_int, C.c_int, abi.CFG, abi.W,
+                                                        abi.BS]),
+    "mla_decode_compressed_bf16_batch_bf16": (C.c_int, [abi.f32p, abi.f32p, C.POINTER(C.c_int), C.c_int,
+                                                        abi.CFG, abi.W, BSP]),
+    "mla_decode_compressed_bf16_batch_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, abi.CFG, abi.W,
+                                                          BSP, C.c_uint]),
+    "mla_compressed_bf16_state_fill_synthetic": (C.c_int, [abi.BS, C.c_int, C.c_int, C.c_uint64]),
+    "mla_compressed_bf16_state_pull": (C.c_int, [abi.BS, C.c_int, C.c_int]),
 }
 
 # stage 1 is the fused append + query preparation of the compressed formats (the expanded

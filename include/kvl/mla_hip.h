@@ -28,6 +28,45 @@
 extern "C" {
 #endif
 
+/* BF16-latent history: the layout of the FP32 compressed state (include/kvl/
+ * mla_compressed_state.h:7-14 of the reference) with each normalised latent row and each rotated
+ * RoPE key stored as bf16, rounded to nearest even with the rule of
+ * src/mla_compressed_q8_state.c:9-16 (Inf/NaN words truncated): 2 * (kv_lora_rank + qk_rope_dim)
+ * bytes per row, 1152 B at kv_lora_rank 512 / qk_rope_dim 64, half the FP32 state's 2304 B.
+ * Decoding it computes the reference's FP32 decode (src/mla_compressed_state.c:86-161) over the
+ * bf16-rounded rows. The host arrays stay authoritative as for the reference's states. */
+typedef struct {
+    int capacity;
+    int len;
+    int kv_lora_rank;
+    int qk_rope_dim;
+    uint16_t *latent; /* [capacity, kv_lora_rank] host, bf16 */
+    uint16_t *rope;   /* [capacity, qk_rope_dim] host, bf16, RoPE already applied */
+} KvlMlaCompressedBF16State;
+
+/* Life cycle, with the checks and return values of the FP32 state's
+ * (src/mla_compressed_state.c:24-50): init allocates zeroed host arrays (capacity > 0,
+ * qk_rope_dim even); truncate needs 0 <= new_len <= len; bytes counts the struct and the arrays. */
+int kvl_mla_compressed_bf16_state_init(KvlMlaCompressedBF16State *state, const KvlMlaConfig *cfg,
+                                       int capacity);
+void kvl_mla_compressed_bf16_state_reset(KvlMlaCompressedBF16State *state);
+int kvl_mla_compressed_bf16_state_truncate(KvlMlaCompressedBF16State *state, int new_len);
+void kvl_mla_compressed_bf16_state_free(KvlMlaCompressedBF16State *state);
+size_t kvl_mla_compressed_bf16_state_bytes(const KvlMlaCompressedBF16State *state);
+/* State prefill (src/mla_compressed_state.c:52-84 with bf16 rows): empty state, seq_len <=
+ * capacity. */
+int kvl_mla_compressed_bf16_state_prefill_bf16(const float *x, int seq_len, const KvlMlaConfig *cfg,
+                                               const KvlMlaBF16 *w, KvlMlaCompressedBF16State *state);
+/* One decode token (src/mla_compressed_state.c:86-161 with the appended row stored as bf16):
+ * position must equal len; host buffers, synchronous, host rows written. */
+int kvl_mla_decode_compressed_bf16_bf16(float *out, const float *x, int position, const KvlMlaConfig *cfg,
+                                        const KvlMlaBF16 *w, KvlMlaCompressedBF16State *state);
+/* count tokens at start_position (= len) .. + count - 1, equal bit for bit to count single-token
+ * decodes (src/mla_compressed_state.c:163-184 loops them). */
+int kvl_mla_decode_compressed_bf16_block_bf16(float *out, const float *x, int count, int start_position,
+                                              const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                              KvlMlaCompressedBF16State *state);
+
 /* Last error of the calling thread ("" when none). */
 const char *kvl_mla_last_error(void);
 
@@ -48,6 +87,7 @@ int kvl_mla_release_weights(const KvlMlaBF16 *w);
 int kvl_mla_compressed_state_sync(KvlMlaCompressedState *state);
 int kvl_mla_compressed_q8_state_sync(KvlMlaCompressedQ8State *state);
 int kvl_mla_state_sync(KvlMlaState *state);
+int kvl_mla_compressed_bf16_state_sync(KvlMlaCompressedBF16State *state);
 
 /* One decode token for each of `batch` sequences: x [batch, hidden], out [batch, hidden],
  * positions[i] must equal states[i]->len (the reference rule, checked for every sequence
@@ -60,6 +100,10 @@ int kvl_mla_decode_compressed_q8_batch_bf16(float *out, const float *x, const in
                                             int batch, const KvlMlaConfig *cfg,
                                             const KvlMlaBF16 *w,
                                             KvlMlaCompressedQ8State *const *states);
+int kvl_mla_decode_compressed_bf16_batch_bf16(float *out, const float *x, const int *positions,
+                                              int batch, const KvlMlaConfig *cfg,
+                                              const KvlMlaBF16 *w,
+                                              KvlMlaCompressedBF16State *const *states);
 
 /* Block decode over the Q8 history, the counterpart of kvl_mla_decode_compressed_block_bf16
  * (which the reference defines for the FP32 state only, src/mla_compressed_state.c:163-184):
@@ -87,6 +131,10 @@ int kvl_mla_decode_compressed_batch_device(float *d_out, const float *d_x, int b
                                            const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
                                            KvlMlaCompressedState *const *states,
                                            unsigned flags);
+int kvl_mla_decode_compressed_bf16_batch_device(float *d_out, const float *d_x, int batch,
+                                                const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                                KvlMlaCompressedBF16State *const *states,
+                                                unsigned flags);
 
 /* No counterpart in the reference: for callers that cannot allocate device memory (code under
  * HIP graph capture, serving loops, harnesses that forbid hipMalloc). The same computation and
@@ -200,14 +248,18 @@ int kvl_mla_q8_pack_rows(int8_t *codes, float *scales, uint16_t *rope_bf16, cons
 
 /* Synthetic histories generated on the device (benchmarks): rows [row0, row0 + nrows) of the
  * state's device copy get latents ~ approx. N(0,1) (Irwin-Hall of four 24-bit uniforms from
- * SplitMix64(seed)), Q8-quantised (Q8 state) or rounded to BF16 (FP32 state). Sets
- * len = row0 + nrows. The host arrays are only written by the *_pull calls. */
+ * SplitMix64(seed)), Q8-quantised (Q8 state) or rounded to BF16 (FP32 and BF16 states: one
+ * seed gives both the same values). Sets len = row0 + nrows. The host arrays are only written
+ * by the *_pull calls. */
 int kvl_mla_compressed_q8_state_fill_synthetic(KvlMlaCompressedQ8State *state, int row0,
                                                int nrows, uint64_t seed);
 int kvl_mla_compressed_state_fill_synthetic(KvlMlaCompressedState *state, int row0, int nrows,
                                             uint64_t seed);
 int kvl_mla_compressed_q8_state_pull(KvlMlaCompressedQ8State *state, int row0, int nrows);
 int kvl_mla_compressed_state_pull(KvlMlaCompressedState *state, int row0, int nrows);
+int kvl_mla_compressed_bf16_state_fill_synthetic(KvlMlaCompressedBF16State *state, int row0, int nrows,
+                                                 uint64_t seed);
+int kvl_mla_compressed_bf16_state_pull(KvlMlaCompressedBF16State *state, int row0, int nrows);
 
 #ifdef __cplusplus
 }

@@ -450,6 +450,46 @@ done:
     return rc;
 }
 
+/* The library's BF16-latent history (an extension with no function of its own in the reference):
+ * the FP32 decode above, src/mla_compressed_state.c:86-161, with the appended latent row and
+ * rotated key rounded to bf16 (src/mla_compressed_q8_state.c:9-16, orc_f32_to_bf16_rne) before
+ * they are stored and attended. Over an FP32 state whose earlier rows are bf16 values, this is
+ * what the library's BF16 state computes: its rows, widened to fp32, are these rows. */
+int orc_mla_decode_compressed_bf16_rows(float *out, const float *x, int position,
+                                        const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                        KvlMlaCompressedState *s) {
+    Dims d;
+    if (!out || !x || !cfg || !weights_ok(w) || !s || position != s->len || position < 0 ||
+        position >= s->capacity || s->kv_lora_rank != cfg->kv_lora_rank ||
+        s->qk_rope_dim != cfg->qk_rope_dim || dims_of(cfg, &d) != 0)
+        return -1;
+    float *qtmp = (float *)malloc((size_t)d.QO * sizeof(float));
+    float *katmp = (float *)malloc((size_t)d.KVO * sizeof(float));
+    float *qrope = (float *)malloc((size_t)d.DR * sizeof(float));
+    float *q_lat = (float *)malloc((size_t)d.R * sizeof(float));
+    double *mixacc = (double *)malloc((size_t)d.R * sizeof(double));
+    float *scores = (float *)malloc((size_t)(position + 1) * sizeof(float));
+    float *ho = (float *)malloc((size_t)d.HO * sizeof(float));
+    int rc = -1;
+    if (!qtmp || !katmp || !qrope || !q_lat || !mixacc || !scores || !ho) goto done;
+
+    orc_matvec_bf16(qtmp, x, w->q_proj, d.H, d.QO);
+    orc_matvec_bf16(katmp, x, w->kv_a_proj, d.H, d.KVO);
+    float *lat = s->latent + (size_t)position * d.R, *rope = s->rope + (size_t)position * d.DR;
+    orc_rmsnorm_bf16(lat, katmp, w->kv_a_norm, d.R, cfg->rms_eps);
+    orc_rope_interleaved(rope, katmp + d.R, d.DR, position, cfg->rope_theta);
+    for (int r = 0; r < d.R; ++r) lat[r] = orc_bf16_to_f32(orc_f32_to_bf16_rne(lat[r]));
+    for (int k = 0; k < d.DR; ++k) rope[k] = orc_bf16_to_f32(orc_f32_to_bf16_rne(rope[k]));
+    attend_latent(ho, qtmp, position, &d, cfg, w->kv_b_proj, s->latent, s->rope, qrope, q_lat,
+                  scores, mixacc);
+    orc_matvec_bf16(out, ho, w->o_proj, d.HO, d.H);
+    s->len = position + 1;
+    rc = 0;
+done:
+    free(qtmp); free(katmp); free(qrope); free(q_lat); free(mixacc); free(scores); free(ho);
+    return rc;
+}
+
 /* src/mla_compressed_state.c:163-184 */
 int orc_mla_decode_compressed_block_bf16(float *out, const float *x, int count, int start_position,
                                          const KvlMlaConfig *cfg, const KvlMlaBF16 *w,

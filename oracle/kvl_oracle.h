@@ -78,6 +78,11 @@ int orc_mla_compressed_state_prefill_bf16(const float *x, int seq_len, const Kvl
 int orc_mla_decode_compressed_bf16(float *out, const float *x, int position,
                                    const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
                                    KvlMlaCompressedState *s);
+/* The FP32 decode with the appended row rounded to bf16 before it is stored and attended: the
+ * library's BF16-latent history, restated over an FP32 state of bf16 values. */
+int orc_mla_decode_compressed_bf16_rows(float *out, const float *x, int position,
+                                        const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                        KvlMlaCompressedState *s);
 int orc_mla_decode_compressed_block_bf16(float *out, const float *x, int count, int start_position,
                                          const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
                                          KvlMlaCompressedState *s);

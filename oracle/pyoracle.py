@@ -36,6 +36,7 @@ _EXTRA = {
     "mla_prefill_materialized": (C.c_int, [abi.f32p, abi.f32p, C.c_int, abi.CFG, abi.W]),
     "mla_prefill_streaming_rows": (C.c_int, [abi.f32p, abi.f32p, C.c_int, C.POINTER(C.c_int), C.c_int,
                                              abi.CFG, abi.W]),
+    "mla_decode_compressed_bf16_rows": (C.c_int, [abi.f32p, abi.f32p, C.c_int, abi.CFG, abi.W, abi.CS]),
 }
 
 _cache = {}

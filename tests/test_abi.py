@@ -49,6 +49,9 @@ def test_struct_sizes_ctypes():
     assert C.sizeof(abi.KvlMlaState) == 40
     assert C.sizeof(abi.KvlMlaCompressedState) == 32
     assert C.sizeof(abi.KvlMlaCompressedQ8State) == 40
+    # the BF16-latent extension state: the FP32 state's layout with bf16 arrays
+    assert C.sizeof(abi.KvlMlaCompressedBF16State) == 32
+    assert abi.KvlMlaCompressedBF16State.rope.offset == abi.KvlMlaCompressedState.rope.offset == 24
 
 
 LAYOUT_C = r"""
@@ -98,8 +101,9 @@ def test_host_helpers_match_reference_formulas():
     kvl_bf16_to_f32 over every BF16 word is the word shifted into the high half
     (src/ops.c:12-17); the *_state_bytes of the three state kinds are sizeof(struct) plus
     capacity x the per-row bytes of the reference layouts (src/mla_state.c:57-64,
-    src/mla_compressed_state.c:47-50, src/mla_compressed_q8_state.c:104-109), and 0 for a
-    freed state."""
+    src/mla_compressed_state.c:47-50, src/mla_compressed_q8_state.c:104-109; the BF16-latent
+    extension state: 2 bytes per element, 1152 B per row at the Kimi dims), and 0 for a freed
+    state."""
     L = lib.load()
     words = np.arange(65536, dtype=np.uint32)
     got = np.array([L.kvl_bf16_to_f32(int(u)) for u in words], dtype=np.float32)
@@ -116,10 +120,33 @@ def test_host_helpers_match_reference_formulas():
         QD, DV = cfg.qk_nope_dim + cfg.qk_rope_dim, cfg.v_head_dim
         cases = ((abi.KvlMlaCompressedQ8State, "compressed_q8_state", R + 4 + 2 * DR),
                  (abi.KvlMlaCompressedState, "compressed_state", 4 * (R + DR)),
-                 (abi.KvlMlaState, "state", 4 * NH * (QD + DV)))
+                 (abi.KvlMlaState, "state", 4 * NH * (QD + DV)),
+                 (abi.KvlMlaCompressedBF16State, "compressed_bf16_state", 2 * (R + DR)))
         for T, name, per_row in cases:
             st = T()
             assert getattr(L, f"kvl_mla_{name}_init")(C.byref(st), C.byref(cfg), cap) == 0
             assert getattr(L, f"kvl_mla_{name}_bytes")(C.byref(st)) == C.sizeof(T) + cap * per_row, name
             getattr(L, f"kvl_mla_{name}_free")(C.byref(st))
             assert getattr(L, f"kvl_mla_{name}_bytes")(C.byref(st)) == 0, name
+
+
+def test_bf16_state_life_cycle_checks():
+    """The BF16-latent state keeps the FP32 state's argument rules (src/mla_compressed_state.c:
+    24-50): init rejects an odd qk_rope_dim or capacity <= 0, truncate only shortens, reset empties.
+    Host-only calls (no HIP call is made)."""
+    L = lib.load()
+    cfg = inputs.config(**inputs.KIMI)
+    st = abi.KvlMlaCompressedBF16State()
+    assert L.kvl_mla_compressed_bf16_state_init(C.byref(st), C.byref(cfg), 0) == -1
+    odd = inputs.config(**dict(inputs.KIMI, qk_rope_dim=63))
+    assert L.kvl_mla_compressed_bf16_state_init(C.byref(st), C.byref(odd), 8) == -1
+    assert L.kvl_mla_compressed_bf16_state_init(C.byref(st), C.byref(cfg), 8) == 0
+    assert (st.capacity, st.len, st.kv_lora_rank, st.qk_rope_dim) == (8, 0, 512, 64)
+    assert L.kvl_mla_compressed_bf16_state_truncate(C.byref(st), 1) == -1
+    st.len = 5
+    assert L.kvl_mla_compressed_bf16_state_truncate(C.byref(st), 3) == 0 and st.len == 3
+    assert L.kvl_mla_compressed_bf16_state_truncate(C.byref(st), -1) == -1
+    L.kvl_mla_compressed_bf16_state_reset(C.byref(st))
+    assert st.len == 0
+    L.kvl_mla_compressed_bf16_state_free(C.byref(st))
+    assert st.capacity == 0 and not st.latent and not st.rope

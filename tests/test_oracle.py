@@ -447,3 +447,83 @@ def test_prefill_rows_equal_full_prefill(name, dims, std, S, rows):
     bad = np.ascontiguousarray([0, S], dtype=np.int32)
     assert ORC.orc_mla_prefill_streaming_rows(f32(part), f32(x), S, bad.ctypes.data_as(C.POINTER(C.c_int)), 2,
                                               C.byref(cfg), C.byref(w)) == -1
+
+
+def absorbed_decode_f64(cfg, layer, xt, lat, rope):
+    """Decode output of token xt at position len(lat) - 1 over the given history rows (lat [L, R],
+    rope [L, DR], rotated keys), in float64 from the model definition: per head
+    q_lat = W_UK^T q_nope, scores (q_lat . c_j + RoPE(q_rope) . k_j) / sqrt(QD), softmax,
+    W_UV . sum_j p_j c_j, then o_proj."""
+    NH, DN, DR, DV = cfg.num_heads, cfg.qk_nope_dim, cfg.qk_rope_dim, cfg.v_head_dim
+    R = cfg.kv_lora_rank
+    f = lambda a: bf16_bits_to_f32(a).astype(np.float64)  # noqa: E731
+    Wq, Wb, Wo = f(layer.q_proj), f(layer.kv_b_proj).reshape(NH, DN + DV, R), f(layer.o_proj)
+    t = lat.shape[0] - 1
+    q = (Wq @ xt.astype(np.float64)).reshape(NH, DN + DR)
+    inv = cfg.rope_theta ** (-np.arange(0, DR, 2) / DR)
+    c, s = np.cos(t * inv), np.sin(t * inv)
+    C64, K64 = lat.astype(np.float64), rope.astype(np.float64)
+    heads = []
+    for h in range(NH):
+        a, b = q[h, DN::2], q[h, DN + 1::2]
+        qr = np.concatenate([a * c - b * s, b * c + a * s])
+        ql = Wb[h, :DN].T @ q[h, :DN]
+        sc = (C64 @ ql + K64 @ qr) / np.sqrt(DN + DR)
+        p = np.exp(sc - sc.max())
+        p /= p.sum()
+        heads.append(Wb[h, DN:] @ (p @ C64))
+    return Wo @ np.concatenate(heads)
+
+
+@pytest.mark.parametrize("dims,S,P", [(TINY, 9, 4), (LAB, 17, 8), (inputs.KIMI, 12, 6)],
+                         ids=["tiny", "lab", "kimi"])
+def test_bf16_rows_decode_pinned(dims, S, P):
+    """orc_mla_decode_compressed_bf16_rows (the checker of the library's BF16-latent state):
+    its appended rows are the bf16 rounding of the FP32 decode's rows (orc_f32_to_bf16_rne, bit
+    for bit), and its outputs equal the float64 absorbed decode over its own rows; the same
+    float64 decode over the FP32 decode's rows reproduces the FP32 decode (bit-exact with the
+    reference build), which pins the float64 restatement itself."""
+    cfg, layer, x = model(dims, 83, std=0.1 if dims is not inputs.KIMI else 0.02, n=S, xstd=0.5)
+    w = layer.struct()
+    R, DR, H = cfg.kv_lora_rank, cfg.qk_rope_dim, cfg.hidden_size
+    sts = []
+    for _ in range(2):
+        st = abi_state(cfg, S + 1)
+        assert O.mla_compressed_state_prefill_bf16(f32(x[:P]), P, C.byref(cfg), C.byref(w), C.byref(st)) == 0
+        sts.append(st)
+    fp, bf = sts
+    # both start from the same bf16-valued prefix
+    for st in sts:
+        lat = np.ctypeslib.as_array(st.latent, ((S + 1) * R,))
+        rope = np.ctypeslib.as_array(st.rope, ((S + 1) * DR,))
+        lat[:P * R] = bf16_bits_to_f32(f32_to_bf16_bits(lat[:P * R].copy()))
+        rope[:P * DR] = bf16_bits_to_f32(f32_to_bf16_bits(rope[:P * DR].copy()))
+    moved = 0
+    for t in range(P, S):
+        o_fp, o_bf = np.zeros(H, np.float32), np.zeros(H, np.float32)
+        # the FP32 decode over the same history (its own row t stays fp32)
+        assert O.mla_decode_compressed_bf16(f32(o_fp), f32(x[t]), t, C.byref(cfg), C.byref(w), C.byref(fp)) == 0
+        assert ORC.orc_mla_decode_compressed_bf16_rows(f32(o_bf), f32(x[t]), t, C.byref(cfg), C.byref(w),
+                                                       C.byref(bf)) == 0
+        assert bf.len == t + 1
+        lf = np.ctypeslib.as_array(fp.latent, ((S + 1) * R,)).reshape(S + 1, R)
+        rf = np.ctypeslib.as_array(fp.rope, ((S + 1) * DR,)).reshape(S + 1, DR)
+        lb = np.ctypeslib.as_array(bf.latent, ((S + 1) * R,)).reshape(S + 1, R)
+        rb = np.ctypeslib.as_array(bf.rope, ((S + 1) * DR,)).reshape(S + 1, DR)
+        np.testing.assert_array_equal(lb[t].view(np.uint32), (f32_to_bf16_bits(lf[t].copy()).astype(np.uint32) << 16))
+        np.testing.assert_array_equal(rb[t].view(np.uint32), (f32_to_bf16_bits(rf[t].copy()).astype(np.uint32) << 16))
+        assert rel_err(o_fp, absorbed_decode_f64(cfg, layer, x[t], lf[:t + 1], rf[:t + 1])) < 2e-6
+        assert rel_err(o_bf, absorbed_decode_f64(cfg, layer, x[t], lb[:t + 1], rb[:t + 1])) < 2e-6
+        moved += int(np.any(o_bf != o_fp))
+        # continue both from the bf16 row, so the next step again shares its history
+        lf[t], rf[t] = lb[t], rb[t]
+    assert moved > 0  # the rounding of the appended row is visible in the outputs
+    for st in sts:
+        O.mla_compressed_state_free(C.byref(st))
+
+
+def abi_state(cfg, cap):
+    from kvl_mla import abi
+    st = abi.KvlMlaCompressedState()
+    assert O.mla_compressed_state_init(C.byref(st), C.byref(cfg), cap) == 0
+    return st
