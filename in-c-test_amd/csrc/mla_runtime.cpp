@@ -642,30 +642,55 @@ struct SeqIn {
     int pos;
 };
 
-// Balanced split-K plan of the MFMA attention kernels: about wg_per_cu workgroups per CU in
-// total, shared among the sequences of a launch in proportion to their lengths (len of
-// total_rows); rows per split a multiple of the kernel's chunk (rounded down), at least four
-// chunks, at most 1024 rows for Q8 (every split < 2048 rows). The last split of a sequence
-// takes the remainder: nsplit = max(1, len / rows).
-long split_rows(int kind, long len, long total_rows, int ncu) {
-    const int chunk = kind == kAttnQ8Mfma ? 64 : kind == kAttnBF16Mfma ? 32 : 16;
-    const int wg_per_cu = kind == kAttnQ8Mfma || kind == kAttnBF16Mfma ? 1 : 3;
-    const double target = (double)wg_per_cu * ncu;
-    const long want = std::max(1L, std::lround(target * (double)len / (double)total_rows));
-    long r = len / (want * chunk) * chunk;
-    r = std::max<long>(r, 4L * chunk);
+// Split-K plan of the MFMA attention kernels. The kernels run about wg_per_cu workgroups per CU
+// (one for the Q8 and BF16 kernels, whose LDS rings fill a CU), so a launch should have at most
+// that many splits: one more makes a second round of workgroups that doubles the launch time.
+int plan_chunk(int kind) { return kind == kAttnQ8Mfma ? 64 : kind == kAttnBF16Mfma ? 32 : 16; }
+int plan_wg_per_cu(int kind) { return kind == kAttnQ8Mfma || kind == kAttnBF16Mfma ? 1 : 3; }
+
+// Splits of a history of len rows at r rows per split. Q8: a remainder of at most r/8 rows past
+// the last full split joins that split (its 1024-row cap would otherwise leave a one-row split
+// past the CU count, e.g. 8 x 32769 rows); the other kinds: ceil(len / r).
+long nsplit_of(int kind, long len, long r) {
+    if (kind == kAttnQ8Mfma) return std::max(1L, (len + r - 1 - r / 8) / r);
+    return std::max(1L, (len + r - 1) / r);
+}
+
+// Rows per split shared by the sequences of a launch: the smallest multiple of the kernel's chunk
+// (at least four chunks) whose split count sum_i nsplit_of(len_i, r) fits wg_per_cu x ncu, so the
+// launch runs as one round of workgroups. Q8: at most 1024 rows (long batches then take more
+// than one round).
+long plan_rows(int kind, const int *lens, int n, int ncu) {
+    const long chunk = plan_chunk(kind), target = (long)plan_wg_per_cu(kind) * ncu;
+    auto count = [&](long r) {
+        long c = 0;
+        for (int i = 0; i < n; ++i) c += nsplit_of(kind, lens[i], r);
+        return c;
+    };
+    long lo = 4, hi = 4;  // in chunks
+    for (int i = 0; i < n; ++i) hi = std::max(hi, ((long)lens[i] + chunk - 1) / chunk);
+    while (lo < hi) {  // count() does not increase with r
+        const long mid = (lo + hi) / 2;
+        if (count(mid * chunk) <= target) hi = mid;
+        else lo = mid + 1;
+    }
+    long r = lo * chunk;
     if (kind == kAttnQ8Mfma) r = std::min<long>(r, 1024L);
-    // at most kMaxSplits splits per sequence (the combine's per-split staging): very long
-    // histories get longer splits
-    const long rmin = (len + kMaxSplits - 1) / kMaxSplits;
-    if (r < rmin) r = (rmin + chunk - 1) / chunk * chunk;
     return r;
 }
 
-// Number of splits of a sequence whose attention reads `rows` (>= 1) rows.
-long plan_nsplit(int kind, long rows, long total_rows, int ncu) {
-    if (kind == kAttnGeneric) return 1;
-    return std::max(1L, rows / split_rows(kind, rows, total_rows, ncu));
+// Rows per split of one sequence under the launch's r. Q8: r (the last split takes the rest).
+// Other kinds: the sequence's nsplit_of(len, r) splits made equal (ceil(len / n) rows, rounded
+// up to the chunk), so its longest split is not longer than r. At most kMaxSplits splits per
+// sequence (the combine's per-split staging): very long histories get longer splits.
+long seq_rows(int kind, long len, long r) {
+    const long chunk = plan_chunk(kind), rmin = (len + kMaxSplits - 1) / kMaxSplits;
+    long rps = r;
+    if (kind != kAttnQ8Mfma) {
+        const long n = nsplit_of(kind, len, r);
+        rps = ((len + n - 1) / n + chunk - 1) / chunk * chunk;
+    }
+    return rps < rmin ? (rmin + chunk - 1) / chunk * chunk : rps;
 }
 
 // Attention plan of a launch group: the per-sequence descriptors with their split-K layout,
@@ -684,7 +709,6 @@ void plan_group(int fmt, const Dims &d, const SeqIn *seqs, int B, bool solo, Gro
     SeqTable &t = p.t;
     memset(&t, 0, sizeof t);
     t.n = B;
-    long total_rows = 0;
     p.lmax = 0;
     for (int i = 0; i < B; ++i) {
         SeqDesc &s = t.s[i];
@@ -693,7 +717,6 @@ void plan_group(int fmt, const Dims &d, const SeqIn *seqs, int B, bool solo, Gro
         s.c = seqs[i].m->c;
         s.pos = seqs[i].pos;
         s.len = seqs[i].pos + 1;
-        total_rows += s.len;
         p.lmax = std::max(p.lmax, s.len);
     }
     p.rps = 0;
@@ -705,11 +728,14 @@ void plan_group(int fmt, const Dims &d, const SeqIn *seqs, int B, bool solo, Gro
         }
         p.total_splits = fmt == kFmtExp ? B * d.NH : B;
     } else {
+        int lens[kMaxBatch];
+        for (int i = 0; i < B; ++i) lens[i] = t.s[i].len;
+        const long r = solo ? 0 : plan_rows(p.kind, lens, B, ncu);
         for (int i = 0; i < B; ++i) {
             SeqDesc &s = t.s[i];
             s.split0 = p.total_splits;
-            s.nsplit = (int)plan_nsplit(p.kind, s.len, solo ? s.len : total_rows, ncu);
-            s.rps = (int)split_rows(p.kind, s.len, solo ? s.len : total_rows, ncu);
+            s.rps = (int)seq_rows(p.kind, s.len, solo ? plan_rows(p.kind, &lens[i], 1, ncu) : r);
+            s.nsplit = (int)nsplit_of(p.kind, s.len, s.rps);
             p.total_splits += s.nsplit;
             p.rps = std::max(p.rps, s.rps);
         }
