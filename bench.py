@@ -317,20 +317,28 @@ def main():
                                                                 C.byref(wstructs[0]), C.byref(bst)), "block decode")
             lib.check(L.kvl_mla_compressed_q8_state_truncate(C.byref(bst), CTX), "truncate")
 
+        def single():
+            lib.check(L.kvl_mla_decode_compressed_q8_bf16(fp(o_ser[0]), fp(xb[0]), CTX, C.byref(cfg),
+                                                          C.byref(wstructs[0]), C.byref(bst)), "single decode")
+            lib.check(L.kvl_mla_compressed_q8_state_truncate(C.byref(bst), CTX), "truncate")
+
         times = {}
-        for name, fn in (("serial", serial), ("block", block)):
+        for name, fn in (("single", single), ("serial", serial), ("block", block)):
             fn()
-            reps = 5
-            ts = time.perf_counter()
+            reps = 10
+            ts = []
             for _ in range(reps):
+                t0 = time.perf_counter()
                 fn()
-            times[name] = (time.perf_counter() - ts) * 1e3 / reps
+                ts.append(time.perf_counter() - t0)
+            times[name] = sorted(ts)[reps // 2] * 1e3  # median
         same = bool(np.array_equal(o_blk, o_ser))
-        result["block_verify"] = {"tokens": T, "context": CTX, "block_ms": round(times["block"], 3),
-                                  "serial_ms": round(times["serial"], 3), "bit_identical": same,
-                                  "api": "host buffers, synchronous"}
-        log(f"[bench] block verify {T} tokens @{CTX}: block {times['block']:.3f} ms, "
-            f"serial {times['serial']:.3f} ms, identical {same}")
+        result["block_verify"] = {"tokens": T, "context": CTX, "block_ms": round(times["block"], 4),
+                                  "serial_ms": round(times["serial"], 4), "single_ms": round(times["single"], 4),
+                                  "block_over_single": round(times["block"] / times["single"], 3),
+                                  "bit_identical": same, "api": "host buffers, synchronous (median of 10)"}
+        log(f"[bench] block verify {T} tokens @{CTX}: block {times['block']:.4f} ms, "
+            f"serial {times['serial']:.4f} ms, single {times['single']:.4f} ms, identical {same}")
         L.kvl_mla_compressed_q8_state_free(C.byref(bst))
 
     # ---- causal prefill, 4096 tokens -----------------------------------------------------

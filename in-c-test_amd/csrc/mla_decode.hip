@@ -1070,7 +1070,10 @@ struct AttnArgs {
     float *scores;
     int rps, lmax;
     float smscale;
+    int members;  // > 0: a block launch of that many members (split_of)
 };
+
+constexpr int kXcds = 8;  // XCDs of an MI355X; workgroups are dispatched to them round-robin
 
 // Block -> (sequence, split): splits of the sequences are numbered consecutively.
 __device__ __forceinline__ int find_seq(const SeqTable &t, int bid) {
@@ -1078,6 +1081,29 @@ __device__ __forceinline__ int find_seq(const SeqTable &t, int bid) {
     for (int i = 1; i < t.n; ++i)
         if (bid >= t.s[i].split0) b = i;
     return b;
+}
+
+// Workgroup -> (sequence b, split, index of its partial). A normal launch numbers the splits of
+// its sequences consecutively. A block launch (members > 0: the sequences are the tokens of one
+// block over a shared history, each with the split plan of its lone decode) goes split-major and
+// XCD-affine: workgroup i runs on XCD i % kXcds, and split s of every member sits at position
+// members * (s / kXcds) + member of XCD s % kXcds's order, so the members of a split run at the
+// same time on one XCD and its L2 serves the history rows they share. A workgroup past its
+// member's last split has nothing to do (false).
+__device__ __forceinline__ bool split_of(const AttnArgs &a, int &b, int &split, int &pidx) {
+    const int sid = blockIdx.x;
+    if (a.members > 0) {
+        const int j = sid / kXcds;
+        b = j % a.members;
+        split = kXcds * (j / a.members) + sid % kXcds;
+        if (split >= a.t.s[b].nsplit) return false;
+        pidx = a.t.s[b].split0 + split;
+        return true;
+    }
+    b = find_seq(a.t, sid);
+    split = sid - a.t.s[b].split0;
+    pidx = sid;
+    return true;
 }
 
 // ---- generic VALU path: any dims and formats, one block per problem -----------------
@@ -1181,9 +1207,9 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float rows[kF32Ch * kF32Rs];
     __shared__ float sp[4][16][16];
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
-    const int b = find_seq(a.t, blockIdx.x);
+    int b, split, pidx;
+    if (!split_of(a, b, split, pidx)) return;
     const SeqDesc &s = a.t.s[b];
-    const int split = blockIdx.x - s.split0;
     const int r0 = split * s.rps;
     const int r1 = split == s.nsplit - 1 ? s.len : r0 + s.rps;  // last split takes the rest
     const float *glat = (const float *)s.a;
@@ -1283,7 +1309,7 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
             for (int k = 0; k < 4; ++k) acc[t] = mfma_f32(pr4[k], rows[(4 * k + g) * kF32Rs + col], acc[t]);
         }
     }
-    float *P = a.part + (size_t)blockIdx.x * 16 * 514;
+    float *P = a.part + (size_t)pidx * 16 * 514;
 #pragma unroll
     for (int t = 0; t < 8; ++t)
 #pragma unroll
@@ -1352,10 +1378,9 @@ __global__ __launch_bounds__(256) void k_attn_bf16_mfma(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t smem[kB16SmemB];
     const int tid = threadIdx.x, l = tid & 63, n = l & 15, g = l >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int sid = blockIdx.x;
-    const int b = find_seq(a.t, sid);
+    int b, split, pidx;
+    if (!split_of(a, b, split, pidx)) return;
     const SeqDesc &s = a.t.s[b];
-    const int split = sid - s.split0;
     const int r0 = split * s.rps;
     const int r1 = split == s.nsplit - 1 ? s.len : r0 + s.rps;  // last split takes the rest
     const int nch = (r1 - r0 + kB16Ch - 1) / kB16Ch;
@@ -1488,7 +1513,7 @@ __global__ __launch_bounds__(256) void k_attn_bf16_mfma(AttnArgs a) {
             acc[t] = mfma_bf16(pl, bt, acc[t]);
         }
     }
-    float *P = a.part + (size_t)sid * 16 * 514;
+    float *P = a.part + (size_t)pidx * 16 * 514;
 #pragma unroll
     for (int t = 0; t < 8; ++t)
 #pragma unroll
@@ -1940,20 +1965,19 @@ __device__ __forceinline__ void q8_mix_role(const AttnArgs &a, uint8_t *smem, in
 __global__ __launch_bounds__(512) void k_attn_q8_mfma(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t smem[kQ8SmemB];
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int sid = blockIdx.x;
-    const int b = find_seq(a.t, sid);
+    int b, split, pidx;
+    if (!split_of(a, b, split, pidx)) return;
     const SeqDesc &s = a.t.s[b];
-    const int split = sid - s.split0;
     const int r0 = split * s.rps;
     const int r1 = split == s.nsplit - 1 ? s.len : r0 + s.rps;  // last split takes the rest
     const int nch = (r1 - r0 + kQ8Ch - 1) / kQ8Ch;
-    if (w >= 4) q8_mix_role(a, smem, w - 4, b, r0, r1, nch, sid);
-    else q8_score_role(a, smem, w, b, r0, r1, nch, sid);
+    if (w >= 4) q8_mix_role(a, smem, w - 4, b, r0, r1, nch, pidx);
+    else q8_score_role(a, smem, w, b, r0, r1, nch, pidx);
 }
 
 hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t, const Dims &d,
                             int rows_per_split, int total_splits, int lmax,
-                            const DecodeWork &w) {
+                            const DecodeWork &w, int members) {
     AttnArgs a;
     a.t = t;
     a.d = d;
@@ -1968,12 +1992,19 @@ hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t
     a.rps = rows_per_split;
     a.lmax = lmax;
     a.smscale = 1.0f / sqrtf((float)d.QD);
+    a.members = kind == kAttnGeneric ? 0 : members;
+    int grid = total_splits;
+    if (a.members > 0) {
+        int maxns = 0;
+        for (int i = 0; i < t.n; ++i) maxns = max(maxns, t.s[i].nsplit);
+        grid = kXcds * t.n * ((maxns + kXcds - 1) / kXcds);
+    }
     if (kind == kAttnQ8Mfma) {
-        hipLaunchKernelGGL(k_attn_q8_mfma, dim3(total_splits), dim3(512), 0, st, a);
+        hipLaunchKernelGGL(k_attn_q8_mfma, dim3(grid), dim3(512), 0, st, a);
     } else if (kind == kAttnF32Mfma) {
-        hipLaunchKernelGGL(k_attn_f32_mfma, dim3(total_splits), dim3(256), 0, st, a);
+        hipLaunchKernelGGL(k_attn_f32_mfma, dim3(grid), dim3(256), 0, st, a);
     } else if (kind == kAttnBF16Mfma) {
-        hipLaunchKernelGGL(k_attn_bf16_mfma, dim3(total_splits), dim3(256), 0, st, a);
+        hipLaunchKernelGGL(k_attn_bf16_mfma, dim3(grid), dim3(256), 0, st, a);
     } else {
         const int P = fmt == kFmtExp ? t.n * d.NH : t.n;
         if (fmt == kFmtQ8)
@@ -2118,17 +2149,21 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
     }
 }
 
-// Compressed formats with R = 512, DV = 128: the same algebra in fewer serial phases, over
-// 2 blocks per (sequence, head): block half computes the whole mix (thread k: latent column k)
-// and W_UV rows [64 half, 64 half + 64) of the head output. Wave 0 requests the split maxima
-// and denominators before anything else, so its wait covers one round trip; the W_UV slice
-// (thread t: row t / 8, columns 64 (t % 8) .. + 63) and the first 32 partials of each column
-// are requested meanwhile and consumed after the barrier. The head output is also written as
-// bf16 hi | lo planes (w.hos), the operand format of launch_gemv_xs.
-constexpr int kCombPre = 32;
-__global__ __launch_bounds__(512) void k_combine_r512(CombineArgs a) {
+// Compressed formats with R = 512, DV = 128: the same algebra in one round of memory requests,
+// over 2 blocks of 1024 threads per (sequence, head) (twice the blocks of one per head, which
+// measured faster than reading each partial once). Block half computes the whole mix and W_UV
+// rows [64 half, 64 half + 64) of the head output. Every load is issued up front: wave 0 the
+// split maxima and denominators; thread t the partials of latent columns 4 (t % 128) .. +3 for
+// the splits s = t / 128 (mod 8), 16 bytes per split (the first kCombPre of them; longer
+// histories loop), and its W_UV slice (row t / 16, columns 32 (t % 16) .. + 31). After the
+// split weights are in LDS, each thread sums its splits in order, the 8 split groups are added
+// in group order through LDS, and 16 lanes per W_UV row reduce its dot product. The head output
+// is also written as bf16 hi | lo planes (w.hos), the operand format of launch_gemv_xs.
+constexpr int kCombPre = 8;
+__global__ __launch_bounds__(1024) void k_combine_r512(CombineArgs a) {
     __shared__ float mx[512];
     __shared__ float wts[kMaxSplits];
+    __shared__ v4f red[8][128];
     __shared__ float sinv;
     const int NH = a.d.NH, tid = threadIdx.x;
     const int half = blockIdx.x & 1, bh = blockIdx.x >> 1, b = bh / NH, h = bh % NH;
@@ -2137,17 +2172,22 @@ __global__ __launch_bounds__(512) void k_combine_r512(CombineArgs a) {
     const size_t stride = (size_t)NH * (512 + 2);
     const float *P = a.part + (size_t)s.split0 * stride;
     const float *Pm = P + (size_t)NH * 512 + h;  // split i: m at Pm[i * stride], l at + NH
-    const int i0 = min(tid, ns - 1);
-    const float m0 = Pm[(size_t)i0 * stride], l0 = Pm[(size_t)i0 * stride + NH];
-    const int dd = 64 * half + (tid >> 3), q = tid & 7;
-    const uint16_t *row = a.kv_b + ((size_t)h * (a.d.DN + 128) + a.d.DN + dd) * 512 + 64 * q;
-    v4i wv[8];
+    float m0 = 0.f, l0 = 0.f;
+    if (tid < 64) {
+        const int i0 = min(tid, ns - 1);
+        m0 = Pm[(size_t)i0 * stride];
+        l0 = Pm[(size_t)i0 * stride + NH];
+    }
+    const int dd = 64 * half + (tid >> 4), q = tid & 15;
+    const uint16_t *row = a.kv_b + ((size_t)h * (a.d.DN + 128) + a.d.DN + dd) * 512 + 32 * q;
+    v4i wv[4];
 #pragma unroll
-    for (int c = 0; c < 8; ++c) wv[c] = *(const v4i *)(row + 8 * c);
-    const float *Pg = P + (size_t)h * 512 + tid;
-    float pre[kCombPre];
+    for (int c = 0; c < 4; ++c) wv[c] = *(const v4i *)(row + 8 * c);
+    const int c4 = tid & 127, sg = tid >> 7;
+    const float *Pg = P + (size_t)h * 512 + 4 * c4;
+    v4f pre[kCombPre];
 #pragma unroll
-    for (int i = 0; i < kCombPre; ++i) pre[i] = Pg[(size_t)min(i, ns - 1) * stride];
+    for (int i = 0; i < kCombPre; ++i) pre[i] = *(const v4f *)(Pg + (size_t)min(sg + 8 * i, ns - 1) * stride);
     if (tid < 64) {
         float m = tid < ns ? m0 : -INFINITY;
         for (int i = tid + 64; i < ns; i += 64) m = fmaxf(m, Pm[(size_t)i * stride]);
@@ -2167,37 +2207,43 @@ __global__ __launch_bounds__(512) void k_combine_r512(CombineArgs a) {
         if (tid == 0) sinv = 1.0f / den;
     }
     __syncthreads();
-    float v0 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f;
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < kCombPre; i += 4) {
-        if (i < ns) v0 = fmaf(pre[i], wts[i], v0);
-        if (i + 1 < ns) v1 = fmaf(pre[i + 1], wts[i + 1], v1);
-        if (i + 2 < ns) v2 = fmaf(pre[i + 2], wts[i + 2], v2);
-        if (i + 3 < ns) v3 = fmaf(pre[i + 3], wts[i + 3], v3);
-    }
-    int i = kCombPre;
-    for (; i + 8 <= ns; i += 8) {
-        float p[8];
+    for (int i = 0; i < kCombPre; ++i) {
+        const int sp = sg + 8 * i;
+        if (sp < ns) {
+            const float wt = wts[sp];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) p[u] = Pg[(size_t)(i + u) * stride];
-        v0 = fmaf(p[0], wts[i], v0);
-        v1 = fmaf(p[1], wts[i + 1], v1);
-        v2 = fmaf(p[2], wts[i + 2], v2);
-        v3 = fmaf(p[3], wts[i + 3], v3);
-        v0 = fmaf(p[4], wts[i + 4], v0);
-        v1 = fmaf(p[5], wts[i + 5], v1);
-        v2 = fmaf(p[6], wts[i + 6], v2);
-        v3 = fmaf(p[7], wts[i + 7], v3);
+            for (int e = 0; e < 4; ++e) acc[e] = fmaf(pre[i][e], wt, acc[e]);
+        }
     }
-    for (; i < ns; ++i) v0 = fmaf(Pg[(size_t)i * stride], wts[i], v0);
-    const float v = ((v0 + v1) + (v2 + v3)) * sinv;
-    if (half == 0) a.mix[((size_t)b * NH + h) * 512 + tid] = v;
-    mx[tid] = v;
+    for (int sp = sg + 8 * kCombPre; sp < ns; sp += 8 * kCombPre) {
+        v4f more[kCombPre];
+#pragma unroll
+        for (int i = 0; i < kCombPre; ++i) more[i] = *(const v4f *)(Pg + (size_t)min(sp + 8 * i, ns - 1) * stride);
+#pragma unroll
+        for (int i = 0; i < kCombPre; ++i) {
+            if (sp + 8 * i < ns) {
+                const float wt = wts[sp + 8 * i];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[e] = fmaf(more[i][e], wt, acc[e]);
+            }
+        }
+    }
+    red[sg][c4] = acc;
     __syncthreads();
-    const float *mh = mx + 64 * q;
+    if (tid < 512) {
+        const int cq = tid >> 2, e = tid & 3;
+        float v = red[0][cq][e];
+#pragma unroll
+        for (int g8 = 1; g8 < 8; ++g8) v += red[g8][cq][e];
+        mx[tid] = v * sinv;
+    }
+    __syncthreads();
+    const float *mh = mx + 32 * q;
     float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
+    for (int c = 0; c < 4; ++c) {
         const v4f m0v = *(const v4f *)(mh + 8 * c);
         const v4f m1v = *(const v4f *)(mh + 8 * c + 4);
         const uint32_t u0 = (uint32_t)wv[c][0], u1 = (uint32_t)wv[c][1];
@@ -2211,15 +2257,12 @@ __global__ __launch_bounds__(512) void k_combine_r512(CombineArgs a) {
         acc0 = fmaf(__uint_as_float(u3 << 16), m1v.z, acc0);
         acc1 = fmaf(__uint_as_float(u3 & 0xffff0000u), m1v.w, acc1);
     }
-    float acc = acc0 + acc1;
-    acc += dpp_f32<0xB1>(acc);   // quad_perm [1,0,3,2]: lanes t ^ 1
-    acc += dpp_f32<0x4E>(acc);   // quad_perm [2,3,0,1]: lanes t ^ 2
-    acc += dpp_f32<0x12C>(acc);  // row_ror:12 (lane i reads lane i + 4 of its row): t % 8 == 0 completes
+    const float hsum = row16_sum(acc0 + acc1);  // the 16 lanes of row dd
     if (q == 0) {
         const size_t o = (size_t)b * a.d.HO + (size_t)h * 128 + dd;
-        a.ho[o] = acc;
+        a.ho[o] = hsum;
         uint16_t hi, lo;
-        split_bf16(acc, hi, lo);
+        split_bf16(hsum, hi, lo);
         a.hos[o] = hi;
         a.hos[(size_t)a.t.n * a.d.HO + o] = lo;
     }
@@ -2230,7 +2273,7 @@ hipError_t launch_combine(hipStream_t st, int fmt, const SeqTable &t, const Dims
     if (d.R > kMaxR) return hipErrorInvalidValue;
     CombineArgs a{t, d, w.part, kv_b, w.mix, w.ho, w.hos, fmt};
     if (combine_writes_hos(fmt, d))
-        hipLaunchKernelGGL(k_combine_r512, dim3(2 * t.n * d.NH), dim3(512), 0, st, a);
+        hipLaunchKernelGGL(k_combine_r512, dim3(2 * t.n * d.NH), dim3(1024), 0, st, a);
     else
         hipLaunchKernelGGL(k_combine, dim3(t.n * d.NH), dim3(256), 0, st, a);
     return hipGetLastError();

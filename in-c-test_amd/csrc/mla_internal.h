@@ -139,9 +139,12 @@ hipError_t launch_append_qprep(hipStream_t st, int fmt, const SeqTable &t, const
 // kind: 0 = generic VALU (any dims, one split per problem), 1 = fp32 MFMA (Kimi dims),
 // 2 = int8 MFMA (Kimi dims, Q8 rows), 3 = bf16 MFMA (Kimi dims, BF16 rows).
 enum AttnKind : int { kAttnGeneric = 0, kAttnF32Mfma = 1, kAttnQ8Mfma = 2, kAttnBF16Mfma = 3 };
+// members > 0: the sequences are the members of one block (tokens of one sequence, each with
+// the split plan of its lone decode); the workgroups then go split-major, the members of a split
+// together on one XCD, so that they share the history rows in its L2.
 hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t, const Dims &d,
                             int rows_per_split, int total_splits, int lmax,
-                            const DecodeWork &w);
+                            const DecodeWork &w, int members = 0);
 
 // Normalise the split partials into mix[(b*G + g), DVm] and, for the compressed formats,
 // apply W_UV: ho[b, h*DV + d] = sum_r kv_b[h*(DN+DV) + DN + d, r] * mix[b*NH + h, r].

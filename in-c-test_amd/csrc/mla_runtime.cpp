@@ -659,9 +659,15 @@ long nsplit_of(int kind, long len, long r) {
 // Rows per split shared by the sequences of a launch: the smallest multiple of the kernel's chunk
 // (at least four chunks) whose split count sum_i nsplit_of(len_i, r) fits wg_per_cu x ncu, so the
 // launch runs as one round of workgroups. Q8: at most 1024 rows (long batches then take more
-// than one round).
+// than one round). A lone sequence gets at most lone_splits(kind) splits (about 0.6 MB of a
+// 32K-row history each): its launch is bound by the workgroups' start-up and the combine, not
+// by bandwidth, and the lone plan is also the plan of each token of a block decode
+// (bit-identical to single decodes), whose Q8 workgroups (32 x tokens) then fit one round for
+// blocks of up to 8 tokens.
+long lone_splits(int kind) { return kind == kAttnQ8Mfma ? 32 : kind == kAttnBF16Mfma ? 64 : 128; }
 long plan_rows(int kind, const int *lens, int n, int ncu) {
-    const long chunk = plan_chunk(kind), target = (long)plan_wg_per_cu(kind) * ncu;
+    const long chunk = plan_chunk(kind);
+    const long target = n == 1 ? lone_splits(kind) : (long)plan_wg_per_cu(kind) * ncu;
     auto count = [&](long r) {
         long c = 0;
         for (int i = 0; i < n; ++i) c += nsplit_of(kind, lens[i], r);
@@ -869,7 +875,7 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
     }
     {
         StageTimer tm(3);
-        HIP_TRY(launch_attention(st, kind, fmt, t, d, rps, total_splits, lmax, w));
+        HIP_TRY(launch_attention(st, kind, fmt, t, d, rps, total_splits, lmax, w, solo ? B : 0));
     }
     {
         StageTimer tm(4);
