@@ -7,6 +7,7 @@
  * mla_compressed_q8_state.h) keeps its exact semantics: host buffers in and out, host
  * state arrays authoritative, synchronous calls. These extensions add what a GPU library
  * needs on top of it:
+ *   - a BF16-latent history state (1152 B per row at the Kimi-VL shapes);
  *   - pinned device copies of a layer's weights (the reference borrows them per call);
  *   - explicit re-synchronisation of a state whose rows were edited in place on the host;
  *   - batched (ragged) decode over many sequences in one call;
