@@ -1060,8 +1060,10 @@ hipError_t launch_append_qprep(hipStream_t st, int fmt, const SeqTable &t, const
 // ================================================================ attention ============
 
 struct AttnArgs {
-    SeqTable t;
-    Dims d;
+    // Read first by every workgroup (kernel arguments live in device memory and the first read
+    // of each 64-byte line is a round trip): the fields the start-up needs come before the
+    // sequence table, so that one round trip brings them and a second one the workgroup's
+    // SeqDesc.
     float *part;
     const float *qf;
     const int8_t *qhi, *qlo;
@@ -1071,6 +1073,12 @@ struct AttnArgs {
     int rps, lmax;
     float smscale;
     int members;  // > 0: a block launch of that many members (split_of)
+    int nseq;     // = t.n
+    // first split of each sequence (t.s[i].split0), contiguous: the workgroup -> sequence lookup
+    // reads it with a few wide scalar loads instead of walking t.s
+    int sp0[kMaxBatch];
+    Dims d;
+    SeqTable t;
 };
 
 constexpr int kXcds = 8;  // XCDs of an MI355X; workgroups are dispatched to them round-robin
@@ -1100,8 +1108,12 @@ __device__ __forceinline__ bool split_of(const AttnArgs &a, int &b, int &split, 
         pidx = a.t.s[b].split0 + split;
         return true;
     }
-    b = find_seq(a.t, sid);
-    split = sid - a.t.s[b].split0;
+    // the splits of the sequences are numbered consecutively: b = #{i >= 1 : sp0[i] <= sid}
+    int bb = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxBatch; ++i) bb += (i < a.nseq && sid >= a.sp0[i]) ? 1 : 0;
+    b = bb;
+    split = sid - a.sp0[b];
     pidx = sid;
     return true;
 }
@@ -1646,8 +1658,8 @@ __device__ __forceinline__ void put_q8_weights(int8_t *wqc, const float *pv, flo
 // same LDS flags after A, so all eight take the same barriers. Everything the score waves read
 // per chunk (codes, RoPE keys, scales) arrives in LDS by the mix waves' DMA, so their steps
 // never wait on global-memory latency.
-__device__ __forceinline__ void q8_score_role(const AttnArgs &a, uint8_t *smem, int w, int b, int r0, int r1, int nch,
-                                              int sid) {
+__device__ __forceinline__ void q8_score_role(const AttnArgs &a, const SeqDesc &sd, uint8_t *smem, int w, int b,
+                                              int r0, int r1, int nch, int sid) {
     int8_t *wq = (int8_t *)(smem + kQ8WqOff);
     int *oflag = (int *)(smem + kQ8FlagOff);
     float *mloc = (float *)(smem + kQ8MlOff);
@@ -1655,7 +1667,7 @@ __device__ __forceinline__ void q8_score_role(const AttnArgs &a, uint8_t *smem, 
     float *lsum = (float *)(smem + kQ8LsOff);
     float *smx = (float *)(smem + kQ8SmOff);
     const int tid = threadIdx.x, l = tid & 63, n = l & 15, g = l >> 4;
-    const float *gscl = (const float *)a.t.s[b].b;
+    const float *gscl = (const float *)sd.b;
     const int rowl = 16 * w + n;  // chunk row of this lane
     int sc_base[2], rp_off[2];
 #pragma unroll
@@ -1683,9 +1695,14 @@ __device__ __forceinline__ void q8_score_role(const AttnArgs &a, uint8_t *smem, 
     {
         const int nr = r1 - r0;
         float sv[8];
+        // rows past the split end re-read its last row (a duplicate does not change the max)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) sv[i] = tid + 256 * i < nr ? gscl[r0 + tid + 256 * i] : 0.f;
+        for (int i = 0; i < 8; ++i) sv[i] = gscl[r0 + min(tid + 256 * i, nr - 1)];
         lds_barrier();  // P0
+        // the loads complete after P0: the mix waves' first DMA is not held up by them (without
+        // this the compiler may compute the max, and so wait for the loads, before the barrier)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(sv[i]));
         float m = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) m = fmaxf(m, sv[i]);
@@ -1806,17 +1823,17 @@ __device__ __forceinline__ void q8_score_role(const AttnArgs &a, uint8_t *smem, 
     }
 }
 
-__device__ __forceinline__ void q8_mix_role(const AttnArgs &a, uint8_t *smem, int mw, int b, int r0, int r1, int nch,
-                                            int sid) {
+__device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const SeqDesc &sd, uint8_t *smem, int mw, int b,
+                                            int r0, int r1, int nch, int sid) {
     const int8_t *wq = (const int8_t *)(smem + kQ8WqOff);
     const int *oflag = (const int *)(smem + kQ8FlagOff);
     const float *abuf = (const float *)(smem + kQ8AlOff);
     const float *smx = (const float *)(smem + kQ8SmOff);
     const uint32_t sbase = lds_addr(smem);
     const int l = threadIdx.x & 63, n = l & 15, g = l >> 4;
-    const int8_t *gcodes = (const int8_t *)a.t.s[b].a;
-    const float *gscl = (const float *)a.t.s[b].b;
-    const uint16_t *grope = (const uint16_t *)a.t.s[b].c;
+    const int8_t *gcodes = (const int8_t *)sd.a;
+    const float *gscl = (const float *)sd.b;
+    const uint16_t *grope = (const uint16_t *)sd.c;
     // DMA plan. Codes: mix wave mw copies row pairs 8mw .. 8mw+7 of a chunk; lane l of
     // instruction k takes row 2(8mw + k) + (l >> 5), physical slot l & 31 (logical slot
     // (l & 31) ^ swz). RoPE keys: instruction k of wave mw covers rows 8(2mw + k) .. +7, lane l
@@ -1971,8 +1988,8 @@ __global__ __launch_bounds__(512) void k_attn_q8_mfma(AttnArgs a) {
     const int r0 = split * s.rps;
     const int r1 = split == s.nsplit - 1 ? s.len : r0 + s.rps;  // last split takes the rest
     const int nch = (r1 - r0 + kQ8Ch - 1) / kQ8Ch;
-    if (w >= 4) q8_mix_role(a, smem, w - 4, b, r0, r1, nch, pidx);
-    else q8_score_role(a, smem, w, b, r0, r1, nch, pidx);
+    if (w >= 4) q8_mix_role(a, s, smem, w - 4, b, r0, r1, nch, pidx);
+    else q8_score_role(a, s, smem, w, b, r0, r1, nch, pidx);
 }
 
 hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t, const Dims &d,
@@ -1993,6 +2010,8 @@ hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t
     a.lmax = lmax;
     a.smscale = 1.0f / sqrtf((float)d.QD);
     a.members = kind == kAttnGeneric ? 0 : members;
+    a.nseq = t.n;
+    for (int i = 0; i < kMaxBatch; ++i) a.sp0[i] = i < t.n ? t.s[i].split0 : 0;
     int grid = total_splits;
     if (a.members > 0) {
         int maxns = 0;
