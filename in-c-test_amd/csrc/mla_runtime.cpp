@@ -1594,6 +1594,19 @@ int kvl_mla_prefill_compressed_q8_state_device(float *d_out, const float *d_x, i
     return prefill_state_device(d_out, d_x, seq_len, cfg, w, state, false);
 }
 
+int kvl_mla_prefill_compressed_bf16_state_bf16(float *out, const float *x, int seq_len, const KvlMlaConfig *cfg,
+                                               const KvlMlaBF16 *w, KvlMlaCompressedBF16State *state) {
+    Guard guard;
+    return prefill_state(out, x, seq_len, cfg, w, state);
+}
+
+int kvl_mla_prefill_compressed_bf16_state_device(float *d_out, const float *d_x, int seq_len,
+                                                 const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                                 KvlMlaCompressedBF16State *state) {
+    Guard guard;
+    return prefill_state_device(d_out, d_x, seq_len, cfg, w, state, false);
+}
+
 // ---- include/kvl/mla_state.h (expanded state) ------------------------------------------
 
 int kvl_mla_state_init(KvlMlaState *state, const KvlMlaConfig *cfg, int capacity) {
@@ -2019,6 +2032,14 @@ int kvl_mla_attention_layer_device(float *d_h, float *d_n2, int batch, const Kvl
                                    const KvlMlaBF16 *w, const uint16_t *input_norm,
                                    const uint16_t *post_attn_norm, KvlMlaCompressedState *const *states,
                                    unsigned flags) {
+    Guard guard;
+    return attention_layer_device(d_h, d_n2, batch, cfg, w, input_norm, post_attn_norm, states, flags);
+}
+
+int kvl_mla_attention_layer_bf16_device(float *d_h, float *d_n2, int batch, const KvlMlaConfig *cfg,
+                                        const KvlMlaBF16 *w, const uint16_t *input_norm,
+                                        const uint16_t *post_attn_norm,
+                                        KvlMlaCompressedBF16State *const *states, unsigned flags) {
     Guard guard;
     return attention_layer_device(d_h, d_n2, batch, cfg, w, input_norm, post_attn_norm, states, flags);
 }

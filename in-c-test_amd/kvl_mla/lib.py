@@ -87,6 +87,11 @@ EXT_API = {
                                                           BSP, C.c_uint]),
     "mla_compressed_bf16_state_fill_synthetic": (C.c_int, [abi.BS, C.c_int, C.c_int, C.c_uint64]),
     "mla_compressed_bf16_state_pull": (C.c_int, [abi.BS, C.c_int, C.c_int]),
+    "mla_prefill_compressed_bf16_state_bf16": (C.c_int, [abi.f32p, abi.f32p, C.c_int, abi.CFG, abi.W, abi.BS]),
+    "mla_prefill_compressed_bf16_state_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, abi.CFG, abi.W,
+                                                           abi.BS]),
+    "mla_attention_layer_bf16_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, abi.CFG, abi.W, abi.u16p,
+                                                   abi.u16p, BSP, C.c_uint]),
 }
 
 # stage 1 is the fused append + query preparation of the compressed formats (the expanded

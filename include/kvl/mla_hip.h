@@ -171,6 +171,10 @@ int kvl_mla_attention_layer_device(float *d_h, float *d_n2, int batch, const Kvl
                                    const KvlMlaBF16 *w, const uint16_t *input_norm,
                                    const uint16_t *post_attn_norm, KvlMlaCompressedState *const *states,
                                    unsigned flags);
+int kvl_mla_attention_layer_bf16_device(float *d_h, float *d_n2, int batch, const KvlMlaConfig *cfg,
+                                        const KvlMlaBF16 *w, const uint16_t *input_norm,
+                                        const uint16_t *post_attn_norm,
+                                        KvlMlaCompressedBF16State *const *states, unsigned flags);
 
 /* Stream-ordered causal prefill over device buffers (d_x, d_out [seq_len, hidden] fp32);
  * same arithmetic as kvl_mla_prefill_bf16. */
@@ -201,6 +205,13 @@ int kvl_mla_prefill_compressed_state_device(float *d_out, const float *d_x, int 
 int kvl_mla_prefill_compressed_q8_state_device(float *d_out, const float *d_x, int seq_len,
                                                const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
                                                KvlMlaCompressedQ8State *state);
+/* The same pair for the BF16-latent state (rows bit-identical to its state prefill's). */
+int kvl_mla_prefill_compressed_bf16_state_bf16(float *out, const float *x, int seq_len,
+                                               const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                               KvlMlaCompressedBF16State *state);
+int kvl_mla_prefill_compressed_bf16_state_device(float *d_out, const float *d_x, int seq_len,
+                                                 const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
+                                                 KvlMlaCompressedBF16State *state);
 
 /* The library's HIP stream (hipStream_t) and helpers for callers without a HIP binding. */
 void *kvl_mla_stream(void);

@@ -342,3 +342,110 @@ def test_device_api_graph_replay_and_truncate():
     for s in sts + [st]:
         L.kvl_mla_compressed_bf16_state_free(C.byref(s))
     L.kvl_mla_release_weights(C.byref(w))
+
+
+def test_fused_prefill_fills_the_same_rows():
+    """kvl_mla_prefill_compressed_bf16_state_* (src/generate.c:208-210 as one call): state rows
+    bit-identical to the state prefill's, output within the rounding of kv_a of the plain
+    prefill's, the device variant equal to the host variant; then a decode continues from it."""
+    cfg, layer, x = model(KIMI, 0xB6, n=300)
+    w = layer.struct()
+    S, H = 297, cfg.hidden_size
+    xs = np.ascontiguousarray(x[:S])
+    plain = np.zeros((S, H), np.float32)
+    lib.check(L.kvl_mla_prefill_bf16(f32(plain), f32(xs), S, C.byref(cfg), C.byref(w)), "prefill")
+    sep = new_bf16(cfg, S + 3)
+    lib.check(L.kvl_mla_compressed_bf16_state_prefill_bf16(f32(xs), S, C.byref(cfg), C.byref(w), C.byref(sep)),
+              "state prefill")
+    fus = new_bf16(cfg, S + 3)
+    out = np.zeros_like(plain)
+    lib.check(L.kvl_mla_prefill_compressed_bf16_state_bf16(f32(out), f32(xs), S, C.byref(cfg), C.byref(w),
+                                                           C.byref(fus)), "fused")
+    assert sep.len == fus.len == S
+    for a, b in zip(rows_of(fus, S), rows_of(sep, S)):
+        np.testing.assert_array_equal(a, b)
+    print(f"[bf16] fused vs plain prefill {rel_err(out, plain):.3e}", flush=True)
+    assert rel_err(out, plain) <= 1e-4
+    dev = new_bf16(cfg, S + 3)
+    dx, do = L.kvl_mla_device_alloc(xs.nbytes), L.kvl_mla_device_alloc(xs.nbytes)
+    lib.check(L.kvl_mla_copy_to_device(dx, xs.ctypes.data, xs.nbytes), "h2d")
+    lib.check(L.kvl_mla_prefill_compressed_bf16_state_device(do, dx, S, C.byref(cfg), C.byref(w), C.byref(dev)),
+              "fused device")
+    od = np.zeros_like(out)
+    lib.check(L.kvl_mla_copy_to_host(od.ctypes.data, do, od.nbytes), "d2h")
+    lib.check(L.kvl_mla_compressed_bf16_state_pull(C.byref(dev), 0, S), "pull")
+    np.testing.assert_array_equal(od, out)
+    for a, b in zip(rows_of(dev, S), rows_of(fus, S)):
+        np.testing.assert_array_equal(a, b)
+    L.kvl_mla_device_free(dx)
+    L.kvl_mla_device_free(do)
+    got = np.zeros(H, np.float32)
+    lib.check(L.kvl_mla_decode_compressed_bf16_bf16(f32(got), f32(x[S]), S, C.byref(cfg), C.byref(w), C.byref(fus)),
+              "decode after fused prefill")
+    twin = new_twin(cfg, S + 3)
+    ref, _ = oracle_decode(cfg, w, twin, fus, x[S], S)
+    assert rel_err(got, ref) <= TOL
+    for s in (sep, fus, dev):
+        L.kvl_mla_compressed_bf16_state_free(C.byref(s))
+    O.mla_compressed_state_free(C.byref(twin))
+
+
+def test_attention_layer_bf16():
+    """kvl_mla_attention_layer_bf16_device (src/generate.c:34-67 for a batch): bit-identical to the
+    same composition through the host API, and the attention increment within 2e-3 of the
+    oracle's composition over the same bf16 rows."""
+    cfg, layer, _ = model(KIMI, 0xB7)
+    w = layer.struct()
+    H = cfg.hidden_size
+    rng = np.random.default_rng(0xB7)
+    in_norm = inputs.f32_to_bf16_bits(1.0 + 0.02 * rng.standard_normal(H).astype(np.float32))
+    post_norm = inputs.f32_to_bf16_bits(1.0 + 0.02 * rng.standard_normal(H).astype(np.float32))
+    lens = [700, 1200, 333]
+    B = len(lens)
+    h0 = np.ascontiguousarray(inputs.hidden(cfg, 0xB8, B))
+
+    def states():
+        sts = []
+        for i, n in enumerate(lens):
+            st = new_bf16(cfg, n + 2)
+            lib.check(L.kvl_mla_compressed_bf16_state_fill_synthetic(C.byref(st), 0, n, 0xB70 + i), "fill")
+            lib.check(L.kvl_mla_compressed_bf16_state_pull(C.byref(st), 0, n), "pull")
+            sts.append(st)
+        return sts, (BSP * B)(*[C.pointer(s) for s in sts])
+
+    dsts, darr = states()
+    d_h, d_n2 = L.kvl_mla_device_alloc(h0.nbytes), L.kvl_mla_device_alloc(h0.nbytes)
+    lib.check(L.kvl_mla_copy_to_device(d_h, h0.ctypes.data, h0.nbytes), "h2d")
+    lib.check(L.kvl_mla_attention_layer_bf16_device(d_h, d_n2, B, C.byref(cfg), C.byref(w),
+                                                    in_norm.ctypes.data_as(abi.u16p),
+                                                    post_norm.ctypes.data_as(abi.u16p), darr, 0), "layer")
+    h1, n2 = np.zeros_like(h0), np.zeros_like(h0)
+    lib.check(L.kvl_mla_copy_to_host(h1.ctypes.data, d_h, h0.nbytes), "d2h")
+    lib.check(L.kvl_mla_copy_to_host(n2.ctypes.data, d_n2, h0.nbytes), "d2h")
+    assert [s.len for s in dsts] == [n + 1 for n in lens]
+    hsts, harr = states()
+    n1 = np.zeros_like(h0)
+    for b in range(B):
+        L.kvl_rmsnorm_bf16(f32(n1[b]), f32(h0[b]), in_norm.ctypes.data_as(abi.u16p), H, np.float32(cfg.rms_eps))
+    attn = np.zeros_like(h0)
+    pos = np.array(lens, np.int32)
+    lib.check(L.kvl_mla_decode_compressed_bf16_batch_bf16(f32(attn), f32(n1), pos.ctypes.data_as(C.POINTER(C.c_int)),
+                                                          B, C.byref(cfg), C.byref(w), harr), "host decode")
+    r1 = (h0 + attn).astype(np.float32)
+    n2h = np.zeros_like(h0)
+    for b in range(B):
+        L.kvl_rmsnorm_bf16(f32(n2h[b]), f32(r1[b]), post_norm.ctypes.data_as(abi.u16p), H, np.float32(cfg.rms_eps))
+    np.testing.assert_array_equal(h1, r1)
+    np.testing.assert_array_equal(n2, n2h)
+    twin = new_twin(cfg, max(lens) + 2)
+    worst = 0.0
+    for b in range(B):
+        ref, _ = oracle_decode(cfg, w, twin, hsts[b], n1[b], lens[b])
+        worst = max(worst, rel_err(h1[b] - h0[b], ref))
+    print(f"[bf16] attention layer increment vs oracle {worst:.3e}", flush=True)
+    assert worst <= TOL
+    L.kvl_mla_device_free(d_h)
+    L.kvl_mla_device_free(d_n2)
+    for s in dsts + hsts:
+        L.kvl_mla_compressed_bf16_state_free(C.byref(s))
+    O.mla_compressed_state_free(C.byref(twin))
