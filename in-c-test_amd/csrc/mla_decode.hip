@@ -1359,10 +1359,10 @@ __device__ __forceinline__ void wait_vm(int n) {
 //     k-blocks 9 (w >> 1) .. +8 of 32 against the bf16 hi | lo split of q * softmax scale (two
 //     v_mfma_f32_16x16x32_bf16 per block); the two k-halves are summed through LDS;
 //   softmax: every wave keeps the online statistics of all 16 heads (the same arithmetic in
-//     each wave); lane group g takes chunk rows 8g .. 8g+7;
+//     each wave); lane group g takes chunk rows 8g .. 8g+7; the reference max moves lazily (p <= 4);
 //   mix: wave w owns latent columns 128w .. +127 (M = heads, N = 16 columns, K = the 32 rows),
 //     p split into bf16 hi | lo, the rows read transposed by ds_read_b64_tr_b16, fp32
-//     accumulators rescaled by exp(m_old - m_new) every chunk.
+//     accumulators rescaled by exp(m_old - m_new) when the reference max moves.
 // The 16-byte slots of a latent row are XOR-swizzled by b16_swz(row), so that the score reads
 // (16 rows, one slot) and the transposed reads (4 rows x 32 bytes per 16 lanes, 8 rows per half
 // wave) spread over the LDS banks.
@@ -1378,6 +1378,25 @@ static_assert(kB16SmemB <= 160 * 1024, "LDS of one CU");
 // bits (r3, r2, r1, r0) of a chunk row -> slot XOR (r3, r1, r0, r2): a bijection on 16 rows, and
 // (r3, r1, r0) -> distinct slot pairs for the 8 rows of a transposed half-wave read
 __device__ __forceinline__ int b16_swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1) | (row & 8); }
+
+// Max / sum over lanes l, l ^ 16, l ^ 32, l ^ 48 with the gfx950 lane-swap instructions (VALU,
+// no LDS round trip): v_permlane16_swap with both operands v gives every lane the values of its
+// lane pair (l & ~16, l | 16), v_permlane32_swap those of (l & ~32, l | 32); the lower lane's value
+// comes first, so every lane computes the same result.
+__device__ __forceinline__ float xgroup_max(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+__device__ __forceinline__ float xgroup_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
+constexpr float kB16LnPmax = 1.3862944f;  // ln 4: the weights p_j = exp(s_j - m) stay <= 4
 
 typedef short v4s __attribute__((ext_vector_type(4)));
 // ds_read_b64_tr_b16: within each 16-lane group, destination lane i element e is element i & 3
@@ -1402,26 +1421,6 @@ __global__ __launch_bounds__(256) void k_attn_bf16_mfma(AttnArgs a) {
     float *sp = (float *)(smem + kB16SpOff);
     const int rb = w & 1, kh = w >> 1;
 
-    // query operands (A of the score MFMAs: head n, k = 32 kb + 8g .. +7), loaded and split
-    // before the first history DMA is issued
-    v8bf qh[9], ql[9];
-    {
-        const float *qrow = a.qf + ((size_t)b * 16 + n) * 576 + 8 * g + 32 * 9 * kh;
-        v4f qv[18];
-#pragma unroll
-        for (int j = 0; j < 9; ++j) {
-            qv[2 * j] = *(const v4f *)(qrow + 32 * j);
-            qv[2 * j + 1] = *(const v4f *)(qrow + 32 * j + 4);
-        }
-#pragma unroll
-        for (int j = 0; j < 9; ++j) {
-            split8(qv[2 * j] * a.smscale, qv[2 * j + 1] * a.smscale, qh[j], ql[j]);
-            // the operands exist before the DMA below is issued: the wait for these loads then
-            // does not count the history loads
-            asm volatile("" ::"v"(qh[j]), "v"(ql[j]));
-        }
-    }
-
     // DMA per chunk and wave: latent rows 8w .. 8w+7, one 1 KB instruction per row (lane i
     // writes physical slot i, which holds logical slot i ^ b16_swz(row)); RoPE rows 8w .. 8w+7,
     // one instruction (lane i: row 8w + (i >> 3), physical slot i & 7 = logical (i & 7) ^
@@ -1440,6 +1439,28 @@ __global__ __launch_bounds__(256) void k_attn_bf16_mfma(AttnArgs a) {
         const int gr = min(rbase + row, r1 - 1);
         dma_b128(grope + (size_t)gr * 64 + 8 * ((l & 7) ^ (row & 7)), buf + (uint32_t)(kB16LatB + w * 1024));
     };
+
+    // query operands (A of the score MFMAs: head n, k = 32 kb + 8g .. +7). Chunk 0's DMA goes out
+    // first; the query loads follow it and are split before chunks 1 and 2 are issued, so the
+    // compiler's wait for them (which does not count the DMA) covers chunk 0 and nothing more.
+    v8bf qh[9], ql[9];
+    issue(0);
+    {
+        const float *qrow = a.qf + ((size_t)b * 16 + n) * 576 + 8 * g + 32 * 9 * kh;
+        v4f qv[18];
+#pragma unroll
+        for (int j = 0; j < 9; ++j) {
+            qv[2 * j] = *(const v4f *)(qrow + 32 * j);
+            qv[2 * j + 1] = *(const v4f *)(qrow + 32 * j + 4);
+        }
+#pragma unroll
+        for (int j = 0; j < 9; ++j) {
+            split8_cvt(qv[2 * j] * a.smscale, qv[2 * j + 1] * a.smscale, qh[j], ql[j]);
+            asm volatile("" ::"v"(qh[j]), "v"(ql[j]));  // before chunks 1 and 2 are issued
+        }
+    }
+    if (nch > 1) issue(1);
+    if (nch > 2) issue(2);
 
     // score operand offsets (row srow of the chunk, slot 4 kb + g of its latents / RoPE key)
     const int srow = 16 * rb + n;
@@ -1461,9 +1482,6 @@ __global__ __launch_bounds__(256) void k_attn_bf16_mfma(AttnArgs a) {
             tro[h][t] = row * 1024 + 16 * ((2 * (8 * w + t) + ((n >> 1) & 1)) ^ b16_swz(row)) + 8 * (n & 1);
     }
 
-    issue(0);
-    if (nch > 1) issue(1);
-    if (nch > 2) issue(2);
     float m_run = -INFINITY, l_run = 0.f;  // head n
     v4f acc[8];
 #pragma unroll
@@ -1494,33 +1512,40 @@ __global__ __launch_bounds__(256) void k_attn_bf16_mfma(AttnArgs a) {
             sc[e] = 8 * g + e < nv ? a0[e] + c0[e] : -INFINITY;
             sc[e + 4] = 8 * g + e + 4 < nv ? a1[e] + c1[e] : -INFINITY;
         }
-        float cmax = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
-        const float mnew = fmaxf(m_run, cmax);
-        const float alpha = __expf(m_run - mnew);
+        const float cmax = xgroup_max(
+            fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7]))));
+        // lazy reference max: it moves only when the chunk exceeds it by more than ln 4 (every
+        // head in the first chunk, where it is -inf); then the accumulators of the heads concerned
+        // are rescaled by alpha = exp(m_old - m_new) (0 from -inf). All four waves hold the same
+        // statistics, so they take the same branch.
+        const bool mv = cmax > m_run + kB16LnPmax;
+        if (__any(mv)) {
+            const float mnew = mv ? cmax : m_run;
+            const float alpha = mv ? __expf(m_run - mnew) : 1.0f;
+            m_run = mnew;
+            l_run *= alpha;
+            float ad[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ad[i] = __shfl(alpha, 4 * g + i);
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[t][i] *= ad[i];
+        }
         float p[8], psum = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            p[e] = __expf(sc[e] - mnew);
+            p[e] = __expf(sc[e] - m_run);
             psum += p[e];
         }
-        psum += __shfl_xor(psum, 16);
-        psum += __shfl_xor(psum, 32);
-        l_run = fmaf(l_run, alpha, psum);
-        m_run = mnew;
+        l_run += xgroup_sum(psum);
         v8bf ph, pl;
-        split8(v4f{p[0], p[1], p[2], p[3]}, v4f{p[4], p[5], p[6], p[7]}, ph, pl);
-        float ad[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ad[i] = __shfl(alpha, 4 * g + i);
+        split8_cvt(v4f{p[0], p[1], p[2], p[3]}, v4f{p[4], p[5], p[6], p[7]}, ph, pl);
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             const v4s lo4 = lds_read_tr16(buf + tro[0][t]);
             const v4s hi4 = lds_read_tr16(buf + tro[1][t]);
             const v8bf bt = __builtin_bit_cast(v8bf, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[t][i] *= ad[i];
             acc[t] = mfma_bf16(ph, bt, acc[t]);
             acc[t] = mfma_bf16(pl, bt, acc[t]);
         }

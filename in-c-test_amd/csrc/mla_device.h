@@ -58,6 +58,26 @@ __device__ __forceinline__ void split8(const v4f &x0, const v4f &x1, v8bf &hi, v
 typedef float v2f __attribute__((ext_vector_type(2)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 
+// split8 with the hardware conversion (v_cvt_pk_bf16_f32: round to nearest even, one instruction
+// per pair): hi = bf16(x), lo = bf16(x - hi), x - hi being exact. For finite values the same
+// words as split8, in about a fifth of the VALU instructions.
+__device__ __forceinline__ void split8_cvt(const v4f &x0, const v4f &x1, v8bf &hi, v8bf &lo) {
+    const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    v2bf h[4], l[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const v2f xp = {x[2 * p], x[2 * p + 1]};
+        h[p] = __builtin_convertvector(xp, v2bf);
+        const v2f hf = {(float)h[p].x, (float)h[p].y};
+        const v2f r = {xp.x - hf.x, xp.y - hf.y};
+        l[p] = __builtin_convertvector(r, v2bf);
+    }
+    hi = __builtin_shufflevector(__builtin_shufflevector(h[0], h[1], 0, 1, 2, 3),
+                                 __builtin_shufflevector(h[2], h[3], 0, 1, 2, 3), 0, 1, 2, 3, 4, 5, 6, 7);
+    lo = __builtin_shufflevector(__builtin_shufflevector(l[0], l[1], 0, 1, 2, 3),
+                                 __builtin_shufflevector(l[2], l[3], 0, 1, 2, 3), 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
 // One half of the split x ~= hi + lo of 8 fp32 values as a bf16x8 MFMA operand: part 0 the hi
 // halves, part 1 the lo halves (both round to nearest even, v_cvt_pk_bf16_f32). Finite inputs.
 __device__ __forceinline__ v8bf split8_part(const v4f &x0, const v4f &x1, int part) {
