@@ -2231,7 +2231,8 @@ __global__ __launch_bounds__(1024) void k_combine_r512(CombineArgs a) {
     const float *Pg = P + (size_t)h * 512 + 4 * c4;
     v4f pre[kCombPre];
 #pragma unroll
-    for (int i = 0; i < kCombPre; ++i) pre[i] = *(const v4f *)(Pg + (size_t)min(sg + 8 * i, ns - 1) * stride);
+    for (int i = 0; i < kCombPre; ++i)  // sg is uniform within a wave: splits past ns are not loaded
+        pre[i] = sg + 8 * i < ns ? *(const v4f *)(Pg + (size_t)(sg + 8 * i) * stride) : v4f{0.f, 0.f, 0.f, 0.f};
     if (tid < 64) {
         float m = tid < ns ? m0 : -INFINITY;
         for (int i = tid + 64; i < ns; i += 64) m = fmaxf(m, Pm[(size_t)i * stride]);
@@ -2264,7 +2265,8 @@ __global__ __launch_bounds__(1024) void k_combine_r512(CombineArgs a) {
     for (int sp = sg + 8 * kCombPre; sp < ns; sp += 8 * kCombPre) {
         v4f more[kCombPre];
 #pragma unroll
-        for (int i = 0; i < kCombPre; ++i) more[i] = *(const v4f *)(Pg + (size_t)min(sp + 8 * i, ns - 1) * stride);
+        for (int i = 0; i < kCombPre; ++i)
+            more[i] = sp + 8 * i < ns ? *(const v4f *)(Pg + (size_t)(sp + 8 * i) * stride) : v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < kCombPre; ++i) {
             if (sp + 8 * i < ns) {
