@@ -134,7 +134,9 @@ struct GemvSplitArgs {
 // k-blocks for all four tiles, so every activation value a wave converts serves four MFMAs.
 // Splitting k keeps the weight bytes per block at 64 KB while each block reads only a quarter
 // of the activations (a 16-row block over the full k range would read all of them). The
-// consumer adds the kGemvKs partials in kq order. Requires in = kGemvKs * 16 * 32 * KPW.
+// consumer adds the kGemvKs partials in kq order. The block takes the 16-token groups
+// 16 blockIdx.z, + 16 gridDim.z, ... in turn with its weights held in registers, so a batch of
+// many tokens reads each weight once. Requires in = kGemvKs * 16 * 32 * KPW.
 template <int NG, int KPW>
 __global__ __launch_bounds__(1024) void k_gemv_ksplit(GemvSplitArgs a) {
     __shared__ v4f red[16][4 * NG][64];
@@ -146,115 +148,131 @@ __global__ __launch_bounds__(1024) void k_gemv_ksplit(GemvSplitArgs a) {
         const int row = min(row0 + 16 * t + n, out - 1);  // rows past the end are never stored
         wr[t] = row < a.out0 ? a.W0 + (size_t)row * a.in : a.W1 + (size_t)(row - a.out0) * a.in;
     }
-    const int bz = 16 * blockIdx.z;
-    const float *xr[NG];
-#pragma unroll
-    for (int gi = 0; gi < NG; ++gi) xr[gi] = a.X + (size_t)min(bz + 8 * gi + (n & 7), a.B - 1) * a.ldx;
-    v4f acc[4][NG];
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int gi = 0; gi < NG; ++gi) acc[t][gi] = v4f{0.f, 0.f, 0.f, 0.f};
     const int kbase = kq * (16 * 32 * KPW) + w * (32 * KPW) + g * 8;
     v4i wa[KPW][4];
-    v4f xa[KPW][NG], xb[KPW][NG];
-#pragma unroll
-    for (int kb = 0; kb < KPW; ++kb) {
-        const int k = kbase + 32 * kb;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) wa[kb][t] = *(const v4i *)(wr[t] + k);
-#pragma unroll
-        for (int gi = 0; gi < NG; ++gi) {
-            xa[kb][gi] = *(const v4f *)(xr[gi] + k);
-            xb[kb][gi] = *(const v4f *)(xr[gi] + k + 4);
-        }
-    }
 #pragma unroll
     for (int kb = 0; kb < KPW; ++kb)
 #pragma unroll
+        for (int t = 0; t < 4; ++t) wa[kb][t] = *(const v4i *)(wr[t] + kbase + 32 * kb);
+    // the activations of token group bz (issued one group ahead: their loads overlap the
+    // reduction of the previous group)
+    v4f xa[KPW][NG], xb[KPW][NG];
+    auto load_x = [&](int bz) __attribute__((always_inline)) {
+#pragma unroll
         for (int gi = 0; gi < NG; ++gi) {
-            const v8bf xv = split8_part(xa[kb][gi], xb[kb][gi], part);
+            const float *xr = a.X + (size_t)min(bz + 8 * gi + (n & 7), a.B - 1) * a.ldx;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) acc[t][gi] = mfma_bf16(__builtin_bit_cast(v8bf, wa[kb][t]), xv, acc[t][gi]);
-        }
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int gi = 0; gi < NG; ++gi) red[w][t * NG + gi][l] = acc[t][gi];
-    __syncthreads();
-    if (w >= 4) return;
-    // wave t sums row tile t over the 16 waves in order
-#pragma unroll
-    for (int gi = 0; gi < NG; ++gi) {
-        v4f s = red[0][w * NG + gi][l];
-#pragma unroll
-        for (int q = 1; q < 16; ++q) s += red[q][w * NG + gi][l];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s[i] += dpp_f32<0x128>(s[i]);  // row_ror:8 = lane ^ 8
-        const int b = bz + 8 * gi + n;
-        if (n < 8 && b < a.B) {
-            float *y = a.Y + (size_t)kq * a.pstride + (size_t)b * a.ldy;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = row0 + 16 * w + 4 * g + i;
-                if (r < out) y[r] = s[i];
+            for (int kb = 0; kb < KPW; ++kb) {
+                const int k = kbase + 32 * kb;
+                xa[kb][gi] = *(const v4f *)(xr + k);
+                xb[kb][gi] = *(const v4f *)(xr + k + 4);
             }
         }
+    };
+    load_x(16 * blockIdx.z);
+    for (int bz = 16 * blockIdx.z; bz < a.B; bz += 16 * gridDim.z) {
+        v4f acc[4][NG];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int gi = 0; gi < NG; ++gi) acc[t][gi] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < KPW; ++kb)
+#pragma unroll
+            for (int gi = 0; gi < NG; ++gi) {
+                const v8bf xv = split8_part(xa[kb][gi], xb[kb][gi], part);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) acc[t][gi] = mfma_bf16(__builtin_bit_cast(v8bf, wa[kb][t]), xv, acc[t][gi]);
+            }
+        if (bz + 16 * gridDim.z < a.B) load_x(bz + 16 * gridDim.z);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int gi = 0; gi < NG; ++gi) red[w][t * NG + gi][l] = acc[t][gi];
+        __syncthreads();
+        if (w < 4) {
+            // wave t sums row tile t over the 16 waves in order
+#pragma unroll
+            for (int gi = 0; gi < NG; ++gi) {
+                v4f s = red[0][w * NG + gi][l];
+#pragma unroll
+                for (int q = 1; q < 16; ++q) s += red[q][w * NG + gi][l];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) s[i] += dpp_f32<0x128>(s[i]);  // row_ror:8 = lane ^ 8
+                const int b = bz + 8 * gi + n;
+                if (n < 8 && b < a.B) {
+                    float *y = a.Y + (size_t)kq * a.pstride + (size_t)b * a.ldy;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int r = row0 + 16 * w + 4 * g + i;
+                        if (r < out) y[r] = s[i];
+                    }
+                }
+            }
+        }
+        __syncthreads();  // red is rewritten by the next group
     }
 }
 
 // Y[b, o] (+)= sum_k W[o, k] (hi + lo)[b, k] with the activations already split into bf16
 // planes by their producer: 16 output rows per block, 16 waves splitting k, one 16-byte
-// activation load and one MFMA per k-block and sequence group. Requires in = 16 * 32 * KPW.
+// activation load and one MFMA per k-block and sequence group; the 16-token groups are taken
+// in turn with the weights held in registers. Requires in = 16 * 32 * KPW.
 template <int NG, int KPW>
 __global__ __launch_bounds__(1024) void k_gemv_xs(GemvSplitArgs a) {
     __shared__ v4f red[16][NG][64];
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
     const int out = a.out0, part = n >> 3;
     const uint16_t *wrow = a.W0 + (size_t)min((int)blockIdx.x * 16 + n, out - 1) * a.in;
-    const int bz = 16 * blockIdx.z;
-    const uint16_t *xr[NG];
-#pragma unroll
-    for (int gi = 0; gi < NG; ++gi)
-        xr[gi] = a.XS + ((size_t)part * a.B + min(bz + 8 * gi + (n & 7), a.B - 1)) * a.in;
     const int kbase = w * (32 * KPW) + g * 8;
-    v4i wa[KPW], xv[KPW][NG];
+    v4i wa[KPW];
 #pragma unroll
-    for (int kb = 0; kb < KPW; ++kb) {
-        wa[kb] = *(const v4i *)(wrow + kbase + 32 * kb);
+    for (int kb = 0; kb < KPW; ++kb) wa[kb] = *(const v4i *)(wrow + kbase + 32 * kb);
+    v4i xv[KPW][NG];  // activations of a token group, loaded one group ahead
+    auto load_x = [&](int bz) __attribute__((always_inline)) {
 #pragma unroll
-        for (int gi = 0; gi < NG; ++gi) xv[kb][gi] = *(const v4i *)(xr[gi] + kbase + 32 * kb);
-    }
-    v4f acc[NG];
+        for (int gi = 0; gi < NG; ++gi) {
+            const uint16_t *xr = a.XS + ((size_t)part * a.B + min(bz + 8 * gi + (n & 7), a.B - 1)) * a.in;
 #pragma unroll
-    for (int gi = 0; gi < NG; ++gi) acc[gi] = v4f{0.f, 0.f, 0.f, 0.f};
+            for (int kb = 0; kb < KPW; ++kb) xv[kb][gi] = *(const v4i *)(xr + kbase + 32 * kb);
+        }
+    };
+    load_x(16 * blockIdx.z);
+    for (int bz = 16 * blockIdx.z; bz < a.B; bz += 16 * gridDim.z) {
+        v4f acc[NG];
 #pragma unroll
-    for (int kb = 0; kb < KPW; ++kb)
+        for (int gi = 0; gi < NG; ++gi) acc[gi] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int gi = 0; gi < NG; ++gi)
-            acc[gi] = mfma_bf16(__builtin_bit_cast(v8bf, wa[kb]), __builtin_bit_cast(v8bf, xv[kb][gi]), acc[gi]);
+        for (int kb = 0; kb < KPW; ++kb)
 #pragma unroll
-    for (int gi = 0; gi < NG; ++gi) red[w][gi][l] = acc[gi];
-    __syncthreads();
-    if (w != 0) return;
+            for (int gi = 0; gi < NG; ++gi)
+                acc[gi] = mfma_bf16(__builtin_bit_cast(v8bf, wa[kb]), __builtin_bit_cast(v8bf, xv[kb][gi]), acc[gi]);
+        if (bz + 16 * gridDim.z < a.B) load_x(bz + 16 * gridDim.z);
 #pragma unroll
-    for (int gi = 0; gi < NG; ++gi) {
-        v4f s = red[0][gi][l];
+        for (int gi = 0; gi < NG; ++gi) red[w][gi][l] = acc[gi];
+        __syncthreads();
+        if (w == 0) {
 #pragma unroll
-        for (int q = 1; q < 16; ++q) s += red[q][gi][l];
+            for (int gi = 0; gi < NG; ++gi) {
+                v4f s = red[0][gi][l];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s[i] += dpp_f32<0x128>(s[i]);
-        const int b = bz + 8 * gi + n;
-        if (n < 8 && b < a.B) {
+                for (int q = 1; q < 16; ++q) s += red[q][gi][l];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = blockIdx.x * 16 + 4 * g + i;
-                if (r < out) {
-                    float *yp = a.Y + (size_t)b * a.ldy + r;
-                    *yp = a.acc ? *yp + s[i] : s[i];
+                for (int i = 0; i < 4; ++i) s[i] += dpp_f32<0x128>(s[i]);
+                const int b = bz + 8 * gi + n;
+                if (n < 8 && b < a.B) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int r = blockIdx.x * 16 + 4 * g + i;
+                        if (r < out) {
+                            float *yp = a.Y + (size_t)b * a.ldy + r;
+                            *yp = a.acc ? *yp + s[i] : s[i];
+                        }
+                    }
                 }
             }
         }
+        __syncthreads();  // red is rewritten by the next group
     }
 }
 
@@ -267,7 +285,7 @@ hipError_t launch_gemv_ksplit(hipStream_t st, float *Y, size_t pstride, int ldy,
         (W1 && ((uintptr_t)W1 % 16) != 0) || out0 + out1 <= 0 || (B + 15) / 16 > 65535)
         return hipErrorInvalidValue;
     GemvSplitArgs a{Y, X, nullptr, W0, W1, pstride, ldy, ldx, B, out0, out1, in, 0};
-    const dim3 grid((out0 + out1 + 63) / 64, kGemvKs, (B + 15) / 16);
+    const dim3 grid((out0 + out1 + 63) / 64, kGemvKs, 1);  // the block loops over the token groups
     const bool two = B > 8;
     if (in == 2048) {
         if (two) hipLaunchKernelGGL((k_gemv_ksplit<2, 1>), grid, dim3(1024), 0, st, a);
@@ -520,7 +538,7 @@ hipError_t launch_gemv_xs(hipStream_t st, float *Y, int ldy, const uint16_t *XS,
         (B + 15) / 16 > 65535)
         return hipErrorInvalidValue;
     GemvSplitArgs a{Y, nullptr, XS, W, nullptr, 0, ldy, 0, B, out, 0, in, accumulate ? 1 : 0};
-    const dim3 grid((out + 15) / 16, 1, (B + 15) / 16);
+    const dim3 grid((out + 15) / 16, 1, (B + 31) / 32);  // a block takes two token groups in turn
     const bool two = B > 8;
     if (in == 2048) {
         if (two) hipLaunchKernelGGL((k_gemv_xs<2, 4>), grid, dim3(1024), 0, st, a);
@@ -2074,6 +2092,7 @@ struct CombineArgs {
     float *ho;
     uint16_t *hos;
     int fmt;
+    int spb;  // k_combine_r512: sequences per block (taken in turn)
 };
 
 bool combine_writes_hos(int fmt, const Dims &d) { return fmt != kFmtExp && d.R == 512 && d.DV == 128; }
@@ -2202,126 +2221,246 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
 // histories loop), and its W_UV slice (row t / 16, columns 32 (t % 16) .. + 31). After the
 // split weights are in LDS, each thread sums its splits in order, the 8 split groups are added
 // in group order through LDS, and 16 lanes per W_UV row reduce its dot product. The head output
-// is also written as bf16 hi | lo planes (w.hos), the operand format of launch_gemv_xs.
+// is also written as bf16 hi | lo planes (w.hos), the operand format of launch_gemv_xs. Large
+// batches give a block spb sequences of the same (head, half), taken in turn with the W_UV slice
+// loaded once, so that the grid stays within one round of the CUs.
+// LDS position of mix column c: the 4-column groups of each 32-column row are XOR-permuted by the
+// row, so that the W_UV dot's reads (lane q: columns 32 q + 8 c' .. + 7) fall in distinct banks.
+__device__ __forceinline__ int mx_pos(int c) { return c ^ (((c >> 5) & 7) << 2); }
 constexpr int kCombPre = 8;
+constexpr int kCombBlocks = 256;  // k_combine_r512 grid target: one round on the CUs of an MI355X
+constexpr int kCombWide = 16;     // k_combine_r512x8: at most this many splits per sequence
 __global__ __launch_bounds__(1024) void k_combine_r512(CombineArgs a) {
     __shared__ float mx[512];
     __shared__ float wts[kMaxSplits];
     __shared__ v4f red[8][128];
     __shared__ float sinv;
     const int NH = a.d.NH, tid = threadIdx.x;
-    const int half = blockIdx.x & 1, bh = blockIdx.x >> 1, b = bh / NH, h = bh % NH;
-    const SeqDesc &s = a.t.s[b];
-    const int ns = s.nsplit;
+    const int half = blockIdx.x & 1, gh = blockIdx.x >> 1, grp = gh / NH, h = gh % NH;
+    const int dd = 64 * half + (tid >> 4), q = tid & 15;
+    const uint16_t *row = a.kv_b + ((size_t)h * (a.d.DN + 128) + a.d.DN + dd) * 512 + 32 * q;
+    v4i wv[4];  // held for every sequence of the block
+#pragma unroll
+    for (int c = 0; c < 4; ++c) wv[c] = *(const v4i *)(row + 8 * c);
+    // split group: uniform within a wave (128-thread groups)
+    const int sg = __builtin_amdgcn_readfirstlane(tid >> 7);
     const size_t stride = (size_t)NH * (512 + 2);
-    const float *P = a.part + (size_t)s.split0 * stride;
-    const float *Pm = P + (size_t)NH * 512 + h;  // split i: m at Pm[i * stride], l at + NH
-    float m0 = 0.f, l0 = 0.f;
-    if (tid < 64) {
-        const int i0 = min(tid, ns - 1);
-        m0 = Pm[(size_t)i0 * stride];
-        l0 = Pm[(size_t)i0 * stride + NH];
+    const int b_end = min((grp + 1) * a.spb, a.t.n);
+    for (int b = grp * a.spb; b < b_end; ++b) {
+        // column group of this thread, opaque to the compiler so that the per-split addresses
+        // below are formed in each iteration instead of being held (spilled) across the loop
+        int c4 = tid & 127;
+        asm volatile("" : "+v"(c4));
+        const SeqDesc &s = a.t.s[b];
+        const int ns = s.nsplit;
+        const float *P = a.part + (size_t)s.split0 * stride;
+        const float *Pm = P + (size_t)NH * 512 + h;  // split i: m at Pm[i * stride], l at + NH
+        float m0 = 0.f, l0 = 0.f;
+        if (tid < 64) {
+            const int i0 = min(tid, ns - 1);
+            m0 = Pm[(size_t)i0 * stride];
+            l0 = Pm[(size_t)i0 * stride + NH];
+        }
+        const float *Pg = P + (size_t)h * 512 + 4 * c4;
+        v4f pre[kCombPre];
+#pragma unroll
+        for (int i = 0; i < kCombPre; ++i)  // sg is uniform within a wave: splits past ns are not loaded
+            pre[i] = sg + 8 * i < ns ? *(const v4f *)(Pg + (size_t)(sg + 8 * i) * stride) : v4f{0.f, 0.f, 0.f, 0.f};
+        if (tid < 64) {
+            float m = tid < ns ? m0 : -INFINITY;
+            for (int i = tid + 64; i < ns; i += 64) m = fmaxf(m, Pm[(size_t)i * stride]);
+            m = wave_max(m);
+            float den = 0.f;
+            if (tid < ns) {
+                const float e = __expf(m0 - m);
+                wts[tid] = e;
+                den = l0 * e;
+            }
+            for (int i = tid + 64; i < ns; i += 64) {
+                const float e = __expf(Pm[(size_t)i * stride] - m);
+                wts[i] = e;
+                den = fmaf(Pm[(size_t)i * stride + NH], e, den);
+            }
+            den = wave_sum(den);
+            if (tid == 0) sinv = 1.0f / den;
+        }
+        __syncthreads();
+        v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < kCombPre; ++i) {
+            const int sp = sg + 8 * i;
+            if (sp < ns) {
+                const float wt = wts[sp];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[e] = fmaf(pre[i][e], wt, acc[e]);
+            }
+        }
+        for (int sp = sg + 8 * kCombPre; sp < ns; sp += 8 * kCombPre) {
+            v4f more[kCombPre];
+#pragma unroll
+            for (int i = 0; i < kCombPre; ++i)
+                more[i] = sp + 8 * i < ns ? *(const v4f *)(Pg + (size_t)(sp + 8 * i) * stride) : v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < kCombPre; ++i) {
+                if (sp + 8 * i < ns) {
+                    const float wt = wts[sp + 8 * i];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[e] = fmaf(more[i][e], wt, acc[e]);
+                }
+            }
+        }
+        red[sg][c4] = acc;
+        __syncthreads();
+        if (tid < 512) {
+            const int cq = tid >> 2, e = tid & 3;
+            float v = red[0][cq][e];
+#pragma unroll
+            for (int g8 = 1; g8 < 8; ++g8) v += red[g8][cq][e];
+            mx[mx_pos(tid)] = v * sinv;
+        }
+        __syncthreads();
+        float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const v4f m0v = *(const v4f *)(mx + mx_pos(32 * q + 8 * c));
+            const v4f m1v = *(const v4f *)(mx + mx_pos(32 * q + 8 * c + 4));
+            const uint32_t u0 = (uint32_t)wv[c][0], u1 = (uint32_t)wv[c][1];
+            const uint32_t u2 = (uint32_t)wv[c][2], u3 = (uint32_t)wv[c][3];
+            acc0 = fmaf(__uint_as_float(u0 << 16), m0v.x, acc0);
+            acc1 = fmaf(__uint_as_float(u0 & 0xffff0000u), m0v.y, acc1);
+            acc0 = fmaf(__uint_as_float(u1 << 16), m0v.z, acc0);
+            acc1 = fmaf(__uint_as_float(u1 & 0xffff0000u), m0v.w, acc1);
+            acc0 = fmaf(__uint_as_float(u2 << 16), m1v.x, acc0);
+            acc1 = fmaf(__uint_as_float(u2 & 0xffff0000u), m1v.y, acc1);
+            acc0 = fmaf(__uint_as_float(u3 << 16), m1v.z, acc0);
+            acc1 = fmaf(__uint_as_float(u3 & 0xffff0000u), m1v.w, acc1);
+        }
+        const float hsum = row16_sum(acc0 + acc1);  // the 16 lanes of row dd
+        if (q == 0) {
+            const size_t o = (size_t)b * a.d.HO + (size_t)h * 128 + dd;
+            a.ho[o] = hsum;
+            uint16_t hi, lo;
+            split_bf16(hsum, hi, lo);
+            a.hos[o] = hi;
+            a.hos[(size_t)a.t.n * a.d.HO + o] = lo;
+        }
+        __syncthreads();  // wts, red and mx are rewritten for the next sequence
     }
+}
+
+// The same combine for 8 sequences of one (head, half) per block, for large batches: the 128
+// threads of sequence j (waves 2j, 2j+1) merge its splits -- wave 2j computes the split maxima,
+// weights and denominator exactly as wave 0 of k_combine_r512 does, and thread (j, c) forms
+// each split group's sum of columns 4c .. 4c+3 and adds the eight group sums in group order,
+// the operations k_combine_r512 spreads over its threads -- then every thread takes its W_UV row
+// slice through the eight mixes. The outputs equal k_combine_r512's bit for bit, with W_UV read
+// once per 8 sequences and 8 times fewer blocks.
+__global__ __launch_bounds__(1024) void k_combine_r512x8(CombineArgs a) {
+    __shared__ float mx[8][512];
+    __shared__ float wts[8][kCombWide];
+    __shared__ float sinv[8];
+    const int NH = a.d.NH, tid = threadIdx.x;
+    const int half = blockIdx.x & 1, gh = blockIdx.x >> 1, grp = gh / NH, h = gh % NH;
     const int dd = 64 * half + (tid >> 4), q = tid & 15;
     const uint16_t *row = a.kv_b + ((size_t)h * (a.d.DN + 128) + a.d.DN + dd) * 512 + 32 * q;
     v4i wv[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) wv[c] = *(const v4i *)(row + 8 * c);
-    const int c4 = tid & 127, sg = tid >> 7;
+    const int j = __builtin_amdgcn_readfirstlane(tid >> 7), c4 = tid & 127, lw = tid & 127;
+    const int b = grp * 8 + j;
+    const bool live = b < a.t.n;
+    const size_t stride = (size_t)NH * (512 + 2);
+    const SeqDesc &s = a.t.s[live ? b : 0];
+    const int ns = live ? s.nsplit : 0;
+    const float *P = a.part + (size_t)s.split0 * stride;
+    const float *Pm = P + (size_t)NH * 512 + h;
     const float *Pg = P + (size_t)h * 512 + 4 * c4;
-    v4f pre[kCombPre];
+    v4f pre[kCombWide];
 #pragma unroll
-    for (int i = 0; i < kCombPre; ++i)  // sg is uniform within a wave: splits past ns are not loaded
-        pre[i] = sg + 8 * i < ns ? *(const v4f *)(Pg + (size_t)(sg + 8 * i) * stride) : v4f{0.f, 0.f, 0.f, 0.f};
-    if (tid < 64) {
-        float m = tid < ns ? m0 : -INFINITY;
-        for (int i = tid + 64; i < ns; i += 64) m = fmaxf(m, Pm[(size_t)i * stride]);
+    for (int i = 0; i < kCombWide; ++i)
+        pre[i] = i < ns ? *(const v4f *)(Pg + (size_t)i * stride) : v4f{0.f, 0.f, 0.f, 0.f};
+    if (lw < 64 && live) {
+        const float m0 = Pm[(size_t)min(lw, ns - 1) * stride];
+        const float l0 = Pm[(size_t)min(lw, ns - 1) * stride + NH];
+        float m = lw < ns ? m0 : -INFINITY;
         m = wave_max(m);
         float den = 0.f;
-        if (tid < ns) {
+        if (lw < ns) {
             const float e = __expf(m0 - m);
-            wts[tid] = e;
+            wts[j][lw] = e;
             den = l0 * e;
         }
-        for (int i = tid + 64; i < ns; i += 64) {
-            const float e = __expf(Pm[(size_t)i * stride] - m);
-            wts[i] = e;
-            den = fmaf(Pm[(size_t)i * stride + NH], e, den);
-        }
         den = wave_sum(den);
-        if (tid == 0) sinv = 1.0f / den;
+        if (lw == 0) sinv[j] = 1.0f / den;
     }
     __syncthreads();
-    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    if (live) {
+        // split group g8 holds splits g8, g8 + 8, ...; the groups are added in order
+        v4f v = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < kCombPre; ++i) {
-        const int sp = sg + 8 * i;
-        if (sp < ns) {
-            const float wt = wts[sp];
+        for (int g8 = 0; g8 < 8; ++g8) {
+            v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[e] = fmaf(pre[i][e], wt, acc[e]);
-        }
-    }
-    for (int sp = sg + 8 * kCombPre; sp < ns; sp += 8 * kCombPre) {
-        v4f more[kCombPre];
+            for (int i = g8; i < kCombWide; i += 8) {
+                if (i < ns) {
+                    const float wt = wts[j][i];
 #pragma unroll
-        for (int i = 0; i < kCombPre; ++i)
-            more[i] = sp + 8 * i < ns ? *(const v4f *)(Pg + (size_t)(sp + 8 * i) * stride) : v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int i = 0; i < kCombPre; ++i) {
-            if (sp + 8 * i < ns) {
-                const float wt = wts[sp + 8 * i];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc[e] = fmaf(more[i][e], wt, acc[e]);
+                    for (int e = 0; e < 4; ++e) acc[e] = fmaf(pre[i][e], wt, acc[e]);
+                }
             }
+            if (g8 == 0) v = acc;
+            else v += acc;
         }
-    }
-    red[sg][c4] = acc;
-    __syncthreads();
-    if (tid < 512) {
-        const int cq = tid >> 2, e = tid & 3;
-        float v = red[0][cq][e];
-#pragma unroll
-        for (int g8 = 1; g8 < 8; ++g8) v += red[g8][cq][e];
-        mx[tid] = v * sinv;
+        *(v4f *)(&mx[j][mx_pos(4 * c4)]) = v * sinv[j];
     }
     __syncthreads();
-    const float *mh = mx + 32 * q;
-    float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll 1
+    for (int jj = 0; jj < 8 && grp * 8 + jj < a.t.n; ++jj) {
+        const float *mh = mx[jj];
+        float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const v4f m0v = *(const v4f *)(mh + 8 * c);
-        const v4f m1v = *(const v4f *)(mh + 8 * c + 4);
-        const uint32_t u0 = (uint32_t)wv[c][0], u1 = (uint32_t)wv[c][1];
-        const uint32_t u2 = (uint32_t)wv[c][2], u3 = (uint32_t)wv[c][3];
-        acc0 = fmaf(__uint_as_float(u0 << 16), m0v.x, acc0);
-        acc1 = fmaf(__uint_as_float(u0 & 0xffff0000u), m0v.y, acc1);
-        acc0 = fmaf(__uint_as_float(u1 << 16), m0v.z, acc0);
-        acc1 = fmaf(__uint_as_float(u1 & 0xffff0000u), m0v.w, acc1);
-        acc0 = fmaf(__uint_as_float(u2 << 16), m1v.x, acc0);
-        acc1 = fmaf(__uint_as_float(u2 & 0xffff0000u), m1v.y, acc1);
-        acc0 = fmaf(__uint_as_float(u3 << 16), m1v.z, acc0);
-        acc1 = fmaf(__uint_as_float(u3 & 0xffff0000u), m1v.w, acc1);
-    }
-    const float hsum = row16_sum(acc0 + acc1);  // the 16 lanes of row dd
-    if (q == 0) {
-        const size_t o = (size_t)b * a.d.HO + (size_t)h * 128 + dd;
-        a.ho[o] = hsum;
-        uint16_t hi, lo;
-        split_bf16(hsum, hi, lo);
-        a.hos[o] = hi;
-        a.hos[(size_t)a.t.n * a.d.HO + o] = lo;
+        for (int c = 0; c < 4; ++c) {
+            const v4f m0v = *(const v4f *)(mh + mx_pos(32 * q + 8 * c));
+            const v4f m1v = *(const v4f *)(mh + mx_pos(32 * q + 8 * c + 4));
+            const uint32_t u0 = (uint32_t)wv[c][0], u1 = (uint32_t)wv[c][1];
+            const uint32_t u2 = (uint32_t)wv[c][2], u3 = (uint32_t)wv[c][3];
+            acc0 = fmaf(__uint_as_float(u0 << 16), m0v.x, acc0);
+            acc1 = fmaf(__uint_as_float(u0 & 0xffff0000u), m0v.y, acc1);
+            acc0 = fmaf(__uint_as_float(u1 << 16), m0v.z, acc0);
+            acc1 = fmaf(__uint_as_float(u1 & 0xffff0000u), m0v.w, acc1);
+            acc0 = fmaf(__uint_as_float(u2 << 16), m1v.x, acc0);
+            acc1 = fmaf(__uint_as_float(u2 & 0xffff0000u), m1v.y, acc1);
+            acc0 = fmaf(__uint_as_float(u3 << 16), m1v.z, acc0);
+            acc1 = fmaf(__uint_as_float(u3 & 0xffff0000u), m1v.w, acc1);
+        }
+        const float hsum = row16_sum(acc0 + acc1);
+        if (q == 0) {
+            const size_t o = (size_t)(grp * 8 + jj) * a.d.HO + (size_t)h * 128 + dd;
+            a.ho[o] = hsum;
+            uint16_t hi, lo;
+            split_bf16(hsum, hi, lo);
+            a.hos[o] = hi;
+            a.hos[(size_t)a.t.n * a.d.HO + o] = lo;
+        }
     }
 }
 
 hipError_t launch_combine(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
                           const uint16_t *kv_b, const DecodeWork &w) {
     if (d.R > kMaxR) return hipErrorInvalidValue;
-    CombineArgs a{t, d, w.part, kv_b, w.mix, w.ho, w.hos, fmt};
-    if (combine_writes_hos(fmt, d))
-        hipLaunchKernelGGL(k_combine_r512, dim3(2 * t.n * d.NH), dim3(1024), 0, st, a);
-    else
+    CombineArgs a{t, d, w.part, kv_b, w.mix, w.ho, w.hos, fmt, 1};
+    int maxns = 0;
+    for (int i = 0; i < t.n; ++i) maxns = max(maxns, t.s[i].nsplit);
+    if (combine_writes_hos(fmt, d) && t.n >= 32 && maxns <= kCombWide) {
+        hipLaunchKernelGGL(k_combine_r512x8, dim3(2 * ((t.n + 7) / 8) * d.NH), dim3(1024), 0, st, a);
+    } else if (combine_writes_hos(fmt, d)) {
+        // up to kCombBlocks blocks; a block takes spb sequences of one (head, half) in turn
+        a.spb = max(1, (2 * t.n * d.NH + kCombBlocks - 1) / kCombBlocks);
+        const int groups = (t.n + a.spb - 1) / a.spb;
+        hipLaunchKernelGGL(k_combine_r512, dim3(2 * groups * d.NH), dim3(1024), 0, st, a);
+    } else {
         hipLaunchKernelGGL(k_combine, dim3(t.n * d.NH), dim3(256), 0, st, a);
+    }
     return hipGetLastError();
 }
 
@@ -2335,15 +2474,22 @@ __global__ __launch_bounds__(256) void k_copy(v4i *dst, const v4i *src, size_t n
 // Streaming read of n 16-byte words, four independent loads in flight per thread, folded by
 // XOR; the fold reaches memory only for one (practically never occurring) pattern, which keeps
 // every load live: a read-bandwidth probe.
+// Each block streams a contiguous 1/gridDim of the buffer with 8 loads of 16 bytes in flight per
+// thread: contiguous per-block ranges reached 6.2-6.3 TB/s on MI355X, a grid-stride order over the
+// same bytes 5.1-5.5 TB/s.
 __global__ __launch_bounds__(256) void k_read(const v4i *src, size_t n, v4i *sink) {
-    const size_t stride = (size_t)gridDim.x * 256;
-    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t per = (n + gridDim.x - 1) / gridDim.x;
+    const size_t b0 = (size_t)blockIdx.x * per, b1 = b0 + per < n ? b0 + per : n;
     v4i acc = {0, 0, 0, 0};
-    for (; i + 3 * stride < n; i += 4 * stride) {
-        const v4i a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
-        acc ^= (a ^ b) ^ (c ^ d);
+    size_t i = b0 + threadIdx.x;
+    for (; i + 7 * 256 < b1; i += 8 * 256) {
+        v4i v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = src[i + 256 * u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc ^= v[u];
     }
-    for (; i < n; i += stride) acc ^= src[i];
+    for (; i < b1; i += 256) acc ^= src[i];
     if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x5a17c3e1) sink[(size_t)blockIdx.x * 256 + threadIdx.x] = acc;
 }
 

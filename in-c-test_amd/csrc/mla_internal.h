@@ -162,7 +162,7 @@ hipError_t launch_fill_history(hipStream_t st, int fmt, void *a, void *b, void *
 hipError_t launch_copy(hipStream_t st, void *dst, const void *src, size_t bytes);
 // Streaming read of `bytes` (a multiple of 16) by kReadBlocks x 256 threads; sink: device
 // memory of kReadBlocks x 256 x 16 bytes (written only for one improbable bit pattern).
-constexpr int kReadBlocks = 2048;
+constexpr int kReadBlocks = 8192;
 hipError_t launch_read(hipStream_t st, const void *src, size_t bytes, void *sink);
 
 // ---- prefill (mla_prefill.hip) ----
