@@ -1231,7 +1231,11 @@ __global__ __launch_bounds__(256) void k_attn_generic(AttnArgs a) {
 // LDS. Softmax statistics are kept per head in every wave (online rescaling). Mix: each
 // wave owns 128 latent columns, M = heads, N = 16 columns, K = 4 rows per instruction.
 constexpr int kF32Ch = 16;
-constexpr int kF32Rs = 580;  // LDS row stride (floats): 576 + 4, conflict-free b128 reads
+constexpr int kF32Rs = 576;  // LDS row stride (floats)
+// Column XOR of LDS row r (multiples of 4, so 16-byte groups stay whole): the score reads (rows
+// 0..7 of one group per 8 lanes) and the mix reads (rows 4k + g and 4k + g + 1, 16 columns each,
+// per 32 lanes) fall in distinct banks.
+__device__ __forceinline__ int f32_swz(int r) { return (4 * (r & 7)) ^ (16 * (r & 1)); }
 
 __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float rows[kF32Ch * kF32Rs];
@@ -1277,10 +1281,10 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const int p = tid + 256 * k, row = p >> 7, c4 = p & 127;
-            *(v4f *)(rows + row * kF32Rs + 4 * c4) = pl[k];
+            *(v4f *)(rows + row * kF32Rs + ((4 * c4) ^ f32_swz(row))) = pl[k];
         }
         const int row = tid >> 4, c4 = tid & 15;
-        *(v4f *)(rows + row * kF32Rs + 512 + 4 * c4) = pr;
+        *(v4f *)(rows + row * kF32Rs + ((512 + 4 * c4) ^ f32_swz(row))) = pr;
     };
 
     const int nch = (r1 - r0 + kF32Ch - 1) / kF32Ch;
@@ -1292,10 +1296,11 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
         if (c + 1 < nch) prefetch(c + 1);
         const int base = r0 + c * kF32Ch;
         v4f dp = {0.f, 0.f, 0.f, 0.f};
-        const float *brow = rows + n * kF32Rs + 144 * w + 36 * g;
+        const float *brow = rows + n * kF32Rs;
+        const int nsw = f32_swz(n);
 #pragma unroll
         for (int t = 0; t < 36; t += 4) {
-            const v4f bv = *(const v4f *)(brow + t);
+            const v4f bv = *(const v4f *)(brow + ((144 * w + 36 * g + t) ^ nsw));
             dp = mfma_f32(qa[t], bv.x, dp);
             dp = mfma_f32(qa[t + 1], bv.y, dp);
             dp = mfma_f32(qa[t + 2], bv.z, dp);
@@ -1336,7 +1341,7 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
             for (int i = 0; i < 4; ++i) acc[t][i] *= ad[i];
             const int col = 128 * w + 16 * t + n;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) acc[t] = mfma_f32(pr4[k], rows[(4 * k + g) * kF32Rs + col], acc[t]);
+            for (int k = 0; k < 4; ++k) acc[t] = mfma_f32(pr4[k], rows[(4 * k + g) * kF32Rs + (col ^ f32_swz(4 * k + g))], acc[t]);
         }
     }
     float *P = a.part + (size_t)pidx * 16 * 514;
