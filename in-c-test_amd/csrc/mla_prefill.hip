@@ -659,27 +659,14 @@ void k_flash_prefill(FlashArgs a) {
     wait_vmcnt<0>();
     lds_barrier();
 
-    auto qk = [&](int j, v4f (&s)[4][2]) __attribute__((always_inline)) {
-        const uint8_t *kt = smem + (j & 1) * 2 * kFKB;
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int u = 0; u < 2; ++u) s[t][u] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kb = 0; kb < 6; ++kb)
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const v8h kh = *(const v8h *)(kt + t * 16 * 384 + krd[kb]);
-                const v8h kl = *(const v8h *)(kt + kFKB + t * 16 * 384 + krd[kb]);
-#pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    s[t][u] = mfma_f16(kh, qa[u][kb], s[t][u]);
-                    s[t][u] = mfma_f16(kh, qb[u][kb], s[t][u]);
-                    s[t][u] = mfma_f16(kl, qa[u][kb], s[t][u]);
-                }
-            }
-    };
-
+    // Step j: QK of tile j+1 (unless it is the last step) with the softmax of tile j, the DMA
+    // of K(j+2) and V(j+1), and the reads of tile j's V fragments spread over its MFMAs, then PV
+    // of tile j. With one wave per SIMD, VALU, DMA-issue and LDS instructions run under the
+    // MFMAs only when they are interleaved with them in the wave's instruction stream, so the
+    // step is laid out as 18 groups of eight independent QK MFMAs (k-block kb, pass p) separated
+    // by scheduling fences, each carrying its share of the other work, and the scheduler is asked
+    // to alternate MFMAs and VALU within a group. Each QK accumulator receives its products in
+    // the order kb-major, Kh Qh, Kh Ql, Kl Qh; the softmax arithmetic is unchanged.
     float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
     v4f acc[8][2];
 #pragma unroll
@@ -687,80 +674,190 @@ void k_flash_prefill(FlashArgs a) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) acc[dt][u] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    auto softmax_pv = [&](auto mask_tag, v4f (&s)[4][2], int j) __attribute__((always_inline)) {
-        constexpr bool kMask = decltype(mask_tag)::value;
-        const int k0 = j * kFK;
-        v8h pb[2][2];
-        float alpha[2];
-        bool moved = false;
+    v4f sc[4][2];
+    auto load_k = [&](const uint8_t *kt, int kb, v8h (&kh)[4], v8h (&kl)[4]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int t = 0; t < 4; ++t) {
+            kh[t] = *(const v8h *)(kt + t * 16 * 384 + krd[kb]);
+            kl[t] = *(const v8h *)(kt + kFKB + t * 16 * 384 + krd[kb]);
+        }
+    };
+    auto qk_pass = [&](v4f (&s)[4][2], const v8h (&kf)[4], const v8h (&qf)[2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) s[t][u] = mfma_f16(kf[t], qf[u], s[t][u]);
+    };
+    {  // QK of tile 0
+        const uint8_t *kt = smem;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) sc[t][u] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 6; ++kb) {
+            v8h kh[4], kl[4];
+            load_k(kt, kb, kh, kl);
+            const v8h q0[2] = {qa[0][kb], qa[1][kb]}, q1[2] = {qb[0][kb], qb[1][kb]};
+            qk_pass(sc, kh, q0);
+            qk_pass(sc, kh, q1);
+            qk_pass(sc, kl, q0);
+        }
+    }
+
+    auto step = [&](auto mask_tag, auto next_tag, int j) __attribute__((always_inline)) {
+        constexpr bool kMask = decltype(mask_tag)::value;
+        constexpr bool kNext = decltype(next_tag)::value;
+        wait_vmcnt<0>();
+        lds_barrier();
+        const bool dk = j + 2 < nt, dv = j + 1 < nt;
+        const uint32_t kdst = sbase + (j & 1) * 2 * kFKB + (uint32_t)(6 * w) * 1024;  // K(j+2)
+        const size_t kso = (size_t)(j + 2) * kFK * 384;
+        const uint32_t vdst = sbase + 4 * kFKB + ((j + 1) & 1) * kFVB + (uint32_t)(4 * w) * 1024;  // V(j+1)
+        auto dma_k = [&](int i) __attribute__((always_inline)) {
+            if (dk) {
+                dma_b128(gkh + kso + koff[i], kdst + i * 1024);
+                dma_b128(gkl + kso + koff[i], kdst + kFKB + i * 1024);
+            }
+        };
+        auto dma_v = [&](int i) __attribute__((always_inline)) {
+            if (dv) dma_b128(gv + (size_t)(j + 1) * 128 + voff[i], vdst + i * 1024);
+        };
+        // softmax of tile j in pieces (per 16-query tile u: A mask + local max, B row max and
+        // reference max, C(t) weights of key tile t, D denominator)
+        const int k0 = j * kFK;
+        float mloc[2], mnew[2], alpha[2], ps[2];
+        bool moved = false;
+        v8h pb[2][2];
+        auto smA = [&](int u) __attribute__((always_inline)) {
             const int q = qw + 16 * u + n;
             float mx = -INFINITY;
 #pragma unroll
             for (int t = 0; t < 4; ++t)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    float v = s[t][u][i];
+                    float v = sc[t][u][i];
                     if constexpr (kMask) {
                         const int key = k0 + 16 * t + 4 * g + i;
                         if (key > q || key >= S) v = -INFINITY;
-                        s[t][u][i] = v;
+                        sc[t][u][i] = v;
                     }
                     mx = fmaxf(mx, v);
                 }
-            mx = xrow_max(mx) * sl2;
+            mloc[u] = mx;
+        };
+        auto smB = [&](int u) __attribute__((always_inline)) {
+            const float mx = xrow_max(mloc[u]) * sl2;
             const float mref = m_run[u];
             const bool mv = mx > mref + kFLazy;
-            const float mnew = mv ? mx : mref;
-            alpha[u] = __builtin_amdgcn_exp2f(mref - mnew);
-            m_run[u] = mnew;
+            mnew[u] = mv ? mx : mref;
+            alpha[u] = __builtin_amdgcn_exp2f(mref - mnew[u]);
+            m_run[u] = mnew[u];
             moved |= mv;
-            float ps = 0.f;
+            ps[u] = 0.f;
+        };
+        auto smC = [&](int u, int t) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float p = __builtin_amdgcn_exp2f(fmaf(sc[t][u][i], sl2, -mnew[u]));
+                ps[u] += p;
+                pb[u][t >> 1][4 * (t & 1) + i] = (_Float16)p;
+            }
+        };
+        auto smD = [&](int u) __attribute__((always_inline)) { l_run[u] = fmaf(l_run[u], alpha[u], ps[u]); };
+        // V fragments of tile j: row 16 dt + n, logical slot 4c + g
+        const uint8_t *vt = smem + 4 * kFKB + (j & 1) * kFVB;
+        v8h vv[2][8];
+        auto load_v = [&](int f) __attribute__((always_inline)) {
+            vv[f >> 3][f & 7] = *(const v8h *)(vt + (f & 7) * 16 * 128 + vrd[f >> 3]);
+        };
+        // the work carried by group gi (kb = gi / 3, pass = gi % 3)
+        auto extra = [&](int gi) __attribute__((always_inline)) {
+            switch (gi) {
+            case 0: smA(0); dma_k(0); break;
+            case 1: smB(0); dma_k(1); break;
+            case 2: smC(0, 0); dma_k(2); break;
+            case 3: smC(0, 1); dma_k(3); break;
+            case 4: smC(0, 2); dma_k(4); break;
+            case 5: smC(0, 3); smD(0); dma_k(5); break;
+            case 6: smA(1); dma_v(0); break;
+            case 7: smB(1); dma_v(1); break;
+            case 8: smC(1, 0); dma_v(2); break;
+            case 9: smC(1, 1); dma_v(3); break;
+            case 10: smC(1, 2); break;
+            case 11: smC(1, 3); smD(1); break;
+            case 12: load_v(0); load_v(1); load_v(2); break;
+            case 13: load_v(3); load_v(4); load_v(5); break;
+            case 14: load_v(6); load_v(7); load_v(8); break;
+            case 15: load_v(9); load_v(10); load_v(11); break;
+            case 16: load_v(12); load_v(13); break;
+            case 17: load_v(14); load_v(15); break;
+            default: break;
+            }
+        };
+        if constexpr (kNext) {
+            const uint8_t *kt = smem + ((j + 1) & 1) * 2 * kFKB;  // K tile j+1
+            v4f sn[4][2];
 #pragma unroll
             for (int t = 0; t < 4; ++t)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float p = __builtin_amdgcn_exp2f(fmaf(s[t][u][i], sl2, -mnew));
-                    ps += p;
-                    pb[u][t >> 1][4 * (t & 1) + i] = (_Float16)p;
+                for (int u = 0; u < 2; ++u) sn[t][u] = v4f{0.f, 0.f, 0.f, 0.f};
+            v8h kh[2][4], kl[2][4];
+            load_k(kt, 0, kh[0], kl[0]);
+#pragma unroll
+            for (int kb = 0; kb < 6; ++kb) {
+                const int cb = kb & 1;
+                if (kb + 1 < 6) load_k(kt, kb + 1, kh[cb ^ 1], kl[cb ^ 1]);
+                const v8h q0[2] = {qa[0][kb], qa[1][kb]}, q1[2] = {qb[0][kb], qb[1][kb]};
+#pragma unroll
+                for (int p = 0; p < 3; ++p) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    qk_pass(sn, p == 2 ? kl[cb] : kh[cb], p == 1 ? q1 : q0);
+                    extra(3 * kb + p);
+#pragma unroll
+                    for (int m = 0; m < 8; ++m) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // up to three VALU
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
                 }
-            l_run[u] = fmaf(l_run[u], alpha[u], ps);
-        }
-        if (__any(moved)) {
-#pragma unroll
-            for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-                for (int u = 0; u < 2; ++u) acc[dt][u] *= alpha[u];
-        }
-        const uint8_t *vt = smem + 4 * kFKB + (j & 1) * kFVB;
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-            for (int dt = 0; dt < 8; ++dt) {
-                const v8h vv = *(const v8h *)(vt + dt * 16 * 128 + vrd[c]);
-#pragma unroll
-                for (int u = 0; u < 2; ++u) acc[dt][u] = mfma_f16(vv, pb[u][c], acc[dt][u]);
             }
-    };
-
-    v4f sc[4][2];
-    qk(0, sc);
-    // step j: QK of tile j+1 (if NEXT), softmax + PV of tile j; DMA of K(j+2), V(j+1).
-    auto step = [&](auto mask_tag, auto next_tag, int j) __attribute__((always_inline)) {
-        constexpr bool kNext = decltype(next_tag)::value;
-        wait_vmcnt<0>();
-        lds_barrier();
-        if (j + 2 < nt) issue_k(j + 2);
-        if (j + 1 < nt) issue_v(j + 1);
-        v4f sn[4][2];
-        if constexpr (kNext) qk(j + 1, sn);
-        softmax_pv(mask_tag, sc, j);
-        if constexpr (kNext) {
+            // the softmax results stay in the groups above (the compiler would otherwise sink
+            // them past the rescale branch, to their uses)
+            asm volatile("" ::"v"(pb[0][0]), "v"(pb[0][1]), "v"(pb[1][0]), "v"(pb[1][1]), "v"(l_run[0]),
+                         "v"(l_run[1]));
+            const bool any = __any(moved);
+            if (any) {
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) acc[dt][u] *= alpha[u];
+            }
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) acc[dt][u] = mfma_f16(vv[c][dt], pb[u][c], acc[dt][u]);
 #pragma unroll
             for (int t = 0; t < 4; ++t)
 #pragma unroll
                 for (int u = 0; u < 2; ++u) sc[t][u] = sn[t][u];
+        } else {
+#pragma unroll
+            for (int gi = 0; gi < 18; ++gi) extra(gi);
+            if (__any(moved)) {
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) acc[dt][u] *= alpha[u];
+            }
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) acc[dt][u] = mfma_f16(vv[c][dt], pb[u][c], acc[dt][u]);
         }
     };
     using F = std::false_type;
