@@ -63,19 +63,23 @@ __global__ void k_zero_int(int *p, int n) {
 // columns of C may come from two weight matrices (B0 for n < N0, B1 for the N1 after it),
 // so the q and kv_a projections of the same tokens run as one launch.
 //
-// Block tile 256 x BN (BN = 256 or 128), eight waves (2 per SIMD) in a WM x WN grid, each
+// Block tile 256 x BN (BN = 256 or 128), eight math waves (2 per SIMD) in a WM x WN grid, each
 // owning a (256 / WM) x (BN / WN) quadrant of v_mfma_f32_16x16x32 tiles. Large tiles keep
 // the L2 traffic at 24-32 bytes per clock per CU at the MFMA rate. The lo operand, when it
 // is given and needed, is a second pass over k: the k loop runs over [Ah | Al] against
 // [B | B], so each stage is one A and one B tile with a k step of 64, and all stages have
 // the same shape. They stream into an LDS ring of 3 stages (2 where 3 do not fit) by
-// global_load_lds_dwordx4 DMA (the later stages in flight while one is computed); 128-byte
-// rows with slot s at s ^ (r & 7) spread the 8 rows one ds_read_b128 phase touches over
-// distinct banks. Each wave reads all its fragments of a 32-deep k-sub before its MFMAs.
+// global_load_lds_dwordx4 DMA, issued by four more waves that do nothing else: a DMA
+// instruction holds its wave until the memory system accepts it (about a quarter of a math
+// wave's time when the math waves issued their own), so the math waves only compute and meet
+// the DMA waves at one barrier per stage (the DMA waves wait for stage kt's data before it).
+// 128-byte rows with slot s at s ^ (r & 7) spread the 8 rows one ds_read_b128 phase touches
+// over distinct banks. Each wave reads all its fragments of a 32-deep k-sub before its MFMAs.
 // The lo pass runs when Al is given and either no flag is given or *lo_flag != 0 (the flag
 // is raised by the producer of Al when some lo word is non-zero). Requires K % 64 == 0, lda
 // and ldb multiples of 8.
 constexpr int kGBm = 256;
+constexpr int kGemmMath = 8, kGemmDma = 4;  // waves of a GEMM block
 
 template <int BN>
 struct GemmShape {
@@ -119,8 +123,19 @@ __device__ __forceinline__ v4f mfma16(const v8bf &a, const v8bf &b, const v4f &c
     else return mfma_bf16(a, b, c);
 }
 
+// s_waitcnt vmcnt(PER * min(later, MAXL)) for a wave-uniform count of later stages in flight.
+template <int PER, int MAXL>
+__device__ __forceinline__ void wait_stages(int later) {
+    if constexpr (MAXL == 0) {
+        wait_vmcnt<0>();
+    } else {
+        if (later >= MAXL) wait_vmcnt<PER * MAXL>();
+        else wait_stages<PER, MAXL - 1>(later);
+    }
+}
+
 template <int BN, int EPI, bool F16>
-__global__ __launch_bounds__(512) void k_gemm16(GemmArgs a, GemmEpi e) {
+__global__ __launch_bounds__(64 * (kGemmMath + kGemmDma)) void k_gemm16(GemmArgs a, GemmEpi e) {
     using Sh = GemmShape<BN>;
     constexpr int BK = Sh::BK, RowB = Sh::RowB, Spr = Sh::Spr;
     constexpr int TM = Sh::TM, TN = Sh::TN;
@@ -145,35 +160,50 @@ __global__ __launch_bounds__(512) void k_gemm16(GemmArgs a, GemmEpi e) {
     const int m0 = mt * kGBm;
     const bool use_lo = a.Al && (!a.lo_flag || *a.lo_flag);
 
-    // DMA: thread (w, l), instruction i fills slot (8i + w) * 64 + l of a tile: row p / Spr,
-    // physical slot p % Spr holding logical slot (p % Spr) ^ swz(row). Rows past the end of A
-    // or B are clamped to the last row (their results are never stored).
-    constexpr int NA = Sh::ATile / 8192, NB = Sh::BTile / 8192;  // instructions per thread
-    uint32_t aoff[NA], boff[NB];
-#pragma unroll
-    for (int i = 0; i < NA; ++i) {
-        const int p = (8 * i + w) * 64 + l, row = p / Spr, s = (p % Spr) ^ Sh::swz(row);
-        aoff[i] = (uint32_t)(min(m0 + row, M - 1) - m0) * lda * 2 + 16 * s;
-    }
-#pragma unroll
-    for (int i = 0; i < NB; ++i) {
-        const int p = (8 * i + w) * 64 + l, row = p / Spr, s = (p % Spr) ^ Sh::swz(row);
-        boff[i] = (uint32_t)(min(nb0 + row, Nseg - 1) - nb0) * ldb * 2 + 16 * s;
-    }
-    const uint8_t *gah = (const uint8_t *)(a.Ah + (size_t)m0 * lda);
-    const uint8_t *gal = use_lo ? (const uint8_t *)(a.Al + (size_t)m0 * lda) : gah;
-    const uint8_t *gb = (const uint8_t *)(B + (size_t)nb0 * ldb);
     const int nk = K / BK, nkt = use_lo ? 2 * nk : nk;  // k steps of the hi pass, of all passes
-    auto issue = [&](int kt, int stage) __attribute__((always_inline)) {
-        const uint32_t dst = sbase + stage * Sh::Stage + (uint32_t)w * 1024;
-        const bool lo = kt >= nk;
-        const uint8_t *ga = lo ? gal : gah;
-        const size_t ko = (size_t)(lo ? kt - nk : kt) * BK * 2;
+    constexpr int NS = Sh::Stages;
+    if (w >= kGemmMath) {
+        // DMA wave dw: instruction i fills slot (4i + dw) * 64 + l of a tile: row p / Spr,
+        // physical slot p % Spr holding logical slot (p % Spr) ^ swz(row). Rows past the end of
+        // A or B are clamped to the last row (their results are never stored).
+        const int dw = w - kGemmMath;
+        constexpr int NA = Sh::ATile / (kGemmDma * 1024), NB = Sh::BTile / (kGemmDma * 1024);
+        uint32_t aoff[NA], boff[NB];
 #pragma unroll
-        for (int i = 0; i < NA; ++i) dma_b128(ga + ko + aoff[i], dst + i * 8192);
+        for (int i = 0; i < NA; ++i) {
+            const int p = (kGemmDma * i + dw) * 64 + l, row = p / Spr, s = (p % Spr) ^ Sh::swz(row);
+            aoff[i] = (uint32_t)(min(m0 + row, M - 1) - m0) * lda * 2 + 16 * s;
+        }
 #pragma unroll
-        for (int i = 0; i < NB; ++i) dma_b128(gb + ko + boff[i], dst + Sh::ATile + i * 8192);
-    };
+        for (int i = 0; i < NB; ++i) {
+            const int p = (kGemmDma * i + dw) * 64 + l, row = p / Spr, s = (p % Spr) ^ Sh::swz(row);
+            boff[i] = (uint32_t)(min(nb0 + row, Nseg - 1) - nb0) * ldb * 2 + 16 * s;
+        }
+        const uint8_t *gah = (const uint8_t *)(a.Ah + (size_t)m0 * lda);
+        const uint8_t *gal = use_lo ? (const uint8_t *)(a.Al + (size_t)m0 * lda) : gah;
+        const uint8_t *gb = (const uint8_t *)(B + (size_t)nb0 * ldb);
+        auto issue = [&](int kt, int stage) __attribute__((always_inline)) {
+            const uint32_t dst = sbase + stage * Sh::Stage + (uint32_t)dw * 1024;
+            const bool lo = kt >= nk;
+            const uint8_t *ga = lo ? gal : gah;
+            const size_t ko = (size_t)(lo ? kt - nk : kt) * BK * 2;
+#pragma unroll
+            for (int i = 0; i < NA; ++i) dma_b128(ga + ko + aoff[i], dst + i * (kGemmDma * 1024));
+#pragma unroll
+            for (int i = 0; i < NB; ++i) dma_b128(gb + ko + boff[i], dst + Sh::ATile + i * (kGemmDma * 1024));
+        };
+#pragma unroll
+        for (int q = 0; q < NS - 1; ++q)
+            if (q < nkt) issue(q, q);
+        for (int kt = 0; kt < nkt; ++kt) {
+            // stage kt has landed when at most min(NS - 2, nkt - 1 - kt) later stages are in flight
+            wait_stages<NA + NB, NS - 2>(min(NS - 2, nkt - 1 - kt));
+            lds_barrier();  // stage kt is in LDS; every math wave is done with stage kt - 1
+            if (kt + NS - 1 < nkt) issue(kt + NS - 1, (kt + NS - 1) % NS);
+        }
+        lds_barrier();  // the math waves' epilogue barrier
+        return;
+    }
     // fragment rows 16 * tile + n (n & 7 = row & 7), logical slot 4 ks + g of k-sub ks
     int frd[BK / 32];
 #pragma unroll
@@ -185,16 +215,8 @@ __global__ __launch_bounds__(512) void k_gemm16(GemmArgs a, GemmEpi e) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    constexpr int NS = Sh::Stages;
-#pragma unroll
-    for (int q = 0; q < NS - 1; ++q)
-        if (q < nkt) issue(q, q);
     for (int kt = 0; kt < nkt; ++kt) {
-        // stage kt has landed when at most min(NS - 2, nkt - 1 - kt) later stages are in flight
-        if (NS == 3 && kt + 1 < nkt) wait_vmcnt<NA + NB>();
-        else wait_vmcnt<0>();
-        lds_barrier();  // also: every wave is done with stage kt - 1, whose slot is refilled next
-        if (kt + NS - 1 < nkt) issue(kt + NS - 1, (kt + NS - 1) % NS);
+        lds_barrier();  // stage kt has landed (the DMA waves waited for it)
         const uint8_t *st = smem + (kt % NS) * Sh::Stage;
 #pragma unroll
         for (int ks = 0; ks < BK / 32; ++ks) {
@@ -331,8 +353,9 @@ static hipError_t gemm(hipStream_t st, const uint16_t *Ah, const uint16_t *Al, c
     const int t128 = tm * ((N0 + 127) / 128 + (N1 + 127) / 128);
     const bool big = 2 * ((t256 + 255) / 256) <= (t128 + 255) / 256;
     if (K % 64) return hipErrorInvalidValue;
-    if (big) hipLaunchKernelGGL((k_gemm16<256, EPI, F16>), dim3(t256), dim3(512), 0, st, a, e);
-    else hipLaunchKernelGGL((k_gemm16<128, EPI, F16>), dim3(t128), dim3(512), 0, st, a, e);
+    constexpr int nt = 64 * (kGemmMath + kGemmDma);
+    if (big) hipLaunchKernelGGL((k_gemm16<256, EPI, F16>), dim3(t256), dim3(nt), 0, st, a, e);
+    else hipLaunchKernelGGL((k_gemm16<128, EPI, F16>), dim3(t128), dim3(nt), 0, st, a, e);
     return hipGetLastError();
 }
 
