@@ -680,6 +680,12 @@ void k_flash_prefill(FlashArgs a) {
 #pragma unroll
         for (int kb = 0; kb < 6; ++kb) asm volatile("" : "+v"(qa[u][kb]), "+v"(qb[u][kb]));
     wait_vmcnt<0>();
+    // the query operands live in AGPRs (MFMA reads its A/B operands from either file), which
+    // leaves the VGPRs to the score accumulators the softmax reads
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int kb = 0; kb < 6; ++kb) asm volatile("" : "+a"(qa[u][kb]), "+a"(qb[u][kb]));
     lds_barrier();
 
     // Step j: QK of tile j+1 (unless it is the last step) with the softmax of tile j, the DMA
