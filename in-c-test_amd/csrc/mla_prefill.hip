@@ -47,14 +47,10 @@ __global__ __launch_bounds__(256) void k_split(const float *src, int ld_src, uin
     // Blocks with a non-zero lo word store 1. Every writer stores the same value and the reader
     // is a later kernel, so a workgroup-scope store (cached in the XCD's L2, written back at
     // the kernel's end) suffices; device-coherent stores or atomics to one address from every
-    // block serialise at memory (measured 13-65 us for 2048 blocks). The flag starts at 0.
+    // block serialise at memory (measured 13-65 us for 2048 blocks). The flag is only raised
+    // here; k_kva_pack clears it after the q GEMM has read it.
     if (flag && __syncthreads_or(any) && threadIdx.x == 0)
         __hip_atomic_store(flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-
-__global__ void k_zero_int(int *p, int n) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = 0;
 }
 
 // ================================================================ GEMM =================
@@ -430,10 +426,12 @@ struct KvaPackArgs {
     size_t pstride;  // np partials of y, pstride floats apart, summed in order
     int np, S, Sp, NH, ldy, R, DN, DR, DV;
     float eps;
+    int *x_flag;     // the x lo flag, cleared for the next prefill (its one reader has run)
 };
 
 __global__ __launch_bounds__(256) void k_kva_pack(KvaPackArgs a) {
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+    if (blockIdx.x == 0 && threadIdx.x == 0 && a.x_flag) *a.x_flag = 0;
     if (t >= a.Sp) return;
     const int QD = a.DN + a.DR, half = a.DR / 2, R = a.R;
     if (t >= a.S) {
@@ -1101,7 +1099,10 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
         _Float16 *vt = (_Float16 *)take(2 * (size_t)d.NH * d.DV * Sp);
         _Float16 *heads = (_Float16 *)take(2 * (size_t)S * d.HO);
         const GemmEpi ep{qh, ql, kh, kl, vt, cs, Sp, d.DN, d.DR, d.DV};
-        hipLaunchKernelGGL(k_zero_int, dim3(1), dim3(64), 0, st, flags, 8);
+        // flags[0] (any x lo word non-zero) is raised by k_split and cleared by k_kva_pack after
+        // the q GEMM has read it, so no launch clears it first. A value left raised (a call
+        // that failed in between, or the buffer reused by another call) only costs the GEMM's lo
+        // pass over an exact plane: the flag is never clear while a lo word is non-zero.
         const int split_blocks = std::min(2048, S);
         hipLaunchKernelGGL(k_split, dim3(split_blocks), dim3(256), 0, st, x, d.H, xh, xl, d.H, S, d.H, flags + 0);
         if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -1121,7 +1122,7 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
             return e;
         }
         KvaPackArgs ka{ykva, wnorm, cs, lath, latl, qh, ql, kh, kl, vt, (size_t)S * d.KVO, np,
-                       S, Sp, d.NH, d.KVO, d.R, d.DN, d.DR, d.DV, eps};
+                       S, Sp, d.NH, d.KVO, d.R, d.DN, d.DR, d.DV, eps, flags + 0};
         hipLaunchKernelGGL(k_kva_pack, dim3((Sp + 3) / 4), dim3(256), 0, st, ka);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // kv_b (-> K nope part, V^T hi/lo)
