@@ -743,12 +743,12 @@ void k_flash_prefill(FlashArgs a) {
         const uint32_t vdst = sbase + 4 * kFKB + ((j + 1) & 1) * kFVB + (uint32_t)(4 * w) * 1024;  // V(j+1)
         auto dma_k = [&](int i) __attribute__((always_inline)) {
             if (dk) {
-                dma_b128(gkh + kso + koff[i], kdst + i * 1024);
-                dma_b128(gkl + kso + koff[i], kdst + kFKB + i * 1024);
+                dma_b128_s(gkh + kso, koff[i], kdst + i * 1024);
+                dma_b128_s(gkl + kso, koff[i], kdst + kFKB + i * 1024);
             }
         };
         auto dma_v = [&](int i) __attribute__((always_inline)) {
-            if (dv) dma_b128(gv + (size_t)(j + 1) * 128 + voff[i], vdst + i * 1024);
+            if (dv) dma_b128_s(gv + (size_t)(j + 1) * 128, voff[i], vdst + i * 1024);
         };
         // softmax of tile j in pieces (per 16-query tile u: A mask + local max, B row max and
         // reference max, C(t) weights of key tile t, D denominator)
