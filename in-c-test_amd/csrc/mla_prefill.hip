@@ -184,9 +184,9 @@ __global__ __launch_bounds__(64 * (kGemmMath + kGemmDma)) void k_gemm16(GemmArgs
             const uint8_t *ga = lo ? gal : gah;
             const size_t ko = (size_t)(lo ? kt - nk : kt) * BK * 2;
 #pragma unroll
-            for (int i = 0; i < NA; ++i) dma_b128(ga + ko + aoff[i], dst + i * (kGemmDma * 1024));
+            for (int i = 0; i < NA; ++i) dma_b128_s(ga + ko, aoff[i], dst + i * (kGemmDma * 1024));
 #pragma unroll
-            for (int i = 0; i < NB; ++i) dma_b128(gb + ko + boff[i], dst + Sh::ATile + i * (kGemmDma * 1024));
+            for (int i = 0; i < NB; ++i) dma_b128_s(gb + ko, boff[i], dst + Sh::ATile + i * (kGemmDma * 1024));
         };
 #pragma unroll
         for (int q = 0; q < NS - 1; ++q)
