@@ -116,3 +116,30 @@ def test_prefill_rejects_bad_arguments():
     assert L.kvl_mla_prefill_bf16(f32(out), f32(out), 0, C.byref(cfg), C.byref(w)) == -1
     bad = inputs.config(**dict(STREAM, qk_rope_dim=5))
     assert L.kvl_mla_prefill_bf16(f32(out), f32(out), 1, C.byref(bad), C.byref(w)) == -1
+
+
+def test_prefill_x_lo_flag_across_calls():
+    """The q GEMM runs its lo pass only when some x value is not bf16-exact: the flag is raised
+    by the split kernel and cleared by a later kernel of the same call. x, then bf16(x), then x
+    again on the same weights: the two x calls are bit-identical, both differ from the bf16(x)
+    call (their lo pass ran, also after the bf16(x) call left the flag clear), and all three
+    match the oracle."""
+    cfg = inputs.config(**inputs.KIMI)
+    layer = inputs.make_layer(cfg, 0xF1, std=0.02)
+    w = layer.struct()
+    S = 192
+    x32 = inputs.hidden(cfg, 0xF1, S, bf16_exact=False)
+    xbf = np.ascontiguousarray(inputs.bf16_bits_to_f32(inputs.f32_to_bf16_bits(x32)))
+    assert not np.array_equal(x32, xbf)
+    outs = []
+    for i, x in enumerate([x32, xbf, x32]):
+        a = np.zeros((S, cfg.hidden_size), np.float32)
+        b = np.zeros((S, cfg.hidden_size), np.float32)
+        lib.check(L.kvl_mla_prefill_bf16(f32(a), f32(x), S, C.byref(cfg), C.byref(w)), "prefill")
+        assert ORC.orc_mla_prefill_streaming(f32(b), f32(x), S, C.byref(cfg), C.byref(w)) == 0
+        e = rel_err(a, b)
+        print(f"[prefill] call {i}: {e:.3e}", flush=True)
+        assert e <= TOL, (i, e)
+        outs.append(a)
+    np.testing.assert_array_equal(outs[0], outs[2])
+    assert not np.array_equal(outs[0], outs[1])
