@@ -1699,9 +1699,10 @@ __device__ __forceinline__ void put_q8_weights(int8_t *wqc, const float *pv, flo
 
 
 // The two roles run separate code (their registers do not overlap) with the same sequence of
-// workgroup barriers: two in the prologue (P0: the score waves' query and scale loads are
-// issued before the mix waves' first DMA burst, so they do not queue behind it; P: chunk 0 has
-// landed), per step k = 0 .. nch one (A) plus two more (B, C) when the flags read after A ask
+// workgroup barriers: two in the prologue (P0: the query operands, copied once by DMA into code
+// slot 3, have landed, and only chunk 0 is requested ahead of them; P: chunk 0 has landed, and the
+// score waves have read the query out of slot 3, which the chunk-3 DMA of step 0 then
+// overwrites), per step k = 0 .. nch one (A) plus two more (B, C) when the flags read after A ask
 // for an exchange, and one at the end. Every wave reads the
 // same LDS flags after A, so all eight take the same barriers. Everything the score waves read
 // per chunk (codes, RoPE keys, scales) arrives in LDS by the mix waves' DMA, so their steps
@@ -1728,17 +1729,17 @@ __device__ __forceinline__ void q8_score_role(const AttnArgs &a, const SeqDesc &
     v4i qh[8], ql[8];
     v8bf qrh[2], qrl[2];
     float qsd[4], m_run[4], l_lane[4];
-    const size_t qo = ((size_t)b * 16 + n) * 512;
+    // the sequence's query operands (hi, lo codes: 8 KB each; RoPE hi, lo: 2 KB each) once into
+    // code slot 3 by DMA (wave w: 1 KB pieces 5w .. 5w+4), read from there by all four waves
+    const uint32_t qslot = lds_addr(smem) + 3 * kQ8CodeB;
 #pragma unroll
-    for (int kb = 0; kb < 8; ++kb) {
-        qh[kb] = *(const v4i *)(a.qhi + qo + 64 * kb + 16 * g);
-        ql[kb] = *(const v4i *)(a.qlo + qo + 64 * kb + 16 * g);
-    }
-    const size_t ro = ((size_t)b * 16 + n) * 64;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-        qrh[kb] = *(const v8bf *)(a.qrhi + ro + 8 * (4 * kb + g));
-        qrl[kb] = *(const v8bf *)(a.qrlo + ro + 8 * (4 * kb + g));
+    for (int i = 0; i < 5; ++i) {
+        const int p = 5 * w + i;
+        const int8_t *src = p < 8 ? a.qhi + (size_t)b * 8192 + p * 1024
+                          : p < 16 ? a.qlo + (size_t)b * 8192 + (p - 8) * 1024
+                          : p < 18 ? (const int8_t *)(a.qrhi + (size_t)b * 1024) + (p - 16) * 1024
+                                   : (const int8_t *)(a.qrlo + (size_t)b * 1024) + (p - 18) * 1024;
+        dma_b128(src + 16 * l, qslot + (uint32_t)(p * 1024));
     }
     {
         const int nr = r1 - r0;
@@ -1746,7 +1747,21 @@ __device__ __forceinline__ void q8_score_role(const AttnArgs &a, const SeqDesc &
         // rows past the split end re-read its last row (a duplicate does not change the max)
 #pragma unroll
         for (int i = 0; i < 8; ++i) sv[i] = gscl[r0 + min(tid + 256 * i, nr - 1)];
+        wait_vm(8);     // this wave's query pieces have landed (the 8 scale loads may not have)
         lds_barrier();  // P0
+        {
+            const uint8_t *qb = smem + 3 * kQ8CodeB;
+#pragma unroll
+            for (int kb = 0; kb < 8; ++kb) {
+                qh[kb] = *(const v4i *)(qb + n * 512 + 64 * kb + 16 * g);
+                ql[kb] = *(const v4i *)(qb + 8192 + n * 512 + 64 * kb + 16 * g);
+            }
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                qrh[kb] = *(const v8bf *)(qb + 16384 + 2 * (n * 64 + 8 * (4 * kb + g)));
+                qrl[kb] = *(const v8bf *)(qb + 18432 + 2 * (n * 64 + 8 * (4 * kb + g)));
+            }
+        }
         // the loads complete after P0: the mix waves' first DMA is not held up by them (without
         // this the compiler may compute the max, and so wait for the loads, before the barrier)
 #pragma unroll
@@ -1942,11 +1957,12 @@ __device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const SeqDesc &sd
         alo[t] = v4i{0, 0, 0, 0};
         alo2[t] = v4i{0, 0, 0, 0};
     }
-    // prologue: codes of chunks 0 .. 2 and keys of chunks 0, 1 in flight, chunk 0 first; the
-    // issue order codes(c+1) before keys(c) keeps the per-step wait count below uniform
-    lds_barrier();  // P0
+    // prologue: codes of chunks 0 .. 2 and keys of chunks 0, 1 in flight, chunk 0 first (beside
+    // the score waves' query DMA, before P0) and the rest after it; the issue order codes(c+1)
+    // before keys(c) keeps the per-step wait count below uniform
     issue_codes(0);
     issue_rope(0);
+    lds_barrier();  // P0
     if (nch > 1) issue_codes(1);
     if (nch > 2) issue_codes(2);
     if (nch > 1) issue_rope(1);
