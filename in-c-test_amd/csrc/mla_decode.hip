@@ -1272,10 +1272,12 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const int p = tid + 256 * k, row = p >> 7, c4 = p & 127, gr = base + row;
-            pl[k] = gr < r1 ? *(const v4f *)(glat + (size_t)gr * 512 + 4 * c4) : v4f{0.f, 0.f, 0.f, 0.f};
+            // history rows are read once: non-temporal loads
+            pl[k] = gr < r1 ? __builtin_nontemporal_load((const v4f *)(glat + (size_t)gr * 512 + 4 * c4))
+                            : v4f{0.f, 0.f, 0.f, 0.f};
         }
         const int row = tid >> 4, c4 = tid & 15, gr = base + row;
-        pr = gr < r1 ? *(const v4f *)(grope + (size_t)gr * 64 + 4 * c4) : v4f{0.f, 0.f, 0.f, 0.f};
+        pr = gr < r1 ? __builtin_nontemporal_load((const v4f *)(grope + (size_t)gr * 64 + 4 * c4)) : v4f{0.f, 0.f, 0.f, 0.f};
     };
     auto stash = [&]() {
 #pragma unroll
@@ -1456,11 +1458,11 @@ __global__ __launch_bounds__(256) void k_attn_bf16_mfma(AttnArgs a) {
         for (int k = 0; k < 8; ++k) {
             const int row = 8 * w + k;
             const int gr = min(rbase + row, r1 - 1);
-            dma_b128(glat + (size_t)gr * 512 + 8 * (l ^ b16_swz(row)), buf + (uint32_t)(row * 1024));
+            dma_b128_nt(glat + (size_t)gr * 512 + 8 * (l ^ b16_swz(row)), buf + (uint32_t)(row * 1024));
         }
         const int row = 8 * w + (l >> 3);
         const int gr = min(rbase + row, r1 - 1);
-        dma_b128(grope + (size_t)gr * 64 + 8 * ((l & 7) ^ (row & 7)), buf + (uint32_t)(kB16LatB + w * 1024));
+        dma_b128_nt(grope + (size_t)gr * 64 + 8 * ((l & 7) ^ (row & 7)), buf + (uint32_t)(kB16LatB + w * 1024));
     };
 
     // query operands (A of the score MFMAs: head n, k = 32 kb + 8g .. +7). Chunk 0's DMA goes out
@@ -1922,13 +1924,13 @@ __device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const SeqDesc &sd
         if (rb0 + kQ8Ch <= r1) {
             const int8_t *gc = gcodes + (size_t)rb0 * 512;
 #pragma unroll
-            for (int k = 0; k < 8; ++k) dma_b128(gc + code_off[k], buf + (uint32_t)((mw * 8 + k) * 1024));
+            for (int k = 0; k < 8; ++k) dma_b128_nt(gc + code_off[k], buf + (uint32_t)((mw * 8 + k) * 1024));
         } else {
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 const int row = code_off[k] >> 9;
                 const int gro = min(rb0 + row, r1 - 1);
-                dma_b128(gcodes + (size_t)gro * 512 + (code_off[k] & 511), buf + (uint32_t)((mw * 8 + k) * 1024));
+                dma_b128_nt(gcodes + (size_t)gro * 512 + (code_off[k] & 511), buf + (uint32_t)((mw * 8 + k) * 1024));
             }
         }
     };
@@ -1938,9 +1940,9 @@ __device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const SeqDesc &sd
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             const int gro = min(rb0 + rope_row[k], r1 - 1);
-            dma_b128(grope + (size_t)gro * 64 + rope_el[k], buf + (uint32_t)((2 * mw + k) * 1024));
+            dma_b128_nt(grope + (size_t)gro * 64 + rope_el[k], buf + (uint32_t)((2 * mw + k) * 1024));
         }
-        if (mw == 0) dma_b32(gscl + min(rb0 + l, r1 - 1), buf + (uint32_t)kQ8RopeB);
+        if (mw == 0) dma_b32_nt(gscl + min(rb0 + l, r1 - 1), buf + (uint32_t)kQ8RopeB);
     };
     // transposed reads: rows 16g + (n >> 1) and 16g + 8 + (n >> 1) share the swizzle (+4096)
     int tr_off[8];
