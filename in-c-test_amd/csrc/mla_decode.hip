@@ -149,11 +149,12 @@ __global__ __launch_bounds__(1024) void k_gemv_ksplit(GemvSplitArgs a) {
         wr[t] = row < a.out0 ? a.W0 + (size_t)row * a.in : a.W1 + (size_t)(row - a.out0) * a.in;
     }
     const int kbase = kq * (16 * 32 * KPW) + w * (32 * KPW) + g * 8;
+    // the weights are read once per call: non-temporal loads keep them out of the caches
     v4i wa[KPW][4];
 #pragma unroll
     for (int kb = 0; kb < KPW; ++kb)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) wa[kb][t] = *(const v4i *)(wr[t] + kbase + 32 * kb);
+        for (int t = 0; t < 4; ++t) wa[kb][t] = __builtin_nontemporal_load((const v4i *)(wr[t] + kbase + 32 * kb));
     // the activations of token group bz (issued one group ahead: their loads overlap the
     // reduction of the previous group)
     v4f xa[KPW][NG], xb[KPW][NG];
@@ -227,7 +228,7 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(GemvSplitArgs a) {
     const int kbase = w * (32 * KPW) + g * 8;
     v4i wa[KPW];
 #pragma unroll
-    for (int kb = 0; kb < KPW; ++kb) wa[kb] = *(const v4i *)(wrow + kbase + 32 * kb);
+    for (int kb = 0; kb < KPW; ++kb) wa[kb] = __builtin_nontemporal_load((const v4i *)(wrow + kbase + 32 * kb));
     v4i xv[KPW][NG];  // activations of a token group, loaded one group ahead
     auto load_x = [&](int bz) __attribute__((always_inline)) {
 #pragma unroll
