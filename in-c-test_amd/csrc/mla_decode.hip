@@ -240,6 +240,16 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(GemvSplitArgs a) {
     };
     load_x(16 * blockIdx.z);
     for (int bz = 16 * blockIdx.z; bz < a.B; bz += 16 * gridDim.z) {
+        // the residual values this lane of wave 0 adds to, requested before the MFMAs and the
+        // reduction so that their latency is not added at the end
+        float yres[NG][4];
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int b = bz + 8 * gi + n, r = blockIdx.x * 16 + 4 * g + i;
+                yres[gi][i] = w == 0 && a.acc && n < 8 && b < a.B && r < out ? a.Y[(size_t)b * a.ldy + r] : 0.f;
+            }
         v4f acc[NG];
 #pragma unroll
         for (int gi = 0; gi < NG; ++gi) acc[gi] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -265,10 +275,7 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(GemvSplitArgs a) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int r = blockIdx.x * 16 + 4 * g + i;
-                        if (r < out) {
-                            float *yp = a.Y + (size_t)b * a.ldy + r;
-                            *yp = a.acc ? *yp + s[i] : s[i];
-                        }
+                        if (r < out) a.Y[(size_t)b * a.ldy + r] = a.acc ? yres[gi][i] + s[i] : s[i];
                     }
                 }
             }
@@ -2495,12 +2502,12 @@ __global__ __launch_bounds__(256) void k_copy(v4i *dst, const v4i *src, size_t n
         dst[i] = src[i];
 }
 
-// Streaming read of n 16-byte words, four independent loads in flight per thread, folded by
-// XOR; the fold reaches memory only for one (practically never occurring) pattern, which keeps
-// every load live: a read-bandwidth probe.
-// Each block streams a contiguous 1/gridDim of the buffer with 8 loads of 16 bytes in flight per
-// thread: contiguous per-block ranges reached 6.2-6.3 TB/s on MI355X, a grid-stride order over the
-// same bytes 5.1-5.5 TB/s.
+// Streaming read of n 16-byte words, folded by XOR; the fold reaches memory only for one
+// (practically never occurring) pattern, which keeps every load live: a read-bandwidth probe.
+// Each block streams a contiguous 1/gridDim of the buffer with 8 non-temporal loads of 16 bytes
+// in flight per thread: contiguous per-block ranges reached 6.2-6.3 TB/s on MI355X, a
+// grid-stride order over the same bytes 5.1-5.5 TB/s (plain loads; non-temporal ones, as the
+// decode's history streams use, 5-10 % more in a grid-stride order).
 __global__ __launch_bounds__(256) void k_read(const v4i *src, size_t n, v4i *sink) {
     const size_t per = (n + gridDim.x - 1) / gridDim.x;
     const size_t b0 = (size_t)blockIdx.x * per, b1 = b0 + per < n ? b0 + per : n;
@@ -2509,11 +2516,11 @@ __global__ __launch_bounds__(256) void k_read(const v4i *src, size_t n, v4i *sin
     for (; i + 7 * 256 < b1; i += 8 * 256) {
         v4i v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = src[i + 256 * u];
+        for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(src + i + 256 * u);
 #pragma unroll
         for (int u = 0; u < 8; ++u) acc ^= v[u];
     }
-    for (; i < b1; i += 256) acc ^= src[i];
+    for (; i < b1; i += 256) acc ^= __builtin_nontemporal_load(src + i);
     if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x5a17c3e1) sink[(size_t)blockIdx.x * 256 + threadIdx.x] = acc;
 }
 
