@@ -1245,6 +1245,9 @@ constexpr int kF32Rs = 576;  // LDS row stride (floats)
 // per 32 lanes) fall in distinct banks.
 __device__ __forceinline__ int f32_swz(int r) { return (4 * (r & 7)) ^ (16 * (r & 1)); }
 
+// ONCE: the history rows are read by one workgroup each (not a block launch): non-temporal
+// loads. A block launch's members read the same rows (cached loads).
+template <bool ONCE>
 __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float rows[kF32Ch * kF32Rs];
     __shared__ float sp[4][16][16];
@@ -1256,6 +1259,7 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
     const int r1 = split == s.nsplit - 1 ? s.len : r0 + s.rps;  // last split takes the rest
     const float *glat = (const float *)s.a;
     const float *grope = (const float *)s.b;
+    constexpr bool once = ONCE;
 
     float qa[36];
     {
@@ -1280,12 +1284,13 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const int p = tid + 256 * k, row = p >> 7, c4 = p & 127, gr = base + row;
-            // history rows are read once: non-temporal loads
-            pl[k] = gr < r1 ? __builtin_nontemporal_load((const v4f *)(glat + (size_t)gr * 512 + 4 * c4))
-                            : v4f{0.f, 0.f, 0.f, 0.f};
+            // rows read once: non-temporal loads (a block launch's members share them: cached)
+            const v4f *src = (const v4f *)(glat + (size_t)gr * 512 + 4 * c4);
+            pl[k] = gr < r1 ? (once ? __builtin_nontemporal_load(src) : *src) : v4f{0.f, 0.f, 0.f, 0.f};
         }
         const int row = tid >> 4, c4 = tid & 15, gr = base + row;
-        pr = gr < r1 ? __builtin_nontemporal_load((const v4f *)(grope + (size_t)gr * 64 + 4 * c4)) : v4f{0.f, 0.f, 0.f, 0.f};
+        const v4f *src = (const v4f *)(grope + (size_t)gr * 64 + 4 * c4);
+        pr = gr < r1 ? (once ? __builtin_nontemporal_load(src) : *src) : v4f{0.f, 0.f, 0.f, 0.f};
     };
     auto stash = [&]() {
 #pragma unroll
@@ -1438,6 +1443,7 @@ __device__ __forceinline__ v4s lds_read_tr16(const uint8_t *p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s *)(p));
 }
 
+template <bool ONCE>  // as for k_attn_f32_mfma
 __global__ __launch_bounds__(256) void k_attn_bf16_mfma(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t smem[kB16SmemB];
     const int tid = threadIdx.x, l = tid & 63, n = l & 15, g = l >> 4;
@@ -1450,6 +1456,7 @@ __global__ __launch_bounds__(256) void k_attn_bf16_mfma(AttnArgs a) {
     const int nch = (r1 - r0 + kB16Ch - 1) / kB16Ch;
     const uint16_t *glat = (const uint16_t *)s.a;
     const uint16_t *grope = (const uint16_t *)s.b;
+    constexpr bool once = ONCE;
     const uint32_t sbase = lds_addr(smem);
     float *sp = (float *)(smem + kB16SpOff);
     const int rb = w & 1, kh = w >> 1;
@@ -1466,11 +1473,11 @@ __global__ __launch_bounds__(256) void k_attn_bf16_mfma(AttnArgs a) {
         for (int k = 0; k < 8; ++k) {
             const int row = 8 * w + k;
             const int gr = min(rbase + row, r1 - 1);
-            dma_b128_nt(glat + (size_t)gr * 512 + 8 * (l ^ b16_swz(row)), buf + (uint32_t)(row * 1024));
+            dma_hist_b128(glat + (size_t)gr * 512 + 8 * (l ^ b16_swz(row)), buf + (uint32_t)(row * 1024), once);
         }
         const int row = 8 * w + (l >> 3);
         const int gr = min(rbase + row, r1 - 1);
-        dma_b128_nt(grope + (size_t)gr * 64 + 8 * ((l & 7) ^ (row & 7)), buf + (uint32_t)(kB16LatB + w * 1024));
+        dma_hist_b128(grope + (size_t)gr * 64 + 8 * ((l & 7) ^ (row & 7)), buf + (uint32_t)(kB16LatB + w * 1024), once);
     };
 
     // query operands (A of the score MFMAs: head n, k = 32 kb + 8g .. +7). Chunk 0's DMA goes out
@@ -1896,6 +1903,7 @@ __device__ __forceinline__ void q8_score_role(const AttnArgs &a, const SeqDesc &
     }
 }
 
+template <bool ONCE>
 __device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const SeqDesc &sd, uint8_t *smem, int mw, int b,
                                             int r0, int r1, int nch, int sid) {
     const int8_t *wq = (const int8_t *)(smem + kQ8WqOff);
@@ -1907,6 +1915,7 @@ __device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const SeqDesc &sd
     const int8_t *gcodes = (const int8_t *)sd.a;
     const float *gscl = (const float *)sd.b;
     const uint16_t *grope = (const uint16_t *)sd.c;
+    constexpr bool once = ONCE;
     // DMA plan. Codes: mix wave mw copies row pairs 8mw .. 8mw+7 of a chunk; lane l of
     // instruction k takes row 2(8mw + k) + (l >> 5), physical slot l & 31 (logical slot
     // (l & 31) ^ swz). RoPE keys: instruction k of wave mw covers rows 8(2mw + k) .. +7, lane l
@@ -1932,13 +1941,13 @@ __device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const SeqDesc &sd
         if (rb0 + kQ8Ch <= r1) {
             const int8_t *gc = gcodes + (size_t)rb0 * 512;
 #pragma unroll
-            for (int k = 0; k < 8; ++k) dma_b128_nt(gc + code_off[k], buf + (uint32_t)((mw * 8 + k) * 1024));
+            for (int k = 0; k < 8; ++k) dma_hist_b128(gc + code_off[k], buf + (uint32_t)((mw * 8 + k) * 1024), once);
         } else {
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 const int row = code_off[k] >> 9;
                 const int gro = min(rb0 + row, r1 - 1);
-                dma_b128_nt(gcodes + (size_t)gro * 512 + (code_off[k] & 511), buf + (uint32_t)((mw * 8 + k) * 1024));
+                dma_hist_b128(gcodes + (size_t)gro * 512 + (code_off[k] & 511), buf + (uint32_t)((mw * 8 + k) * 1024), once);
             }
         }
     };
@@ -1948,9 +1957,9 @@ __device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const SeqDesc &sd
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             const int gro = min(rb0 + rope_row[k], r1 - 1);
-            dma_b128_nt(grope + (size_t)gro * 64 + rope_el[k], buf + (uint32_t)((2 * mw + k) * 1024));
+            dma_hist_b128(grope + (size_t)gro * 64 + rope_el[k], buf + (uint32_t)((2 * mw + k) * 1024), once);
         }
-        if (mw == 0) dma_b32_nt(gscl + min(rb0 + l, r1 - 1), buf + (uint32_t)kQ8RopeB);
+        if (mw == 0) dma_hist_b32(gscl + min(rb0 + l, r1 - 1), buf + (uint32_t)kQ8RopeB, once);
     };
     // transposed reads: rows 16g + (n >> 1) and 16g + 8 + (n >> 1) share the swizzle (+4096)
     int tr_off[8];
@@ -2053,6 +2062,7 @@ __device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const SeqDesc &sd
     }
 }
 
+template <bool ONCE>  // as for k_attn_f32_mfma
 __global__ __launch_bounds__(512) void k_attn_q8_mfma(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t smem[kQ8SmemB];
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -2062,7 +2072,7 @@ __global__ __launch_bounds__(512) void k_attn_q8_mfma(AttnArgs a) {
     const int r0 = split * s.rps;
     const int r1 = split == s.nsplit - 1 ? s.len : r0 + s.rps;  // last split takes the rest
     const int nch = (r1 - r0 + kQ8Ch - 1) / kQ8Ch;
-    if (w >= 4) q8_mix_role(a, s, smem, w - 4, b, r0, r1, nch, pidx);
+    if (w >= 4) q8_mix_role<ONCE>(a, s, smem, w - 4, b, r0, r1, nch, pidx);
     else q8_score_role(a, s, smem, w, b, r0, r1, nch, pidx);
 }
 
@@ -2093,11 +2103,14 @@ hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t
         grid = kXcds * t.n * ((maxns + kXcds - 1) / kXcds);
     }
     if (kind == kAttnQ8Mfma) {
-        hipLaunchKernelGGL(k_attn_q8_mfma, dim3(grid), dim3(512), 0, st, a);
+        if (a.members > 0) hipLaunchKernelGGL(k_attn_q8_mfma<false>, dim3(grid), dim3(512), 0, st, a);
+        else hipLaunchKernelGGL(k_attn_q8_mfma<true>, dim3(grid), dim3(512), 0, st, a);
     } else if (kind == kAttnF32Mfma) {
-        hipLaunchKernelGGL(k_attn_f32_mfma, dim3(grid), dim3(256), 0, st, a);
+        if (a.members > 0) hipLaunchKernelGGL(k_attn_f32_mfma<false>, dim3(grid), dim3(256), 0, st, a);
+        else hipLaunchKernelGGL(k_attn_f32_mfma<true>, dim3(grid), dim3(256), 0, st, a);
     } else if (kind == kAttnBF16Mfma) {
-        hipLaunchKernelGGL(k_attn_bf16_mfma, dim3(grid), dim3(256), 0, st, a);
+        if (a.members > 0) hipLaunchKernelGGL(k_attn_bf16_mfma<false>, dim3(grid), dim3(256), 0, st, a);
+        else hipLaunchKernelGGL(k_attn_bf16_mfma<true>, dim3(grid), dim3(256), 0, st, a);
     } else {
         const int P = fmt == kFmtExp ? t.n * d.NH : t.n;
         if (fmt == kFmtQ8)

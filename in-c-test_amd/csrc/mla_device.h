@@ -227,12 +227,30 @@ __device__ __forceinline__ void dma_b128_s(const void *sbase, uint32_t voff, uin
                  : "s"(lds_base), "v"(voff), "s"(sbase)
                  : "memory");
 }
+__device__ __forceinline__ void dma_b32(const void *gptr, uint32_t lds_base) {
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %2, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "s"(lds_base), "v"(gptr)
+                 : "memory");
+}
 __device__ __forceinline__ void dma_b32_nt(const void *gptr, uint32_t lds_base) {
     uint32_t saved;
     asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %2, off nt\n\ts_mov_b32 m0, %0"
                  : "=&s"(saved)
                  : "s"(lds_base), "v"(gptr)
                  : "memory");
+}
+// History rows of a decode: non-temporal when each row is read by one workgroup (`once`),
+// cached when the members of a block launch read the same rows at about the same time on one
+// XCD (its L2 then serves the later members). `once` is wave-uniform.
+__device__ __forceinline__ void dma_hist_b128(const void *gptr, uint32_t lds_base, bool once) {
+    if (once) dma_b128_nt(gptr, lds_base);
+    else dma_b128(gptr, lds_base);
+}
+__device__ __forceinline__ void dma_hist_b32(const void *gptr, uint32_t lds_base, bool once) {
+    if (once) dma_b32_nt(gptr, lds_base);
+    else dma_b32(gptr, lds_base);
 }
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
