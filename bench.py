@@ -510,6 +510,28 @@ def main():
                                        "attention_frac_of_measured_read": round(roofline["achieved"] / rpeak, 4)}
             roofline["measured_read_peak"] = round(rpeak, 1)
             log(f"[bench] measured bandwidth: streaming read {rpeak:.1f} GB/s, copy {peak:.1f} GB/s (read + write)")
+            # the fixed cost of a kernel boundary in a HIP graph: 100 empty kernels back to back
+            if not args.eager:
+                lib.check(L.kvl_mla_capture_begin(), "capture begin")
+                try:
+                    for _ in range(100):
+                        lib.check(L.kvl_mla_empty_kernel(), "empty kernel")
+                finally:
+                    ge = C.c_void_p()
+                    rc = L.kvl_mla_capture_end(C.byref(ge))
+                lib.check(rc, "capture end")
+                lib.check(L.kvl_mla_graph_launch(ge), "graph launch")
+                lib.check(L.kvl_mla_synchronize(), "sync")
+                c4 = L.kvl_mla_event_record()
+                for _ in range(5):
+                    lib.check(L.kvl_mla_graph_launch(ge), "graph launch")
+                c5 = L.kvl_mla_event_record()
+                floor_us = L.kvl_mla_event_elapsed_ms(c4, c5) / 500 * 1e3
+                for e in (c4, c5):
+                    L.kvl_mla_event_destroy(e)
+                L.kvl_mla_graph_destroy(ge)
+                result["measured_peak"]["kernel_boundary_us"] = round(floor_us, 3)
+                log(f"[bench] kernel boundary in a HIP graph (empty 256 x 1024 kernels): {floor_us:.2f} us")
         for q in (pa, pb):
             if q:
                 L.kvl_mla_device_free(q)

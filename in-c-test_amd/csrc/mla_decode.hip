@@ -2544,6 +2544,14 @@ hipError_t launch_read(hipStream_t st, const void *src, size_t bytes, void *sink
     return hipGetLastError();
 }
 
+// Launch-cost probe: a kernel whose workgroups do nothing.
+__global__ __launch_bounds__(1024) void k_empty() {}
+
+hipError_t launch_empty(hipStream_t st) {
+    hipLaunchKernelGGL(k_empty, dim3(256), dim3(1024), 0, st);
+    return hipGetLastError();
+}
+
 hipError_t launch_copy(hipStream_t st, void *dst, const void *src, size_t bytes) {
     const size_t n = bytes / 16;
     if (n == 0) return hipSuccess;

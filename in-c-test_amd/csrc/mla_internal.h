@@ -164,6 +164,7 @@ hipError_t launch_copy(hipStream_t st, void *dst, const void *src, size_t bytes)
 // memory of kReadBlocks x 256 x 16 bytes (written only for one improbable bit pattern).
 constexpr int kReadBlocks = 8192;
 hipError_t launch_read(hipStream_t st, const void *src, size_t bytes, void *sink);
+hipError_t launch_empty(hipStream_t st);
 
 // ---- prefill (mla_prefill.hip) ----
 // Device workspace bytes of a causal prefill of S tokens.

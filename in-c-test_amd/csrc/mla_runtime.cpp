@@ -2296,6 +2296,13 @@ int kvl_mla_copy_kernel(void *dst, const void *src, size_t bytes) {
     return 0;
 }
 
+int kvl_mla_empty_kernel(void) {
+    Guard guard;
+    if (ensure_ready() != 0) return -1;
+    HIP_TRY(launch_empty(ctx().stream));
+    return 0;
+}
+
 int kvl_mla_read_kernel(const void *src, size_t bytes) {
     Guard guard;
     if (!src || bytes % 16 != 0 || ((uintptr_t)src % 16) != 0) {

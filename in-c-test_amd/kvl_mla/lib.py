@@ -64,6 +64,7 @@ EXT_API = {
     "mla_event_destroy": (C.c_int, [C.c_void_p]),
     "mla_copy_kernel": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "mla_read_kernel": (C.c_int, [C.c_void_p, C.c_size_t]),
+    "mla_empty_kernel": (C.c_int, []),
     "mla_q8_pack_rows": (C.c_int, [abi.i8p, abi.f32p, abi.u16p, abi.f32p, abi.f32p,
                                    C.POINTER(C.c_int), C.c_int, C.c_int, C.c_int, C.c_float]),
     "mla_compressed_q8_state_fill_synthetic": (C.c_int, [abi.QS, C.c_int, C.c_int, C.c_uint64]),

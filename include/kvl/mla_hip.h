@@ -249,6 +249,10 @@ int kvl_mla_copy_kernel(void *dst, const void *src, size_t bytes);
 /* A streaming read of bytes (% 16 == 0) from a 16-byte aligned device buffer, enqueued on
  * kvl_mla_stream(): the measured read-bandwidth ceiling beside the nominal HBM peak. */
 int kvl_mla_read_kernel(const void *src, size_t bytes);
+/* An empty kernel (256 workgroups of 1024 threads that do nothing), enqueued on
+ * kvl_mla_stream(): captured back to back in a graph, it measures the per-launch cost of a
+ * kernel boundary, the fixed cost every stage of a decode step pays. */
+int kvl_mla_empty_kernel(void);
 
 /* Quantiser boundary, computed on the GPU: for row i, latent [n, R] (already normalised) ->
  * int8 codes [n, R] + fp32 scale [n]; k_rope_raw [n, DR] (before rotation) -> RoPE at
