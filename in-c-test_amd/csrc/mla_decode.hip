@@ -857,9 +857,31 @@ hipError_t launch_store_expanded(hipStream_t st, const SeqTable &t, const Dims &
 
 // ================================================================ query prep ===========
 
+// W_UK^T in the order the query preparation's MFMA A operands are loaded (R = 512, DN = 128):
+// fragment (head h, wave w, tile t, k-step ks) is 64 lanes x 16 bytes, contiguous, lane l holding
+// W_UK[d = 32 ks + 8 (l >> 4) + e, latent column j = 128 w + 16 t + (l & 15)], e = 0..7, where
+// W_UK[d, j] = kv_b[h * (DN + DV) + d, j]. One load instruction then reads 1 KB in one run. One
+// thread per output element.
+__global__ __launch_bounds__(256) void k_wuk_t(uint16_t *dst, const uint16_t *kv_b, int NH, int DN, int DV, int R) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, n = (size_t)NH * R * DN;
+    if (i >= n) return;
+    const int e = (int)(i & 7), l = (int)((i >> 3) & 63), ks = (int)((i >> 9) & 3), t = (int)((i >> 11) & 7),
+              w = (int)((i >> 14) & 3), h = (int)(i >> 16);
+    const int dd = 32 * ks + 8 * (l >> 4) + e, j = 128 * w + 16 * t + (l & 15);
+    dst[i] = kv_b[((size_t)h * (DN + DV) + dd) * R + j];
+}
+
+hipError_t launch_wuk_transpose(hipStream_t st, uint16_t *dst, const uint16_t *kv_b, const Dims &d) {
+    if (d.R != 512 || d.DN != 128) return hipErrorInvalidValue;
+    const size_t n = (size_t)d.NH * d.R * d.DN;
+    hipLaunchKernelGGL(k_wuk_t, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, dst, kv_b, d.NH, d.DN, d.DV, d.R);
+    return hipGetLastError();
+}
+
 struct QprepArgs {
     const float *y;  // projection rows: np partials pstride apart, summed in order
     const uint16_t *kv_b;
+    const uint16_t *ukt;  // W_UK^T [NH, R, DN] bf16 (the MFMA operand of the Kimi-shape path) or null
     const float2 *cs;
     float *qf;
     int8_t *qhi, *qlo;
@@ -875,7 +897,7 @@ struct QprepArgs {
 // With `quantize`, q_lat ~= qs * (hi + lo/254) (int8 hi, lo) and q_rope / sqrt(QD) = hi + lo
 // (bf16).
 __device__ __forceinline__ void qprep_body(const SeqTable &t, const Dims &d, const QprepArgs &a, int blk) {
-    __shared__ float qn[kMaxDN];
+    __shared__ __attribute__((aligned(16))) float qn[kMaxDN];
     __shared__ float qr[kMaxDR];  // RoPE input of the head
     __shared__ float ql[kMaxR];
     __shared__ float redf[4];
@@ -883,14 +905,18 @@ __device__ __forceinline__ void qprep_body(const SeqTable &t, const Dims &d, con
     const SeqDesc &s = t.s[b];
     const float *qh = a.y + (size_t)b * a.ldy + (size_t)h * d.QD;
     const int half = d.DR / 2, nq = d.DN + d.DR;
-    // Kimi shapes: the W_UK rows of this wave (lane l: latent columns 8l .. 8l+7 of rows
-    // 32w .. 32w+31) do not depend on q, so they are requested before q is.
-    const bool fast = a.fmt != kFmtExp && d.R == 512 && d.DN == 128;
-    v4i wpre[32];
+    // Kimi shapes: q_lat = W_UK^T q_nope on MFMA. Wave w owns latent columns 128 w .. +127 as
+    // eight 16-column tiles; the A operands come from the copy of W_UK^T made with the weights,
+    // stored in fragment order (k_wuk_t): lane (g, n) of fragment (t, ks) holds latent column
+    // 128 w + 16 t + n, d = 32 ks + 8 g .. +7. Requested before q since they do not depend on it.
+    const bool fast = a.fmt != kFmtExp && d.R == 512 && d.DN == 128 && a.ukt != nullptr;
+    v8bf wa[8][4];
     if (fast) {
-        const uint16_t *wuk = a.kv_b + (size_t)h * (d.DN + d.DV) * d.R + (size_t)(tid >> 6) * 32 * 512 + 8 * (tid & 63);
+        const uint16_t *ut = a.ukt + ((size_t)(h * 4 + (tid >> 6)) * 32 * 64 + (tid & 63)) * 8;
 #pragma unroll
-        for (int q = 0; q < 32; ++q) wpre[q] = *(const v4i *)(wuk + (size_t)q * 512);
+        for (int t = 0; t < 8; ++t)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) wa[t][ks] = *(const v8bf *)(ut + (size_t)(t * 4 + ks) * 64 * 8);
     }
     // the query head (partials summed) and this thread's RoPE pair, in one round trip
     {
@@ -913,49 +939,41 @@ __device__ __forceinline__ void qprep_body(const SeqTable &t, const Dims &d, con
         for (int i = tid; i < d.DN; i += 256) qrow[i] = qn[i];
     } else {
         const uint16_t *wuk = a.kv_b + (size_t)h * (d.DN + d.DV) * d.R;
-        if (d.R == 512 && (d.DN & 3) == 0) {
-            // wave w: k in [w*DN/4, (w+1)*DN/4); lane l: latent columns 8l .. 8l+7
-            __shared__ v4f part[4][64][2];
-            const int w = tid >> 6, l = tid & 63, kq = d.DN >> 2;
-            float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            if (fast) {
+        if (fast) {
+            // B operand: column 0 = bf16 hi of q_nope, column 1 = its lo part (hi + lo keeps ~16
+            // bits; the products are exact in the fp32 accumulator), columns 2-15 zero. D row
+            // 4 g + i of tile t is latent column 128 w + 16 t + 4 g + i; columns 0 and 1 (lanes
+            // n = 0, 1) are added by one DPP swap.
+            const int w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
+            // every lane splits its 8 values (no divergence), lanes n = 0 / 1 keep hi / lo
+            const int m0 = n == 0 ? -1 : 0, m1 = n == 1 ? -1 : 0;
+            v8bf qb[4];
 #pragma unroll
-                for (int q = 0; q < 32; ++q) {
-                    const float qv = qn[w * 32 + q];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const uint32_t u = (uint32_t)wpre[q][e];
-                        acc[2 * e] = fmaf(__uint_as_float(u << 16), qv, acc[2 * e]);
-                        acc[2 * e + 1] = fmaf(__uint_as_float(u & 0xffff0000u), qv, acc[2 * e + 1]);
-                    }
-                }
+            for (int ks = 0; ks < 4; ++ks) {
+                const v4f x0 = *(const v4f *)(qn + 32 * ks + 8 * g), x1 = *(const v4f *)(qn + 32 * ks + 8 * g + 4);
+                v8bf hi, lo;
+                split8_cvt(x0, x1, hi, lo);
+                const v4i hv = __builtin_bit_cast(v4i, hi), lv = __builtin_bit_cast(v4i, lo);
+                qb[ks] = __builtin_bit_cast(v8bf, (hv & m0) | (lv & m1));
             }
-            for (int k0 = 0; k0 < (fast ? 0 : kq); k0 += 8) {
-                v4i wv[8];
+            v4f acc[8];
 #pragma unroll
-                for (int q = 0; q < 8; ++q)
-                    if (k0 + q < kq) wv[q] = *(const v4i *)(wuk + (size_t)(w * kq + k0 + q) * 512 + 8 * l);
+            for (int t = 0; t < 8; ++t) {
+                acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    if (k0 + q < kq) {
-                        const float qv = qn[w * kq + k0 + q];
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const uint32_t u = (uint32_t)wv[q][e];
-                            acc[2 * e] = fmaf(__uint_as_float(u << 16), qv, acc[2 * e]);
-                            acc[2 * e + 1] = fmaf(__uint_as_float(u & 0xffff0000u), qv, acc[2 * e + 1]);
-                        }
-                    }
-                }
+                for (int ks = 0; ks < 4; ++ks) acc[t] = mfma_bf16(wa[t][ks], qb[ks], acc[t]);
             }
-            part[w][l][0] = v4f{acc[0], acc[1], acc[2], acc[3]};
-            part[w][l][1] = v4f{acc[4], acc[5], acc[6], acc[7]};
-            __syncthreads();
-            for (int r = tid; r < 512; r += 256) {
-                const int ll = r >> 3, e = r & 7, hv = e >> 2, c = e & 3;
-                const float v = (part[0][ll][hv][c] + part[1][ll][hv][c]) + (part[2][ll][hv][c] + part[3][ll][hv][c]);
-                ql[r] = v;
-                qrow[r] = v;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                v4f v;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = acc[t][i] + dpp_f32<0xB1>(acc[t][i]);  // quad_perm [1,0,3,2]
+                if (n == 0) {
+                    const int r = 128 * w + 16 * t + 4 * g;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) ql[r + i] = v[i];
+                    *(v4f *)(qrow + r) = v;
+                }
             }
         } else if ((d.R & 1) == 0) {
             // two adjacent latent columns per thread (one 4-byte load per k), 4 k in flight
@@ -1041,11 +1059,12 @@ __global__ __launch_bounds__(256) void k_append_qprep(SeqTable t, Dims d, Append
     else qprep_body(t, d, qa, blockIdx.x - na);
 }
 
-static QprepArgs qprep_args(int fmt, const Dims &d, const uint16_t *kv_b, const float2 *rope_cs,
-                            const DecodeWork &w, bool quantize) {
+static QprepArgs qprep_args(int fmt, const Dims &d, const uint16_t *kv_b, const uint16_t *ukt,
+                            const float2 *rope_cs, const DecodeWork &w, bool quantize) {
     QprepArgs a;
     a.y = w.y;
     a.kv_b = kv_b;
+    a.ukt = ukt;
     a.cs = rope_cs;
     a.qf = w.qf;
     a.qhi = w.qhi;
@@ -1065,7 +1084,7 @@ hipError_t launch_qprep(hipStream_t st, int fmt, const SeqTable &t, const Dims &
                         const uint16_t *kv_b, const float2 *rope_cs, const DecodeWork &w,
                         bool quantize) {
     if (d.R > kMaxR || d.DN > kMaxDN || d.DR > kMaxDR) return hipErrorInvalidValue;
-    const QprepArgs a = qprep_args(fmt, d, kv_b, rope_cs, w, quantize);
+    const QprepArgs a = qprep_args(fmt, d, kv_b, nullptr, rope_cs, w, quantize);
     hipLaunchKernelGGL(k_qprep, dim3(t.n * d.NH), dim3(256), 0, st, t, d, a);
     return hipGetLastError();
 }
@@ -1073,12 +1092,12 @@ hipError_t launch_qprep(hipStream_t st, int fmt, const SeqTable &t, const Dims &
 hipError_t launch_append_qprep(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
                                const float *y, int ldy, int koff, int ynp, size_t ypstride,
                                const uint16_t *kv_a_norm, float eps, const float2 *rope_cs,
-                               const uint16_t *kv_b, const DecodeWork &w, bool quantize) {
+                               const uint16_t *kv_b, const uint16_t *ukt, const DecodeWork &w, bool quantize) {
     if (d.R > kMaxR || d.DN > kMaxDN || d.DR > kMaxDR || (ynp != 1 && ynp != kGemvKs))
         return hipErrorInvalidValue;
     const AppendArgs aa = append_args(fmt, d, y, ldy, koff, ynp, ypstride, kv_a_norm, eps, rope_cs, w,
                                       false, 0);
-    const QprepArgs qa = qprep_args(fmt, d, kv_b, rope_cs, w, quantize);
+    const QprepArgs qa = qprep_args(fmt, d, kv_b, ukt, rope_cs, w, quantize);
     hipLaunchKernelGGL(k_append_qprep, dim3(t.n + t.n * d.NH), dim3(256), 0, st, t, d, aa, qa, t.n);
     return hipGetLastError();
 }

@@ -133,7 +133,10 @@ hipError_t launch_qprep(hipStream_t st, int fmt, const SeqTable &t, const Dims &
 hipError_t launch_append_qprep(hipStream_t st, int fmt, const SeqTable &t, const Dims &d,
                                const float *y, int ldy, int koff, int ynp, size_t ypstride,
                                const uint16_t *kv_a_norm, float eps, const float2 *rope_cs,
-                               const uint16_t *kv_b, const DecodeWork &w, bool quantize);
+                               const uint16_t *kv_b, const uint16_t *ukt, const DecodeWork &w, bool quantize);
+// W_UK^T from kv_b (the first DN rows of each head) in the fragment order of the query
+// preparation's MFMA operands (R = 512, DN = 128 only): ukt of launch_append_qprep.
+hipError_t launch_wuk_transpose(hipStream_t st, uint16_t *dst, const uint16_t *kv_b, const Dims &d);
 
 // Split-K attention over the history; writes partials (acc | m | l) per split.
 // kind: 0 = generic VALU (any dims, one split per problem), 1 = fp32 MFMA (Kimi dims),

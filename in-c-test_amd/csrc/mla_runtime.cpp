@@ -133,6 +133,8 @@ struct WeightEntry {
     void *dev = nullptr;
     void *dev16 = nullptr;  // fp16 copy (prefill o_proj), valid when f16_ok
     bool f16_ok = false;
+    void *devt = nullptr;   // W_UK^T of a kv_b array (decode query preparation), valid when t_ok
+    bool t_ok = false;
     int pins = 0;
 };
 
@@ -325,8 +327,13 @@ int dev_weight(const uint16_t *host, size_t elems, const uint16_t **out) {
         HIP_TRY(dev_free(e.dev16));
         e.dev16 = nullptr;
     }
+    if (e.devt && e.bytes != bytes) {
+        HIP_TRY(dev_free(e.devt));
+        e.devt = nullptr;
+    }
     e.bytes = bytes;
     e.f16_ok = false;
+    e.t_ok = false;
     HIP_TRY(hipMemcpy(e.dev, host, bytes, hipMemcpyHostToDevice));
     e.digest = sample_digest(host, bytes);
     c.weights[host] = e;
@@ -353,8 +360,31 @@ int dev_weight_f16(const uint16_t *host, size_t elems, const _Float16 **out) {
     return 0;
 }
 
+// W_UK^T of a kv_b array in MFMA fragment order (transposed on the device from its bf16 copy,
+// stream-ordered): the A operands of the decode's query preparation for the Kimi shapes.
+bool ukt_shape(const Dims &d) { return d.R == 512 && d.DN == 128; }
+
+int dev_weight_ukt(const uint16_t *host, const Dims &d, const uint16_t **out) {
+    Ctx &c = ctx();
+    const uint16_t *kvb;
+    if (dev_weight(host, (size_t)d.KVB * d.R, &kvb) != 0) return -1;
+    WeightEntry &e = c.weights[host];
+    if (!e.t_ok) {
+        if (c.capturing) {
+            set_err("W_UK transpose during graph capture (bind the weights or run one call first)");
+            return -1;
+        }
+        if (!e.devt) HIP_TRY(hipMalloc(&e.devt, (size_t)d.NH * d.R * d.DN * sizeof(uint16_t)));
+        HIP_TRY(launch_wuk_transpose(c.stream, (uint16_t *)e.devt, kvb, d));
+        e.t_ok = true;
+    }
+    *out = (const uint16_t *)e.devt;
+    return 0;
+}
+
 struct DevWeights {
     const uint16_t *q, *kva, *norm, *kvb, *o;
+    const uint16_t *ukt = nullptr;  // W_UK^T (Kimi shapes), else null
 };
 
 int dev_weights(const KvlMlaBF16 *w, const Dims &d, DevWeights &dw) {
@@ -363,6 +393,8 @@ int dev_weights(const KvlMlaBF16 *w, const Dims &d, DevWeights &dw) {
     if (dev_weight(w->kv_a_norm, (size_t)d.R, &dw.norm) != 0) return -1;
     if (dev_weight(w->kv_b_proj, (size_t)d.KVB * d.R, &dw.kvb) != 0) return -1;
     if (dev_weight(w->o_proj, (size_t)d.H * d.HO, &dw.o) != 0) return -1;
+    dw.ukt = nullptr;
+    if (ukt_shape(d) && dev_weight_ukt(w->kv_b_proj, d, &dw.ukt) != 0) return -1;
     return 0;
 }
 
@@ -870,8 +902,8 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
     } else {
         // append and query preparation in one launch (timed as stage 1)
         StageTimer tm(1);
-        HIP_TRY(launch_append_qprep(st, fmt, t, d, w.y, ldy, d.QO, w.ynp, w.ypstride, dw.norm, eps, cs, dw.kvb, w,
-                                    kind == kAttnQ8Mfma));
+        HIP_TRY(launch_append_qprep(st, fmt, t, d, w.y, ldy, d.QO, w.ynp, w.ypstride, dw.norm, eps, cs, dw.kvb,
+                                    dw.ukt, w, kind == kAttnQ8Mfma));
     }
     {
         StageTimer tm(3);
@@ -1196,6 +1228,13 @@ int decode_q8_noalloc(float *d_out, const float *d_x, int B, const KvlMlaConfig 
             return -1;
         }
         *slot[k] = (const uint16_t *)it->second.dev;
+        if (k == 3 && ukt_shape(d)) {
+            if (!it->second.t_ok) {
+                set_err("weights must be bound (kvl_mla_bind_weights) before a no-allocation call");
+                return -1;
+            }
+            dw.ukt = (const uint16_t *)it->second.devt;
+        }
     }
     SeqIn seqs[kNoAllocMaxBatch];
     for (int i = 0; i < B; ++i) {
@@ -1958,6 +1997,7 @@ int kvl_mla_release_weights(const KvlMlaBF16 *w) {
         if (it->second.pins == 0) {
             (void)dev_free(it->second.dev);
             if (it->second.dev16) (void)dev_free(it->second.dev16);
+            if (it->second.devt) (void)dev_free(it->second.devt);
             c.weights.erase(it);
         }
     }
