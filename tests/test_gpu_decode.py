@@ -196,6 +196,36 @@ def test_errors_leave_state_unchanged():
     assert s.capacity == 0
 
 
+@pytest.mark.parametrize("bound", [False, True], ids=["unbound", "bound"])
+def test_kv_b_rewritten_in_place_refreshes_device_copies(bound):
+    """Weights are cached on the device by host address. Rewriting the kv_b array in place (same
+    address, new contents) must refresh its bf16 copy and the W_UK^T copy derived from it (the
+    query preparation's operand at the Kimi shapes): unbound weights through the sampled digest,
+    bound weights through release + bind."""
+    cfg, layer, x = model(KIMI, 0xD3, n=6)
+    w = layer.struct()
+    old = layer.kv_b_proj.copy()
+    new = inputs.normal_bf16(0xD4, "kv_b", old.shape, std=0.02)
+    print(f"[decode] kv_b rewrite bound={bound}", flush=True)
+    for kind in ("f32", "q8"):
+        layer.kv_b_proj[...] = old
+        if bound:
+            lib.check(L.kvl_mla_bind_weights(C.byref(cfg), C.byref(w)), "bind")
+        a0, _ = decode_seq(G, kind, cfg, w, x, prefix=3)
+        if bound:
+            L.kvl_mla_release_weights(C.byref(w))
+        layer.kv_b_proj[...] = new
+        if bound:
+            lib.check(L.kvl_mla_bind_weights(C.byref(cfg), C.byref(w)), "bind")
+        a1, _ = decode_seq(G, kind, cfg, w, x, prefix=3)
+        if bound:
+            L.kvl_mla_release_weights(C.byref(w))
+        b1, _ = decode_seq(O, kind, cfg, w, x, prefix=3)
+        print(f"[decode]   {kind}: max|d|/max|ref| = {rel_err(a1, b1):.3e}", flush=True)
+        assert rel_err(a1, b1) <= TOL, (kind, rel_err(a1, b1))
+        assert rel_err(a0, b1) > 10 * TOL, (kind, "stale kv_b copy")
+
+
 @pytest.mark.parametrize("dims", [LAB, KIMI], ids=["lab", "kimi"])
 def test_block_equals_serial_and_rollback_exact(dims):
     """src/spec_q8_lab_probe.c:86-173 on the GPU: block decode == per-token decode exactly;
