@@ -7,6 +7,7 @@
 namespace kvl {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
@@ -100,6 +101,31 @@ __device__ __forceinline__ v4f mfma_bf16(const v8bf &a, const v8bf &b, const v4f
 __device__ __forceinline__ v4f mfma_f16(const v8h &a, const v8h &b, const v4f &c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
+
+// C += (A x 2^-11) . B with A, B bf8 (e5m2) operands, 16 x 16 x 128 (E8M0 scales 116 and 127).
+// Lane (row or column c, group g) holds 32 bytes; byte p of A lane (r, g) multiplies byte p of
+// B lane (c, g), and the result has the layout of mfma_f16.
+__device__ __forceinline__ v4f mfma_bf8_s11(const v8i &a, const v8i &b, const v4f &c) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 1, 1, 0, 116, 0, 127);
+}
+
+// bf8 (e5m2: the sign, exponent and top two mantissa bits of fp16) of an fp16 value, rounded to
+// nearest with ties away from zero, saturating at +-57344.
+__device__ __forceinline__ uint32_t f16_to_bf8(_Float16 x) {
+    const uint32_t h = __builtin_bit_cast(uint16_t, x), m = h & 0x7fffu;
+    return ((h >> 8) & 0x80u) | (m > 0x7b7fu ? 0x7bu : (m + 0x80u) >> 8);
+}
+
+// K8 row (384 bytes) of a key: 24 slots of 16 bytes, slot (part, k-block pair p, lane group g)
+// at 12 part + 4 p + g holding the bf8 of dims 32 kb + 8 g + e for kb = 2p, 2p + 1, e = 0 .. 7 in
+// that order: part 0 the fp16 hi parts, part 1 the lo parts x 2^11 (kK8Lo bytes further). A
+// lane of group g reads its 96-byte correction operand as slots 4j + g, j = 0 .. 5, and 16
+// lanes writing 64 consecutive dims write 64 contiguous bytes of each part.
+constexpr int kK8Lo = 192;
+__device__ __forceinline__ int k8_hi_byte(int d) {
+    return 16 * (4 * (d >> 6) + ((d >> 3) & 3)) + 8 * ((d >> 5) & 1) + (d & 7);
+}
+__device__ __forceinline__ uint32_t bf8_lo_s11(_Float16 lo) { return f16_to_bf8((_Float16)((float)lo * 2048.0f)); }
 
 // x ~= hi + lo with hi, lo fp16 (round to nearest even): the split keeps ~22 mantissa bits of
 // an fp32 operand of moderate range; products of fp16 operands are exact in fp32.

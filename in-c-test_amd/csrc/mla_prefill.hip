@@ -99,11 +99,14 @@ struct GemmArgs {
 // Epilogues. kEpiPlain: C fp32. kEpiQ (q | kv_a projection): the N0 = NH * QD q columns go
 // to Q [NH, Sp, QD] as hi/lo fp16 with the rope half rotated (src/mla_prefill_streaming.c:
 // 139-147: pairs (2i, 2i+1) -> i and DR/2 + i), the kv_a columns to C (ldc = N1). kEpiKV
-// (kv_b projection): k_nope -> K [NH, Sp, QD] hi/lo fp16, values -> V^T [NH, DV, Sp] fp16
-// with the keys of each 32-key group in vt_perm order.
+// (kv_b projection): k_nope -> K hi [NH, Sp, QD] fp16 and K8 [NH, Sp, 384 bytes] (bf8 of the
+// hi parts and of the lo parts x 2^11, k8_hi_byte order), values -> V^T [NH, DV, Sp] fp16 with
+// the keys of each 32-key group in vt_perm order.
 enum { kEpiPlain = 0, kEpiQ = 1, kEpiKV = 2 };
 struct GemmEpi {
-    _Float16 *qh, *ql, *kh, *kl, *vt;
+    _Float16 *qh, *ql, *kh;
+    uint8_t *k8;
+    _Float16 *vt;
     const float2 *cs;
     int Sp, DN, DR, DV;
 };
@@ -324,16 +327,20 @@ __global__ __launch_bounds__(64 * (kGemmMath + kGemmDma)) void k_gemm16(GemmArgs
             } else {  // kEpiKV, k_nope columns
                 const int h = nl0 / KH, k0 = nl0 % KH;
                 const size_t o = ((size_t)h * e.Sp + t) * QD + k0;
-                v4h hi, lo;
+                v4h hi;
+                uint32_t h8 = 0, l8 = 0;
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     _Float16 hh, ll;
                     split_f16(v[u], hh, ll);
                     hi[u] = hh;
-                    lo[u] = ll;
+                    h8 |= f16_to_bf8(hh) << (8 * u);
+                    l8 |= bf8_lo_s11(ll) << (8 * u);
                 }
                 *(v4h *)(e.kh + o) = hi;
-                *(v4h *)(e.kl + o) = lo;
+                uint8_t *row = e.k8 + ((size_t)h * e.Sp + t) * 384 + k8_hi_byte(k0);
+                *(uint32_t *)row = h8;
+                *(uint32_t *)(row + kK8Lo) = l8;
             }
         }
     }
@@ -425,7 +432,9 @@ struct KvaPackArgs {
     const uint16_t *norm;
     const float2 *cs;
     uint16_t *lath, *latl;
-    _Float16 *qh, *ql, *kh, *kl, *vt;
+    _Float16 *qh, *ql, *kh;
+    uint8_t *k8;
+    _Float16 *vt;
     size_t pstride;  // np partials of y, pstride floats apart, summed in order
     int np, S, Sp, NH, ldy, R, DN, DR, DV;
     float eps;
@@ -445,18 +454,20 @@ __global__ __launch_bounds__(256) void k_kva_pack(KvaPackArgs a) {
                 a.qh[qo + k] = 0;
                 a.ql[qo + k] = 0;
                 a.kh[qo + k] = 0;
-                a.kl[qo + k] = 0;
             }
+            for (int k = l; k < 96; k += 64) ((uint32_t *)(a.k8 + ((size_t)h * a.Sp + t) * 384))[k] = 0;
             for (int d = l; d < a.DV; d += 64) a.vt[((size_t)h * a.DV + d) * a.Sp + tv] = 0;
         }
         return;
     }
     const float *kat = a.y + (size_t)t * a.ldy;
-    if (R == 512 && a.DR == 64 && (a.DN & 7) == 0 && (a.ldy & 3) == 0 && (a.pstride & 3) == 0) {
+    if (R == 512 && a.DR == 64 && (a.DN & 63) == 0 && (a.ldy & 3) == 0 && (a.pstride & 3) == 0) {
         // lane l: latent columns 8l .. 8l+7 (16-byte loads and stores); the rotated RoPE key
-        // goes through LDS so that each head's 128-byte hi and lo rows are written by 8 lanes
-        // of 16 bytes, four heads per store instruction
-        __shared__ __attribute__((aligned(16))) _Float16 rp[4][2][64];
+        // goes through LDS so that each head's 128-byte fp16 hi row and its 128 K8 bytes (the
+        // rope dims are k-block pair DN / 64: 4 hi slots, 4 lo slots) are written by 16 lanes of
+        // 16 bytes, four heads per store instruction
+        __shared__ __attribute__((aligned(16))) _Float16 rp[4][64];
+        __shared__ __attribute__((aligned(16))) uint8_t k8p[4][8][16];  // [wave][part * 4 + g]
         const int w = threadIdx.x >> 6;
         float v[8];
         {
@@ -495,17 +506,29 @@ __global__ __launch_bounds__(256) void k_kva_pack(KvaPackArgs a) {
                 od += kat[(size_t)q * a.pstride + R + 2 * l + 1];
             }
             const float ec = ev * cs.x, os = od * cs.y, oc = od * cs.x, es = ev * cs.y;
-            split_f16(ec - os, rp[w][0][l], rp[w][1][l]);
-            split_f16(oc + es, rp[w][0][32 + l], rp[w][1][32 + l]);
+            _Float16 h0, l0, h1, l1;
+            split_f16(ec - os, h0, l0);
+            split_f16(oc + es, h1, l1);
+            rp[w][l] = h0;
+            rp[w][32 + l] = h1;
+            // dims DN + l (k-block 2p) and DN + 32 + l (2p + 1): group (l >> 3) & 3, element l & 7
+            const int g8 = (l >> 3) & 3, e = l & 7;
+            k8p[w][g8][e] = (uint8_t)f16_to_bf8(h0);
+            k8p[w][g8][8 + e] = (uint8_t)f16_to_bf8(h1);
+            k8p[w][4 + g8][e] = (uint8_t)bf8_lo_s11(l0);
+            k8p[w][4 + g8][8 + e] = (uint8_t)bf8_lo_s11(l1);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // lanes of part 0: 16 bytes of the fp16 hi row (dims DN + 8c ..); part 1: K8 slot c & 3 of
+        // the hi (c < 4) or lo part
         const int part = (l >> 3) & 1, c = l & 7;
-        const v4i rv = *(const v4i *)&rp[w][part][8 * c];
-        _Float16 *dst = part ? a.kl : a.kh;
-        for (int h = l >> 4; h < a.NH; h += 4)
-            *(v4i *)(dst + ((size_t)h * a.Sp + t) * QD + a.DN + 8 * c) = rv;
+        const v4i rv = part ? *(const v4i *)k8p[w][c] : *(const v4i *)&rp[w][8 * c];
+        uint8_t *dst = part ? a.k8 + (size_t)t * 384 + (c < 4 ? 0 : kK8Lo) + 16 * (4 * (a.DN >> 6) + (c & 3))
+                            : (uint8_t *)(a.kh + (size_t)t * QD + a.DN + 8 * c);
+        const size_t hs = part ? (size_t)a.Sp * 384 : (size_t)a.Sp * QD * sizeof(_Float16);
+        for (int h = l >> 4; h < a.NH; h += 4) *(v4i *)(dst + h * hs) = rv;
         return;
     }
     auto kv = [&](int r) {
@@ -537,12 +560,18 @@ __global__ __launch_bounds__(256) void k_kva_pack(KvaPackArgs a) {
         _Float16 h0, l0, h1, l1;
         split_f16(ec - os, h0, l0);
         split_f16(oc + es, h1, l1);
+        const int b0 = k8_hi_byte(a.DN + i), b1 = k8_hi_byte(a.DN + half + i);
+        const uint8_t h0b = (uint8_t)f16_to_bf8(h0), l0b = (uint8_t)bf8_lo_s11(l0);
+        const uint8_t h1b = (uint8_t)f16_to_bf8(h1), l1b = (uint8_t)bf8_lo_s11(l1);
         for (int h = 0; h < a.NH; ++h) {
             const size_t o = ((size_t)h * a.Sp + t) * QD + a.DN;
+            uint8_t *row = a.k8 + ((size_t)h * a.Sp + t) * 384;
             a.kh[o + i] = h0;
-            a.kl[o + i] = l0;
+            row[b0] = h0b;
+            row[b0 + kK8Lo] = l0b;
             a.kh[o + half + i] = h1;
-            a.kl[o + half + i] = l1;
+            row[b1] = h1b;
+            row[b1 + kK8Lo] = l1b;
         }
     }
 }
@@ -553,10 +582,14 @@ __global__ __launch_bounds__(256) void k_kva_pack(KvaPackArgs a) {
 // u = 0, 1), keys in tiles of 64. QD = 192, DV = 128. Operands are fp16 (11 significant bits,
 // ample range for these values): Q and K as hi + lo pairs, V and P rounded once.
 //
-// Scores are computed transposed, S^T = K Q^T (v_mfma_f32_16x16x32_f16, A = K from LDS,
-// B = Q^T from registers) in three passes, Kh Qh + Kh Ql + Kl Qh (the Kl Ql term is below
-// 2^-22 of the product): the score error stays near fp32 even for large logits, where a
-// single rounding of K would be amplified by the logit size. Lane (g, n) then holds
+// Scores are computed transposed, S^T = K Q^T (A = K from LDS, B = Q^T from registers), as
+// Kh Qh (v_mfma_f32_16x16x32_f16) plus the correction Kh Ql + Kl Qh as one bf8 product over
+// 384 concatenated dims (v_mfma_scale_f32_16x16x128_f8f6f4, three per 16 x 16 tile): K8 rows
+// hold bf8(Kh) and bf8(Kl 2^11) per lane group, the query operand bf8(Ql 2^11) and bf8(Qh) in
+// the matching byte order, and the MFMA scales the product by 2^-11. The correction terms are
+// 2^-11 of the product and bf8 keeps them to 2^-3, so the score error stays near 2^-14 of
+// |K||Q| even for large logits, where a single rounding of K would be amplified by the logit
+// size (the Kl Ql term is below 2^-22). Lane (g, n) then holds
 // S^T[key 16t + 4g + i][query n], exactly the values it must supply as the B operand of
 // O^T = V^T P^T when the k-slots of a 32-key chunk c are ordered (16-key tile 2c: i = 0..3,
 // tile 2c+1: i = 0..3) per lane group g; V^T is stored with its keys permuted to that order
@@ -575,7 +608,9 @@ constexpr int kFSmem = 2 * 2 * kFKB + 2 * kFVB;
 constexpr float kFLazy = 8.0f;       // log2 headroom of the lazy max
 
 struct FlashArgs {
-    const _Float16 *qh, *ql, *kh, *kl, *vt;  // Q, K: [NH, Sp, 192]; V^T: [NH, 128, Sp]
+    const _Float16 *qh, *ql, *kh;            // Q, K hi: [NH, Sp, 192]
+    const uint8_t *k8;                       // K8 rows: [NH, Sp, 384 bytes]
+    const _Float16 *vt;                      // V^T: [NH, 128, Sp]
     _Float16 *o;                             // [S, ldo] fp16 (input of the o_proj GEMM)
     int S, Sp, NH, ldo;
     float sl2;                               // softmax scale * log2(e)
@@ -621,7 +656,7 @@ void k_flash_prefill(FlashArgs a) {
     const size_t hq = (size_t)h * Sp;
 
     // Q^T B operands: query qw + 16u + n, dims 32kb + 8g .. +7
-    v8h qa[2][6], qb[2][6];
+    v8h qa[2][6], qb[2][6];  // hi (main pass), lo (folded into the bf8 operands below)
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const _Float16 *ph = a.qh + (hq + qw + 16 * u + n) * 192 + 8 * g;
@@ -637,7 +672,7 @@ void k_flash_prefill(FlashArgs a) {
     // 1536-slot tile; slot (row, s') holds logical slot s = s' ^ (row & 7) (within groups
     // of 8). V^T tile: slots (4w + i) * 64 + l of 1024; row d, slot s' holds s' ^ (d & 7).
     const uint8_t *gkh = (const uint8_t *)(a.kh + hq * 192);
-    const uint8_t *gkl = (const uint8_t *)(a.kl + hq * 192);
+    const uint8_t *gkl = a.k8 + hq * 384;
     const uint8_t *gv = (const uint8_t *)(a.vt + (size_t)h * 128 * Sp);
     uint32_t koff[6], voff[4];
 #pragma unroll
@@ -672,6 +707,15 @@ void k_flash_prefill(FlashArgs a) {
     for (int kb = 0; kb < 6; ++kb) krd[kb] = n * 384 + 16 * (8 * (kb >> 1) + ((4 * (kb & 1) + g) ^ (n & 7)));
 #pragma unroll
     for (int c = 0; c < 2; ++c) vrd[c] = n * 128 + 16 * ((4 * c + g) ^ (n & 7));
+    // K8 (A operand of correction MFMA m): row 16t + n, logical slots 8m + g and 8m + 4 + g
+    int f8rd[3][2];
+#pragma unroll
+    for (int m = 0; m < 3; ++m)
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+            const int ls = 8 * m + 4 * h2 + g;
+            f8rd[m][h2] = n * 384 + 16 * ((ls & ~7) | ((ls & 7) ^ (n & 7)));
+        }
 
     issue_k(0);
     issue_k(1);
@@ -681,12 +725,40 @@ void k_flash_prefill(FlashArgs a) {
 #pragma unroll
         for (int kb = 0; kb < 6; ++kb) asm volatile("" : "+v"(qa[u][kb]), "+v"(qb[u][kb]));
     wait_vmcnt<0>();
+    // correction operands: per u, 96 bytes = bf8(Ql 2^11) then bf8(Qh), each in (k-block,
+    // element) order, so that byte p meets byte p of the lane group's K8 bytes (hi, then lo);
+    // MFMA m takes bytes 32m .. 32m+31
+    v8i q8[2][3];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        uint32_t wd[24];
+#pragma unroll
+        for (int kb = 0; kb < 6; ++kb)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                uint32_t lo = 0, hi = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    lo |= bf8_lo_s11(qb[u][kb][4 * hf + i]) << (8 * i);
+                    hi |= f16_to_bf8(qa[u][kb][4 * hf + i]) << (8 * i);
+                }
+                wd[2 * kb + hf] = lo;
+                wd[12 + 2 * kb + hf] = hi;
+            }
+#pragma unroll
+        for (int m = 0; m < 3; ++m)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) q8[u][m][j] = (int)wd[8 * m + j];
+    }
     // the query operands live in AGPRs (MFMA reads its A/B operands from either file), which
     // leaves the VGPRs to the score accumulators the softmax reads
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < 2; ++u) {
 #pragma unroll
-        for (int kb = 0; kb < 6; ++kb) asm volatile("" : "+a"(qa[u][kb]), "+a"(qb[u][kb]));
+        for (int kb = 0; kb < 6; ++kb) asm volatile("" : "+a"(qa[u][kb]));
+#pragma unroll
+        for (int m = 0; m < 3; ++m) asm volatile("" : "+a"(q8[u][m]));
+    }
     lds_barrier();
 
     // Step j: QK of tile j+1 (unless it is the last step) with the softmax of tile j, the DMA
@@ -696,7 +768,7 @@ void k_flash_prefill(FlashArgs a) {
     // step is laid out as 18 groups of eight independent QK MFMAs (k-block kb, pass p) separated
     // by scheduling fences, each carrying its share of the other work, and the scheduler is asked
     // to alternate MFMAs and VALU within a group. Each QK accumulator receives its products in
-    // the order kb-major, Kh Qh, Kh Ql, Kl Qh; the softmax arithmetic is unchanged.
+    // the order Kh Qh for kb = 0 .. 5, then the corrections m = 0 .. 2.
     float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
     v4f acc[8][2];
 #pragma unroll
@@ -705,18 +777,29 @@ void k_flash_prefill(FlashArgs a) {
         for (int u = 0; u < 2; ++u) acc[dt][u] = v4f{0.f, 0.f, 0.f, 0.f};
 
     v4f sc[4][2];
-    auto load_k = [&](const uint8_t *kt, int kb, v8h (&kh)[4], v8h (&kl)[4]) __attribute__((always_inline)) {
+    auto load_kh = [&](const uint8_t *kt, int kb, v8h (&kh)[4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) kh[t] = *(const v8h *)(kt + t * 16 * 384 + krd[kb]);
+    };
+    auto load_k8 = [&](const uint8_t *kt, int m, v8i (&k8)[4]) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            kh[t] = *(const v8h *)(kt + t * 16 * 384 + krd[kb]);
-            kl[t] = *(const v8h *)(kt + kFKB + t * 16 * 384 + krd[kb]);
+            const v4i x0 = *(const v4i *)(kt + kFKB + t * 16 * 384 + f8rd[m][0]);
+            const v4i x1 = *(const v4i *)(kt + kFKB + t * 16 * 384 + f8rd[m][1]);
+            k8[t] = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
         }
     };
-    auto qk_pass = [&](v4f (&s)[4][2], const v8h (&kf)[4], const v8h (&qf)[2]) __attribute__((always_inline)) {
+    auto qk_main = [&](v4f (&s)[4][2], const v8h (&kf)[4], int kb) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int u = 0; u < 2; ++u) s[t][u] = mfma_f16(kf[t], qf[u], s[t][u]);
+            for (int u = 0; u < 2; ++u) s[t][u] = mfma_f16(kf[t], qa[u][kb], s[t][u]);
+    };
+    auto qk_corr = [&](v4f (&s)[4][2], const v8i (&kf)[4], int m) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) s[t][u] = mfma_bf8_s11(kf[t], q8[u][m], s[t][u]);
     };
     {  // QK of tile 0
         const uint8_t *kt = smem;
@@ -726,12 +809,15 @@ void k_flash_prefill(FlashArgs a) {
             for (int u = 0; u < 2; ++u) sc[t][u] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kb = 0; kb < 6; ++kb) {
-            v8h kh[4], kl[4];
-            load_k(kt, kb, kh, kl);
-            const v8h q0[2] = {qa[0][kb], qa[1][kb]}, q1[2] = {qb[0][kb], qb[1][kb]};
-            qk_pass(sc, kh, q0);
-            qk_pass(sc, kh, q1);
-            qk_pass(sc, kl, q0);
+            v8h kh[4];
+            load_kh(kt, kb, kh);
+            qk_main(sc, kh, kb);
+        }
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            v8i k8[4];
+            load_k8(kt, m, k8);
+            qk_corr(sc, k8, m);
         }
     }
 
@@ -801,27 +887,19 @@ void k_flash_prefill(FlashArgs a) {
         auto load_v = [&](int f) __attribute__((always_inline)) {
             vv[f >> 3][f & 7] = *(const v8h *)(vt + (f & 7) * 16 * 128 + vrd[f >> 3]);
         };
-        // the work carried by group gi (kb = gi / 3, pass = gi % 3)
+        // the work carried by group gi (gi < 6: main pass kb = gi, eight MFMAs of 16 cycles;
+        // gi = 6 .. 8: correction m = gi - 6, eight MFMAs of 32 cycles)
         auto extra = [&](int gi) __attribute__((always_inline)) {
             switch (gi) {
-            case 0: smA(0); dma_k(0); break;
-            case 1: smB(0); dma_k(1); break;
-            case 2: smC(0, 0); dma_k(2); break;
-            case 3: smC(0, 1); dma_k(3); break;
-            case 4: smC(0, 2); dma_k(4); break;
-            case 5: smC(0, 3); smD(0); dma_k(5); break;
-            case 6: smA(1); dma_v(0); break;
-            case 7: smB(1); dma_v(1); break;
-            case 8: smC(1, 0); dma_v(2); break;
-            case 9: smC(1, 1); dma_v(3); break;
-            case 10: smC(1, 2); break;
-            case 11: smC(1, 3); smD(1); break;
-            case 12: load_v(0); load_v(1); load_v(2); break;
-            case 13: load_v(3); load_v(4); load_v(5); break;
-            case 14: load_v(6); load_v(7); load_v(8); break;
-            case 15: load_v(9); load_v(10); load_v(11); break;
-            case 16: load_v(12); load_v(13); break;
-            case 17: load_v(14); load_v(15); break;
+            case 0: smA(0); dma_k(0); dma_k(1); break;
+            case 1: smB(0); dma_k(2); dma_k(3); break;
+            case 2: smC(0, 0); smC(0, 1); dma_k(4); dma_k(5); break;
+            case 3: smC(0, 2); smC(0, 3); smD(0); dma_v(0); dma_v(1); break;
+            case 4: smA(1); dma_v(2); dma_v(3); break;
+            case 5: smB(1); load_v(0); load_v(1); break;
+            case 6: smC(1, 0); smC(1, 1); load_v(2); load_v(3); load_v(4); load_v(5); break;
+            case 7: smC(1, 2); smC(1, 3); smD(1); load_v(6); load_v(7); load_v(8); load_v(9); break;
+            case 8: load_v(10); load_v(11); load_v(12); load_v(13); load_v(14); load_v(15); break;
             default: break;
             }
         };
@@ -832,25 +910,37 @@ void k_flash_prefill(FlashArgs a) {
             for (int t = 0; t < 4; ++t)
 #pragma unroll
                 for (int u = 0; u < 2; ++u) sn[t][u] = v4f{0.f, 0.f, 0.f, 0.f};
-            v8h kh[2][4], kl[2][4];
-            load_k(kt, 0, kh[0], kl[0]);
+            v8h kh[2][4];
+            v8i k8[2][4];
+            load_kh(kt, 0, kh[0]);
 #pragma unroll
             for (int kb = 0; kb < 6; ++kb) {
                 const int cb = kb & 1;
-                if (kb + 1 < 6) load_k(kt, kb + 1, kh[cb ^ 1], kl[cb ^ 1]);
-                const v8h q0[2] = {qa[0][kb], qa[1][kb]}, q1[2] = {qb[0][kb], qb[1][kb]};
+                if (kb + 1 < 6) load_kh(kt, kb + 1, kh[cb ^ 1]);
+                if (kb == 4) load_k8(kt, 0, k8[0]);
+                if (kb == 5) load_k8(kt, 1, k8[1]);
+                __builtin_amdgcn_sched_barrier(0);
+                qk_main(sn, kh[cb], kb);
+                extra(kb);
 #pragma unroll
-                for (int p = 0; p < 3; ++p) {
-                    __builtin_amdgcn_sched_barrier(0);
-                    qk_pass(sn, p == 2 ? kl[cb] : kh[cb], p == 1 ? q1 : q0);
-                    extra(3 * kb + p);
-#pragma unroll
-                    for (int m = 0; m < 8; ++m) {
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // up to three VALU
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
+                for (int i = 0; i < 8; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // up to three VALU
                 }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int m = 0; m < 3; ++m) {
+                if (m == 1) load_k8(kt, 2, k8[0]);  // k8[0] is free once correction 0 has issued
+                __builtin_amdgcn_sched_barrier(0);
+                qk_corr(sn, k8[m & 1], m);
+                extra(6 + m);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // up to six VALU
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
             // the softmax results stay in the groups above (the compiler would otherwise sink
             // them past the rescale branch, to their uses)
@@ -875,7 +965,7 @@ void k_flash_prefill(FlashArgs a) {
                 for (int u = 0; u < 2; ++u) sc[t][u] = sn[t][u];
         } else {
 #pragma unroll
-            for (int gi = 0; gi < 18; ++gi) extra(gi);
+            for (int gi = 0; gi < 9; ++gi) extra(gi);
             if (__any(moved)) {
 #pragma unroll
                 for (int dt = 0; dt < 8; ++dt)
@@ -1098,10 +1188,10 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
         _Float16 *qh = (_Float16 *)take(2 * (size_t)d.NH * Sp * d.QD);
         _Float16 *ql = (_Float16 *)take(2 * (size_t)d.NH * Sp * d.QD);
         _Float16 *kh = (_Float16 *)take(2 * (size_t)d.NH * Sp * d.QD);
-        _Float16 *kl = (_Float16 *)take(2 * (size_t)d.NH * Sp * d.QD);
+        uint8_t *k8 = (uint8_t *)take((size_t)d.NH * Sp * 384);
         _Float16 *vt = (_Float16 *)take(2 * (size_t)d.NH * d.DV * Sp);
         _Float16 *heads = (_Float16 *)take(2 * (size_t)S * d.HO);
-        const GemmEpi ep{qh, ql, kh, kl, vt, cs, Sp, d.DN, d.DR, d.DV};
+        const GemmEpi ep{qh, ql, kh, k8, vt, cs, Sp, d.DN, d.DR, d.DV};
         // flags[0] (any x lo word non-zero) is raised by k_split and cleared by k_kva_pack after
         // the q GEMM has read it, so no launch clears it first. A value left raised (a call
         // that failed in between, or the buffer reused by another call) only costs the GEMM's lo
@@ -1124,7 +1214,7 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
                                     d.H, ep)) != hipSuccess) {
             return e;
         }
-        KvaPackArgs ka{ykva, wnorm, cs, lath, latl, qh, ql, kh, kl, vt, (size_t)S * d.KVO, np,
+        KvaPackArgs ka{ykva, wnorm, cs, lath, latl, qh, ql, kh, k8, vt, (size_t)S * d.KVO, np,
                        S, Sp, d.NH, d.KVO, d.R, d.DN, d.DR, d.DV, eps, flags + 0};
         hipLaunchKernelGGL(k_kva_pack, dim3((Sp + 3) / 4), dim3(256), 0, st, ka);
         if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -1132,7 +1222,7 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
         if ((e = gemm<kEpiKV>(st, lath, latl, nullptr, d.R, wkvb, d.KVB, nullptr, 0, d.R, nullptr, 0, S, d.R,
                               ep)) != hipSuccess)
             return e;
-        FlashArgs fa{qh, ql, kh, kl, vt, heads, S, Sp, d.NH, d.HO, smscale * 1.4426950408889634f};
+        FlashArgs fa{qh, ql, kh, k8, vt, heads, S, Sp, d.NH, d.HO, smscale * 1.4426950408889634f};
         hipLaunchKernelGGL(k_flash_prefill, dim3(Sp / kFQ * d.NH), dim3(256), 0, st, fa);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // out = heads . o_proj^T in fp16 (heads rounded once, o_proj converted exactly)

@@ -75,8 +75,10 @@ CASES = [("stream", STREAM, 37, 0.2, False), ("kimi", KIMI, 130, 0.02, False), (
 def test_fused_equals_prefill_then_state_prefill(name, dims, S, std, bf16_x, kind):
     """State bit-identical to the state prefill's. Generic route (stream-probe shapes, the fill
     computes its own kv_a): output bit-identical too. Kimi-VL MFMA route (one kv_a for the
-    attention and the state, in the decode's summation order): output within the rounding of
-    kv_a of the plain prefill's. S not a multiple of the tiles."""
+    attention and the state, in the decode's summation order): output within 5e-4 of the plain
+    prefill's (a last-bit change of kv_a can move the bf8 rounding of a score correction
+    operand, 2^-14 of |K||Q|; each output is within 2e-3 of the oracle's). S not a multiple of
+    the tiles."""
     print(f"[fused] {kind} {name} S={S}", flush=True)
     cfg = inputs.config(**dims)
     layer = inputs.make_layer(cfg, 0xF0 + S, std=std)
@@ -89,7 +91,7 @@ def test_fused_equals_prefill_then_state_prefill(name, dims, S, std, bf16_x, kin
         np.testing.assert_array_equal(ob, oa)
     else:
         print(f"[fused]   vs plain prefill max|d|/max|ref| = {rel_err(ob, oa):.3e}", flush=True)
-        assert rel_err(ob, oa) <= 1e-4
+        assert rel_err(ob, oa) <= 5e-4
     assert_snap_equal(snapshot(kind, sb, cfg), snapshot(kind, sa, cfg))
     free_state(G, kind, sa)
     free_state(G, kind, sb)
