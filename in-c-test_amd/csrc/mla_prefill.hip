@@ -6,9 +6,11 @@
 //   gemm      [q | kv_a] = x . W^T           (bf16 MFMA, fp32 accumulate, lo pass skipped
 //                                             when the operand is exactly bf16); epilogue:
 //                                             Q = [q_nope | RoPE(q_rope)] as hi/lo fp16
-//   kva_pack  RMSNorm -> latent (hi/lo bf16), RoPE(k_rope) -> rope part of K (hi/lo fp16)
-//   gemm      kv = latent . kv_b^T           epilogue: k_nope -> K (hi/lo fp16), V^T (fp16)
-//   flash     causal attention per (128-query tile, head), online softmax
+//   kva_pack  RMSNorm -> latent (hi/lo bf16), RoPE(k_rope) -> rope part of K (fp16 hi + K8)
+//   gemm      kv = latent . kv_b^T           epilogue: k_nope -> K (fp16 hi + K8), V^T (fp16)
+//   flash     causal attention per (128-query tile, head), online softmax; scores Kh Qh in
+//             fp16 plus the Kh Ql + Kl Qh correction from bf8 operands (K8: bf8 of the hi
+//             parts and of the lo parts x 2^11)
 //   gemm      out = heads . o_proj^T          (fp16 heads and fp16 copy of o_proj, one pass)
 // Generic route (any shape): the same stages with VALU kernels.
 #include "mla_device.h"
@@ -424,9 +426,9 @@ __global__ __launch_bounds__(256) void k_kva_epi(KvaEpiArgs a) {
 
 // MFMA route, one wave per token t: latent = RMSNorm(kv_a[t, :R]) * w (as k_kva_epi) as
 // hi/lo bf16 [S, R] for the kv_b GEMM (whose lo pass always runs), and the rotated k_rope
-// (src/mla_prefill_streaming.c:131-138) as hi/lo fp16 into the rope part of K for every
-// head. Tokens S .. Sp-1 zero their Q, K and V^T entries, so padding keys contribute 0 * 0
-// in the flash kernel.
+// (src/mla_prefill_streaming.c:131-138) into the rope part of K for every head, as the fp16
+// hi row and the K8 bytes (bf8 of hi and of lo x 2^11). Tokens S .. Sp-1 zero their Q, K, K8
+// and V^T entries, so padding keys contribute 0 * 0 in the flash kernel.
 struct KvaPackArgs {
     const float *y;  // [S, ldy] kv_a projection
     const uint16_t *norm;
@@ -1218,7 +1220,7 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
                        S, Sp, d.NH, d.KVO, d.R, d.DN, d.DR, d.DV, eps, flags + 0};
         hipLaunchKernelGGL(k_kva_pack, dim3((Sp + 3) / 4), dim3(256), 0, st, ka);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        // kv_b (-> K nope part, V^T hi/lo)
+        // kv_b (-> K nope part as fp16 hi + K8, V^T)
         if ((e = gemm<kEpiKV>(st, lath, latl, nullptr, d.R, wkvb, d.KVB, nullptr, 0, d.R, nullptr, 0, S, d.R,
                               ep)) != hipSuccess)
             return e;
