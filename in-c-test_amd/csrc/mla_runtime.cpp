@@ -181,8 +181,15 @@ Ctx &ctx() {
     return *c;
 }
 
+// Frees library memory after the work queued on the library stream (which may still read it)
+// has finished.
 hipError_t dev_free(void *p) {
-    ++ctx().free_gen;
+    Ctx &c = ctx();
+    ++c.free_gen;
+    if (c.stream && !c.capturing) {
+        const hipError_t e = hipStreamSynchronize(c.stream);
+        if (e != hipSuccess) return e;
+    }
     return hipFree(p);
 }
 
@@ -314,6 +321,10 @@ int dev_weight(const uint16_t *host, size_t elems, const uint16_t **out) {
             return 0;
         }
     }
+    if (c.capturing) {
+        set_err("weight upload during graph capture (bind the weights or run one call first)");
+        return -1;
+    }
     WeightEntry e;
     if (it != c.weights.end()) {
         e = it->second;
@@ -334,6 +345,11 @@ int dev_weight(const uint16_t *host, size_t elems, const uint16_t **out) {
     e.bytes = bytes;
     e.f16_ok = false;
     e.t_ok = false;
+    // The blocking copy runs on the null stream, which does not wait for the library's
+    // non-blocking stream: when it overwrites a buffer that queued kernels may still read (an
+    // unbound array rewritten in place and used again by a stream-ordered device call), finish
+    // that work first.
+    if (it != c.weights.end()) HIP_TRY(hipStreamSynchronize(c.stream));
     HIP_TRY(hipMemcpy(e.dev, host, bytes, hipMemcpyHostToDevice));
     e.digest = sample_digest(host, bytes);
     c.weights[host] = e;

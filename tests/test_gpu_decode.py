@@ -226,6 +226,63 @@ def test_kv_b_rewritten_in_place_refreshes_device_copies(bound):
         assert rel_err(a0, b1) > 10 * TOL, (kind, "stale kv_b copy")
 
 
+def test_unbound_kv_b_reloaded_between_queued_device_calls():
+    """Stream-ordered calls return before their kernels run. Rewriting an unbound kv_b array in
+    place and calling again must not let the re-upload overtake kernels of earlier calls that
+    still read the old copy: calls queued with the old kv_b (no synchronisation in between) give
+    the old-weight result, the call after the rewrite the new-weight result."""
+    cfg, layer, _ = model(KIMI, 0xD5)
+    w = layer.struct()
+    old = layer.kv_b_proj.copy()
+    new = inputs.normal_bf16(0xD6, "kv_b", old.shape, std=0.02)
+    B, n = 8, 16384
+    states = []
+    for i in range(B):
+        st = abi.KvlMlaCompressedQ8State()
+        assert G.mla_compressed_q8_state_init(C.byref(st), C.byref(cfg), n + 8) == 0
+        lib.check(L.kvl_mla_compressed_q8_state_fill_synthetic(C.byref(st), 0, n, 91 + i), "fill")
+        states.append(st)
+    arr = (C.POINTER(abi.KvlMlaCompressedQ8State) * B)(*[C.pointer(s) for s in states])
+    xb = np.ascontiguousarray(inputs.hidden(cfg, 0xD5, B, tag="q"))
+    nbytes = xb.nbytes
+    dx, da, db = (L.kvl_mla_device_alloc(nbytes) for _ in range(3))
+    assert dx and da and db
+    lib.check(L.kvl_mla_copy_to_device(dx, xb.ctypes.data, nbytes), "h2d")
+
+    def run(dout):
+        lib.check(L.kvl_mla_decode_compressed_q8_batch_device(dout, dx, B, C.byref(cfg), C.byref(w), arr,
+                                                              lib.NO_ADVANCE), "device decode")
+
+    def fetch(dout):
+        got = np.zeros_like(xb)
+        lib.check(L.kvl_mla_copy_to_host(got.ctypes.data, dout, nbytes), "d2h")
+        return got
+
+    print("[decode] unbound kv_b reload between queued device calls", flush=True)
+    run(da)  # reference results, synchronised
+    lib.check(L.kvl_mla_synchronize(), "sync")
+    ref_old = fetch(da)
+    layer.kv_b_proj[...] = new
+    run(db)
+    lib.check(L.kvl_mla_synchronize(), "sync")
+    ref_new = fetch(db)
+    assert rel_err(ref_old, ref_new) > 10 * TOL
+    layer.kv_b_proj[...] = old
+    run(da)
+    lib.check(L.kvl_mla_synchronize(), "sync")
+    for _ in range(40):  # keep the stream busy with old-weight calls (a few ms of kernels)
+        run(da)
+    layer.kv_b_proj[...] = new  # rewrite in place while they run
+    run(db)
+    lib.check(L.kvl_mla_synchronize(), "sync")
+    np.testing.assert_array_equal(fetch(da), ref_old, err_msg="queued old-weight calls saw the new kv_b")
+    np.testing.assert_array_equal(fetch(db), ref_new)
+    for p in (dx, da, db):
+        L.kvl_mla_device_free(p)
+    for st in states:
+        G.mla_compressed_q8_state_free(C.byref(st))
+
+
 @pytest.mark.parametrize("dims", [LAB, KIMI], ids=["lab", "kimi"])
 def test_block_equals_serial_and_rollback_exact(dims):
     """src/spec_q8_lab_probe.c:86-173 on the GPU: block decode == per-token decode exactly;

@@ -97,7 +97,97 @@ def test_noalloc_refusals():
     assert nx(d_x, d_x, 1, C.byref(cfg), C.byref(w), one, 0) == -1       # no device copy yet
     assert fresh.len == 0 and all(s.len == 100 for s in states)
     L.kvl_mla_compressed_q8_state_free(C.byref(fresh))
-    L.kvl_mla_device_free(d_x)
     for st in states:
+        L.kvl_mla_compressed_q8_state_free(C.byref(st))
+    # a split plan whose partials overflow the fixed array: 16 sequences of 50,000 rows make
+    # 16 x 48 splits of 32.9 KB (25 MB > 24 MiB). The RoPE table is built first by an allocating
+    # call, so the partials are what is refused.
+    print("[noalloc] refusals: partials beyond the fixed array, position beyond the RoPE table", flush=True)
+    big = make_states(cfg, [50000] * 16, 0xB40)
+    barr = (Q8P * 16)(*[C.pointer(s) for s in big])
+    xb = np.ascontiguousarray(inputs.hidden(cfg, 0xB4, 16, tag="q"))
+    d_b = L.kvl_mla_device_alloc(xb.nbytes)
+    lib.check(L.kvl_mla_copy_to_device(d_b, xb.ctypes.data, xb.nbytes), "h2d")
+    lib.check(L.kvl_mla_decode_compressed_q8_batch_device(d_b, d_b, 1, C.byref(cfg), C.byref(w), barr,
+                                                          lib.NO_ADVANCE), "allocating call")
+    assert nx(d_b, d_b, 16, C.byref(cfg), C.byref(w), barr, 0) == -1
+    assert "partials" in lib.last_error(), lib.last_error()
+    assert all(s.len == 50000 for s in big)
+    for st in big:
+        L.kvl_mla_compressed_q8_state_free(C.byref(st))
+    # a position no allocating call has reached: the RoPE table (grown by those calls in powers
+    # of two, 65,536 positions at most in these tests) does not cover it
+    far = make_states(cfg, [150000], 0xB50)
+    farr = (Q8P * 1)(C.pointer(far[0]))
+    assert nx(d_b, d_b, 1, C.byref(cfg), C.byref(w), farr, 0) == -1
+    assert "RoPE table" in lib.last_error(), lib.last_error()
+    assert far[0].len == 150000
+    L.kvl_mla_compressed_q8_state_free(C.byref(far[0]))
+    L.kvl_mla_device_free(d_b)
+    L.kvl_mla_device_free(d_x)
+    L.kvl_mla_release_weights(C.byref(w))
+
+
+def test_noalloc_under_capture_and_after_a_larger_plan():
+    """The entry point under graph capture on the library stream (capture refuses every device
+    allocation the library would make, so a stray one fails the capture), its replays against
+    the eager call, and a call whose split plan is larger than the allocating calls before it
+    made: it must not move library memory, so a graph captured before it still launches."""
+    cfg = inputs.config(**inputs.KIMI)
+    layer = inputs.make_layer(cfg, 0xAB)
+    w = layer.struct()
+    lib.check(L.kvl_mla_bind_weights(C.byref(cfg), C.byref(w)), "bind")
+    small = make_states(cfg, [3000, 1200], 0xC00)
+    sarr = (Q8P * 2)(*[C.pointer(s) for s in small])
+    xs = np.ascontiguousarray(inputs.hidden(cfg, 0xAC, 16, tag="q"))
+    d_x = L.kvl_mla_device_alloc(xs.nbytes)
+    d_o = L.kvl_mla_device_alloc(xs.nbytes)
+    lib.check(L.kvl_mla_copy_to_device(d_x, xs.ctypes.data, xs.nbytes), "h2d")
+    # warm up (the RoPE table to 65,536 positions) and capture an allocating-path graph
+    big = make_states(cfg, [40000] * 16, 0xC10)
+    barr = (Q8P * 16)(*[C.pointer(s) for s in big])
+    lib.check(L.kvl_mla_decode_compressed_q8_batch_device(d_o, d_x, 1, C.byref(cfg), C.byref(w), barr,
+                                                          lib.NO_ADVANCE), "warm-up")
+    lib.check(L.kvl_mla_decode_compressed_q8_batch_device(d_o, d_x, 2, C.byref(cfg), C.byref(w), sarr,
+                                                          lib.NO_ADVANCE), "warm-up")
+    lib.check(L.kvl_mla_synchronize(), "sync")
+    lib.check(L.kvl_mla_capture_begin(), "capture begin")
+    rc = L.kvl_mla_decode_compressed_q8_batch_device(d_o, d_x, 2, C.byref(cfg), C.byref(w), sarr, lib.NO_ADVANCE)
+    g0 = C.c_void_p()
+    lib.check(L.kvl_mla_capture_end(C.byref(g0)), "capture end")
+    lib.check(rc, "captured allocating-path call")
+    # 16 x 40,000 rows: 624 splits, more than any earlier call of this test made
+    print("[noalloc] larger plan: 16 x 40000 rows", flush=True)
+    nx = L.kvl_mla_decode_compressed_q8_batch_device_noalloc
+    d_big = L.kvl_mla_device_alloc(xs.nbytes)
+    lib.check(nx(d_big, d_x, 16, C.byref(cfg), C.byref(w), barr, lib.NO_ADVANCE), "no-allocation call, large plan")
+    lib.check(L.kvl_mla_synchronize(), "sync")
+    lib.check(L.kvl_mla_graph_launch(g0), "graph captured before the large no-allocation call")
+    lib.check(L.kvl_mla_synchronize(), "sync")
+    lib.check(L.kvl_mla_graph_destroy(g0), "graph destroy")
+    # under capture
+    print("[noalloc] captured no-allocation call, three replays", flush=True)
+    lib.check(nx(d_o, d_x, 16, C.byref(cfg), C.byref(w), barr, lib.NO_ADVANCE), "eager")
+    eager = np.zeros_like(xs)
+    lib.check(L.kvl_mla_copy_to_host(eager.ctypes.data, d_o, xs.nbytes), "d2h")
+    lib.check(L.kvl_mla_capture_begin(), "capture begin")
+    rc = nx(d_o, d_x, 16, C.byref(cfg), C.byref(w), barr, lib.NO_ADVANCE)
+    g1 = C.c_void_p()
+    lib.check(L.kvl_mla_capture_end(C.byref(g1)), "capture end")
+    lib.check(rc, "captured no-allocation call")
+    for rep in range(3):
+        junk = np.full_like(xs, 3.0)
+        lib.check(L.kvl_mla_copy_to_device(d_o, junk.ctypes.data, xs.nbytes), "clear")
+        lib.check(L.kvl_mla_graph_launch(g1), "graph launch")
+        lib.check(L.kvl_mla_synchronize(), "sync")
+        got = np.zeros_like(xs)
+        lib.check(L.kvl_mla_copy_to_host(got.ctypes.data, d_o, xs.nbytes), "d2h")
+        np.testing.assert_array_equal(got, eager, err_msg=f"replay {rep}")
+        lib.check(nx(d_big, d_x, 2, C.byref(cfg), C.byref(w), sarr, lib.NO_ADVANCE), "eager between replays")
+        lib.check(L.kvl_mla_synchronize(), "sync")
+    lib.check(L.kvl_mla_graph_destroy(g1), "graph destroy")
+    for p in (d_x, d_o, d_big):
+        L.kvl_mla_device_free(p)
+    for st in small + big:
         L.kvl_mla_compressed_q8_state_free(C.byref(st))
     L.kvl_mla_release_weights(C.byref(w))
