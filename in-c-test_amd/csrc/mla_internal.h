@@ -170,8 +170,8 @@ hipError_t launch_read(hipStream_t st, const void *src, size_t bytes, void *sink
 hipError_t launch_empty(hipStream_t st);
 
 // ---- prefill (mla_prefill.hip) ----
-// Device workspace bytes of a causal prefill of S tokens.
-size_t prefill_bytes(const Dims &d, int S);
+// Device workspace bytes of a causal prefill of S tokens (generic: on the generic route).
+size_t prefill_bytes(const Dims &d, int S, bool generic = false);
 // Causal MLA prefill of S tokens: x [S,H] -> out [S,H] (device pointers), ws of
 // prefill_bytes(d, S) bytes, rope_cs table covering positions [0, S).
 // wo16: o_proj converted to fp16 (launch_bf16_to_f16), used by the MFMA route (the attention
@@ -185,11 +185,22 @@ struct PrefillKva {
     int ldy, np;
     size_t pstride;
 };
+// Range handling of the MFMA route (mla_prefill.hip): vscale (V) and oscale (the fp16 o_proj
+// copy) are powers of two; sticky (optional) is raised with the call's own flag (the int after
+// the first of ws: prefill_range_flag) when a query row falls outside the route's range.
+// generic: take the generic route whatever the dims.
+struct PrefillRange {
+    float vscale = 1.0f, oscale = 1.0f;
+    int *sticky = nullptr;
+    bool generic = false;
+};
+// The per-call range flag of a prefill whose workspace is ws (MFMA route).
+inline int *prefill_range_flag(void *ws) { return (int *)ws + 1; }
 hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, const float *x,
                               float *out, const uint16_t *wq, const uint16_t *wkva,
                               const uint16_t *wnorm, const uint16_t *wkvb, const uint16_t *wo,
                               const _Float16 *wo16, const float2 *rope_cs, void *ws,
-                              PrefillKva *kva = nullptr);
+                              PrefillKva *kva = nullptr, const PrefillRange *range = nullptr);
 // True when a prefill of these dims can give its kv_a projection in the decode arithmetic.
 bool prefill_kva_exact(const Dims &d);
 // True when the prefill of these dims takes the MFMA route (needs the fp16 o_proj copy).
@@ -198,7 +209,8 @@ bool prefill_mfma_shape(const Dims &d);
 // even). cols % 8 == 0, 16-byte aligned rows.
 hipError_t launch_split(hipStream_t st, const float *src, int ld_src, uint16_t *hi, uint16_t *lo,
                         int ld_dst, int rows, int cols);
-// dst[i] = (fp16) bf16 src[i]: exact for |x| >= 2^-17 (bf16 has 8 significant bits).
-hipError_t launch_bf16_to_f16(hipStream_t st, _Float16 *dst, const uint16_t *src, size_t n);
+// dst[i] = (fp16)(bf16 src[i] * scale), scale a power of two: exact while the scaled value is a
+// normal fp16 (bf16 has 8 significant bits).
+hipError_t launch_bf16_to_f16(hipStream_t st, _Float16 *dst, const uint16_t *src, size_t n, float scale);
 
 }  // namespace kvl

@@ -13,6 +13,15 @@
 //             parts and of the lo parts x 2^11)
 //   gemm      out = heads . o_proj^T          (fp16 heads and fp16 copy of o_proj, one pass)
 // Generic route (any shape): the same stages with VALU kernels.
+//
+// Range of the 16-bit operands. V (and so the attention output) and the fp16 o_proj copy carry
+// power-of-two scales chosen by the host from bounds it knows (|V| <= sqrt(R) max|norm weight|
+// max ||kv_b row||_2; max|o_proj|), undone exactly by the o_proj epilogue. Q and K depend on x
+// and are not scaled; the flash kernel checks every query row instead: a row whose reference
+// max logit exceeds kFLogitMax (beyond it the bf8 score correction's error grows past the 2e-3
+// budget) or whose output is not finite raises a per-call flag (and a sticky flag for callers
+// that read it later). The o_proj epilogue then writes NaN, and the host-buffer entry points
+// run the call again on the generic route.
 #include "mla_device.h"
 #include "mla_internal.h"
 
@@ -32,6 +41,10 @@ __global__ __launch_bounds__(256) void k_split(const float *src, int ld_src, uin
                                                int *flag) {
     const int c8 = cols / 8;
     int any = 0;
+    // flag[1]: the range flag of this call (raised by the flash kernel, read by the o_proj
+    // epilogue), cleared here, in the call's first kernel
+    if (flag && blockIdx.x == 0 && threadIdx.x == 0)
+        __hip_atomic_store(flag + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     // rows over blocks, 8-column groups over threads (no index division in the loop)
     for (int r = blockIdx.x; r < rows; r += gridDim.x) {
         const float *s = src + (size_t)r * ld_src;
@@ -111,6 +124,9 @@ struct GemmEpi {
     _Float16 *vt;
     const float2 *cs;
     int Sp, DN, DR, DV;
+    float vscale = 1.0f;             // kEpiKV: V^T = vscale * v (a power of two)
+    float alpha = 1.0f;              // kEpiPlain: C = alpha * acc (a power of two)
+    const int *nan_flag = nullptr;   // kEpiPlain: C = NaN when *nan_flag != 0
 };
 
 // Position of key k (0..31 within its 32-key group) in the permuted V^T rows: the 8 keys
@@ -248,6 +264,9 @@ __global__ __launch_bounds__(64 * (kGemmMath + kGemmDma)) void k_gemm16(GemmArgs
     const bool vt_wave = EPI == kEpiKV && ((nb0 + cw) % KH) >= e.DN;
     const int rr = l >> 4, cc = (l & 15) * 4;    // staged row (+ 4 q) / first column of this lane
     const int nl0 = nb0 + cw + cc;               // segment column of v[0]
+    float alpha = e.alpha;
+    if (EPI == kEpiPlain && e.nan_flag && __hip_atomic_load(e.nan_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+        alpha = __builtin_nanf("");
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         const int rbase = m0 + wm * TM * 16 + 16 * i;
@@ -258,8 +277,8 @@ __global__ __launch_bounds__(64 * (kGemmMath + kGemmDma)) void k_gemm16(GemmArgs
                 const int nl = nb0 + cw + 16 * j + n;
                 if (nl >= Nseg) continue;
                 const int h = nl / KH, d = nl % KH - e.DN;
-                const v4h hv = {(_Float16)acc[i][j][0], (_Float16)acc[i][j][1], (_Float16)acc[i][j][2],
-                                (_Float16)acc[i][j][3]};
+                const v4h hv = {(_Float16)(acc[i][j][0] * e.vscale), (_Float16)(acc[i][j][1] * e.vscale),
+                                (_Float16)(acc[i][j][2] * e.vscale), (_Float16)(acc[i][j][3] * e.vscale)};
                 const size_t o = ((size_t)h * e.DV + d) * e.Sp + (row0 & ~31) + vt_perm(row0 & 31);
                 if (row0 + 3 < M) {
                     *(v4h *)(e.vt + o) = hv;
@@ -286,7 +305,7 @@ __global__ __launch_bounds__(64 * (kGemmMath + kGemmDma)) void k_gemm16(GemmArgs
             const float v[4] = {vq[q].x, vq[q].y, vq[q].z, vq[q].w};
             if (EPI == kEpiPlain || (EPI == kEpiQ && seg1)) {
                 float *dst = EPI == kEpiPlain ? a.C + (size_t)t * a.ldc + c0 + cw + cc : a.C + (size_t)t * a.ldc + nl0;
-                *(v4f *)dst = vq[q];
+                *(v4f *)dst = EPI == kEpiPlain ? vq[q] * alpha : vq[q];
             } else if (EPI == kEpiQ) {
                 // Q (50 MB at 4096 tokens) is read once, by the flash kernel's workgroup of its
                 // query tile: non-temporal stores keep it from evicting the K/V and weight
@@ -614,9 +633,15 @@ struct FlashArgs {
     const uint8_t *k8;                       // K8 rows: [NH, Sp, 384 bytes]
     const _Float16 *vt;                      // V^T: [NH, 128, Sp]
     _Float16 *o;                             // [S, ldo] fp16 (input of the o_proj GEMM)
+    int *flag_call, *flag_sticky;            // range flags (flag_sticky may be null)
     int S, Sp, NH, ldo;
     float sl2;                               // softmax scale * log2(e)
 };
+
+// Largest |row max logit| (natural units, scale included) for which the scores' bf8
+// correction keeps the attention within the 2e-3 budget with margin: measured at 256 tokens,
+// row-max logits up to ~150 give 3e-4, ~500 give 6e-4, ~1450 give 1.7e-3, ~4400 give 2.3e-3.
+constexpr float kFLogitMax = 512.0f;
 
 // Max / sum over the four lanes n, n + 16, n + 32, n + 48 (one per 16-lane row).
 __device__ __forceinline__ float xrow_max(float v) {
@@ -988,16 +1013,29 @@ void k_flash_prefill(FlashArgs a) {
     step(T{}, T{}, nt - 2);
     step(T{}, F{}, nt - 1);
 
+    // range check of each query row: the reference max m_run (log2 units, within kFLazy of the
+    // row's true max) and every output value (NaN or Inf from operands beyond the fp16 range)
+    bool bad = false;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int q = qw + 16 * u + n;
         const float inv = 1.0f / xrow_sum(l_run[u]);
         if (q >= S) continue;
+        bad |= !(fabsf(m_run[u]) <= kFLogitMax * 1.4426950408889634f);  // m_run = logit * log2(e)
         _Float16 *o = a.o + (size_t)q * ldo + (size_t)h * 128 + 4 * g;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-            *(v4h *)(o + 16 * dt) = v4h{(_Float16)(acc[dt][u][0] * inv), (_Float16)(acc[dt][u][1] * inv),
-                                        (_Float16)(acc[dt][u][2] * inv), (_Float16)(acc[dt][u][3] * inv)};
+        for (int dt = 0; dt < 8; ++dt) {
+            const v4h ov = {(_Float16)(acc[dt][u][0] * inv), (_Float16)(acc[dt][u][1] * inv),
+                            (_Float16)(acc[dt][u][2] * inv), (_Float16)(acc[dt][u][3] * inv)};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bad |= !__builtin_isfinite((float)ov[i]);
+            *(v4h *)(o + 16 * dt) = ov;
+        }
+    }
+    // any writer stores the same value; the readers are later kernels
+    if (__builtin_amdgcn_ballot_w64(bad) != 0 && l == 0) {
+        __hip_atomic_store(a.flag_call, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (a.flag_sticky) __hip_atomic_store(a.flag_sticky, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
 }
 
@@ -1053,10 +1091,12 @@ __global__ __launch_bounds__(256) void k_gen_attn(GenAttnArgs a) {
     for (int j = tid; j < L; j += 256) {
         const float *kj = a.kv + (size_t)j * a.NH * KH + (size_t)h * KH;
         const float *rj = a.krope + (size_t)j * a.DR;
-        float acc = 0.f;
-        for (int k = 0; k < a.DN; ++k) acc = fmaf(q[k], kj[k], acc);
-        for (int k = 0; k < a.DR; ++k) acc = fmaf(q[a.DN + k], rj[k], acc);
-        sc[j] = acc * a.smscale;
+        // the dots in double and the score as (float)dot * scale, as
+        // src/mla_prefill_streaming.c:171-174
+        double acc = 0.0;
+        for (int k = 0; k < a.DN; ++k) acc = fma((double)q[k], (double)kj[k], acc);
+        for (int k = 0; k < a.DR; ++k) acc = fma((double)q[a.DN + k], (double)rj[k], acc);
+        sc[j] = (float)acc * a.smscale;
     }
     __syncthreads();
     float m = -INFINITY;
@@ -1095,9 +1135,9 @@ hipError_t launch_gemv(hipStream_t st, float *Y, int ldy, const float *X, int ld
                        const uint16_t *W0, int out0, const uint16_t *W1, int out1, int in,
                        bool accumulate);
 
-__global__ __launch_bounds__(256) void k_bf16_to_f16(_Float16 *dst, const uint16_t *src, size_t n) {
+__global__ __launch_bounds__(256) void k_bf16_to_f16(_Float16 *dst, const uint16_t *src, size_t n, float scale) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
-        dst[i] = (_Float16)bf16_to_f32(src[i]);
+        dst[i] = (_Float16)(bf16_to_f32(src[i]) * scale);
 }
 
 hipError_t launch_split(hipStream_t st, const float *src, int ld_src, uint16_t *hi, uint16_t *lo,
@@ -1111,9 +1151,9 @@ hipError_t launch_split(hipStream_t st, const float *src, int ld_src, uint16_t *
     return hipGetLastError();
 }
 
-hipError_t launch_bf16_to_f16(hipStream_t st, _Float16 *dst, const uint16_t *src, size_t n) {
+hipError_t launch_bf16_to_f16(hipStream_t st, _Float16 *dst, const uint16_t *src, size_t n, float scale) {
     const int blocks = (int)std::min<size_t>(4096, (n + 255) / 256);
-    hipLaunchKernelGGL(k_bf16_to_f16, dim3(blocks), dim3(256), 0, st, dst, src, n);
+    hipLaunchKernelGGL(k_bf16_to_f16, dim3(blocks), dim3(256), 0, st, dst, src, n, scale);
     return hipGetLastError();
 }
 
@@ -1132,11 +1172,11 @@ static int gen_query_tile(const Dims &d, int S) {
     return (int)std::max<size_t>(1, std::min<size_t>((size_t)S, cap / per_query));
 }
 
-size_t prefill_bytes(const Dims &d, int S) {
+size_t prefill_bytes(const Dims &d, int S, bool generic) {
     const size_t Sp = (size_t)(S + 127) / 128 * 128;
     size_t b = 0;
     auto add = [&](size_t n) { b += (n + 255) / 256 * 256 + 256; };
-    if (prefill_mfma_shape(d)) {
+    if (prefill_mfma_shape(d) && !generic) {
         add(4 * 8);                              // flags
         add(2 * (size_t)S * d.H);                // x hi
         add(2 * (size_t)S * d.H);                // x lo
@@ -1164,7 +1204,8 @@ size_t prefill_bytes(const Dims &d, int S) {
 hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, const float *x,
                               float *out, const uint16_t *wq, const uint16_t *wkva,
                               const uint16_t *wnorm, const uint16_t *wkvb, const uint16_t *wo,
-                              const _Float16 *wo16, const float2 *cs, void *ws, PrefillKva *kva) {
+                              const _Float16 *wo16, const float2 *cs, void *ws, PrefillKva *kva,
+                              const PrefillRange *range) {
     const int Sp = (S + 127) / 128 * 128;
     if (kva) *kva = PrefillKva{nullptr, 0, 0, 0};
     char *base = (char *)ws;
@@ -1178,7 +1219,7 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
     const float smscale = 1.0f / sqrtf((float)d.QD);
     const int ldy = d.QO + d.KVO;
     hipError_t e;
-    if (prefill_mfma_shape(d)) {
+    if (prefill_mfma_shape(d) && !(range && range->generic)) {
         int *flags = (int *)take(4 * 8);
         uint16_t *xh = (uint16_t *)take(2 * (size_t)S * d.H);
         uint16_t *xl = (uint16_t *)take(2 * (size_t)S * d.H);
@@ -1193,7 +1234,8 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
         uint8_t *k8 = (uint8_t *)take((size_t)d.NH * Sp * 384);
         _Float16 *vt = (_Float16 *)take(2 * (size_t)d.NH * d.DV * Sp);
         _Float16 *heads = (_Float16 *)take(2 * (size_t)S * d.HO);
-        const GemmEpi ep{qh, ql, kh, k8, vt, cs, Sp, d.DN, d.DR, d.DV};
+        GemmEpi ep{qh, ql, kh, k8, vt, cs, Sp, d.DN, d.DR, d.DV};
+        const float vscale = range ? range->vscale : 1.0f, oscale = range ? range->oscale : 1.0f;
         // flags[0] (any x lo word non-zero) is raised by k_split and cleared by k_kva_pack after
         // the q GEMM has read it, so no launch clears it first. A value left raised (a call
         // that failed in between, or the buffer reused by another call) only costs the GEMM's lo
@@ -1220,15 +1262,21 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
                        S, Sp, d.NH, d.KVO, d.R, d.DN, d.DR, d.DV, eps, flags + 0};
         hipLaunchKernelGGL(k_kva_pack, dim3((Sp + 3) / 4), dim3(256), 0, st, ka);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        // kv_b (-> K nope part as fp16 hi + K8, V^T)
+        // kv_b (-> K nope part as fp16 hi + K8, V^T scaled by vscale)
+        ep.vscale = vscale;
         if ((e = gemm<kEpiKV>(st, lath, latl, nullptr, d.R, wkvb, d.KVB, nullptr, 0, d.R, nullptr, 0, S, d.R,
                               ep)) != hipSuccess)
             return e;
-        FlashArgs fa{qh, ql, kh, k8, vt, heads, S, Sp, d.NH, d.HO, smscale * 1.4426950408889634f};
+        FlashArgs fa{qh, ql, kh, k8, vt, heads, flags + 1, range ? range->sticky : nullptr, S, Sp, d.NH, d.HO,
+                     smscale * 1.4426950408889634f};
         hipLaunchKernelGGL(k_flash_prefill, dim3(Sp / kFQ * d.NH), dim3(256), 0, st, fa);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        // out = heads . o_proj^T in fp16 (heads rounded once, o_proj converted exactly)
+        // out = heads . o_proj^T in fp16 (heads rounded once, o_proj converted exactly), the
+        // two scales undone (or NaN when the range flag of this call is up)
         if (!wo16) return hipErrorInvalidValue;
+        ep.vscale = 1.0f;
+        ep.alpha = 1.0f / (vscale * oscale);
+        ep.nan_flag = flags + 1;
         return gemm<kEpiPlain, true>(st, (const uint16_t *)heads, nullptr, nullptr, d.HO, (const uint16_t *)wo16, d.H,
                                      nullptr, 0, d.HO, out, d.H, S, d.HO, ep);
     }

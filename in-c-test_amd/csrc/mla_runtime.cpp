@@ -131,8 +131,10 @@ struct WeightEntry {
     size_t bytes = 0;
     uint64_t digest = 0;
     void *dev = nullptr;
-    void *dev16 = nullptr;  // fp16 copy (prefill o_proj), valid when f16_ok
+    void *dev16 = nullptr;  // fp16 copy (prefill o_proj) times 2^f16_shift, valid when f16_ok
     bool f16_ok = false;
+    int f16_shift = 0;
+    float row_l2max = -1.0f;  // kv_b: max L2 norm of the V rows (prefill V scale); < 0: not yet
     void *devt = nullptr;   // W_UK^T of a kv_b array (decode query preparation), valid when t_ok
     bool t_ok = false;
     int pins = 0;
@@ -162,6 +164,7 @@ struct Ctx {
     std::unordered_map<const void *, Mirror> mirrors;
     std::unordered_map<uint64_t, RopeTable> ropes;  // key: theta bits << 16 | DR
     DevBuf work, part, scores, prefill, fill, fillx, layer, sink;
+    DevBuf rflag;  // int: raised by a stream-ordered prefill outside the MFMA route's range
     PinBuf pin_in, pin_out;
     bool capturing = false;
     // bumped by every release of library-owned device memory: a graph captured before a bump
@@ -345,6 +348,7 @@ int dev_weight(const uint16_t *host, size_t elems, const uint16_t **out) {
     e.bytes = bytes;
     e.f16_ok = false;
     e.t_ok = false;
+    e.row_l2max = -1.0f;
     // The blocking copy runs on the null stream, which does not wait for the library's
     // non-blocking stream: when it overwrites a buffer that queued kernels may still read (an
     // unbound array rewritten in place and used again by a stream-ordered device call), finish
@@ -357,8 +361,19 @@ int dev_weight(const uint16_t *host, size_t elems, const uint16_t **out) {
     return 0;
 }
 
-// fp16 copy of a weight array (converted on the device from its bf16 copy, stream-ordered).
-int dev_weight_f16(const uint16_t *host, size_t elems, const _Float16 **out) {
+float bf16_abs(uint16_t b) {
+    const uint32_t u = (uint32_t)(b & 0x7fff) << 16;
+    float f;
+    memcpy(&f, &u, sizeof f);
+    return f;
+}
+
+// fp16 copy of a weight array times 2^shift (converted on the device from its bf16 copy,
+// stream-ordered). shift puts the largest |w| in [2^13, 2^14): far from the fp16 maximum
+// (65504) and with the array's small values above the fp16 subnormals as far as the bf16
+// values allow; a power of two, so the conversion stays exact and the product's scale is
+// undone exactly.
+int dev_weight_f16(const uint16_t *host, size_t elems, const _Float16 **out, int *shift) {
     Ctx &c = ctx();
     const uint16_t *d16;
     if (dev_weight(host, elems, &d16) != 0) return -1;
@@ -368,12 +383,53 @@ int dev_weight_f16(const uint16_t *host, size_t elems, const _Float16 **out) {
             set_err("fp16 weight conversion during graph capture");
             return -1;
         }
+        float mx = 0.f;
+        for (size_t i = 0; i < elems; ++i) mx = std::max(mx, bf16_abs(host[i]));
+        int ex = 0;
+        e.f16_shift = 0;
+        if (mx > 0.f && std::isfinite(mx)) {
+            (void)frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
+            e.f16_shift = std::min(100, std::max(-100, 14 - ex));
+        }
         if (!e.dev16) HIP_TRY(hipMalloc(&e.dev16, e.bytes));
-        HIP_TRY(launch_bf16_to_f16(c.stream, (_Float16 *)e.dev16, d16, elems));
+        HIP_TRY(launch_bf16_to_f16(c.stream, (_Float16 *)e.dev16, d16, elems, ldexpf(1.0f, e.f16_shift)));
         e.f16_ok = true;
     }
     *out = (const _Float16 *)e.dev16;
+    *shift = e.f16_shift;
     return 0;
+}
+
+// Power-of-two scale for the prefill's V (and attention output) in fp16: from the bound
+// |v| = |kv_b_row . latent| <= ||kv_b_row||_2 ||latent||_2 with ||latent||_2 <= sqrt(R)
+// max|kv_a_norm| (an RMSNorm output has ||x / rms(x)||_2 <= sqrt(R)), the scale puts the
+// bound below 2^14 (the fp16 maximum is 65504).
+float prefill_vscale(const KvlMlaBF16 *w, const Dims &d) {
+    Ctx &c = ctx();
+    auto it = c.weights.find(w->kv_b_proj);
+    if (it == c.weights.end()) return 1.0f;
+    WeightEntry &e = it->second;
+    if (e.row_l2max < 0.f) {
+        double mx = 0.0;
+        for (int h = 0; h < d.NH; ++h)
+            for (int r = 0; r < d.DV; ++r) {
+                const uint16_t *row = w->kv_b_proj + ((size_t)h * (d.DN + d.DV) + d.DN + r) * d.R;
+                double ss = 0.0;
+                for (int k = 0; k < d.R; ++k) {
+                    const double v = bf16_abs(row[k]);
+                    ss += v * v;
+                }
+                mx = std::max(mx, sqrt(ss));
+            }
+        e.row_l2max = (float)mx;
+    }
+    float nmax = 0.f;
+    for (int k = 0; k < d.R; ++k) nmax = std::max(nmax, bf16_abs(w->kv_a_norm[k]));
+    const double bound = 1.001 * sqrt((double)d.R) * (double)nmax * (double)e.row_l2max;
+    if (!(bound > 0.0) || !std::isfinite(bound)) return 1.0f;
+    int ex = 0;
+    (void)frexp(bound, &ex);  // bound < 2^ex
+    return ldexpf(1.0f, std::min(100, std::max(-100, 14 - ex)));
 }
 
 // W_UK^T of a kv_b array in MFMA fragment order (transposed on the device from its bf16 copy,
@@ -1429,8 +1485,10 @@ int state_prefill(const float *x, int seq_len, const KvlMlaConfig *cfg, const Kv
 }
 
 // Causal prefill (src/mla_prefill_streaming.c:78-206). d_x/d_out device buffers.
+// host_call: the caller checks the call's range flag itself (host-buffer entry points), else
+// the library's sticky flag is raised too. generic: the generic route whatever the dims.
 int prefill_device(float *d_out, const float *d_x, int S, const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
-                   PrefillKva *kva = nullptr) {
+                   PrefillKva *kva = nullptr, bool host_call = false, bool generic = false) {
     Dims d;
     if (!d_out || !d_x || S <= 0 || !weights_ok(w) || !dims_of(cfg, d)) {
         set_err("invalid arguments");
@@ -1442,7 +1500,7 @@ int prefill_device(float *d_out, const float *d_x, int S, const KvlMlaConfig *cf
     if (dev_weights(w, d, dw) != 0) return -1;
     const float2 *cs = nullptr;
     if (rope_table(cfg->rope_theta, d.DR, S, &cs) != 0) return -1;
-    const size_t bytes = prefill_bytes(d, S);
+    const size_t bytes = prefill_bytes(d, S, generic);
     if (c.scores.bytes < bytes) {
         if (c.capturing) {
             set_err("prefill workspace growth during graph capture");
@@ -1451,9 +1509,43 @@ int prefill_device(float *d_out, const float *d_x, int S, const KvlMlaConfig *cf
         if (dev_reserve(c.scores, bytes) != 0) return -1;
     }
     const _Float16 *wo16 = nullptr;
-    if (prefill_mfma_shape(d) && dev_weight_f16(w->o_proj, (size_t)d.H * d.HO, &wo16) != 0) return -1;
+    PrefillRange range;
+    range.generic = generic;
+    if (prefill_mfma_shape(d) && !generic) {
+        int shift = 0;
+        if (dev_weight_f16(w->o_proj, (size_t)d.H * d.HO, &wo16, &shift) != 0) return -1;
+        range.oscale = ldexpf(1.0f, shift);
+        range.vscale = prefill_vscale(w, d);
+        if (!host_call) {
+            if (!c.rflag.p) {
+                if (c.capturing) {
+                    set_err("prefill flag allocation during graph capture (run one prefill first)");
+                    return -1;
+                }
+                if (dev_reserve(c.rflag, 256) != 0) return -1;
+                HIP_TRY(hipMemsetAsync(c.rflag.p, 0, 256, c.stream));
+            }
+            range.sticky = (int *)c.rflag.p;
+        }
+    }
     HIP_TRY(launch_prefill_all(c.stream, d, S, cfg->rms_eps, d_x, d_out, dw.q, dw.kva, dw.norm, dw.kvb,
-                               dw.o, wo16, cs, c.scores.p, kva));
+                               dw.o, wo16, cs, c.scores.p, kva, &range));
+    return 0;
+}
+
+// After a host-buffer prefill has run on the MFMA route (stream synchronised): when a query row
+// fell outside that route's range (the call's flag), the attention output is computed again on
+// the generic route (fp32 operands, double score dots) into d_out. The state rows of a prefill
+// with state fill do not depend on the attention and stay.
+int prefill_range_fallback(float *d_out, const float *d_x, int S, const KvlMlaConfig *cfg, const KvlMlaBF16 *w) {
+    Ctx &c = ctx();
+    Dims d;
+    if (!dims_of(cfg, d) || !prefill_mfma_shape(d)) return 0;
+    int flag = 0;
+    HIP_TRY(hipMemcpy(&flag, prefill_range_flag(c.scores.p), sizeof flag, hipMemcpyDeviceToHost));
+    if (!flag) return 0;
+    if (prefill_device(d_out, d_x, S, cfg, w, nullptr, true, true) != 0) return -1;
+    HIP_TRY(hipStreamSynchronize(c.stream));
     return 0;
 }
 
@@ -1464,7 +1556,7 @@ int prefill_device(float *d_out, const float *d_x, int S, const KvlMlaConfig *cf
 // d_x. Device x and out; host_rows as in fill_rows.
 template <class S>
 int prefill_state_device(float *d_out, const float *d_x, int seq_len, const KvlMlaConfig *cfg,
-                         const KvlMlaBF16 *w, S *s, bool host_rows) {
+                         const KvlMlaBF16 *w, S *s, bool host_rows, bool host_call = false) {
     FillCtx f;
     if (!d_out || !d_x) {
         set_err("invalid arguments");
@@ -1476,7 +1568,7 @@ int prefill_state_device(float *d_out, const float *d_x, int seq_len, const KvlM
     }
     if (fill_begin(seq_len, cfg, w, s, f) != 0) return -1;
     PrefillKva kv{};
-    if (prefill_device(d_out, d_x, seq_len, cfg, w, &kv) != 0) return -1;
+    if (prefill_device(d_out, d_x, seq_len, cfg, w, &kv, host_call) != 0) return -1;
     if (kv.y) {
         if (fill_rows(s, f, kv.y, kv.ldy, kv.np, kv.pstride, 0, seq_len, host_rows) != 0) return -1;
     } else {
@@ -1508,7 +1600,10 @@ int prefill_state(float *out, const float *x, int seq_len, const KvlMlaConfig *c
     float *dx = (float *)c.prefill.p;
     float *dout = (float *)((char *)c.prefill.p + io_al);
     HIP_TRY(hipMemcpyAsync(dx, x, io, hipMemcpyHostToDevice, c.stream));
-    if (prefill_state_device(dout, dx, seq_len, cfg, w, s, true) != 0) return -1;
+    if (prefill_state_device(dout, dx, seq_len, cfg, w, s, true, true) != 0) return -1;
+    HIP_TRY(hipStreamSynchronize(c.stream));
+    // the state rows do not depend on the attention; only the output is computed again
+    if (prefill_range_fallback(dout, dx, seq_len, cfg, w) != 0) return -1;
     HIP_TRY(hipMemcpyAsync(out, dout, io, hipMemcpyDeviceToHost, c.stream));
     HIP_TRY(hipStreamSynchronize(c.stream));
     return 0;
@@ -1610,7 +1705,9 @@ int kvl_mla_prefill_bf16(float *out, const float *x, int seq_len, const KvlMlaCo
     float *dx = (float *)c.prefill.p;
     float *dout = (float *)((char *)c.prefill.p + ((io + 255) & ~(size_t)255));
     HIP_TRY(hipMemcpyAsync(dx, x, io, hipMemcpyHostToDevice, c.stream));
-    if (prefill_device(dout, dx, seq_len, cfg, w) != 0) return -1;
+    if (prefill_device(dout, dx, seq_len, cfg, w, nullptr, true) != 0) return -1;
+    HIP_TRY(hipStreamSynchronize(c.stream));
+    if (prefill_range_fallback(dout, dx, seq_len, cfg, w) != 0) return -1;
     HIP_TRY(hipMemcpyAsync(out, dout, io, hipMemcpyDeviceToHost, c.stream));
     HIP_TRY(hipStreamSynchronize(c.stream));
     return 0;
@@ -2111,6 +2208,26 @@ int kvl_mla_synchronize(void) {
     if (ensure_ready() != 0) return -1;
     HIP_TRY(hipStreamSynchronize(ctx().stream));
     return 0;
+}
+
+int kvl_mla_prefill_range_status(void) {
+    Guard guard;
+    if (ensure_ready() != 0) return -1;
+    Ctx &c = ctx();
+    if (c.capturing) {
+        set_err("range status during graph capture");
+        return -1;
+    }
+    HIP_TRY(hipStreamSynchronize(c.stream));
+    if (!c.rflag.p) return 0;
+    int flag = 0;
+    HIP_TRY(hipMemcpy(&flag, c.rflag.p, sizeof flag, hipMemcpyDeviceToHost));
+    if (flag) {
+        HIP_TRY(hipMemset(c.rflag.p, 0, sizeof flag));
+        set_err("a stream-ordered prefill met query rows outside the MFMA route's range (row max logit beyond "
+                "512 or non-finite operands); its output was written as NaN");
+    }
+    return flag ? 1 : 0;
 }
 
 void *kvl_mla_device_alloc(size_t bytes) {

@@ -41,6 +41,7 @@ EXT_API = {
     "mla_attention_layer_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, abi.CFG, abi.W, abi.u16p,
                                               abi.u16p, CSP, C.c_uint]),
     "mla_prefill_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, abi.CFG, abi.W]),
+    "mla_prefill_range_status": (C.c_int, []),
     "mla_prefill_compressed_state_bf16": (C.c_int, [abi.f32p, abi.f32p, C.c_int, abi.CFG, abi.W, abi.CS]),
     "mla_prefill_compressed_q8_state_bf16": (C.c_int, [abi.f32p, abi.f32p, C.c_int, abi.CFG, abi.W, abi.QS]),
     "mla_prefill_compressed_state_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, abi.CFG, abi.W,

@@ -177,9 +177,23 @@ int kvl_mla_attention_layer_bf16_device(float *d_h, float *d_n2, int batch, cons
                                         KvlMlaCompressedBF16State *const *states, unsigned flags);
 
 /* Stream-ordered causal prefill over device buffers (d_x, d_out [seq_len, hidden] fp32);
- * same arithmetic as kvl_mla_prefill_bf16. */
+ * same arithmetic as kvl_mla_prefill_bf16.
+ * Range: the MFMA route (the Kimi-VL shapes) runs the attention on fp16/bf8 operands. Its
+ * accuracy bound holds while every query row's largest attention logit (scale included) stays
+ * within 512 in magnitude and the operands are finite in fp16. The host-buffer entry points
+ * (kvl_mla_prefill_bf16 and the prefill-with-state-fill calls) check every call and compute
+ * the output of a call outside that range again on the fp32 route, so they always return the
+ * reference's result. A stream-ordered call outside that range writes NaN to d_out and raises
+ * a flag that kvl_mla_prefill_range_status() reports. */
 int kvl_mla_prefill_device(float *d_out, const float *d_x, int seq_len, const KvlMlaConfig *cfg,
                            const KvlMlaBF16 *w);
+
+/* No counterpart in the reference (the C path computes in fp32/double throughout): whether any
+ * stream-ordered prefill (kvl_mla_prefill_device, kvl_mla_prefill_compressed*_state_device)
+ * since the previous call met query rows outside the MFMA route's range (its output is then
+ * NaN). Synchronises the library stream; returns 0 (none), 1 (at least one; the flag is then
+ * cleared and kvl_mla_last_error() says why) or -1. */
+int kvl_mla_prefill_range_status(void);
 
 /* Prefill with the state fill of the same tokens, as src/generate.c:208-210 sequences them
  * (kvl_mla_prefill_bf16(out, x, ...), then kvl_mla_compressed[_q8]_state_prefill_bf16(x, ...)),

@@ -48,16 +48,70 @@ def test_prefill_kimi_shapes(S, bf16_x):
     assert rel_err(a, b) <= TOL, rel_err(a, b)
 
 
-@pytest.mark.parametrize("q_std", [0.08, 0.16])
+@pytest.mark.parametrize("q_std", [0.08, 0.16, 0.24, 0.32, 0.48])
 def test_prefill_sharp_attention(q_std):
-    """Large attention logits (q_proj std 4x / 8x the other weights: logit std ~2.3 / ~4.7,
-    max ~12 / ~25): the score operands' rounding is amplified by the logit size, so this
-    pins the precision of the QK product (a single bf16 rounding of K alone gives ~2e-3 /
-    ~4e-3 here)."""
+    """Large attention logits (q_proj std 4x .. 24x the other weights: logit std ~2.3 .. ~14,
+    row-max logits up to ~60): the score operands' rounding is amplified by the logit size, so
+    this pins the precision of the QK product (a single bf16 rounding of K alone gives ~2e-3 /
+    ~4e-3 at the first two)."""
     print(f"[prefill] kimi sharp q_std={q_std}", flush=True)
     a, b = run(inputs.KIMI, 256, 0xC7, 0.02, True, q_std=q_std)
     assert np.all(np.isfinite(a))
     assert rel_err(a, b) <= TOL, rel_err(a, b)
+
+
+def scaled_layer(cfg, seed, kvb=1.0, o=1.0):
+    layer = inputs.make_layer(cfg, seed)
+    for name, f in (("kv_b_proj", kvb), ("o_proj", o)):
+        if f != 1.0:
+            arr = getattr(layer, name)
+            arr[...] = inputs.f32_to_bf16_bits(inputs.bf16_bits_to_f32(arr) * np.float32(f))
+    return layer
+
+
+@pytest.mark.parametrize("kvb,o,flagged", [(1e5, 1.0, True), (3000.0, 1.0, True), (1.0, 1e-4, False),
+                                           (1.0, 3e6, False), (1e-4, 1.0, False)],
+                         ids=["kv_b_x1e5", "kv_b_x3000", "o_proj_x1e-4", "o_proj_x3e6", "kv_b_x1e-4"])
+def test_prefill_operand_range(kvb, o, flagged):
+    """Operands beyond what the MFMA route's 16-bit attention operands hold.
+    kv_b x 1e5: |K|, |V| ~ 2e5, beyond fp16 (65504); kv_b x 3000: finite, but row-max logits
+    ~4400, beyond the 512 up to which the bf8 score correction keeps the 2e-3 budget (there
+    it gives ~2.3e-3). Both are detected on the device: the host-buffer call computes them again
+    on the fp32 route and matches the oracle; the stream-ordered call writes NaN and
+    kvl_mla_prefill_range_status() reports it once. o_proj x 1e-4 / x 3e6 (fp16 subnormals /
+    beyond the fp16 range) and kv_b x 1e-4 (V of ~2e-4) are handled by the power-of-two scales
+    of the fp16 o_proj copy and of V: no flag, results within the budget."""
+    cfg = inputs.config(**inputs.KIMI)
+    S = 256
+    layer = scaled_layer(cfg, 0xE1, kvb=kvb, o=o)
+    w = layer.struct()
+    x = inputs.hidden(cfg, 0xE1, S, bf16_exact=True)
+    print(f"[prefill] operand range kv_b x{kvb} o_proj x{o}", flush=True)
+    assert L.kvl_mla_prefill_range_status() == 0  # nothing pending from earlier tests
+    a = np.zeros((S, cfg.hidden_size), np.float32)
+    b = np.zeros_like(a)
+    lib.check(L.kvl_mla_prefill_bf16(f32(a), f32(x), S, C.byref(cfg), C.byref(w)), "prefill")
+    assert ORC.orc_mla_prefill_streaming(f32(b), f32(x), S, C.byref(cfg), C.byref(w)) == 0
+    e = rel_err(a, b)
+    print(f"[prefill]   host call max|d|/max|ref| = {e:.3e}", flush=True)
+    assert np.all(np.isfinite(a)) and e <= TOL, e
+    assert L.kvl_mla_prefill_range_status() == 0  # the host call handled its own flag
+    dx = L.kvl_mla_device_alloc(x.nbytes)
+    do = L.kvl_mla_device_alloc(x.nbytes)
+    lib.check(L.kvl_mla_copy_to_device(dx, x.ctypes.data, x.nbytes), "h2d")
+    lib.check(L.kvl_mla_prefill_device(do, dx, S, C.byref(cfg), C.byref(w)), "device prefill")
+    got = np.zeros_like(a)
+    lib.check(L.kvl_mla_copy_to_host(got.ctypes.data, do, x.nbytes), "d2h")
+    if flagged:
+        assert np.all(np.isnan(got))
+        assert L.kvl_mla_prefill_range_status() == 1
+        assert "range" in lib.last_error()
+        assert L.kvl_mla_prefill_range_status() == 0
+    else:
+        assert L.kvl_mla_prefill_range_status() == 0
+        np.testing.assert_array_equal(got, a)
+    L.kvl_mla_device_free(dx)
+    L.kvl_mla_device_free(do)
 
 
 def test_prefill_4096_vs_oracle_every_query_tile():
