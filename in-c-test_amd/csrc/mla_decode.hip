@@ -1252,143 +1252,6 @@ __global__ __launch_bounds__(256) void k_attn_generic(AttnArgs a) {
     }
 }
 
-// ---- fp32 MFMA path (FP32 history, NH=16, R=512, DR=64) -------------------------------
-// Chunks of 16 rows are staged in LDS. Scores: M = 16 heads, N = 16 rows, K = 576 split
-// in four wave-quarters (v_mfma_f32_16x16x4f32, exact fp32 products) and summed through
-// LDS. Softmax statistics are kept per head in every wave (online rescaling). Mix: each
-// wave owns 128 latent columns, M = heads, N = 16 columns, K = 4 rows per instruction.
-constexpr int kF32Ch = 16;
-constexpr int kF32Rs = 576;  // LDS row stride (floats)
-// Column XOR of LDS row r (multiples of 4, so 16-byte groups stay whole): the score reads (rows
-// 0..7 of one group per 8 lanes) and the mix reads (rows 4k + g and 4k + g + 1, 16 columns each,
-// per 32 lanes) fall in distinct banks.
-__device__ __forceinline__ int f32_swz(int r) { return (4 * (r & 7)) ^ (16 * (r & 1)); }
-
-// ONCE: the history rows are read by one workgroup each (not a block launch): non-temporal
-// loads. A block launch's members read the same rows (cached loads).
-template <bool ONCE>
-__global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) float rows[kF32Ch * kF32Rs];
-    __shared__ float sp[4][16][16];
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
-    int b, split, pidx;
-    if (!split_of(a, b, split, pidx)) return;
-    const SeqDesc &s = a.t.s[b];
-    const int r0 = split * s.rps;
-    const int r1 = split == s.nsplit - 1 ? s.len : r0 + s.rps;  // last split takes the rest
-    const float *glat = (const float *)s.a;
-    const float *grope = (const float *)s.b;
-    constexpr bool once = ONCE;
-
-    float qa[36];
-    {
-        const float *qrow = a.qf + ((size_t)b * 16 + n) * 576 + 144 * w + 36 * g;
-#pragma unroll
-        for (int t = 0; t < 36; t += 4) {
-            const v4f v = *(const v4f *)(qrow + t);
-            qa[t] = v.x;
-            qa[t + 1] = v.y;
-            qa[t + 2] = v.z;
-            qa[t + 3] = v.w;
-        }
-    }
-    float m_run = -INFINITY, l_run = 0.f;
-    v4f acc[8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
-
-    v4f pl[8], pr;
-    auto prefetch = [&](int c) {
-        const int base = r0 + c * kF32Ch;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int p = tid + 256 * k, row = p >> 7, c4 = p & 127, gr = base + row;
-            // rows read once: non-temporal loads (a block launch's members share them: cached)
-            const v4f *src = (const v4f *)(glat + (size_t)gr * 512 + 4 * c4);
-            pl[k] = gr < r1 ? (once ? __builtin_nontemporal_load(src) : *src) : v4f{0.f, 0.f, 0.f, 0.f};
-        }
-        const int row = tid >> 4, c4 = tid & 15, gr = base + row;
-        const v4f *src = (const v4f *)(grope + (size_t)gr * 64 + 4 * c4);
-        pr = gr < r1 ? (once ? __builtin_nontemporal_load(src) : *src) : v4f{0.f, 0.f, 0.f, 0.f};
-    };
-    auto stash = [&]() {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int p = tid + 256 * k, row = p >> 7, c4 = p & 127;
-            *(v4f *)(rows + row * kF32Rs + ((4 * c4) ^ f32_swz(row))) = pl[k];
-        }
-        const int row = tid >> 4, c4 = tid & 15;
-        *(v4f *)(rows + row * kF32Rs + ((512 + 4 * c4) ^ f32_swz(row))) = pr;
-    };
-
-    const int nch = (r1 - r0 + kF32Ch - 1) / kF32Ch;
-    prefetch(0);
-    for (int c = 0; c < nch; ++c) {
-        __syncthreads();
-        stash();
-        __syncthreads();
-        if (c + 1 < nch) prefetch(c + 1);
-        const int base = r0 + c * kF32Ch;
-        v4f dp = {0.f, 0.f, 0.f, 0.f};
-        const float *brow = rows + n * kF32Rs;
-        const int nsw = f32_swz(n);
-#pragma unroll
-        for (int t = 0; t < 36; t += 4) {
-            const v4f bv = *(const v4f *)(brow + ((144 * w + 36 * g + t) ^ nsw));
-            dp = mfma_f32(qa[t], bv.x, dp);
-            dp = mfma_f32(qa[t + 1], bv.y, dp);
-            dp = mfma_f32(qa[t + 2], bv.z, dp);
-            dp = mfma_f32(qa[t + 3], bv.w, dp);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sp[w][4 * g + i][n] = dp[i];
-        __syncthreads();
-        float sc[4];
-        float cmax = -INFINITY;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int row = 4 * k + g;
-            const float v = ((sp[0][n][row] + sp[1][n][row]) + sp[2][n][row]) + sp[3][n][row];
-            sc[k] = base + row < r1 ? v * a.smscale : -INFINITY;
-            cmax = fmaxf(cmax, sc[k]);
-        }
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
-        const float mnew = fmaxf(m_run, cmax);
-        const float alpha = __expf(m_run - mnew);
-        float pr4[4], psum = 0.f;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            pr4[k] = __expf(sc[k] - mnew);
-            psum += pr4[k];
-        }
-        psum += __shfl_xor(psum, 16);
-        psum += __shfl_xor(psum, 32);
-        l_run = fmaf(l_run, alpha, psum);
-        m_run = mnew;
-        float ad[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ad[i] = __shfl(alpha, 4 * g + i);
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[t][i] *= ad[i];
-            const int col = 128 * w + 16 * t + n;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) acc[t] = mfma_f32(pr4[k], rows[(4 * k + g) * kF32Rs + (col ^ f32_swz(4 * k + g))], acc[t]);
-        }
-    }
-    float *P = a.part + (size_t)pidx * 16 * 514;
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) P[(4 * g + i) * 512 + 128 * w + 16 * t + n] = acc[t][i];
-    if (w == 0 && g == 0) {
-        P[8192 + n] = m_run;
-        P[8192 + 16 + n] = l_run;
-    }
-}
-
 // s_waitcnt vmcnt(n) for the counts the DMA pipelines of the attention kernels use (n
 // wave-uniform; any other n waits for everything).
 __device__ __forceinline__ void wait_vm(int n) {
@@ -1462,7 +1325,7 @@ __device__ __forceinline__ v4s lds_read_tr16(const uint8_t *p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s *)(p));
 }
 
-template <bool ONCE>  // as for k_attn_f32_mfma
+template <bool ONCE>  // ONCE: each history row is read by one workgroup (non-temporal loads)
 __global__ __launch_bounds__(256) void k_attn_bf16_mfma(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t smem[kB16SmemB];
     const int tid = threadIdx.x, l = tid & 63, n = l & 15, g = l >> 4;
@@ -1620,6 +1483,220 @@ __global__ __launch_bounds__(256) void k_attn_bf16_mfma(AttnArgs a) {
     }
 }
 
+// ---- FP32 history on bf16 MFMA (NH=16, R=512, DR=64) ----------------------------------
+// The BF16 kernel's pipeline over FP32 rows: a chunk is 16 rows (36 KB: 32 KB of latents, 4 KB
+// of RoPE keys, the size of a BF16 chunk), streamed by DMA into the same ring of four LDS slots.
+// Each fp32 row becomes two bf16 "virtual rows", hi = bf16(x) and lo = bf16(x - hi) (x - hi is
+// exact, |x - hi - lo| <= 2^-18 |x|): virtual rows 0-15 are the hi parts of rows 0-15, 16-31 their
+// lo parts, laid out as a 32-row BF16 chunk. Wave w loads rows 4w .. 4w+3 so that their fp32
+// bytes land exactly where their virtual rows go (latent columns 0-255 of row r in virtual row
+// r's kilobyte, 256-511 in virtual row 16 + r's; the four RoPE rows in the wave's quarter of the
+// RoPE area) and converts them in place once its own DMA has landed, before the step barrier:
+// no extra barrier, no extra LDS. The BF16 kernel's score, softmax and mix then run on the 32
+// virtual rows: a row's score is the sum of its two virtual rows' scores (q hi + lo against
+// row hi + lo: all four products), and both virtual rows of a row carry its weight p (hi + lo),
+// so the mix adds p (hi + lo) of the row. Per history byte this is the BF16 kernel's MFMA work.
+// RoPE quarter of wave w (1 KB at kB16LatB + w * 1024): local virtual row k = 0..3 the hi parts,
+// 4..7 the lo parts of rows 4w + (k & 3), 128 bytes each, 16-byte slot s at s ^ f32r_swz(row)
+// (row = the row in the chunk) so that the score reads of 8 rows fall in distinct banks.
+constexpr int kF32Ch = 16;
+typedef int v2i __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ int f32r_swz(int row) { return (row >> 1) & 7; }
+
+template <bool ONCE>  // ONCE: each history row is read by one workgroup (non-temporal loads)
+__global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[kB16SmemB];
+    const int tid = threadIdx.x, l = tid & 63, n = l & 15, g = l >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int b, split, pidx;
+    if (!split_of(a, b, split, pidx)) return;
+    const SeqDesc &s = a.t.s[b];
+    const int r0 = split * s.rps;
+    const int r1 = split == s.nsplit - 1 ? s.len : r0 + s.rps;  // last split takes the rest
+    const int nch = (r1 - r0 + kF32Ch - 1) / kF32Ch;
+    const float *glat = (const float *)s.a;
+    const float *grope = (const float *)s.b;
+    constexpr bool once = ONCE;
+    const uint32_t sbase = lds_addr(smem);
+    float *sp = (float *)(smem + kB16SpOff);
+    const int rb = w & 1, kh = w >> 1;
+
+    // DMA per chunk and wave: rows 4w .. 4w+3, two 1 KB instructions per row (latent columns
+    // 0-255 -> virtual row r, 256-511 -> virtual row 16 + r), one for the four RoPE rows (lane i:
+    // row 4w + (i >> 4), columns 4 (i & 15) .. +3). Rows past the split end (last chunk only)
+    // re-read the split's last row (in bounds); their scores are masked.
+    auto issue = [&](int c) __attribute__((always_inline)) {
+        const uint32_t buf = sbase + (uint32_t)((c % kB16Ring) * kB16Slot);
+        const int rbase = r0 + c * kF32Ch;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 4 * w + i;
+            const int gr = min(rbase + row, r1 - 1);
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+                dma_hist_b128(glat + (size_t)gr * 512 + 256 * hf + 4 * l, buf + (uint32_t)((16 * hf + row) * 1024),
+                              once);
+        }
+        const int row = 4 * w + (l >> 4);
+        const int gr = min(rbase + row, r1 - 1);
+        dma_hist_b128(grope + (size_t)gr * 64 + 4 * (l & 15), buf + (uint32_t)(kB16LatB + w * 1024), once);
+    };
+    // In-place conversion of this wave's rows of chunk c (its DMA has landed): every lane reads
+    // its fp32 values first, then writes the hi and lo words (the wave's bytes only).
+    auto convert = [&](int c) __attribute__((always_inline)) {
+        uint8_t *buf = smem + (c % kB16Ring) * kB16Slot;
+        v4f x[4][2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 4 * w + i;  // columns 8l .. 8l+7: lanes 0-31 in row's kilobyte, 32-63 in 16 + row's
+            const uint8_t *src = buf + (l < 32 ? row * 1024 + 32 * l : (16 + row) * 1024 + 32 * (l - 32));
+            x[i][0] = *(const v4f *)src;
+            x[i][1] = *(const v4f *)(src + 16);
+        }
+        uint8_t *rq = buf + kB16LatB + w * 1024;
+        const v4f xr = *(const v4f *)(rq + 16 * l);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 4 * w + i;
+            v8bf hi, lo;
+            split8_cvt(x[i][0], x[i][1], hi, lo);
+            const int slot = 16 * (l ^ b16_swz(row));
+            *(v8bf *)(buf + row * 1024 + slot) = hi;
+            *(v8bf *)(buf + (16 + row) * 1024 + slot) = lo;
+        }
+        {
+            const int k = l >> 4, row = 4 * w + k;
+            v8bf hi, lo;
+            split8_cvt(xr, v4f{0.f, 0.f, 0.f, 0.f}, hi, lo);
+            const int o = 16 * (((l & 15) >> 1) ^ f32r_swz(row)) + 8 * (l & 1);
+            const v4i hv = __builtin_bit_cast(v4i, hi), lv = __builtin_bit_cast(v4i, lo);
+            *(v2i *)(rq + k * 128 + o) = v2i{hv.x, hv.y};
+            *(v2i *)(rq + (4 + k) * 128 + o) = v2i{lv.x, lv.y};
+        }
+    };
+
+    // query operands (A of the score MFMAs: head n, k = 32 kb + 8g .. +7), as the BF16 kernel
+    v8bf qh[9], ql[9];
+    issue(0);
+    {
+        const float *qrow = a.qf + ((size_t)b * 16 + n) * 576 + 8 * g + 32 * 9 * kh;
+        v4f qv[18];
+#pragma unroll
+        for (int j = 0; j < 9; ++j) {
+            qv[2 * j] = *(const v4f *)(qrow + 32 * j);
+            qv[2 * j + 1] = *(const v4f *)(qrow + 32 * j + 4);
+        }
+#pragma unroll
+        for (int j = 0; j < 9; ++j) {
+            split8_cvt(qv[2 * j] * a.smscale, qv[2 * j + 1] * a.smscale, qh[j], ql[j]);
+            asm volatile("" ::"v"(qh[j]), "v"(ql[j]));  // before chunks 1 and 2 are issued
+        }
+    }
+    if (nch > 1) issue(1);
+    if (nch > 2) issue(2);
+
+    // score operand offsets: virtual row srow = 16 rb + n (row n's hi part for rb = 0, lo for 1)
+    const int srow = 16 * rb + n;
+    int bofs[9];
+#pragma unroll
+    for (int j = 0; j < 9; ++j) {
+        const int kb = 9 * kh + j;
+        bofs[j] = kb < 16 ? srow * 1024 + 16 * ((4 * kb + g) ^ b16_swz(srow))
+                          : kB16LatB + (n >> 2) * 1024 + ((n & 3) + 4 * rb) * 128 +
+                                16 * ((4 * (kb - 16) + g) ^ f32r_swz(n));
+    }
+    // transposed reads of column block 8w + t over the 32 virtual rows (as the BF16 kernel)
+    int tro[2][8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int row = 8 * g + 4 * h + (n >> 2);
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+            tro[h][t] = row * 1024 + 16 * ((2 * (8 * w + t) + ((n >> 1) & 1)) ^ b16_swz(row)) + 8 * (n & 1);
+    }
+
+    float m_run = -INFINITY, l_run = 0.f;  // head n
+    v4f acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+    const int rg = 8 * (g & 1);  // the rows whose softmax weights lane group g holds
+    for (int k = 0; k < nch; ++k) {
+        // this wave's DMA of chunk k has landed (chunks k+1, k+2 may stay in flight)
+        wait_vm(k + 2 < nch ? 18 : (k + 1 < nch ? 9 : 0));
+        convert(k);
+        lds_barrier();  // chunk k converted; every wave is done with chunk k-1's slot and the scores
+        if (k + 3 < nch) issue(k + 3);
+        const uint8_t *buf = smem + (k % kB16Ring) * kB16Slot;
+        v4f dp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 9; ++j) {
+            const v8bf bv = *(const v8bf *)(buf + bofs[j]);
+            dp = mfma_bf16(qh[j], bv, dp);
+            dp = mfma_bf16(ql[j], bv, dp);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sp[(kh * 16 + 4 * g + i) * kB16SpHs + srow] = dp[i];
+        lds_barrier();  // both k-halves of every virtual row's score are in LDS
+        // row rg + e: (hi, first k-half + second) + (lo, first + second)
+        const float *s0 = sp + n * kB16SpHs + rg, *s1 = sp + (16 + n) * kB16SpHs + rg;
+        const v4f a0 = *(const v4f *)s0, a1 = *(const v4f *)(s0 + 4);
+        const v4f c0 = *(const v4f *)s1, c1 = *(const v4f *)(s1 + 4);
+        const v4f a2 = *(const v4f *)(s0 + 16), a3 = *(const v4f *)(s0 + 20);
+        const v4f c2 = *(const v4f *)(s1 + 16), c3 = *(const v4f *)(s1 + 20);
+        const int nv = r1 - (r0 + k * kF32Ch);  // valid rows of the chunk (>= 1)
+        float sc[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            sc[e] = rg + e < nv ? (a0[e] + c0[e]) + (a2[e] + c2[e]) : -INFINITY;
+            sc[e + 4] = rg + e + 4 < nv ? (a1[e] + c1[e]) + (a3[e] + c3[e]) : -INFINITY;
+        }
+        const float cmax = xgroup_max(
+            fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7]))));
+        // lazy reference max, as the BF16 kernel (all four waves hold the same statistics)
+        const bool mv = cmax > m_run + kB16LnPmax;
+        if (__any(mv)) {
+            const float mnew = mv ? cmax : m_run;
+            const float alpha = mv ? __expf(m_run - mnew) : 1.0f;
+            m_run = mnew;
+            l_run *= alpha;
+            float ad[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ad[i] = __shfl(alpha, 4 * g + i);
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[t][i] *= ad[i];
+        }
+        float p[8], psum = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            p[e] = __expf(sc[e] - m_run);
+            psum += p[e];
+        }
+        // lane groups g and g ^ 2 hold the same rows (hi and lo virtual rows): count them once
+        l_run += xgroup_sum(g < 2 ? psum : 0.f);
+        v8bf ph, pl;
+        split8_cvt(v4f{p[0], p[1], p[2], p[3]}, v4f{p[4], p[5], p[6], p[7]}, ph, pl);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const v4s lo4 = lds_read_tr16(buf + tro[0][t]);
+            const v4s hi4 = lds_read_tr16(buf + tro[1][t]);
+            const v8bf bt = __builtin_bit_cast(v8bf, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+            acc[t] = mfma_bf16(ph, bt, acc[t]);
+            acc[t] = mfma_bf16(pl, bt, acc[t]);
+        }
+    }
+    float *P = a.part + (size_t)pidx * 16 * 514;
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) P[(4 * g + i) * 512 + 128 * w + 16 * t + n] = acc[t][i];
+    if (w == 0 && g == 0) {
+        P[8192 + n] = m_run;
+        P[8192 + 16 + n] = l_run;
+    }
+}
+
 // ---- int8 MFMA path (Q8 history, NH=16, R=512, DR=64) ---------------------------------
 // One workgroup of 8 waves (two per SIMD) per CU streams its split-K slice in chunks of 64
 // rows. The waves specialise, and the two roles run one chunk apart:
@@ -1702,7 +1779,6 @@ __device__ __forceinline__ void row16_max4(float &a, float &b, float &c, float &
         : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
 }
 
-typedef int v2i __attribute__((ext_vector_type(2)));
 // ds_read_b64_tr_b8: within each 16-lane group, destination lane j byte i comes from the
 // 8 bytes addressed by source lane 2i + (j >> 3), at byte j & 7.
 __device__ __forceinline__ v2i lds_read_tr8(const uint8_t *p) {
@@ -2081,7 +2157,7 @@ __device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const SeqDesc &sd
     }
 }
 
-template <bool ONCE>  // as for k_attn_f32_mfma
+template <bool ONCE>  // ONCE: each history row is read by one workgroup (non-temporal loads)
 __global__ __launch_bounds__(512) void k_attn_q8_mfma(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t smem[kQ8SmemB];
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);

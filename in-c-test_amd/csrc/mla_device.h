@@ -145,9 +145,6 @@ __device__ __forceinline__ void split8_f16(const float *x, v8h &hi, v8h &lo) {
 __device__ __forceinline__ v4i mfma_i8(const v4i &a, const v4i &b, const v4i &c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ v4f mfma_f32(float a, float b, const v4f &c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
 
 // Reductions over the 16 lanes of each DPP row (lanes 16r .. 16r+15) with DPP moves:
 // quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_ror:4, row_ror:8.
