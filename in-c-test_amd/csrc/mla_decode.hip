@@ -1491,8 +1491,9 @@ __global__ __launch_bounds__(256) void k_attn_bf16_mfma(AttnArgs a) {
 // lo parts, laid out as a 32-row BF16 chunk. Wave w loads rows 4w .. 4w+3 so that their fp32
 // bytes land exactly where their virtual rows go (latent columns 0-255 of row r in virtual row
 // r's kilobyte, 256-511 in virtual row 16 + r's; the four RoPE rows in the wave's quarter of the
-// RoPE area) and converts them in place once its own DMA has landed, before the step barrier:
-// no extra barrier, no extra LDS. The BF16 kernel's score, softmax and mix then run on the 32
+// RoPE area) and converts them in place once its own DMA has landed: chunk k+1 during the mix
+// of chunk k (its VALU work between the mix MFMAs), before the barrier that opens step k+1, so
+// there is no extra barrier and no extra LDS. The BF16 kernel's score, softmax and mix run on the 32
 // virtual rows: a row's score is the sum of its two virtual rows' scores (q hi + lo against
 // row hi + lo: all four products), and both virtual rows of a row carry its weight p (hi + lo),
 // so the mix adds p (hi + lo) of the row. Per history byte this is the BF16 kernel's MFMA work.
@@ -1542,10 +1543,11 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
         dma_hist_b128(grope + (size_t)gr * 64 + 4 * (l & 15), buf + (uint32_t)(kB16LatB + w * 1024), once);
     };
     // In-place conversion of this wave's rows of chunk c (its DMA has landed): every lane reads
-    // its fp32 values first, then writes the hi and lo words (the wave's bytes only).
-    auto convert = [&](int c) __attribute__((always_inline)) {
-        uint8_t *buf = smem + (c % kB16Ring) * kB16Slot;
-        v4f x[4][2];
+    // its fp32 values first (conv_load), then writes the hi and lo words (conv_store; the wave's
+    // bytes only).
+    v4f x[4][2], xr;
+    auto conv_load = [&](int c) __attribute__((always_inline)) {
+        const uint8_t *buf = smem + (c % kB16Ring) * kB16Slot;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = 4 * w + i;  // columns 8l .. 8l+7: lanes 0-31 in row's kilobyte, 32-63 in 16 + row's
@@ -1553,8 +1555,11 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
             x[i][0] = *(const v4f *)src;
             x[i][1] = *(const v4f *)(src + 16);
         }
+        xr = *(const v4f *)(buf + kB16LatB + w * 1024 + 16 * l);
+    };
+    auto conv_store = [&](int c) __attribute__((always_inline)) {
+        uint8_t *buf = smem + (c % kB16Ring) * kB16Slot;
         uint8_t *rq = buf + kB16LatB + w * 1024;
-        const v4f xr = *(const v4f *)(rq + 16 * l);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = 4 * w + i;
@@ -1594,6 +1599,9 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
     }
     if (nch > 1) issue(1);
     if (nch > 2) issue(2);
+    wait_vm(nch > 2 ? 18 : (nch > 1 ? 9 : 0));  // chunk 0 has landed
+    conv_load(0);
+    conv_store(0);
 
     // score operand offsets: virtual row srow = 16 rb + n (row n's hi part for rb = 0, lo for 1)
     const int srow = 16 * rb + n;
@@ -1621,9 +1629,6 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
     for (int t = 0; t < 8; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
     const int rg = 8 * (g & 1);  // the rows whose softmax weights lane group g holds
     for (int k = 0; k < nch; ++k) {
-        // this wave's DMA of chunk k has landed (chunks k+1, k+2 may stay in flight)
-        wait_vm(k + 2 < nch ? 18 : (k + 1 < nch ? 9 : 0));
-        convert(k);
         lds_barrier();  // chunk k converted; every wave is done with chunk k-1's slot and the scores
         if (k + 3 < nch) issue(k + 3);
         const uint8_t *buf = smem + (k % kB16Ring) * kB16Slot;
@@ -1677,14 +1682,31 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
         l_run += xgroup_sum(g < 2 ? psum : 0.f);
         v8bf ph, pl;
         split8_cvt(v4f{p[0], p[1], p[2], p[3]}, v4f{p[4], p[5], p[6], p[7]}, ph, pl);
+        // the mix of chunk k with the conversion of chunk k+1 (this wave's rows, once its DMA has
+        // landed: chunks k+2 and k+3 may stay in flight) between its MFMAs
+        v8bf bt[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             const v4s lo4 = lds_read_tr16(buf + tro[0][t]);
             const v4s hi4 = lds_read_tr16(buf + tro[1][t]);
-            const v8bf bt = __builtin_bit_cast(v8bf, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
-            acc[t] = mfma_bf16(ph, bt, acc[t]);
-            acc[t] = mfma_bf16(pl, bt, acc[t]);
+            bt[t] = __builtin_bit_cast(v8bf, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
         }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            acc[t] = mfma_bf16(ph, bt[t], acc[t]);
+            acc[t] = mfma_bf16(pl, bt[t], acc[t]);
+        }
+        const bool next = k + 1 < nch;
+        if (next) {
+            wait_vm(k + 3 < nch ? 18 : (k + 2 < nch ? 9 : 0));
+            conv_load(k + 1);
+        }
+#pragma unroll
+        for (int t = 4; t < 8; ++t) {
+            acc[t] = mfma_bf16(ph, bt[t], acc[t]);
+            acc[t] = mfma_bf16(pl, bt[t], acc[t]);
+        }
+        if (next) conv_store(k + 1);
     }
     float *P = a.part + (size_t)pidx * 16 * 514;
 #pragma unroll

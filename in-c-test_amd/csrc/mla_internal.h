@@ -140,8 +140,7 @@ hipError_t launch_wuk_transpose(hipStream_t st, uint16_t *dst, const uint16_t *k
 
 // Split-K attention over the history; writes partials (acc | m | l) per split.
 // kind: 0 = generic VALU (any dims, one split per problem), 1 = FP32 rows as bf16 hi + lo on
-// bf16 MFMA (Kimi dims),
-// 2 = int8 MFMA (Kimi dims, Q8 rows), 3 = bf16 MFMA (Kimi dims, BF16 rows).
+// bf16 MFMA (Kimi dims), 2 = int8 MFMA (Kimi dims, Q8 rows), 3 = bf16 MFMA (Kimi dims, BF16 rows).
 enum AttnKind : int { kAttnGeneric = 0, kAttnF32Mfma = 1, kAttnQ8Mfma = 2, kAttnBF16Mfma = 3 };
 // members > 0: the sequences are the members of one block (tokens of one sequence, each with
 // the split plan of its lone decode); the workgroups then go split-major, the members of a split
