@@ -97,6 +97,7 @@ def main():
                     help="also run a plain copy kernel of MIB MiB (memory-counter calibration)")
     ap.add_argument("--no-ragged", action="store_true", help="skip the 64-sequence ragged decode leg")
     ap.add_argument("--no-peak", action="store_true", help="skip the measured copy-bandwidth leg")
+    ap.add_argument("--no-batch1", action="store_true", help="skip the batch-1 decode legs (config 0 and 1)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the MLA path here runs on a single GPU "
@@ -200,11 +201,28 @@ def main():
     L.kvl_mla_event_destroy(e0)
     L.kvl_mla_event_destroy(e1)
     ms_step = (t1 - t0) * 1e3 / K
+    # the per-step distribution: K more steps with an event recorded between consecutive steps
+    evs = [L.kvl_mla_event_record()]
+    for _ in range(K):
+        if graph is not None:
+            lib.check(L.kvl_mla_graph_launch(graph), "graph launch")
+        else:
+            step()
+        evs.append(L.kvl_mla_event_record())
+    lib.check(L.kvl_mla_synchronize(), "sync")
+    per_step = np.array([L.kvl_mla_event_elapsed_ms(evs[i], evs[i + 1]) for i in range(K)])
+    for e in evs:
+        L.kvl_mla_event_destroy(e)
+    step_stats = {"mean": round(float(per_step.mean()), 4), "median": round(float(np.median(per_step)), 4),
+                  "p10": round(float(np.percentile(per_step, 10)), 4),
+                  "p90": round(float(np.percentile(per_step, 90)), 4), "steps": K,
+                  "timing": "HIP events between consecutive steps (a second run of K steps)"}
     wb = weight_bytes(cfg)
     hist_bytes = B * (CTX + 1) * Q8_ROW
     step_bytes = NL * (wb + hist_bytes)
     value = step_bytes / (ms_step * 1e-3) / 1e9
-    log(f"[bench] step {ms_step:.3f} ms wall ({ev_ms:.3f} ms events), {value:.1f} GB/s")
+    log(f"[bench] step {ms_step:.3f} ms wall ({ev_ms:.3f} ms events), {value:.1f} GB/s; per step median "
+        f"{step_stats['median']:.4f} ms, p10 {step_stats['p10']:.4f}, p90 {step_stats['p90']:.4f}")
 
     # the same step captured again with the stage events inside the graph (event-record
     # nodes): after a few replays, each layer's stage durations as the graph runs them
@@ -234,12 +252,36 @@ def main():
         else:
             log(f"[bench] graph-mode stage timing unavailable ({lib.last_error()}); eager events used")
 
-    attn = stages["attention"]
-    attn_gbs = hist_bytes / (attn["ms_per_launch"] * 1e-3) / 1e9
+    # the attention launches alone bracketed inside the step graph (the other stages carry no
+    # event records, so only this launch's own pair of records adds its gap)
+    attn_ms, attn_src = stages["attention"]["ms_per_launch"], timing_source
+    if graph is not None:
+        lib.check(L.kvl_mla_timing_stages(1 << lib.STAGES.index("attention")), "timing mask")
+        lib.check(L.kvl_mla_timing_enable(2), "timing on (graph)")
+        lib.check(L.kvl_mla_capture_begin(), "capture begin")
+        try:
+            step()
+        finally:
+            tg = C.c_void_p()
+            rc = L.kvl_mla_capture_end(C.byref(tg))
+        lib.check(L.kvl_mla_timing_enable(0), "timing off")
+        lib.check(L.kvl_mla_timing_stages(0x3F), "timing mask")
+        if rc == 0:
+            for _ in range(3):
+                lib.check(L.kvl_mla_graph_launch(tg), "graph launch")
+            lib.check(L.kvl_mla_synchronize(), "sync")
+            if L.kvl_mla_timing_read(ms, cnt) == 0 and cnt[3]:
+                attn_ms = ms[3] / cnt[3]
+                attn_src = ("events recorded around the attention launches only, inside the step graph "
+                            "(last of 3 replays)")
+            L.kvl_mla_graph_destroy(tg)
+        else:
+            L.kvl_mla_timing_read(ms, cnt)
+    attn_gbs = hist_bytes / (attn_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_bytes(B, CTX),
                 "kernel": "k_attn_q8_mfma", "algorithmic_bytes_per_launch": hist_bytes,
-                "avg_launch_ms": round(attn["ms_per_launch"], 5), "timing": timing_source}
+                "avg_launch_ms": round(attn_ms, 5), "timing": attn_src}
 
     result = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": K,
@@ -251,10 +293,14 @@ def main():
                    "qk_rope_dim": cfg.qk_rope_dim, "history_row_bytes": Q8_ROW,
                    "bytes_per_step": step_bytes, "mode": "eager" if graph is None else "hip-graph"},
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "step_ms": step_stats,
         "roofline": roofline,
         "stages_ms_per_launch": {k: round(v["ms_per_launch"], 5) for k, v in stages.items() if v["launches"]},
         "stages_eager_ms_per_launch": {k: round(v["ms_per_launch"], 5) for k, v in eager_stages.items()
                                        if v["launches"]},
+        "stages_note": "each stage launch bracketed by its own pair of event records, whose gaps the "
+                       "durations include (they sum to more than the step); the kernel trace in profiles/ "
+                       "gives the launches alone",
     }
 
     # ---- parity spot check + CPU baseline on layer 0 -------------------------------------
@@ -340,6 +386,125 @@ def main():
         log(f"[bench] block verify {T} tokens @{CTX}: block {times['block']:.4f} ms, "
             f"serial {times['serial']:.4f} ms, single {times['single']:.4f} ms, identical {same}")
         L.kvl_mla_compressed_q8_state_free(C.byref(bst))
+
+    # ---- batch-1 decode, the call src/generate.c:61 makes per layer and token ---------------
+    # config 0: FP32 state (KvlMlaCompressedState), 1024 rows from the state prefill of seeded
+    # N(0,1) hidden states; config 1: Q8 state, 8192 rows (synthetic, generated on the device).
+    # Weights: layer 0 of the stack (bound). Host API (host buffers, synchronous, median of 50),
+    # device time of the same decode (stream-ordered call with KVL_MLA_NO_ADVANCE, 20 of them
+    # captured in one HIP graph, replayed), the stage times (events around each launch of eager
+    # device calls), and the reference C path on the same state and token.
+    if not args.no_batch1:
+        fp = lambda a: a.ctypes.data_as(abi.f32p)  # noqa: E731
+        legs = {}
+        for name, kind, ctx_len in (("c0", "f32", 1024), ("c1", "q8", 8192)):
+            T = abi.KvlMlaCompressedState if kind == "f32" else abi.KvlMlaCompressedQ8State
+            pre = "compressed_state" if kind == "f32" else "compressed_q8_state"
+            dec = L.kvl_mla_decode_compressed_bf16 if kind == "f32" else L.kvl_mla_decode_compressed_q8_bf16
+            ddev = (L.kvl_mla_decode_compressed_batch_device if kind == "f32"
+                    else L.kvl_mla_decode_compressed_q8_batch_device)
+            row_b = 4 * (cfg.kv_lora_rank + cfg.qk_rope_dim) if kind == "f32" else Q8_ROW
+            st = T()
+            lib.check(getattr(L, f"kvl_mla_{pre}_init")(C.byref(st), C.byref(cfg), ctx_len + 1), "state init")
+            xs = np.ascontiguousarray(inputs.hidden(cfg, 0xC0 if kind == "f32" else 0xC1, ctx_len + 1))
+            if kind == "f32":
+                lib.check(L.kvl_mla_compressed_state_prefill_bf16(fp(xs[:ctx_len]), ctx_len, C.byref(cfg),
+                                                                  C.byref(wstructs[0]), C.byref(st)), "state prefill")
+            else:
+                lib.check(L.kvl_mla_compressed_q8_state_fill_synthetic(C.byref(st), 0, ctx_len, 0xC1), "fill")
+                lib.check(L.kvl_mla_compressed_q8_state_pull(C.byref(st), 0, ctx_len), "pull")
+            xq = np.ascontiguousarray(xs[ctx_len])
+            out = np.zeros(H, np.float32)
+
+            def host_call():
+                lib.check(dec(fp(out), fp(xq), ctx_len, C.byref(cfg), C.byref(wstructs[0]), C.byref(st)), "decode")
+                lib.check(getattr(L, f"kvl_mla_{pre}_truncate")(C.byref(st), ctx_len), "truncate")
+            for _ in range(5):
+                host_call()
+            ts = []
+            for _ in range(50):
+                t0_ = time.perf_counter()
+                host_call()
+                ts.append(time.perf_counter() - t0_)
+            host_ms = float(np.median(ts)) * 1e3
+            gpu_out = out.copy()
+            # device time: 20 stream-ordered decodes in one graph
+            arr1 = (C.POINTER(T) * 1)(C.pointer(st))
+            d_i = L.kvl_mla_device_alloc(xq.nbytes)
+            d_o = L.kvl_mla_device_alloc(xq.nbytes)
+            lib.check(L.kvl_mla_copy_to_device(d_i, xq.ctypes.data, xq.nbytes), "h2d")
+            for _ in range(3):
+                lib.check(ddev(d_o, d_i, 1, C.byref(cfg), C.byref(wstructs[0]), arr1, lib.NO_ADVANCE), "device decode")
+            lib.check(L.kvl_mla_synchronize(), "sync")
+            lib.check(L.kvl_mla_timing_enable(1), "timing on")
+            for _ in range(20):
+                lib.check(ddev(d_o, d_i, 1, C.byref(cfg), C.byref(wstructs[0]), arr1, lib.NO_ADVANCE), "device decode")
+            lib.check(L.kvl_mla_synchronize(), "sync")
+            lib.check(L.kvl_mla_timing_read(ms, cnt), "timing read")
+            lib.check(L.kvl_mla_timing_enable(0), "timing off")
+            st_ms = {nm: ms[i] / cnt[i] for i, nm in enumerate(lib.STAGES) if cnt[i]}
+            lib.check(L.kvl_mla_capture_begin(), "capture begin")
+            rc = 0
+            try:
+                for _ in range(20):
+                    rc = rc or ddev(d_o, d_i, 1, C.byref(cfg), C.byref(wstructs[0]), arr1, lib.NO_ADVANCE)
+            finally:
+                g1 = C.c_void_p()
+                rc2 = L.kvl_mla_capture_end(C.byref(g1))
+            lib.check(rc, "captured decode")
+            lib.check(rc2, "capture end")
+            lib.check(L.kvl_mla_graph_launch(g1), "graph launch")
+            lib.check(L.kvl_mla_synchronize(), "sync")
+            gt = []
+            for _ in range(5):
+                e0_ = L.kvl_mla_event_record()
+                lib.check(L.kvl_mla_graph_launch(g1), "graph launch")
+                e1_ = L.kvl_mla_event_record()
+                lib.check(L.kvl_mla_synchronize(), "sync")
+                gt.append(L.kvl_mla_event_elapsed_ms(e0_, e1_) / 20)
+                L.kvl_mla_event_destroy(e0_)
+                L.kvl_mla_event_destroy(e1_)
+            L.kvl_mla_graph_destroy(g1)
+            dev_ms = float(np.median(gt))
+            L.kvl_mla_device_free(d_i)
+            L.kvl_mla_device_free(d_o)
+            hist_b = (ctx_len + 1) * row_b
+            total_b = wb + hist_b + 2 * 4 * H
+            entry = {
+                "state": "FP32 (KvlMlaCompressedState)" if kind == "f32" else "Q8 (KvlMlaCompressedQ8State)",
+                "context": ctx_len, "host_api_ms": round(host_ms, 4), "device_ms": round(dev_ms, 4),
+                "device_gbs": round(total_b / (dev_ms * 1e-3) / 1e9, 1), "algorithmic_bytes": total_b,
+                "stages_ms_per_launch": {k: round(v, 5) for k, v in st_ms.items()},
+                "attention_gbs": round(hist_b / (st_ms["attention"] * 1e-3) / 1e9, 1),
+                "timing": "host API: median of 50 synchronous calls; device: 20 stream-ordered calls in one HIP "
+                          "graph, median of 5 replays; stages: events around each launch of eager calls"}
+            if not args.no_cpu:
+                import pyoracle
+                from helpers import rel_err
+                ref = pyoracle.load_reference("avx2")
+                ckind = "reference" if ref is not None else "port"
+                cpu = ref if ref is not None else pyoracle.load_oracle()
+                pfx = "kvl_" if ref is not None else "orc_"
+                cfn = getattr(cpu, pfx + ("mla_decode_compressed_bf16" if kind == "f32"
+                                          else "mla_decode_compressed_q8_bf16"))
+                co = np.zeros(H, np.float32)
+                cts = []
+                for _ in range(4):
+                    t0_ = time.perf_counter()
+                    if cfn(fp(co), fp(xq), ctx_len, C.byref(cfg), C.byref(wstructs[0]), C.byref(st)) != 0:
+                        raise RuntimeError("CPU decode failed")
+                    cts.append(time.perf_counter() - t0_)
+                    st.len = ctx_len
+                cms = float(np.median(cts[1:])) * 1e3
+                entry["cpu_baseline"] = {"ms": round(cms, 3), "gbs": round(total_b / (cms * 1e-3) / 1e9, 3),
+                                         "cores": omp_threads(), "kind": ckind,
+                                         "sample": "the same decode, median of 3 after 1 warm-up"}
+                entry["parity_vs_cpu"] = {"max_rel_err": rel_err(gpu_out, co), "tolerance": 2e-3}
+            legs[name] = entry
+            log(f"[bench] batch-1 {name} ({kind}, {ctx_len} rows): host API {host_ms:.4f} ms, device {dev_ms:.4f} ms "
+                f"({entry['device_gbs']} GB/s), attention {st_ms['attention'] * 1e3:.1f} us")
+            getattr(L, f"kvl_mla_{pre}_free")(C.byref(st))
+        result["batch1_decode"] = legs
 
     # ---- causal prefill, 4096 tokens -----------------------------------------------------
     if not args.no_prefill:

@@ -173,6 +173,7 @@ struct Ctx {
     // per-stage event timing of decode steps (kvl_mla_timing_*)
     bool timing = false;
     bool timing_graph = false;  // also record into a graph being captured (event-record nodes)
+    unsigned timing_mask = (1u << 6) - 1;  // stages bracketed (bit i: stage i)
     std::vector<hipEvent_t> ev_pool;
     std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> ev_used;
 };
@@ -242,7 +243,7 @@ struct StageTimer {
     hipEvent_t a = nullptr, b = nullptr;
     explicit StageTimer(int s) : stage(s) {
         Ctx &c = ctx();
-        if (!c.timing || (c.capturing && !c.timing_graph)) return;
+        if (!c.timing || !((c.timing_mask >> s) & 1u) || (c.capturing && !c.timing_graph)) return;
         a = ev_get();
         b = ev_get();
         // inside a capture, only an external record becomes a timestamped node of the graph
@@ -763,21 +764,27 @@ long nsplit_of(int kind, long len, long r) {
 // Rows per split shared by the sequences of a launch: the smallest multiple of the kernel's chunk
 // (at least four chunks) whose split count sum_i nsplit_of(len_i, r) fits wg_per_cu x ncu, so the
 // launch runs as one round of workgroups. Q8: at most 1024 rows (long batches then take more
-// than one round). A lone sequence gets at most lone_splits(kind) splits (about 0.6 MB of a
-// 32K-row history each): its launch is bound by the workgroups' start-up and the combine, not
-// by bandwidth, and the lone plan is also the plan of each token of a block decode
-// (bit-identical to single decodes), whose Q8 workgroups (32 x tokens) then fit one round for
-// blocks of up to 8 tokens.
-long lone_splits(int kind) { return kind == kAttnQ8Mfma ? 32 : kind == kAttnBF16Mfma ? 64 : 128; }
+// than one round). A lone sequence gets splits of at least two chunks, at most lone_splits(kind,
+// len) of them: its launch is bound by the workgroups' fixed start-up (about 11 us with one or
+// two chunks each) and the combine, whose partials grow with the split count (measured, one
+// decode over 8K / 32K Q8 rows, attention + combine: 19.3 / 31.4 us with 32 splits of >= 4
+// chunks, 17.5 / 23.8 us with 64 of >= 2, 20.7 / 23.8 us with 128 of >= 1). The lone plan is also
+// the plan of each token of a block decode (bit-identical to single decodes): beyond 16K Q8 rows
+// it stays at 32 splits, so that the 32 x 8 workgroups of an 8-token block run as one round (64
+// splits: 41 us for the block's attention + combine at 32K rows against 34 us).
+long lone_splits(int kind, long len) {
+    if (kind == kAttnQ8Mfma) return len <= 16384 ? 64 : 32;
+    return kind == kAttnBF16Mfma ? 64 : 128;
+}
 long plan_rows(int kind, const int *lens, int n, int ncu) {
     const long chunk = plan_chunk(kind);
-    const long target = n == 1 ? lone_splits(kind) : (long)plan_wg_per_cu(kind) * ncu;
+    const long target = n == 1 ? lone_splits(kind, lens[0]) : (long)plan_wg_per_cu(kind) * ncu;
     auto count = [&](long r) {
         long c = 0;
         for (int i = 0; i < n; ++i) c += nsplit_of(kind, lens[i], r);
         return c;
     };
-    long lo = 4, hi = 4;  // in chunks
+    long lo = n == 1 ? 2 : 4, hi = lo;  // in chunks
     for (int i = 0; i < n; ++i) hi = std::max(hi, ((long)lens[i] + chunk - 1) / chunk);
     while (lo < hi) {  // count() does not increase with r
         const long mid = (lo + hi) / 2;
@@ -2399,6 +2406,13 @@ int kvl_mla_timing_enable(int on) {
     if (on < 0 || on > 2) return -1;
     ctx().timing = on != 0;
     ctx().timing_graph = on == 2;
+    return 0;
+}
+
+int kvl_mla_timing_stages(unsigned mask) {
+    Guard guard;
+    if (ensure_ready() != 0) return -1;
+    ctx().timing_mask = mask & ((1u << kStages) - 1);
     return 0;
 }
 

@@ -251,10 +251,14 @@ int kvl_mla_graph_destroy(void *graph_exec);
  * graph before timing anything else). kvl_mla_timing_read() sums the
  * durations (ms) and launch counts of the six stages (gemv_in, append [+ qprep: one launch
  * for the compressed formats], qprep [expanded format], attention,
- * combine, gemv_out) since the last read. Events: record on the library stream, elapsed
- * time between two recorded events (waits for the second). kvl_mla_copy_kernel: a plain
- * 16-byte vector copy kernel (bytes % 16 == 0), for calibrating memory counters. */
+ * combine, gemv_out) since the last read. kvl_mla_timing_stages(mask) limits the bracketing
+ * to the stages whose bit is set (bit i: stage i; all six by default): every bracketed launch
+ * carries its two event records, whose gaps the durations include. Events: record on the
+ * library stream, elapsed time between two recorded events (waits for the second).
+ * kvl_mla_copy_kernel: a plain 16-byte vector copy kernel (bytes % 16 == 0), for calibrating
+ * memory counters. */
 int kvl_mla_timing_enable(int on);
+int kvl_mla_timing_stages(unsigned mask);
 int kvl_mla_timing_read(double *ms, int *count);
 void *kvl_mla_event_record(void);
 double kvl_mla_event_elapsed_ms(void *start, void *end);
