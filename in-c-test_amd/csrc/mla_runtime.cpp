@@ -767,8 +767,8 @@ long nsplit_of(int kind, long len, long r) {
 // than one round). A lone sequence gets splits of at least two chunks, at most lone_splits(kind,
 // len) of them: its launch is bound by the workgroups' fixed start-up (about 11 us with one or
 // two chunks each) and the combine, whose partials grow with the split count (measured, one
-// decode over 8K / 32K Q8 rows, attention + combine: 19.3 / 31.4 us with 32 splits of >= 4
-// chunks, 17.5 / 23.8 us with 64 of >= 2, 20.7 / 23.8 us with 128 of >= 1). The lone plan is also
+// decode over 8K / 32K Q8 rows, attention + combine: 19.3 / 31.3 us with 32 splits of >= 4
+// chunks, 17.5 / 23.7 us with 64 of >= 2, 20.7 / 23.7 us with 128 of >= 1). The lone plan is also
 // the plan of each token of a block decode (bit-identical to single decodes): beyond 16K Q8 rows
 // it stays at 32 splits, so that the 32 x 8 workgroups of an 8-token block run as one round (64
 // splits: 41 us for the block's attention + combine at 32K rows against 34 us).
