@@ -1271,10 +1271,11 @@ __device__ __forceinline__ void wait_vm(int n) {
 }
 
 // ---- bf16 MFMA path (BF16 history, NH=16, R=512, DR=64) -------------------------------
-// One workgroup of four waves per CU streams its split-K slice in chunks of 32 rows (36 KB: 32 KB
-// of latents, 4 KB of RoPE keys) through a ring of four LDS slots filled by
-// global_load_lds_dwordx4: chunk k is computed while chunks k+1 .. k+3 are in flight. The rows
-// are exact bf16 MFMA operands, so only the query side and the softmax weights are split:
+// Two workgroups of four waves per CU (two waves per SIMD, so that one workgroup's softmax, LDS
+// round trips and DMA waits overlap the other's MFMAs) each stream a split-K slice in chunks of
+// 32 rows (36 KB: 32 KB of latents, 4 KB of RoPE keys) through a ring of two LDS slots filled by
+// global_load_lds_dwordx4: chunk k is computed while chunk k+1 lands. The rows are exact bf16
+// MFMA operands, so only the query side and the softmax weights are split:
 //   scores: M = 16 heads, N = 16 rows, K = 576. Wave w takes rows 16 (w & 1) .. +15 and the
 //     k-blocks 9 (w >> 1) .. +8 of 32 against the bf16 hi | lo split of q * softmax scale (two
 //     v_mfma_f32_16x16x32_bf16 per block); the two k-halves are summed through LDS;
@@ -1287,7 +1288,7 @@ __device__ __forceinline__ void wait_vm(int n) {
 // (16 rows, one slot) and the transposed reads (4 rows x 32 bytes per 16 lanes, 8 rows per half
 // wave) spread over the LDS banks.
 constexpr int kB16Ch = 32;
-constexpr int kB16Ring = 4;
+constexpr int kB16Ring = 2;
 constexpr int kB16LatB = kB16Ch * 1024;            // latents of a chunk
 constexpr int kB16Slot = kB16LatB + kB16Ch * 128;  // + RoPE keys
 constexpr int kB16SpHs = 36;                       // floats per head in a score half: 32 + 4
@@ -1326,7 +1327,7 @@ __device__ __forceinline__ v4s lds_read_tr16(const uint8_t *p) {
 }
 
 template <bool ONCE>  // ONCE: each history row is read by one workgroup (non-temporal loads)
-__global__ __launch_bounds__(256) void k_attn_bf16_mfma(AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attn_bf16_mfma(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t smem[kB16SmemB];
     const int tid = threadIdx.x, l = tid & 63, n = l & 15, g = l >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1363,8 +1364,7 @@ __global__ __launch_bounds__(256) void k_attn_bf16_mfma(AttnArgs a) {
     };
 
     // query operands (A of the score MFMAs: head n, k = 32 kb + 8g .. +7). Chunk 0's DMA goes out
-    // first; the query loads follow it and are split before chunks 1 and 2 are issued, so the
-    // compiler's wait for them (which does not count the DMA) covers chunk 0 and nothing more.
+    // first; the query loads follow it.
     v8bf qh[9], ql[9];
     issue(0);
     {
@@ -1378,11 +1378,8 @@ __global__ __launch_bounds__(256) void k_attn_bf16_mfma(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < 9; ++j) {
             split8_cvt(qv[2 * j] * a.smscale, qv[2 * j + 1] * a.smscale, qh[j], ql[j]);
-            asm volatile("" ::"v"(qh[j]), "v"(ql[j]));  // before chunks 1 and 2 are issued
         }
     }
-    if (nch > 1) issue(1);
-    if (nch > 2) issue(2);
 
     // score operand offsets (row srow of the chunk, slot 4 kb + g of its latents / RoPE key)
     const int srow = 16 * rb + n;
@@ -1409,10 +1406,10 @@ __global__ __launch_bounds__(256) void k_attn_bf16_mfma(AttnArgs a) {
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
     for (int k = 0; k < nch; ++k) {
-        // this wave's DMA of chunk k has landed (chunks k+1, k+2 may stay in flight)
-        wait_vm(k + 2 < nch ? 18 : (k + 1 < nch ? 9 : 0));
+        // this wave's DMA of chunk k has landed (the only one in flight)
+        wait_vm(0);
         lds_barrier();  // chunk k complete; every wave is done with chunk k-1's slot and the scores
-        if (k + 3 < nch) issue(k + 3);
+        if (k + 1 < nch) issue(k + 1);
         const uint8_t *buf = smem + (k % kB16Ring) * kB16Slot;
         v4f dp = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1485,15 +1482,16 @@ __global__ __launch_bounds__(256) void k_attn_bf16_mfma(AttnArgs a) {
 
 // ---- FP32 history on bf16 MFMA (NH=16, R=512, DR=64) ----------------------------------
 // The BF16 kernel's pipeline over FP32 rows: a chunk is 16 rows (36 KB: 32 KB of latents, 4 KB
-// of RoPE keys, the size of a BF16 chunk), streamed by DMA into the same ring of four LDS slots.
+// of RoPE keys, the size of a BF16 chunk), streamed by DMA into a ring of two LDS slots (chunk
+// k computed while chunk k+1 lands); two workgroups run on each CU (two waves per SIMD), so that
+// one workgroup's conversion, softmax and DMA waits overlap the other's MFMAs.
 // Each fp32 row becomes two bf16 "virtual rows", hi = bf16(x) and lo = bf16(x - hi) (x - hi is
 // exact, |x - hi - lo| <= 2^-18 |x|): virtual rows 0-15 are the hi parts of rows 0-15, 16-31 their
 // lo parts, laid out as a 32-row BF16 chunk. Wave w loads rows 4w .. 4w+3 so that their fp32
 // bytes land exactly where their virtual rows go (latent columns 0-255 of row r in virtual row
 // r's kilobyte, 256-511 in virtual row 16 + r's; the four RoPE rows in the wave's quarter of the
-// RoPE area) and converts them in place once its own DMA has landed: chunk k+1 during the mix
-// of chunk k (its VALU work between the mix MFMAs), before the barrier that opens step k+1, so
-// there is no extra barrier and no extra LDS. The BF16 kernel's score, softmax and mix run on the 32
+// RoPE area) and converts them in place once its own DMA has landed, before the step barrier:
+// no extra barrier, no extra LDS. The BF16 kernel's score, softmax and mix then run on the 32
 // virtual rows: a row's score is the sum of its two virtual rows' scores (q hi + lo against
 // row hi + lo: all four products), and both virtual rows of a row carry its weight p (hi + lo),
 // so the mix adds p (hi + lo) of the row. Per history byte this is the BF16 kernel's MFMA work.
@@ -1501,12 +1499,15 @@ __global__ __launch_bounds__(256) void k_attn_bf16_mfma(AttnArgs a) {
 // 4..7 the lo parts of rows 4w + (k & 3), 128 bytes each, 16-byte slot s at s ^ f32r_swz(row)
 // (row = the row in the chunk) so that the score reads of 8 rows fall in distinct banks.
 constexpr int kF32Ch = 16;
+constexpr int kF32Ring = 2;
+constexpr int kF32SpOff = kF32Ring * kB16Slot;
+constexpr int kF32SmemB = kF32SpOff + 2 * 16 * kB16SpHs * 4;
 typedef int v2i __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ int f32r_swz(int row) { return (row >> 1) & 7; }
 
 template <bool ONCE>  // ONCE: each history row is read by one workgroup (non-temporal loads)
-__global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t smem[kB16SmemB];
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attn_f32_mfma(AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[kF32SmemB];
     const int tid = threadIdx.x, l = tid & 63, n = l & 15, g = l >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     int b, split, pidx;
@@ -1519,7 +1520,7 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
     const float *grope = (const float *)s.b;
     constexpr bool once = ONCE;
     const uint32_t sbase = lds_addr(smem);
-    float *sp = (float *)(smem + kB16SpOff);
+    float *sp = (float *)(smem + kF32SpOff);
     const int rb = w & 1, kh = w >> 1;
 
     // DMA per chunk and wave: rows 4w .. 4w+3, two 1 KB instructions per row (latent columns
@@ -1527,7 +1528,7 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
     // row 4w + (i >> 4), columns 4 (i & 15) .. +3). Rows past the split end (last chunk only)
     // re-read the split's last row (in bounds); their scores are masked.
     auto issue = [&](int c) __attribute__((always_inline)) {
-        const uint32_t buf = sbase + (uint32_t)((c % kB16Ring) * kB16Slot);
+        const uint32_t buf = sbase + (uint32_t)((c % kF32Ring) * kB16Slot);
         const int rbase = r0 + c * kF32Ch;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -1543,11 +1544,10 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
         dma_hist_b128(grope + (size_t)gr * 64 + 4 * (l & 15), buf + (uint32_t)(kB16LatB + w * 1024), once);
     };
     // In-place conversion of this wave's rows of chunk c (its DMA has landed): every lane reads
-    // its fp32 values first (conv_load), then writes the hi and lo words (conv_store; the wave's
-    // bytes only).
-    v4f x[4][2], xr;
-    auto conv_load = [&](int c) __attribute__((always_inline)) {
-        const uint8_t *buf = smem + (c % kB16Ring) * kB16Slot;
+    // its fp32 values first, then writes the hi and lo words (the wave's bytes only).
+    auto convert = [&](int c) __attribute__((always_inline)) {
+        uint8_t *buf = smem + (c % kF32Ring) * kB16Slot;
+        v4f x[4][2];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = 4 * w + i;  // columns 8l .. 8l+7: lanes 0-31 in row's kilobyte, 32-63 in 16 + row's
@@ -1555,11 +1555,8 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
             x[i][0] = *(const v4f *)src;
             x[i][1] = *(const v4f *)(src + 16);
         }
-        xr = *(const v4f *)(buf + kB16LatB + w * 1024 + 16 * l);
-    };
-    auto conv_store = [&](int c) __attribute__((always_inline)) {
-        uint8_t *buf = smem + (c % kB16Ring) * kB16Slot;
         uint8_t *rq = buf + kB16LatB + w * 1024;
+        const v4f xr = *(const v4f *)(rq + 16 * l);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = 4 * w + i;
@@ -1594,14 +1591,8 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < 9; ++j) {
             split8_cvt(qv[2 * j] * a.smscale, qv[2 * j + 1] * a.smscale, qh[j], ql[j]);
-            asm volatile("" ::"v"(qh[j]), "v"(ql[j]));  // before chunks 1 and 2 are issued
         }
     }
-    if (nch > 1) issue(1);
-    if (nch > 2) issue(2);
-    wait_vm(nch > 2 ? 18 : (nch > 1 ? 9 : 0));  // chunk 0 has landed
-    conv_load(0);
-    conv_store(0);
 
     // score operand offsets: virtual row srow = 16 rb + n (row n's hi part for rb = 0, lo for 1)
     const int srow = 16 * rb + n;
@@ -1629,9 +1620,12 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
     for (int t = 0; t < 8; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
     const int rg = 8 * (g & 1);  // the rows whose softmax weights lane group g holds
     for (int k = 0; k < nch; ++k) {
+        // this wave's DMA of chunk k has landed (the only one in flight)
+        wait_vm(0);
+        convert(k);
         lds_barrier();  // chunk k converted; every wave is done with chunk k-1's slot and the scores
-        if (k + 3 < nch) issue(k + 3);
-        const uint8_t *buf = smem + (k % kB16Ring) * kB16Slot;
+        if (k + 1 < nch) issue(k + 1);
+        const uint8_t *buf = smem + (k % kF32Ring) * kB16Slot;
         v4f dp = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 9; ++j) {
@@ -1682,31 +1676,14 @@ __global__ __launch_bounds__(256) void k_attn_f32_mfma(AttnArgs a) {
         l_run += xgroup_sum(g < 2 ? psum : 0.f);
         v8bf ph, pl;
         split8_cvt(v4f{p[0], p[1], p[2], p[3]}, v4f{p[4], p[5], p[6], p[7]}, ph, pl);
-        // the mix of chunk k with the conversion of chunk k+1 (this wave's rows, once its DMA has
-        // landed: chunks k+2 and k+3 may stay in flight) between its MFMAs
-        v8bf bt[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             const v4s lo4 = lds_read_tr16(buf + tro[0][t]);
             const v4s hi4 = lds_read_tr16(buf + tro[1][t]);
-            bt[t] = __builtin_bit_cast(v8bf, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+            const v8bf bt = __builtin_bit_cast(v8bf, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+            acc[t] = mfma_bf16(ph, bt, acc[t]);
+            acc[t] = mfma_bf16(pl, bt, acc[t]);
         }
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            acc[t] = mfma_bf16(ph, bt[t], acc[t]);
-            acc[t] = mfma_bf16(pl, bt[t], acc[t]);
-        }
-        const bool next = k + 1 < nch;
-        if (next) {
-            wait_vm(k + 3 < nch ? 18 : (k + 2 < nch ? 9 : 0));
-            conv_load(k + 1);
-        }
-#pragma unroll
-        for (int t = 4; t < 8; ++t) {
-            acc[t] = mfma_bf16(ph, bt[t], acc[t]);
-            acc[t] = mfma_bf16(pl, bt[t], acc[t]);
-        }
-        if (next) conv_store(k + 1);
     }
     float *P = a.part + (size_t)pidx * 16 * 514;
 #pragma unroll

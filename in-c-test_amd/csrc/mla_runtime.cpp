@@ -748,10 +748,13 @@ struct SeqIn {
 };
 
 // Split-K plan of the MFMA attention kernels. The kernels run about wg_per_cu workgroups per CU
-// (one for the Q8 and BF16 kernels, whose LDS rings fill a CU), so a launch should have at most
-// that many splits: one more makes a second round of workgroups that doubles the launch time.
+// (one for the Q8 kernel, whose LDS ring fills a CU; two for the BF16 and FP32 kernels, whose
+// two-slot rings take half of it), so a launch should have at most that many splits: one more
+// makes a second round of workgroups that doubles the launch time.
 int plan_chunk(int kind) { return kind == kAttnQ8Mfma ? 64 : kind == kAttnBF16Mfma ? 32 : 16; }
-int plan_wg_per_cu(int kind) { return kind == kAttnQ8Mfma || kind == kAttnBF16Mfma || kind == kAttnF32Mfma ? 1 : 3; }
+int plan_wg_per_cu(int kind) {
+    return kind == kAttnQ8Mfma ? 1 : kind == kAttnF32Mfma || kind == kAttnBF16Mfma ? 2 : 3;
+}
 
 // Splits of a history of len rows at r rows per split. Q8: a remainder of at most r/8 rows past
 // the last full split joins that split (its 1024-row cap would otherwise leave a one-row split
