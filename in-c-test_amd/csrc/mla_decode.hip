@@ -216,15 +216,20 @@ __global__ __launch_bounds__(1024) void k_gemv_ksplit(GemvSplitArgs a) {
 }
 
 // Y[b, o] (+)= sum_k W[o, k] (hi + lo)[b, k] with the activations already split into bf16
-// planes by their producer: 16 output rows per block, 16 waves splitting k, one 16-byte
-// activation load and one MFMA per k-block and sequence group; the 16-token groups are taken
-// in turn with the weights held in registers. Requires in = 16 * 32 * KPW.
-template <int NG, int KPW>
+// planes by their producer: RB (16 or 8) output rows per block, 16 waves splitting k, one
+// 16-byte activation load and one MFMA per k-block and sequence group; the 16-token groups are
+// taken in turn with the weights held in registers. With RB = 8, MFMA rows 8-15 repeat rows
+// 0-7 and are not stored: a block then takes in 32 KB of weights instead of 64 KB beside the
+// 64 KB of activations every block reads, and the grid covers twice the CUs (o_proj at batch 8:
+// 6.9 -> 6.5 us). Each output is the same sum in the same order for either RB.
+// Requires in = 16 * 32 * KPW.
+template <int NG, int KPW, int RB = 16>
 __global__ __launch_bounds__(1024) void k_gemv_xs(GemvSplitArgs a) {
+    static_assert(RB == 16 || RB == 8, "rows per block");
     __shared__ v4f red[16][NG][64];
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
     const int out = a.out0, part = n >> 3;
-    const uint16_t *wrow = a.W0 + (size_t)min((int)blockIdx.x * 16 + n, out - 1) * a.in;
+    const uint16_t *wrow = a.W0 + (size_t)min((int)blockIdx.x * RB + (n % RB), out - 1) * a.in;
     const int kbase = w * (32 * KPW) + g * 8;
     v4i wa[KPW];
 #pragma unroll
@@ -247,8 +252,8 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(GemvSplitArgs a) {
         for (int gi = 0; gi < NG; ++gi)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int b = bz + 8 * gi + n, r = blockIdx.x * 16 + 4 * g + i;
-                yres[gi][i] = w == 0 && a.acc && n < 8 && b < a.B && r < out ? a.Y[(size_t)b * a.ldy + r] : 0.f;
+                const int b = bz + 8 * gi + n, r = blockIdx.x * RB + 4 * g + i;
+                yres[gi][i] = w == 0 && a.acc && n < 8 && 4 * g < RB && b < a.B && r < out ? a.Y[(size_t)b * a.ldy + r] : 0.f;
             }
         v4f acc[NG];
 #pragma unroll
@@ -271,10 +276,10 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(GemvSplitArgs a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) s[i] += dpp_f32<0x128>(s[i]);
                 const int b = bz + 8 * gi + n;
-                if (n < 8 && b < a.B) {
+                if (n < 8 && 4 * g < RB && b < a.B) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const int r = blockIdx.x * 16 + 4 * g + i;
+                        const int r = blockIdx.x * RB + 4 * g + i;
                         if (r < out) a.Y[(size_t)b * a.ldy + r] = a.acc ? yres[gi][i] + s[i] : s[i];
                     }
                 }
@@ -550,7 +555,7 @@ hipError_t launch_gemv_xs(hipStream_t st, float *Y, int ldy, const uint16_t *XS,
     const bool two = B > 8;
     if (in == 2048) {
         if (two) hipLaunchKernelGGL((k_gemv_xs<2, 4>), grid, dim3(1024), 0, st, a);
-        else hipLaunchKernelGGL((k_gemv_xs<1, 4>), grid, dim3(1024), 0, st, a);
+        else hipLaunchKernelGGL((k_gemv_xs<1, 4, 8>), dim3((out + 7) / 8, 1, grid.z), dim3(1024), 0, st, a);
     } else {
         if (two) hipLaunchKernelGGL((k_gemv_xs<2, 8>), grid, dim3(1024), 0, st, a);
         else hipLaunchKernelGGL((k_gemv_xs<1, 8>), grid, dim3(1024), 0, st, a);
