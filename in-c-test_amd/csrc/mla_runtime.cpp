@@ -772,11 +772,12 @@ long nsplit_of(int kind, long len, long r) {
 // two chunks each) and the combine, whose partials grow with the split count (measured, one
 // decode over 8K / 32K Q8 rows, attention + combine: 19.3 / 31.3 us with 32 splits of >= 4
 // chunks, 17.5 / 23.7 us with 64 of >= 2, 20.7 / 23.7 us with 128 of >= 1). The lone plan is also
-// the plan of each token of a block decode (bit-identical to single decodes): beyond 16K Q8 rows
-// it stays at 32 splits, so that the 32 x 8 workgroups of an 8-token block run as one round (64
-// splits: 41 us for the block's attention + combine at 32K rows against 34 us).
+// the plan of each token of a block decode (bit-identical to single decodes): with 64 splits at
+// 32K Q8 rows the 64 x 8 workgroups of an 8-token block take two rounds (host calls: single
+// 0.063 -> 0.057 ms, 8-token block 0.077 -> 0.085 ms, 1.49x the single decode).
 long lone_splits(int kind, long len) {
-    if (kind == kAttnQ8Mfma) return len <= 16384 ? 64 : 32;
+    (void)len;
+    if (kind == kAttnQ8Mfma) return 64;
     return kind == kAttnBF16Mfma ? 64 : 128;
 }
 long plan_rows(int kind, const int *lens, int n, int ncu) {
