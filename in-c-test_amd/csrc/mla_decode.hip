@@ -600,6 +600,41 @@ struct AppendArgs {
     float eps;
 };
 
+// Sequence descriptors without a read that waits on the sequence index: lane i of a fully
+// active wave reads descriptor i of the table (kernel arguments, kMaxBatch = 64 = one entry per
+// lane) in the first round trip beside the other arguments, and the wave then takes the entry
+// of a wave-uniform index from that lane. Indexing the table once the index is known costs one
+// more memory round trip.
+static_assert(kMaxBatch == 64, "one descriptor per lane");
+__device__ __forceinline__ int lane_pick(int v, int b) { return __builtin_amdgcn_readlane(v, b); }
+__device__ __forceinline__ void *lane_pick(void *p, int b) {
+    const uint64_t u = (uint64_t)p;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, b);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), b);
+    return (void *)(((uint64_t)hi << 32) | lo);
+}
+struct DescLane {  // this lane's entry of the table
+    void *a, *b, *c;
+    int len, pos, split0, nsplit, rps;
+};
+__device__ __forceinline__ DescLane desc_lane(const SeqTable &t) {
+    const SeqDesc &m = t.s[threadIdx.x & 63];
+    return DescLane{m.a, m.b, m.c, m.len, m.pos, m.split0, m.nsplit, m.rps};
+}
+__device__ __forceinline__ SeqDesc desc_pick(const DescLane &m, int i) {
+    SeqDesc s;
+    s.a = lane_pick(m.a, i);
+    s.b = lane_pick(m.b, i);
+    s.c = lane_pick(m.c, i);
+    s.len = lane_pick(m.len, i);
+    s.pos = lane_pick(m.pos, i);
+    s.split0 = lane_pick(m.split0, i);
+    s.nsplit = lane_pick(m.nsplit, i);
+    s.rps = lane_pick(m.rps, i);
+    s.pad1 = 0;
+    return s;
+}
+
 // Value of a projection output stored as np partials (np = 1 or kGemvKs) pstride floats
 // apart, added in partial order. The kGemvKs loads are issued together.
 __device__ __forceinline__ float sum_parts(const float *p, int np, size_t pstride) {
@@ -627,7 +662,7 @@ __device__ __forceinline__ void append_body(const SeqTable &t, const Dims &d, co
     __shared__ double redd[4];
     __shared__ float redf[4];
     const int tid = threadIdx.x;
-    const SeqDesc &s = t.s[a.rows_mode ? 0 : b];
+    const SeqDesc s = desc_pick(desc_lane(t), a.rows_mode ? 0 : b);
     const int R = d.R, DR = d.DR, half = DR / 2, pos = s.pos + (a.rows_mode ? b : 0);
     const int nk = R + DR;
     const float *ky = a.y + (size_t)b * a.ldy + a.koff;
@@ -906,8 +941,9 @@ __device__ __forceinline__ void qprep_body(const SeqTable &t, const Dims &d, con
     __shared__ float qr[kMaxDR];  // RoPE input of the head
     __shared__ float ql[kMaxR];
     __shared__ float redf[4];
+    const DescLane dl = desc_lane(t);
     const int b = blk / d.NH, h = blk % d.NH, tid = threadIdx.x;
-    const SeqDesc &s = t.s[b];
+    const SeqDesc s = desc_pick(dl, b);
     const float *qh = a.y + (size_t)b * a.ldy + (size_t)h * d.QD;
     const int half = d.DR / 2, nq = d.DN + d.DR;
     // Kimi shapes: q_lat = W_UK^T q_nope on MFMA. Wave w owns latent columns 128 w .. +127 as
@@ -1111,9 +1147,9 @@ hipError_t launch_append_qprep(hipStream_t st, int fmt, const SeqTable &t, const
 
 struct AttnArgs {
     // Read first by every workgroup (kernel arguments live in device memory and the first read
-    // of each 64-byte line is a round trip): the fields the start-up needs come before the
-    // sequence table, so that one round trip brings them and a second one the workgroup's
-    // SeqDesc.
+    // of each 64-byte line is a round trip): the fields the start-up needs come first; the
+    // workgroup's SeqDesc comes from the lanes' reads of the table (seq_of) in the same round
+    // trip.
     float *part;
     const float *qf;
     const int8_t *qhi, *qlo;
@@ -1122,11 +1158,8 @@ struct AttnArgs {
     float *scores;
     int rps, lmax;
     float smscale;
-    int members;  // > 0: a block launch of that many members (split_of)
+    int members;  // > 0: a block launch of that many members (seq_of)
     int nseq;     // = t.n
-    // first split of each sequence (t.s[i].split0), contiguous: the workgroup -> sequence lookup
-    // reads it with a few wide scalar loads instead of walking t.s
-    int sp0[kMaxBatch];
     Dims d;
     SeqTable t;
 };
@@ -1148,42 +1181,21 @@ __device__ __forceinline__ int find_seq(const SeqTable &t, int bid) {
 // members * (s / kXcds) + member of XCD s % kXcds's order, so the members of a split run at the
 // same time on one XCD and its L2 serves the history rows they share. A workgroup past its
 // member's last split has nothing to do (false).
-// A copy of sequence b's descriptor is taken without a read that waits for b: lane i of the
-// (fully active) wave reads sequence i's descriptor from the argument block (kMaxBatch = 64 =
-// one per lane) in the first round trip, beside the other arguments; b comes from a ballot over
-// the lanes' split0 and the descriptor from lane b. Indexing the table by b once b is known is
-// one more dependent round trip per workgroup (a lone decode's attention launch: 12.5 -> 10.3 us
-// at 8K Q8 rows, 18.3 -> 16.5 us at 32K with b known up front).
-static_assert(kMaxBatch == 64, "one descriptor per lane");
-__device__ __forceinline__ int lane_pick(int v, int b) { return __builtin_amdgcn_readlane(v, b); }
-__device__ __forceinline__ void *lane_pick(void *p, int b) {
-    const uint64_t u = (uint64_t)p;
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, b);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), b);
-    return (void *)(((uint64_t)hi << 32) | lo);
-}
+// Sequence b's descriptor comes from desc_lane / desc_pick, b from a ballot over the lanes'
+// split0 (a lone decode's attention launch: 12.5 -> 10.3 us at 8K Q8 rows, 18.3 -> 16.5 us at
+// 32K against indexing the table by b once b is known).
 __device__ __forceinline__ bool seq_of(const AttnArgs &a, int &b, int &split, int &pidx, SeqDesc &s) {
     const int sid = blockIdx.x, lane = threadIdx.x & 63;
-    const SeqDesc &mine = a.t.s[lane];
-    void *pa = mine.a, *pb = mine.b, *pc = mine.c;
-    const int len = mine.len, pos = mine.pos, sp0 = mine.split0, ns = mine.nsplit, rps = mine.rps;
+    const DescLane m = desc_lane(a.t);
     if (a.members > 0) {
         const int j = sid / kXcds;
         b = j % a.members;
         split = kXcds * (j / a.members) + sid % kXcds;
     } else {
-        b = __builtin_popcountll(__builtin_amdgcn_ballot_w64(lane >= 1 && lane < a.nseq && sid >= sp0));
-        split = sid - lane_pick(sp0, b);
+        b = __builtin_popcountll(__builtin_amdgcn_ballot_w64(lane >= 1 && lane < a.nseq && sid >= m.split0));
+        split = sid - lane_pick(m.split0, b);
     }
-    s.a = lane_pick(pa, b);
-    s.b = lane_pick(pb, b);
-    s.c = lane_pick(pc, b);
-    s.len = lane_pick(len, b);
-    s.pos = lane_pick(pos, b);
-    s.split0 = lane_pick(sp0, b);
-    s.nsplit = lane_pick(ns, b);
-    s.rps = lane_pick(rps, b);
-    s.pad1 = 0;
+    s = desc_pick(m, b);
     if (a.members > 0) {
         if (split >= s.nsplit) return false;
         pidx = s.split0 + split;
@@ -2219,7 +2231,6 @@ hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t
     a.smscale = 1.0f / sqrtf((float)d.QD);
     a.members = kind == kAttnGeneric ? 0 : members;
     a.nseq = t.n;
-    for (int i = 0; i < kMaxBatch; ++i) a.sp0[i] = i < t.n ? t.s[i].split0 : 0;
     int grid = total_splits;
     if (a.members > 0) {
         int maxns = 0;
@@ -2403,6 +2414,7 @@ __global__ __launch_bounds__(1024) void k_combine_r512(CombineArgs a) {
     __shared__ float wts[kMaxSplits];
     __shared__ v4f red[8][128];
     __shared__ float sinv;
+    const DescLane dl = desc_lane(a.t);  // first: the partial loads wait for it
     const int NH = a.d.NH, tid = threadIdx.x;
     const int half = blockIdx.x & 1, gh = blockIdx.x >> 1, grp = gh / NH, h = gh % NH;
     const int dd = 64 * half + (tid >> 4), q = tid & 15;
@@ -2419,9 +2431,8 @@ __global__ __launch_bounds__(1024) void k_combine_r512(CombineArgs a) {
         // below are formed in each iteration instead of being held (spilled) across the loop
         int c4 = tid & 127;
         asm volatile("" : "+v"(c4));
-        const SeqDesc &s = a.t.s[b];
-        const int ns = s.nsplit;
-        const float *P = a.part + (size_t)s.split0 * stride;
+        const int ns = lane_pick(dl.nsplit, b);
+        const float *P = a.part + (size_t)lane_pick(dl.split0, b) * stride;
         const float *Pm = P + (size_t)NH * 512 + h;  // split i: m at Pm[i * stride], l at + NH
         float m0 = 0.f, l0 = 0.f;
         if (tid < 64) {
@@ -2527,6 +2538,7 @@ __global__ __launch_bounds__(1024) void k_combine_r512x8(CombineArgs a) {
     __shared__ float mx[8][512];
     __shared__ float wts[8][kCombWide];
     __shared__ float sinv[8];
+    const DescLane dl = desc_lane(a.t);  // first: the partial loads wait for it
     const int NH = a.d.NH, tid = threadIdx.x;
     const int half = blockIdx.x & 1, gh = blockIdx.x >> 1, grp = gh / NH, h = gh % NH;
     const int dd = 64 * half + (tid >> 4), q = tid & 15;
@@ -2538,9 +2550,8 @@ __global__ __launch_bounds__(1024) void k_combine_r512x8(CombineArgs a) {
     const int b = grp * 8 + j;
     const bool live = b < a.t.n;
     const size_t stride = (size_t)NH * (512 + 2);
-    const SeqDesc &s = a.t.s[live ? b : 0];
-    const int ns = live ? s.nsplit : 0;
-    const float *P = a.part + (size_t)s.split0 * stride;
+    const int ns = live ? lane_pick(dl.nsplit, b) : 0;
+    const float *P = a.part + (size_t)lane_pick(dl.split0, live ? b : 0) * stride;
     const float *Pm = P + (size_t)NH * 512 + h;
     const float *Pg = P + (size_t)h * 512 + 4 * c4;
     v4f pre[kCombWide];
