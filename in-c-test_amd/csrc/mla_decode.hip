@@ -137,11 +137,18 @@ struct GemvSplitArgs {
 // consumer adds the kGemvKs partials in kq order. The block takes the 16-token groups
 // 16 blockIdx.z, + 16 gridDim.z, ... in turn with its weights held in registers, so a batch of
 // many tokens reads each weight once. Requires in = kGemvKs * 16 * 32 * KPW.
+// XCD-aware placement (kGemvKs = 4, workgroup i on XCD i % 8): the blocks of k quarter kq run
+// on XCDs 2 kq and 2 kq + 1, so each XCD's L2 takes in one quarter of the activations (a
+// quarter of the bytes a host-memory x crosses the bus with; the host-API decode reads x there).
+// Block i: kq = (i % 8) / 2, row block 2 (i / 8) + i % 2; blocks past the last row block exit.
+static_assert(kGemvKs == 4, "two XCDs per k quarter");
 template <int NG, int KPW>
 __global__ __launch_bounds__(1024) void k_gemv_ksplit(GemvSplitArgs a) {
     __shared__ v4f red[16][4 * NG][64];
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
-    const int out = a.out0 + a.out1, kq = blockIdx.y, row0 = blockIdx.x * 64, part = n >> 3;
+    const int xcd = blockIdx.x & 7, rb = 2 * (blockIdx.x >> 3) + (xcd & 1);
+    const int out = a.out0 + a.out1, kq = xcd >> 1, row0 = rb * 64, part = n >> 3;
+    if (row0 >= out) return;  // the whole block
     const uint16_t *wr[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -298,7 +305,9 @@ hipError_t launch_gemv_ksplit(hipStream_t st, float *Y, size_t pstride, int ldy,
         (W1 && ((uintptr_t)W1 % 16) != 0) || out0 + out1 <= 0 || (B + 15) / 16 > 65535)
         return hipErrorInvalidValue;
     GemvSplitArgs a{Y, X, nullptr, W0, W1, pstride, ldy, ldx, B, out0, out1, in, 0};
-    const dim3 grid((out0 + out1 + 63) / 64, kGemvKs, 1);  // the block loops over the token groups
+    // 8 blocks per pair of 64-row blocks: row blocks 2m, 2m + 1 for the four k quarters
+    const int nrb = (out0 + out1 + 63) / 64;
+    const dim3 grid(8 * ((nrb + 1) / 2), 1, 1);  // the block loops over the token groups
     const bool two = B > 8;
     if (in == 2048) {
         if (two) hipLaunchKernelGGL((k_gemv_ksplit<2, 1>), grid, dim3(1024), 0, st, a);
