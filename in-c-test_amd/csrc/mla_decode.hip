@@ -1891,6 +1891,10 @@ __device__ __forceinline__ void q8_score_role(const AttnArgs &a, const SeqDesc &
     v4i qh[8], ql[8];
     v8bf qrh[2], qrl[2];
     float qsd[4], m_run[4], l_lane[4];
+    // the query's int8 scales first: the first chunk's scores need them right after P
+    float qsr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qsr[i] = a.qs[(size_t)b * 16 + 4 * g + i];
     // the sequence's query operands (hi, lo codes: 8 KB each; RoPE hi, lo: 2 KB each) once into
     // code slot 3 by DMA (wave w: 1 KB pieces 5w .. 5w+4), read from there by all four waves
     const uint32_t qslot = lds_addr(smem) + 3 * kQ8CodeB;
@@ -1937,7 +1941,7 @@ __device__ __forceinline__ void q8_score_role(const AttnArgs &a, const SeqDesc &
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        qsd[i] = a.qs[(size_t)b * 16 + 4 * g + i] * (a.smscale / 254.0f);
+        qsd[i] = qsr[i] * (a.smscale / 254.0f);
         m_run[i] = -INFINITY;
         l_lane[i] = 0.f;
     }
