@@ -143,7 +143,11 @@ struct GemvSplitArgs {
 // Block i: kq = (i % 8) / 2, row block 2 (i / 8) + i % 2; blocks past the last row block exit.
 static_assert(kGemvKs == 4, "two XCDs per k quarter");
 template <int NG, int KPW>
-__global__ __launch_bounds__(1024) void k_gemv_ksplit(GemvSplitArgs a) {
+__global__ __launch_bounds__(1024) void k_gemv_ksplit(const float *X, const uint16_t *W0, const uint16_t *W1, size_t pstride,
+                                                      int ldy, int ldx, int B, int out0, int out1, int in, float *Y) {
+    // scalar arguments: the first 14 dwords (everything but Y, which only the stores use) are
+    // preloaded into SGPRs at wave start (no argument round trip)
+    const GemvSplitArgs a{Y, X, nullptr, W0, W1, pstride, ldy, ldx, B, out0, out1, in, 0};
     __shared__ v4f red[16][4 * NG][64];
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
     const int xcd = blockIdx.x & 7, rb = 2 * (blockIdx.x >> 3) + (xcd & 1);
@@ -231,7 +235,10 @@ __global__ __launch_bounds__(1024) void k_gemv_ksplit(GemvSplitArgs a) {
 // 6.9 -> 6.5 us). Each output is the same sum in the same order for either RB.
 // Requires in = 16 * 32 * KPW.
 template <int NG, int KPW, int RB = 16>
-__global__ __launch_bounds__(1024) void k_gemv_xs(GemvSplitArgs a) {
+__global__ __launch_bounds__(1024) void k_gemv_xs(float *Y, const uint16_t *XS, const uint16_t *W0, int ldy, int B,
+                                                  int nout, int in, int acc) {
+    // scalar arguments: preloaded into SGPRs at wave start (no argument round trip)
+    const GemvSplitArgs a{Y, nullptr, XS, W0, nullptr, 0, ldy, 0, B, nout, 0, in, acc};
     static_assert(RB == 16 || RB == 8, "rows per block");
     __shared__ v4f red[16][NG][64];
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
@@ -304,17 +311,16 @@ hipError_t launch_gemv_ksplit(hipStream_t st, float *Y, size_t pstride, int ldy,
     if (!gemv_ksplit_ok(in, ldx) || B < 1 || ((uintptr_t)X % 16) != 0 || ((uintptr_t)W0 % 16) != 0 ||
         (W1 && ((uintptr_t)W1 % 16) != 0) || out0 + out1 <= 0 || (B + 15) / 16 > 65535)
         return hipErrorInvalidValue;
-    GemvSplitArgs a{Y, X, nullptr, W0, W1, pstride, ldy, ldx, B, out0, out1, in, 0};
     // 8 blocks per pair of 64-row blocks: row blocks 2m, 2m + 1 for the four k quarters
     const int nrb = (out0 + out1 + 63) / 64;
     const dim3 grid(8 * ((nrb + 1) / 2), 1, 1);  // the block loops over the token groups
     const bool two = B > 8;
     if (in == 2048) {
-        if (two) hipLaunchKernelGGL((k_gemv_ksplit<2, 1>), grid, dim3(1024), 0, st, a);
-        else hipLaunchKernelGGL((k_gemv_ksplit<1, 1>), grid, dim3(1024), 0, st, a);
+        if (two) hipLaunchKernelGGL((k_gemv_ksplit<2, 1>), grid, dim3(1024), 0, st, X, W0, W1, pstride, ldy, ldx, B, out0, out1, in, Y);
+        else hipLaunchKernelGGL((k_gemv_ksplit<1, 1>), grid, dim3(1024), 0, st, X, W0, W1, pstride, ldy, ldx, B, out0, out1, in, Y);
     } else {
-        if (two) hipLaunchKernelGGL((k_gemv_ksplit<2, 2>), grid, dim3(1024), 0, st, a);
-        else hipLaunchKernelGGL((k_gemv_ksplit<1, 2>), grid, dim3(1024), 0, st, a);
+        if (two) hipLaunchKernelGGL((k_gemv_ksplit<2, 2>), grid, dim3(1024), 0, st, X, W0, W1, pstride, ldy, ldx, B, out0, out1, in, Y);
+        else hipLaunchKernelGGL((k_gemv_ksplit<1, 2>), grid, dim3(1024), 0, st, X, W0, W1, pstride, ldy, ldx, B, out0, out1, in, Y);
     }
     return hipGetLastError();
 }
@@ -559,15 +565,14 @@ hipError_t launch_gemv_xs(hipStream_t st, float *Y, int ldy, const uint16_t *XS,
     if (!gemv_xs_ok(in) || B < 1 || ((uintptr_t)XS % 16) != 0 || ((uintptr_t)W % 16) != 0 || out <= 0 ||
         (B + 15) / 16 > 65535)
         return hipErrorInvalidValue;
-    GemvSplitArgs a{Y, nullptr, XS, W, nullptr, 0, ldy, 0, B, out, 0, in, accumulate ? 1 : 0};
     const dim3 grid((out + 15) / 16, 1, (B + 31) / 32);  // a block takes two token groups in turn
     const bool two = B > 8;
     if (in == 2048) {
-        if (two) hipLaunchKernelGGL((k_gemv_xs<2, 4>), grid, dim3(1024), 0, st, a);
-        else hipLaunchKernelGGL((k_gemv_xs<1, 4, 8>), dim3((out + 7) / 8, 1, grid.z), dim3(1024), 0, st, a);
+        if (two) hipLaunchKernelGGL((k_gemv_xs<2, 4>), grid, dim3(1024), 0, st, Y, XS, W, ldy, B, out, in, accumulate ? 1 : 0);
+        else hipLaunchKernelGGL((k_gemv_xs<1, 4, 8>), dim3((out + 7) / 8, 1, grid.z), dim3(1024), 0, st, Y, XS, W, ldy, B, out, in, accumulate ? 1 : 0);
     } else {
-        if (two) hipLaunchKernelGGL((k_gemv_xs<2, 8>), grid, dim3(1024), 0, st, a);
-        else hipLaunchKernelGGL((k_gemv_xs<1, 8>), grid, dim3(1024), 0, st, a);
+        if (two) hipLaunchKernelGGL((k_gemv_xs<2, 8>), grid, dim3(1024), 0, st, Y, XS, W, ldy, B, out, in, accumulate ? 1 : 0);
+        else hipLaunchKernelGGL((k_gemv_xs<1, 8>), grid, dim3(1024), 0, st, Y, XS, W, ldy, B, out, in, accumulate ? 1 : 0);
     }
     return hipGetLastError();
 }
@@ -1173,6 +1178,24 @@ struct AttnArgs {
     SeqTable t;
 };
 
+// The arguments a workgroup needs before its first loads, passed as leading scalar kernel
+// arguments: the leading scalar arguments, up to 14 dwords, are preloaded into SGPRs when the
+// wave starts (-amdgpu-kernarg-preload-count=16), so they cost no memory round trip. The order
+// puts first what the first loads need (members, nseq, the query operands); part, which only
+// the closing stores use, comes last and is read from the argument block.
+struct AttnHot {
+    float *part;
+    const float *qf;
+    const int8_t *qhi, *qlo;
+    const float *qs;
+    const uint16_t *qrhi, *qrlo;
+    int members, nseq;
+};
+#define KVL_ATTN_HOT_PARAMS                                                                        \
+    int members_, int nseq_, const int8_t *qhi_, const int8_t *qlo_, const uint16_t *qrhi_,         \
+        const uint16_t *qrlo_, const float *qs_, const float *qf_, float *part_
+#define KVL_ATTN_HOT_INIT const AttnHot h{part_, qf_, qhi_, qlo_, qs_, qrhi_, qrlo_, members_, nseq_}
+
 constexpr int kXcds = 8;  // XCDs of an MI355X; workgroups are dispatched to them round-robin
 
 // Block -> (sequence, split): splits of the sequences are numbered consecutively.
@@ -1193,19 +1216,19 @@ __device__ __forceinline__ int find_seq(const SeqTable &t, int bid) {
 // Sequence b's descriptor comes from desc_lane / desc_pick, b from a ballot over the lanes'
 // split0 (a lone decode's attention launch: 12.5 -> 10.3 us at 8K Q8 rows, 18.3 -> 16.5 us at
 // 32K against indexing the table by b once b is known).
-__device__ __forceinline__ bool seq_of(const AttnArgs &a, int &b, int &split, int &pidx, SeqDesc &s) {
+__device__ __forceinline__ bool seq_of(const AttnArgs &a, const AttnHot &h, int &b, int &split, int &pidx, SeqDesc &s) {
     const int sid = blockIdx.x, lane = threadIdx.x & 63;
     const DescLane m = desc_lane(a.t);
-    if (a.members > 0) {
+    if (h.members > 0) {
         const int j = sid / kXcds;
-        b = j % a.members;
-        split = kXcds * (j / a.members) + sid % kXcds;
+        b = j % h.members;
+        split = kXcds * (j / h.members) + sid % kXcds;
     } else {
-        b = __builtin_popcountll(__builtin_amdgcn_ballot_w64(lane >= 1 && lane < a.nseq && sid >= m.split0));
+        b = __builtin_popcountll(__builtin_amdgcn_ballot_w64(lane >= 1 && lane < h.nseq && sid >= m.split0));
         split = sid - lane_pick(m.split0, b);
     }
     s = desc_pick(m, b);
-    if (a.members > 0) {
+    if (h.members > 0) {
         if (split >= s.nsplit) return false;
         pidx = s.split0 + split;
     } else {
@@ -1378,13 +1401,14 @@ __device__ __forceinline__ v4s lds_read_tr16(const uint8_t *p) {
 }
 
 template <bool ONCE>  // ONCE: each history row is read by one workgroup (non-temporal loads)
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attn_bf16_mfma(AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attn_bf16_mfma(KVL_ATTN_HOT_PARAMS, AttnArgs a) {
+    KVL_ATTN_HOT_INIT;
     __shared__ __attribute__((aligned(16))) uint8_t smem[kB16SmemB];
     const int tid = threadIdx.x, l = tid & 63, n = l & 15, g = l >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     int b, split, pidx;
     SeqDesc s;
-    if (!seq_of(a, b, split, pidx, s)) return;
+    if (!seq_of(a, h, b, split, pidx, s)) return;
     const int r0 = split * s.rps;
     const int r1 = split == s.nsplit - 1 ? s.len : r0 + s.rps;  // last split takes the rest
     const int nch = (r1 - r0 + kB16Ch - 1) / kB16Ch;
@@ -1419,7 +1443,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     v8bf qh[9], ql[9];
     issue(0);
     {
-        const float *qrow = a.qf + ((size_t)b * 16 + n) * 576 + 8 * g + 32 * 9 * kh;
+        const float *qrow = h.qf + ((size_t)b * 16 + n) * 576 + 8 * g + 32 * 9 * kh;
         v4f qv[18];
 #pragma unroll
         for (int j = 0; j < 9; ++j) {
@@ -1520,7 +1544,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             acc[t] = mfma_bf16(pl, bt, acc[t]);
         }
     }
-    float *P = a.part + (size_t)pidx * 16 * 514;
+    float *P = h.part + (size_t)pidx * 16 * 514;
 #pragma unroll
     for (int t = 0; t < 8; ++t)
 #pragma unroll
@@ -1557,13 +1581,14 @@ typedef int v2i __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ int f32r_swz(int row) { return (row >> 1) & 7; }
 
 template <bool ONCE>  // ONCE: each history row is read by one workgroup (non-temporal loads)
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attn_f32_mfma(AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attn_f32_mfma(KVL_ATTN_HOT_PARAMS, AttnArgs a) {
+    KVL_ATTN_HOT_INIT;
     __shared__ __attribute__((aligned(16))) uint8_t smem[kF32SmemB];
     const int tid = threadIdx.x, l = tid & 63, n = l & 15, g = l >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     int b, split, pidx;
     SeqDesc s;
-    if (!seq_of(a, b, split, pidx, s)) return;
+    if (!seq_of(a, h, b, split, pidx, s)) return;
     const int r0 = split * s.rps;
     const int r1 = split == s.nsplit - 1 ? s.len : r0 + s.rps;  // last split takes the rest
     const int nch = (r1 - r0 + kF32Ch - 1) / kF32Ch;
@@ -1632,7 +1657,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     v8bf qh[9], ql[9];
     issue(0);
     {
-        const float *qrow = a.qf + ((size_t)b * 16 + n) * 576 + 8 * g + 32 * 9 * kh;
+        const float *qrow = h.qf + ((size_t)b * 16 + n) * 576 + 8 * g + 32 * 9 * kh;
         v4f qv[18];
 #pragma unroll
         for (int j = 0; j < 9; ++j) {
@@ -1736,7 +1761,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             acc[t] = mfma_bf16(pl, bt, acc[t]);
         }
     }
-    float *P = a.part + (size_t)pidx * 16 * 514;
+    float *P = h.part + (size_t)pidx * 16 * 514;
 #pragma unroll
     for (int t = 0; t < 8; ++t)
 #pragma unroll
@@ -1869,7 +1894,7 @@ __device__ __forceinline__ void put_q8_weights(int8_t *wqc, const float *pv, flo
 // same LDS flags after A, so all eight take the same barriers. Everything the score waves read
 // per chunk (codes, RoPE keys, scales) arrives in LDS by the mix waves' DMA, so their steps
 // never wait on global-memory latency.
-__device__ __forceinline__ void q8_score_role(const AttnArgs &a, const SeqDesc &sd, uint8_t *smem, int w, int b,
+__device__ __forceinline__ void q8_score_role(const AttnArgs &a, const AttnHot &h, const SeqDesc &sd, uint8_t *smem, int w, int b,
                                               int r0, int r1, int nch, int sid) {
     int8_t *wq = (int8_t *)(smem + kQ8WqOff);
     int *oflag = (int *)(smem + kQ8FlagOff);
@@ -1894,17 +1919,17 @@ __device__ __forceinline__ void q8_score_role(const AttnArgs &a, const SeqDesc &
     // the query's int8 scales first: the first chunk's scores need them right after P
     float qsr[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qsr[i] = a.qs[(size_t)b * 16 + 4 * g + i];
+    for (int i = 0; i < 4; ++i) qsr[i] = h.qs[(size_t)b * 16 + 4 * g + i];
     // the sequence's query operands (hi, lo codes: 8 KB each; RoPE hi, lo: 2 KB each) once into
     // code slot 3 by DMA (wave w: 1 KB pieces 5w .. 5w+4), read from there by all four waves
     const uint32_t qslot = lds_addr(smem) + 3 * kQ8CodeB;
 #pragma unroll
     for (int i = 0; i < 5; ++i) {
         const int p = 5 * w + i;
-        const int8_t *src = p < 8 ? a.qhi + (size_t)b * 8192 + p * 1024
-                          : p < 16 ? a.qlo + (size_t)b * 8192 + (p - 8) * 1024
-                          : p < 18 ? (const int8_t *)(a.qrhi + (size_t)b * 1024) + (p - 16) * 1024
-                                   : (const int8_t *)(a.qrlo + (size_t)b * 1024) + (p - 18) * 1024;
+        const int8_t *src = p < 8 ? h.qhi + (size_t)b * 8192 + p * 1024
+                          : p < 16 ? h.qlo + (size_t)b * 8192 + (p - 8) * 1024
+                          : p < 18 ? (const int8_t *)(h.qrhi + (size_t)b * 1024) + (p - 16) * 1024
+                                   : (const int8_t *)(h.qrlo + (size_t)b * 1024) + (p - 18) * 1024;
         dma_b128(src + 16 * l, qslot + (uint32_t)(p * 1024));
     }
     {
@@ -2042,7 +2067,7 @@ __device__ __forceinline__ void q8_score_role(const AttnArgs &a, const SeqDesc &
         for (int i = 0; i < 4; ++i) lsum[w * 16 + 4 * g + i] = l_lane[i];
     lds_barrier();  // end
     if (w == 0 && n == 0) {
-        float *P = a.part + (size_t)sid * 16 * 514;
+        float *P = h.part + (size_t)sid * 16 * 514;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int hh = 4 * g + i;
@@ -2053,7 +2078,7 @@ __device__ __forceinline__ void q8_score_role(const AttnArgs &a, const SeqDesc &
 }
 
 template <bool ONCE>
-__device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const SeqDesc &sd, uint8_t *smem, int mw, int b,
+__device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const AttnHot &h, const SeqDesc &sd, uint8_t *smem, int mw, int b,
                                             int r0, int r1, int nch, int sid) {
     const int8_t *wq = (const int8_t *)(smem + kQ8WqOff);
     const int *oflag = (const int *)(smem + kQ8FlagOff);
@@ -2204,7 +2229,7 @@ __device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const SeqDesc &sd
     // attention 33.5 -> 32.7 us per launch; the combine, which then reads every partial from
     // memory, +0.15 us). In the BF16 and FP32 kernels the same stores made no difference
     // beyond the noise of the ragged legs (±2 %), and they keep plain stores.
-    float *P = a.part + (size_t)sid * 16 * 514;
+    float *P = h.part + (size_t)sid * 16 * 514;
     const float wfac = kQ8Pmax * smax * (1.0f / (127.0f * 254.0f * 254.0f));
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
@@ -2218,17 +2243,18 @@ __device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const SeqDesc &sd
 }
 
 template <bool ONCE>  // ONCE: each history row is read by one workgroup (non-temporal loads)
-__global__ __launch_bounds__(512) void k_attn_q8_mfma(AttnArgs a) {
+__global__ __launch_bounds__(512) void k_attn_q8_mfma(KVL_ATTN_HOT_PARAMS, AttnArgs a) {
+    KVL_ATTN_HOT_INIT;
     __shared__ __attribute__((aligned(16))) uint8_t smem[kQ8SmemB];
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int b, split, pidx;
     SeqDesc s;
-    if (!seq_of(a, b, split, pidx, s)) return;
+    if (!seq_of(a, h, b, split, pidx, s)) return;
     const int r0 = split * s.rps;
     const int r1 = split == s.nsplit - 1 ? s.len : r0 + s.rps;  // last split takes the rest
     const int nch = (r1 - r0 + kQ8Ch - 1) / kQ8Ch;
-    if (w >= 4) q8_mix_role<ONCE>(a, s, smem, w - 4, b, r0, r1, nch, pidx);
-    else q8_score_role(a, s, smem, w, b, r0, r1, nch, pidx);
+    if (w >= 4) q8_mix_role<ONCE>(a, h, s, smem, w - 4, b, r0, r1, nch, pidx);
+    else q8_score_role(a, h, s, smem, w, b, r0, r1, nch, pidx);
 }
 
 hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t, const Dims &d,
@@ -2257,14 +2283,14 @@ hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t
         grid = kXcds * t.n * ((maxns + kXcds - 1) / kXcds);
     }
     if (kind == kAttnQ8Mfma) {
-        if (a.members > 0) hipLaunchKernelGGL(k_attn_q8_mfma<false>, dim3(grid), dim3(512), 0, st, a);
-        else hipLaunchKernelGGL(k_attn_q8_mfma<true>, dim3(grid), dim3(512), 0, st, a);
+        if (a.members > 0) hipLaunchKernelGGL(k_attn_q8_mfma<false>, dim3(grid), dim3(512), 0, st, a.members, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);
+        else hipLaunchKernelGGL(k_attn_q8_mfma<true>, dim3(grid), dim3(512), 0, st, a.members, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);
     } else if (kind == kAttnF32Mfma) {
-        if (a.members > 0) hipLaunchKernelGGL(k_attn_f32_mfma<false>, dim3(grid), dim3(256), 0, st, a);
-        else hipLaunchKernelGGL(k_attn_f32_mfma<true>, dim3(grid), dim3(256), 0, st, a);
+        if (a.members > 0) hipLaunchKernelGGL(k_attn_f32_mfma<false>, dim3(grid), dim3(256), 0, st, a.members, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);
+        else hipLaunchKernelGGL(k_attn_f32_mfma<true>, dim3(grid), dim3(256), 0, st, a.members, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);
     } else if (kind == kAttnBF16Mfma) {
-        if (a.members > 0) hipLaunchKernelGGL(k_attn_bf16_mfma<false>, dim3(grid), dim3(256), 0, st, a);
-        else hipLaunchKernelGGL(k_attn_bf16_mfma<true>, dim3(grid), dim3(256), 0, st, a);
+        if (a.members > 0) hipLaunchKernelGGL(k_attn_bf16_mfma<false>, dim3(grid), dim3(256), 0, st, a.members, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);
+        else hipLaunchKernelGGL(k_attn_bf16_mfma<true>, dim3(grid), dim3(256), 0, st, a.members, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);
     } else {
         const int P = fmt == kFmtExp ? t.n * d.NH : t.n;
         if (fmt == kFmtQ8)
@@ -2428,30 +2454,31 @@ __device__ __forceinline__ int mx_pos(int c) { return c ^ (((c >> 5) & 7) << 2);
 constexpr int kCombPre = 8;
 constexpr int kCombBlocks = 256;  // k_combine_r512 grid target: one round on the CUs of an MI355X
 constexpr int kCombWide = 16;     // k_combine_r512x8: at most this many splits per sequence
-__global__ __launch_bounds__(1024) void k_combine_r512(CombineArgs a) {
+__global__ __launch_bounds__(1024) void k_combine_r512(const float *part_, const uint16_t *kv_b_, float *ho_, uint16_t *hos_, int spb_, int nh_, int dn_, int n_, CombineArgs a) {
+    // leading scalar arguments: preloaded into SGPRs at wave start (no argument round trip)
     __shared__ float mx[512];
     __shared__ float wts[kMaxSplits];
     __shared__ v4f red[8][128];
     __shared__ float sinv;
     const DescLane dl = desc_lane(a.t);  // first: the partial loads wait for it
-    const int NH = a.d.NH, tid = threadIdx.x;
+    const int NH = nh_, tid = threadIdx.x;
     const int half = blockIdx.x & 1, gh = blockIdx.x >> 1, grp = gh / NH, h = gh % NH;
     const int dd = 64 * half + (tid >> 4), q = tid & 15;
-    const uint16_t *row = a.kv_b + ((size_t)h * (a.d.DN + 128) + a.d.DN + dd) * 512 + 32 * q;
+    const uint16_t *row = kv_b_ + ((size_t)h * (dn_ + 128) + dn_ + dd) * 512 + 32 * q;
     v4i wv[4];  // held for every sequence of the block
 #pragma unroll
     for (int c = 0; c < 4; ++c) wv[c] = *(const v4i *)(row + 8 * c);
     // split group: uniform within a wave (128-thread groups)
     const int sg = __builtin_amdgcn_readfirstlane(tid >> 7);
     const size_t stride = (size_t)NH * (512 + 2);
-    const int b_end = min((grp + 1) * a.spb, a.t.n);
-    for (int b = grp * a.spb; b < b_end; ++b) {
+    const int b_end = min((grp + 1) * spb_, n_);
+    for (int b = grp * spb_; b < b_end; ++b) {
         // column group of this thread, opaque to the compiler so that the per-split addresses
         // below are formed in each iteration instead of being held (spilled) across the loop
         int c4 = tid & 127;
         asm volatile("" : "+v"(c4));
         const int ns = lane_pick(dl.nsplit, b);
-        const float *P = a.part + (size_t)lane_pick(dl.split0, b) * stride;
+        const float *P = part_ + (size_t)lane_pick(dl.split0, b) * stride;
         const float *Pm = P + (size_t)NH * 512 + h;  // split i: m at Pm[i * stride], l at + NH
         float m0 = 0.f, l0 = 0.f;
         if (tid < 64) {
@@ -2536,11 +2563,11 @@ __global__ __launch_bounds__(1024) void k_combine_r512(CombineArgs a) {
         const float hsum = row16_sum(acc0 + acc1);  // the 16 lanes of row dd
         if (q == 0) {
             const size_t o = (size_t)b * a.d.HO + (size_t)h * 128 + dd;
-            a.ho[o] = hsum;
+            ho_[o] = hsum;
             uint16_t hi, lo;
             split_bf16(hsum, hi, lo);
-            a.hos[o] = hi;
-            a.hos[(size_t)a.t.n * a.d.HO + o] = lo;
+            hos_[o] = hi;
+            hos_[(size_t)n_ * a.d.HO + o] = lo;
         }
         __syncthreads();  // wts, red and mx are rewritten for the next sequence
     }
@@ -2553,24 +2580,25 @@ __global__ __launch_bounds__(1024) void k_combine_r512(CombineArgs a) {
 // the operations k_combine_r512 spreads over its threads -- then every thread takes its W_UV row
 // slice through the eight mixes. The outputs equal k_combine_r512's bit for bit, with W_UV read
 // once per 8 sequences and 8 times fewer blocks.
-__global__ __launch_bounds__(1024) void k_combine_r512x8(CombineArgs a) {
+__global__ __launch_bounds__(1024) void k_combine_r512x8(const float *part_, const uint16_t *kv_b_, float *ho_, uint16_t *hos_, int spb_, int nh_, int dn_, int n_, CombineArgs a) {
+    // leading scalar arguments: preloaded into SGPRs at wave start (no argument round trip)
     __shared__ float mx[8][512];
     __shared__ float wts[8][kCombWide];
     __shared__ float sinv[8];
     const DescLane dl = desc_lane(a.t);  // first: the partial loads wait for it
-    const int NH = a.d.NH, tid = threadIdx.x;
+    const int NH = nh_, tid = threadIdx.x;
     const int half = blockIdx.x & 1, gh = blockIdx.x >> 1, grp = gh / NH, h = gh % NH;
     const int dd = 64 * half + (tid >> 4), q = tid & 15;
-    const uint16_t *row = a.kv_b + ((size_t)h * (a.d.DN + 128) + a.d.DN + dd) * 512 + 32 * q;
+    const uint16_t *row = kv_b_ + ((size_t)h * (dn_ + 128) + dn_ + dd) * 512 + 32 * q;
     v4i wv[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) wv[c] = *(const v4i *)(row + 8 * c);
     const int j = __builtin_amdgcn_readfirstlane(tid >> 7), c4 = tid & 127, lw = tid & 127;
     const int b = grp * 8 + j;
-    const bool live = b < a.t.n;
+    const bool live = b < n_;
     const size_t stride = (size_t)NH * (512 + 2);
     const int ns = live ? lane_pick(dl.nsplit, b) : 0;
-    const float *P = a.part + (size_t)lane_pick(dl.split0, live ? b : 0) * stride;
+    const float *P = part_ + (size_t)lane_pick(dl.split0, live ? b : 0) * stride;
     const float *Pm = P + (size_t)NH * 512 + h;
     const float *Pg = P + (size_t)h * 512 + 4 * c4;
     v4f pre[kCombWide];
@@ -2613,7 +2641,7 @@ __global__ __launch_bounds__(1024) void k_combine_r512x8(CombineArgs a) {
     }
     __syncthreads();
 #pragma unroll 1
-    for (int jj = 0; jj < 8 && grp * 8 + jj < a.t.n; ++jj) {
+    for (int jj = 0; jj < 8 && grp * 8 + jj < n_; ++jj) {
         const float *mh = mx[jj];
         float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
@@ -2634,11 +2662,11 @@ __global__ __launch_bounds__(1024) void k_combine_r512x8(CombineArgs a) {
         const float hsum = row16_sum(acc0 + acc1);
         if (q == 0) {
             const size_t o = (size_t)(grp * 8 + jj) * a.d.HO + (size_t)h * 128 + dd;
-            a.ho[o] = hsum;
+            ho_[o] = hsum;
             uint16_t hi, lo;
             split_bf16(hsum, hi, lo);
-            a.hos[o] = hi;
-            a.hos[(size_t)a.t.n * a.d.HO + o] = lo;
+            hos_[o] = hi;
+            hos_[(size_t)n_ * a.d.HO + o] = lo;
         }
     }
 }
@@ -2650,12 +2678,12 @@ hipError_t launch_combine(hipStream_t st, int fmt, const SeqTable &t, const Dims
     int maxns = 0;
     for (int i = 0; i < t.n; ++i) maxns = max(maxns, t.s[i].nsplit);
     if (combine_writes_hos(fmt, d) && t.n >= 32 && maxns <= kCombWide) {
-        hipLaunchKernelGGL(k_combine_r512x8, dim3(2 * ((t.n + 7) / 8) * d.NH), dim3(1024), 0, st, a);
+        hipLaunchKernelGGL(k_combine_r512x8, dim3(2 * ((t.n + 7) / 8) * d.NH), dim3(1024), 0, st, a.part, a.kv_b, a.ho, a.hos, a.spb, d.NH, d.DN, t.n, a);
     } else if (combine_writes_hos(fmt, d)) {
         // up to kCombBlocks blocks; a block takes spb sequences of one (head, half) in turn
         a.spb = max(1, (2 * t.n * d.NH + kCombBlocks - 1) / kCombBlocks);
         const int groups = (t.n + a.spb - 1) / a.spb;
-        hipLaunchKernelGGL(k_combine_r512, dim3(2 * groups * d.NH), dim3(1024), 0, st, a);
+        hipLaunchKernelGGL(k_combine_r512, dim3(2 * groups * d.NH), dim3(1024), 0, st, a.part, a.kv_b, a.ho, a.hos, a.spb, d.NH, d.DN, t.n, a);
     } else {
         hipLaunchKernelGGL(k_combine, dim3(t.n * d.NH), dim3(256), 0, st, a);
     }
