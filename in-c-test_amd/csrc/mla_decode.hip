@@ -943,6 +943,7 @@ struct QprepArgs {
     uint16_t *qrhi, *qrlo;
     size_t pstride;
     int ldy, np, fmt, quantize;
+    int quarter;  // fp32 query rows by qprep_quarter (compressed formats, R = 512, DN = 128, DR = 64)
 };
 
 // One block per (sequence, head). Compressed formats: q_lat[r] = sum_d
@@ -1103,6 +1104,93 @@ __device__ __forceinline__ void qprep_body(const SeqTable &t, const Dims &d, con
     if (tid == 0) a.qs[(size_t)b * d.NH + h] = ok ? amax / 127.0f : 0.f;
 }
 
+// The fp32 query rows (the operands of the BF16 and FP32 attention and of the generic path)
+// for R = 512, DN = 128, DR = 64, a quarter of the latent columns per block: block (g8, h, qq)
+// prepares head h of the (up to) 8 sequences 8 g8 .. 8 g8 + 7 for latent columns 128 qq .. +127,
+// taking in a quarter of W_UK^T (32 KB) instead of all of it (qprep_body: one block per
+// sequence and head). q_lat = W_UK^T q_nope on MFMA with the 16 B-operand columns holding the
+// bf16 hi (0-7) and lo (8-15) parts of the 8 sequences' q_nope: every output element is the
+// same product chain as in qprep_body (hi column + lo column, k-steps in order), so the rows
+// are bit-identical to it. Wave w owns latent columns 128 qq + 32 w .. + 31 (W_UK^T fragments
+// (h, qq, 2w + t, ks)). The quarter-0 blocks also rotate q_rope (one pair per thread).
+__device__ __forceinline__ void qprep_quarter(const SeqTable &t, const QprepArgs &a, int blk, int NH) {
+    __shared__ __attribute__((aligned(16))) float qn8[8][132];  // q_nope of the 8 sequences
+    const DescLane dl = desc_lane(t);
+    const int g8 = blk / (NH * 4), h = (blk / 4) % NH, qq = blk & 3;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
+    const int nseq = min(8, t.n - 8 * g8);
+    v8bf wa[2][4];
+    {
+        const uint16_t *ut = a.ukt + ((size_t)((h * 4 + qq) * 8 + 2 * w) * 4 * 64 + l) * 8;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) wa[tt][ks] = *(const v8bf *)(ut + (size_t)(tt * 4 + ks) * 64 * 8);
+    }
+    // q_nope of sequence js = tid / 32, dims 4 (tid % 32) .. + 3: the partials added in order
+    const int js = tid >> 5, b = 8 * g8 + min(js, nseq - 1);
+    const float *qh = a.y + (size_t)b * a.ldy + (size_t)h * 192;
+    {
+        const float *p = qh + 4 * (tid & 31);
+        v4f v = *(const v4f *)p;
+        if (a.np == kGemvKs) {
+            v4f u[kGemvKs - 1];
+#pragma unroll
+            for (int q = 1; q < kGemvKs; ++q) u[q - 1] = *(const v4f *)(p + (size_t)q * a.pstride);
+#pragma unroll
+            for (int q = 1; q < kGemvKs; ++q) v += u[q - 1];
+        }
+        *(v4f *)&qn8[js][4 * (tid & 31)] = v;
+    }
+    // q_rope pair i = tid % 32 of sequence js (quarter-0 blocks)
+    float ev = 0.f, od = 0.f;
+    float2 cs = {0.f, 0.f};
+    if (qq == 0) {
+        const int i = tid & 31;
+        ev = sum_parts(qh + 128 + 2 * i, a.np, a.pstride);
+        od = sum_parts(qh + 128 + 2 * i + 1, a.np, a.pstride);
+        cs = a.cs[(size_t)__shfl(dl.pos, b) * 32 + i];  // b differs between the wave's halves
+    }
+    __syncthreads();
+    // B operand: column n = hi (n < 8) or lo (n >= 8) of sequence n & 7, k = 32 ks + 8 g .. + 7
+    v8bf qb[4];
+    {
+        const int m0 = n < 8 ? -1 : 0, m1 = n < 8 ? 0 : -1;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const v4f x0 = *(const v4f *)&qn8[n & 7][32 * ks + 8 * g];
+            const v4f x1 = *(const v4f *)&qn8[n & 7][32 * ks + 8 * g + 4];
+            v8bf hi, lo;
+            split8_cvt(x0, x1, hi, lo);
+            const v4i hv = __builtin_bit_cast(v4i, hi), lv = __builtin_bit_cast(v4i, lo);
+            qb[ks] = __builtin_bit_cast(v8bf, (hv & m0) | (lv & m1));
+        }
+    }
+    v4f acc[2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        acc[tt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) acc[tt] = mfma_bf16(wa[tt][ks], qb[ks], acc[tt]);
+    }
+    if (qq == 0 && js < nseq) {
+        const int i = tid & 31;
+        const float ec = ev * cs.x, os = od * cs.y, oc = od * cs.x, es = ev * cs.y;
+        float *qrow = a.qf + ((size_t)b * NH + h) * 576;
+        qrow[512 + i] = ec - os;
+        qrow[544 + i] = oc + es;
+    }
+    // lanes n < 8: q_lat of sequence n = hi column + lo column (lane n + 8: row_ror:8)
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        v4f v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = acc[tt][i] + dpp_f32<0x128>(acc[tt][i]);
+        if (n < 8 && n < nseq)
+            *(v4f *)(a.qf + ((size_t)(8 * g8 + n) * NH + h) * 576 + 128 * qq + 32 * w + 16 * tt + 4 * g) = v;
+    }
+}
+
 __global__ __launch_bounds__(256) void k_qprep(SeqTable t, Dims d, QprepArgs a) {
     qprep_body(t, d, a, blockIdx.x);
 }
@@ -1111,6 +1199,7 @@ __global__ __launch_bounds__(256) void k_qprep(SeqTable t, Dims d, QprepArgs a) 
 // read different parts of the same projection and are independent.
 __global__ __launch_bounds__(256) void k_append_qprep(SeqTable t, Dims d, AppendArgs aa, QprepArgs qa, int na) {
     if ((int)blockIdx.x < na) append_body(t, d, aa, blockIdx.x);
+    else if (qa.quarter) qprep_quarter(t, qa, blockIdx.x - na, d.NH);
     else qprep_body(t, d, qa, blockIdx.x - na);
 }
 
@@ -1132,6 +1221,7 @@ static QprepArgs qprep_args(int fmt, const Dims &d, const uint16_t *kv_b, const 
     a.pstride = w.ypstride;
     a.fmt = fmt;
     a.quantize = quantize ? 1 : 0;
+    a.quarter = 0;
     return a;
 }
 
@@ -1152,8 +1242,12 @@ hipError_t launch_append_qprep(hipStream_t st, int fmt, const SeqTable &t, const
         return hipErrorInvalidValue;
     const AppendArgs aa = append_args(fmt, d, y, ldy, koff, ynp, ypstride, kv_a_norm, eps, rope_cs, w,
                                       false, 0);
-    const QprepArgs qa = qprep_args(fmt, d, kv_b, ukt, rope_cs, w, quantize);
-    hipLaunchKernelGGL(k_append_qprep, dim3(t.n + t.n * d.NH), dim3(256), 0, st, t, d, aa, qa, t.n);
+    QprepArgs qa = qprep_args(fmt, d, kv_b, ukt, rope_cs, w, quantize);
+    // fp32 query rows (no int8 operands): a quarter of the latent columns per block
+    qa.quarter = !quantize && fmt != kFmtExp && d.R == 512 && d.DN == 128 && d.DR == 64 && d.QD == 192 &&
+                 ukt != nullptr ? 1 : 0;
+    const int nq = qa.quarter ? (t.n + 7) / 8 * d.NH * 4 : t.n * d.NH;
+    hipLaunchKernelGGL(k_append_qprep, dim3(t.n + nq), dim3(256), 0, st, t, d, aa, qa, t.n);
     return hipGetLastError();
 }
 
