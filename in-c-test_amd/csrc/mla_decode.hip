@@ -227,20 +227,22 @@ __global__ __launch_bounds__(1024) void k_gemv_ksplit(const float *X, const uint
 }
 
 // Y[b, o] (+)= sum_k W[o, k] (hi + lo)[b, k] with the activations already split into bf16
-// planes by their producer: RB (16 or 8) output rows per block, 16 waves splitting k, one
+// planes by their producer: RB (16 or 8) output rows per block, NW waves splitting k, one
 // 16-byte activation load and one MFMA per k-block and sequence group; the 16-token groups are
 // taken in turn with the weights held in registers. With RB = 8, MFMA rows 8-15 repeat rows
 // 0-7 and are not stored: a block then takes in 32 KB of weights instead of 64 KB beside the
 // 64 KB of activations every block reads, and the grid covers twice the CUs (o_proj at batch 8:
-// 6.9 -> 6.5 us). Each output is the same sum in the same order for either RB.
-// Requires in = 16 * 32 * KPW.
-template <int NG, int KPW, int RB = 16>
-__global__ __launch_bounds__(1024) void k_gemv_xs(float *Y, const uint16_t *XS, const uint16_t *W0, int ldy, int B,
+// 6.9 -> 6.5 us). Each output is the same sum in the same order for either RB and NG. With
+// in = 2048, four waves of 16 k-blocks each (the same loads in flight per block, a quarter of
+// the waves to launch) measured 6.16 -> 5.89 us per launch in the batch-8 decode stack.
+// Requires in = NW * 32 * KPW.
+template <int NG, int KPW, int RB = 16, int NW = 16>
+__global__ __launch_bounds__(64 * NW) void k_gemv_xs(float *Y, const uint16_t *XS, const uint16_t *W0, int ldy, int B,
                                                   int nout, int in, int acc) {
     // scalar arguments: preloaded into SGPRs at wave start (no argument round trip)
     const GemvSplitArgs a{Y, nullptr, XS, W0, nullptr, 0, ldy, 0, B, nout, 0, in, acc};
     static_assert(RB == 16 || RB == 8, "rows per block");
-    __shared__ v4f red[16][NG][64];
+    __shared__ v4f red[NW][NG][64];
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
     const int out = a.out0, part = n >> 3;
     const uint16_t *wrow = a.W0 + (size_t)min((int)blockIdx.x * RB + (n % RB), out - 1) * a.in;
@@ -286,7 +288,7 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(float *Y, const uint16_t *XS, 
             for (int gi = 0; gi < NG; ++gi) {
                 v4f s = red[0][gi][l];
 #pragma unroll
-                for (int q = 1; q < 16; ++q) s += red[q][gi][l];
+                for (int q = 1; q < NW; ++q) s += red[q][gi][l];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) s[i] += dpp_f32<0x128>(s[i]);
                 const int b = bz + 8 * gi + n;
@@ -568,8 +570,10 @@ hipError_t launch_gemv_xs(hipStream_t st, float *Y, int ldy, const uint16_t *XS,
     const dim3 grid((out + 15) / 16, 1, (B + 31) / 32);  // a block takes two token groups in turn
     const bool two = B > 8;
     if (in == 2048) {
-        if (two) hipLaunchKernelGGL((k_gemv_xs<2, 4>), grid, dim3(1024), 0, st, Y, XS, W, ldy, B, out, in, accumulate ? 1 : 0);
-        else hipLaunchKernelGGL((k_gemv_xs<1, 4, 8>), dim3((out + 7) / 8, 1, grid.z), dim3(1024), 0, st, Y, XS, W, ldy, B, out, in, accumulate ? 1 : 0);
+        // four waves at every batch size: each output is the same sum in the same order whatever
+        // the batch (a block decode's members equal lone decodes bit for bit)
+        if (two) hipLaunchKernelGGL((k_gemv_xs<2, 16, 16, 4>), grid, dim3(256), 0, st, Y, XS, W, ldy, B, out, in, accumulate ? 1 : 0);
+        else hipLaunchKernelGGL((k_gemv_xs<1, 16, 8, 4>), dim3((out + 7) / 8, 1, grid.z), dim3(256), 0, st, Y, XS, W, ldy, B, out, in, accumulate ? 1 : 0);
     } else {
         if (two) hipLaunchKernelGGL((k_gemv_xs<2, 8>), grid, dim3(1024), 0, st, Y, XS, W, ldy, B, out, in, accumulate ? 1 : 0);
         else hipLaunchKernelGGL((k_gemv_xs<1, 8>), grid, dim3(1024), 0, st, Y, XS, W, ldy, B, out, in, accumulate ? 1 : 0);
@@ -2548,13 +2552,16 @@ __device__ __forceinline__ int mx_pos(int c) { return c ^ (((c >> 5) & 7) << 2);
 constexpr int kCombPre = 8;
 constexpr int kCombBlocks = 256;  // k_combine_r512 grid target: one round on the CUs of an MI355X
 constexpr int kCombWide = 16;     // k_combine_r512x8: at most this many splits per sequence
-__global__ __launch_bounds__(1024) void k_combine_r512(const float *part_, const uint16_t *kv_b_, float *ho_, uint16_t *hos_, int spb_, int nh_, int dn_, int n_, CombineArgs a) {
+__global__ __launch_bounds__(1024) void k_combine_r512(const float *part_, const uint16_t *kv_b_, float *ho_, uint16_t *hos_, int spb_, int nh_, int dn_, int n_, int un_, CombineArgs a) {
     // leading scalar arguments: preloaded into SGPRs at wave start (no argument round trip)
     __shared__ float mx[512];
     __shared__ float wts[kMaxSplits];
     __shared__ v4f red[8][128];
     __shared__ float sinv;
-    const DescLane dl = desc_lane(a.t);  // first: the partial loads wait for it
+    // un_ > 0: every sequence has un_ splits, sequence b's starting at split b * un_, and the
+    // partial loads need no descriptor (one memory round trip less before them)
+    DescLane dl{};
+    if (un_ == 0) dl = desc_lane(a.t);  // first: the partial loads wait for it
     const int NH = nh_, tid = threadIdx.x;
     const int half = blockIdx.x & 1, gh = blockIdx.x >> 1, grp = gh / NH, h = gh % NH;
     const int dd = 64 * half + (tid >> 4), q = tid & 15;
@@ -2571,8 +2578,8 @@ __global__ __launch_bounds__(1024) void k_combine_r512(const float *part_, const
         // below are formed in each iteration instead of being held (spilled) across the loop
         int c4 = tid & 127;
         asm volatile("" : "+v"(c4));
-        const int ns = lane_pick(dl.nsplit, b);
-        const float *P = part_ + (size_t)lane_pick(dl.split0, b) * stride;
+        const int ns = un_ > 0 ? un_ : lane_pick(dl.nsplit, b);
+        const float *P = part_ + (size_t)(un_ > 0 ? b * un_ : lane_pick(dl.split0, b)) * stride;
         const float *Pm = P + (size_t)NH * 512 + h;  // split i: m at Pm[i * stride], l at + NH
         float m0 = 0.f, l0 = 0.f;
         if (tid < 64) {
@@ -2769,15 +2776,18 @@ hipError_t launch_combine(hipStream_t st, int fmt, const SeqTable &t, const Dims
                           const uint16_t *kv_b, const DecodeWork &w) {
     if (d.R > kMaxR) return hipErrorInvalidValue;
     CombineArgs a{t, d, w.part, kv_b, w.mix, w.ho, w.hos, fmt, 1};
-    int maxns = 0;
-    for (int i = 0; i < t.n; ++i) maxns = max(maxns, t.s[i].nsplit);
+    int maxns = 0, un = t.n > 0 ? t.s[0].nsplit : 0;
+    for (int i = 0; i < t.n; ++i) {
+        maxns = max(maxns, t.s[i].nsplit);
+        if (t.s[i].nsplit != un || t.s[i].split0 != i * un) un = 0;
+    }
     if (combine_writes_hos(fmt, d) && t.n >= 32 && maxns <= kCombWide) {
         hipLaunchKernelGGL(k_combine_r512x8, dim3(2 * ((t.n + 7) / 8) * d.NH), dim3(1024), 0, st, a.part, a.kv_b, a.ho, a.hos, a.spb, d.NH, d.DN, t.n, a);
     } else if (combine_writes_hos(fmt, d)) {
         // up to kCombBlocks blocks; a block takes spb sequences of one (head, half) in turn
         a.spb = max(1, (2 * t.n * d.NH + kCombBlocks - 1) / kCombBlocks);
         const int groups = (t.n + a.spb - 1) / a.spb;
-        hipLaunchKernelGGL(k_combine_r512, dim3(2 * groups * d.NH), dim3(1024), 0, st, a.part, a.kv_b, a.ho, a.hos, a.spb, d.NH, d.DN, t.n, a);
+        hipLaunchKernelGGL(k_combine_r512, dim3(2 * groups * d.NH), dim3(1024), 0, st, a.part, a.kv_b, a.ho, a.hos, a.spb, d.NH, d.DN, t.n, un, a);
     } else {
         hipLaunchKernelGGL(k_combine, dim3(t.n * d.NH), dim3(256), 0, st, a);
     }

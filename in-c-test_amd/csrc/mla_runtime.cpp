@@ -291,28 +291,47 @@ bool kimi_attn(const Dims &d) { return d.NH == 16 && d.R == 512 && d.DR == 64; }
 
 // ---------------------------------------------------------------- weights ---------------
 
-uint64_t fnv(uint64_t h, const void *p, size_t n) {
-    const unsigned char *b = (const unsigned char *)p;
-    for (size_t i = 0; i < n; ++i) {
-        h ^= b[i];
-        h *= 0x100000001b3ull;
+// Word-wise digest state: four independent multiply-xorshift lanes, so the sampled words are
+// mixed in parallel (a byte-serial hash of the 5.8 KB that the five weight arrays' samples
+// hold cost ≈ 5 µs per host call; this takes well under one).
+struct Digest {
+    uint64_t v[4] = {0x243f6a8885a308d3ull, 0x13198a2e03707344ull, 0xa4093822299f31d0ull, 0x082efa98ec4e6c89ull};
+    static uint64_t mix(uint64_t h, uint64_t w) {
+        h = (h ^ w) * 0x9e3779b97f4a7c15ull;
+        return h ^ (h >> 29);
     }
-    return h;
-}
+    // bytes [p, p + n): whole 32-byte groups over the four lanes, then the tail bytes
+    void add(const void *p, size_t n) {
+        const unsigned char *b = (const unsigned char *)p;
+        size_t i = 0;
+        for (; i + 32 <= n; i += 32)
+            for (int k = 0; k < 4; ++k) {
+                uint64_t w;
+                memcpy(&w, b + i + 8 * k, 8);
+                v[k] = mix(v[k], w);
+            }
+        for (int k = 0; i < n; ++i, k = (k + 1) & 3) v[k] = mix(v[k], b[i]);
+    }
+    uint64_t value() const { return mix(mix(v[0], v[1]), mix(v[2], v[3])); }
+};
 
 // Digest of 18 sampled 64-byte windows (first, last and 16 evenly spaced) plus the size.
 uint64_t sample_digest(const void *p, size_t bytes) {
-    uint64_t h = fnv(0xcbf29ce484222325ull, &bytes, sizeof bytes);
+    Digest h;
+    h.add(&bytes, sizeof bytes);
     const unsigned char *b = (const unsigned char *)p;
     const size_t win = 64;
-    if (bytes <= 18 * win) return fnv(h, b, bytes);
-    h = fnv(h, b, win);
-    h = fnv(h, b + bytes - win, win);
+    if (bytes <= 18 * win) {
+        h.add(b, bytes);
+        return h.value();
+    }
+    h.add(b, win);
+    h.add(b + bytes - win, win);
     for (int i = 1; i <= 16; ++i) {
         const size_t off = (bytes - win) / 17 * (size_t)i;
-        h = fnv(h, b + off, win);
+        h.add(b + off, win);
     }
-    return h;
+    return h.value();
 }
 
 int dev_weight(const uint16_t *host, size_t elems, const uint16_t **out) {
