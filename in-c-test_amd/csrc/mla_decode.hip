@@ -2563,7 +2563,12 @@ __global__ __launch_bounds__(1024) void k_combine_r512(const float *part_, const
     DescLane dl{};
     if (un_ == 0) dl = desc_lane(a.t);  // first: the partial loads wait for it
     const int NH = nh_, tid = threadIdx.x;
-    const int half = blockIdx.x & 1, gh = blockIdx.x >> 1, grp = gh / NH, h = gh % NH;
+    // block i takes half i / (grid / 2): both halves of a (sequence, head) run on one XCD
+    // (workgroup i on XCD i % 8, NH % 8 == 0), so its split partials, written to memory with
+    // non-temporal stores by the attention, come into that XCD's L2 once for the two blocks
+    // (the headline stack: 6.34 -> 5.38 us per launch against adjacent halves)
+    const int ngh = (int)gridDim.x >> 1, half = (int)blockIdx.x >= ngh;
+    const int gh = (int)blockIdx.x - half * ngh, grp = gh / NH, h = gh % NH;
     const int dd = 64 * half + (tid >> 4), q = tid & 15;
     const uint16_t *row = kv_b_ + ((size_t)h * (dn_ + 128) + dn_ + dd) * 512 + 32 * q;
     v4i wv[4];  // held for every sequence of the block
