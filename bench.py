@@ -278,13 +278,74 @@ def main():
             L.kvl_mla_graph_destroy(tg)
         else:
             L.kvl_mla_timing_read(ms, cnt)
-    attn_gbs = hist_bytes / (attn_ms * 1e-3) / 1e9
+    # The attention launch of this workload also prepares the queries and appends the rows
+    # (kvl_mla_set_fused_qprep): its algorithmic bytes are the history rows plus W_UK^T, the
+    # q_proj | kv_a partials it reads and the query operands and rows it writes.
+    H_, NH_, R_, DN_, DR_ = cfg.hidden_size, cfg.num_heads, cfg.kv_lora_rank, cfg.qk_nope_dim, cfg.qk_rope_dim
+    QO_, KVO_ = NH_ * (DN_ + DR_), R_ + DR_
+    fused_extra = (2 * NH_ * R_ * DN_ + 4 * 4 * B * (QO_ + KVO_) + B * NH_ * (2 * R_ + 4 + 4 * DR_)
+                   + B * Q8_ROW)
+    attn_bytes = hist_bytes + fused_extra
+    attn_gbs = attn_bytes / (attn_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_bytes(B, CTX),
-                "kernel": "k_attn_q8_mfma", "algorithmic_bytes_per_launch": hist_bytes,
+                "kernel": "k_attn_q8_mfma<true, true> (attention with the query preparation and the "
+                          "row append of its sequences)",
+                "algorithmic_bytes_per_launch": attn_bytes, "history_bytes_per_launch": hist_bytes,
                 "avg_launch_ms": round(attn_ms, 5), "timing": attn_src}
     if attn_only_ms is not None:
         roofline["avg_launch_ms_attention_events_only"] = round(attn_only_ms, 5)
+
+    # The same step in the two-launch form (append + query preparation in a launch of their own,
+    # then the attention alone): its step time, and the attention kernel's rate over the history
+    # bytes, from the stage events inside the step graph as above.
+    two = None
+    if graph is not None:
+        prev_form = L.kvl_mla_set_fused_qprep(0)
+        try:
+            lib.check(L.kvl_mla_capture_begin(), "capture begin")
+            try:
+                step()
+            finally:
+                g2 = C.c_void_p()
+                rc = L.kvl_mla_capture_end(C.byref(g2))
+            lib.check(rc, "capture end (two-launch form)")
+            for _ in range(max(1, args.warmup)):
+                lib.check(L.kvl_mla_graph_launch(g2), "graph launch")
+            lib.check(L.kvl_mla_synchronize(), "sync")
+            t0 = time.perf_counter()
+            for _ in range(K):
+                lib.check(L.kvl_mla_graph_launch(g2), "graph launch")
+            lib.check(L.kvl_mla_synchronize(), "sync")
+            two_ms = (time.perf_counter() - t0) * 1e3 / K
+            L.kvl_mla_graph_destroy(g2)
+            lib.check(L.kvl_mla_timing_enable(2), "timing on (graph)")
+            lib.check(L.kvl_mla_capture_begin(), "capture begin")
+            try:
+                step()
+            finally:
+                g3 = C.c_void_p()
+                rc = L.kvl_mla_capture_end(C.byref(g3))
+            lib.check(L.kvl_mla_timing_enable(0), "timing off")
+            lib.check(rc, "capture end (two-launch form, stage events)")
+            for _ in range(3):
+                lib.check(L.kvl_mla_graph_launch(g3), "graph launch")
+            lib.check(L.kvl_mla_synchronize(), "sync")
+            lib.check(L.kvl_mla_timing_read(ms, cnt), "timing read")
+            L.kvl_mla_graph_destroy(g3)
+            st2 = {name: ms[i] / cnt[i] for i, name in enumerate(lib.STAGES) if cnt[i]}
+            a2 = st2["attention"]
+            two = {"ms_per_step": round(two_ms, 4), "attention_ms": round(a2, 5),
+                   "append_qprep_ms": round(st2.get("append_qprep", 0.0), 5),
+                   "attention_achieved": round(hist_bytes / (a2 * 1e-3) / 1e9, 1),
+                   "attention_frac": round(hist_bytes / (a2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                   "kernel": "k_attn_q8_mfma<true, false>", "timing": "events recorded inside the step graph"}
+            log(f"[bench] two-launch form: step {two_ms:.3f} ms; attention {a2 * 1e3:.2f} us "
+                f"({two['attention_achieved']:.1f} GB/s), append + query prep {two['append_qprep_ms'] * 1e3:.2f} us")
+        finally:
+            L.kvl_mla_set_fused_qprep(prev_form)
+    if two is not None:
+        roofline["two_launch_form"] = two
 
     result = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": K,

@@ -144,7 +144,8 @@ struct GemvSplitArgs {
 static_assert(kGemvKs == 4, "two XCDs per k quarter");
 template <int NG, int KPW>
 __global__ __launch_bounds__(1024) void k_gemv_ksplit(const float *X, const uint16_t *W0, const uint16_t *W1, size_t pstride,
-                                                      int ldy, int ldx, int B, int out0, int out1, int in, float *Y) {
+                                                      int ldy, int ldx, int B, int out0, int out1, int in, float *Y,
+                                                      unsigned *zf, int nz) {
     // scalar arguments: the first 14 dwords (everything but Y, which only the stores use) are
     // preloaded into SGPRs at wave start (no argument round trip)
     const GemvSplitArgs a{Y, X, nullptr, W0, W1, pstride, ldy, ldx, B, out0, out1, in, 0};
@@ -152,6 +153,8 @@ __global__ __launch_bounds__(1024) void k_gemv_ksplit(const float *X, const uint
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
     const int xcd = blockIdx.x & 7, rb = 2 * (blockIdx.x >> 3) + (xcd & 1);
     const int out = a.out0 + a.out1, kq = xcd >> 1, row0 = rb * 64, part = n >> 3;
+    // block 0 (row block 0 of k quarter 0, never empty) clears the next launch's flags
+    if (blockIdx.x == 0 && zf != nullptr && tid < nz) zf[(size_t)tid * kFqFlagStride] = 0u;
     if (row0 >= out) return;  // the whole block
     const uint16_t *wr[4];
 #pragma unroll
@@ -309,20 +312,21 @@ bool gemv_ksplit_ok(int in, int ldx) { return (in == 2048 || in == 4096) && ldx 
 
 hipError_t launch_gemv_ksplit(hipStream_t st, float *Y, size_t pstride, int ldy, const float *X,
                               int ldx, int B, const uint16_t *W0, int out0, const uint16_t *W1,
-                              int out1, int in) {
+                              int out1, int in, unsigned *zero_flags, int nzero) {
     if (!gemv_ksplit_ok(in, ldx) || B < 1 || ((uintptr_t)X % 16) != 0 || ((uintptr_t)W0 % 16) != 0 ||
-        (W1 && ((uintptr_t)W1 % 16) != 0) || out0 + out1 <= 0 || (B + 15) / 16 > 65535)
+        (W1 && ((uintptr_t)W1 % 16) != 0) || out0 + out1 <= 0 || (B + 15) / 16 > 65535 || nzero < 0 ||
+        nzero > 1024 || (nzero > 0 && zero_flags == nullptr))
         return hipErrorInvalidValue;
     // 8 blocks per pair of 64-row blocks: row blocks 2m, 2m + 1 for the four k quarters
     const int nrb = (out0 + out1 + 63) / 64;
     const dim3 grid(8 * ((nrb + 1) / 2), 1, 1);  // the block loops over the token groups
     const bool two = B > 8;
     if (in == 2048) {
-        if (two) hipLaunchKernelGGL((k_gemv_ksplit<2, 1>), grid, dim3(1024), 0, st, X, W0, W1, pstride, ldy, ldx, B, out0, out1, in, Y);
-        else hipLaunchKernelGGL((k_gemv_ksplit<1, 1>), grid, dim3(1024), 0, st, X, W0, W1, pstride, ldy, ldx, B, out0, out1, in, Y);
+        if (two) hipLaunchKernelGGL((k_gemv_ksplit<2, 1>), grid, dim3(1024), 0, st, X, W0, W1, pstride, ldy, ldx, B, out0, out1, in, Y, zero_flags, nzero);
+        else hipLaunchKernelGGL((k_gemv_ksplit<1, 1>), grid, dim3(1024), 0, st, X, W0, W1, pstride, ldy, ldx, B, out0, out1, in, Y, zero_flags, nzero);
     } else {
-        if (two) hipLaunchKernelGGL((k_gemv_ksplit<2, 2>), grid, dim3(1024), 0, st, X, W0, W1, pstride, ldy, ldx, B, out0, out1, in, Y);
-        else hipLaunchKernelGGL((k_gemv_ksplit<1, 2>), grid, dim3(1024), 0, st, X, W0, W1, pstride, ldy, ldx, B, out0, out1, in, Y);
+        if (two) hipLaunchKernelGGL((k_gemv_ksplit<2, 2>), grid, dim3(1024), 0, st, X, W0, W1, pstride, ldy, ldx, B, out0, out1, in, Y, zero_flags, nzero);
+        else hipLaunchKernelGGL((k_gemv_ksplit<1, 2>), grid, dim3(1024), 0, st, X, W0, W1, pstride, ldy, ldx, B, out0, out1, in, Y, zero_flags, nzero);
     }
     return hipGetLastError();
 }
@@ -1275,6 +1279,7 @@ struct AttnArgs {
     int nseq;     // = t.n
     Dims d;
     SeqTable t;
+    FqArgs fq;    // the fused query preparation and append (k_attn_q8_mfma<., true>)
 };
 
 // The arguments a workgroup needs before its first loads, passed as leading scalar kernel
@@ -1919,6 +1924,243 @@ constexpr int kQ8SmOff = kQ8LsOff + 4 * 16 * 4;     // [4] largest row scale per
 constexpr int kQ8SmemB = kQ8SmOff + 4 * 4;
 static_assert(kQ8SmemB <= 160 * 1024, "LDS of one CU");
 
+// ---- query preparation and row append inside the Q8 attention launch ----------------------
+// The Kimi-shape decode with the q_proj | kv_a partials of k_gemv_ksplit: instead of a launch of
+// its own (k_append_qprep), the work is done by the attention's lowest-numbered workgroups ahead
+// of their own split: block i < 16 B prepares the query of (sequence i / 16, head i % 16), block
+// 16 B + b appends sequence b's row, with all 512 threads and the arithmetic of qprep_body /
+// append_body (so the query operands and the rows are bit-identical to theirs). The results are
+// written with device-scope (sc1) stores, which reach memory without a write-back of the L2, and
+// counted on per-sequence flags with device-scope atomics; a workgroup's score waves wait for the
+// 16 heads of its sequence before they load its query, and the split that holds the new row waits
+// for its append before that row's chunk is requested. Workgroups are dispatched in index order,
+// so the producers have started whenever anything waits on them; the waits are bounded anyway
+// (a timeout raises FqArgs::err and the launch ends with wrong values instead of hanging).
+constexpr uint64_t kFqSpinTicks = 2000000;  // 20 ms of the 100 MHz real-time counter
+
+__device__ __forceinline__ void st_sc1_b32(void *p, uint32_t v) {
+    asm volatile("global_store_dword %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void st_sc1_b16(void *p, uint32_t v) {
+    asm volatile("global_store_short %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ float ld_sc1_f32(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Flag words 128 bytes apart (one line each: the polls of one sequence do not queue behind
+// another's at the memory side): query heads of sequence b at kFqFlagStride * b, its row at
+// kFqFlagStride * (kMaxBatch + b).
+__device__ __forceinline__ unsigned *fq_qflag(const FqArgs &f, int b) { return f.flags + (size_t)kFqFlagStride * b; }
+__device__ __forceinline__ unsigned *fq_aflag(const FqArgs &f, int b) {
+    return f.flags + (size_t)kFqFlagStride * (kMaxBatch + b);
+}
+
+// Lane 0 of the calling wave polls *flag until it reaches target (bounded); the wave's later
+// loads are issued after the poll has returned.
+__device__ __forceinline__ void fq_wait(const FqArgs &f, const unsigned *flag, unsigned target) {
+    if ((threadIdx.x & 63) == 0) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+            if (__builtin_amdgcn_s_memrealtime() - t0 > kFqSpinTicks) {
+                __hip_atomic_store(f.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
+}
+
+// Max / double sum over the eight waves of a 512-thread workgroup (waves without values pass
+// 0, the neutral element of both: the results equal block256_max / block256_sum_f64 over the
+// first four waves bit for bit). red8: 8 entries.
+__device__ __forceinline__ float block512_max(float v, float *red8) {
+    v = wave_max(v);
+    if ((threadIdx.x & 63) == 0) red8[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(fmaxf(red8[0], red8[1]), fmaxf(red8[2], red8[3])),
+                 fmaxf(fmaxf(red8[4], red8[5]), fmaxf(red8[6], red8[7])));
+}
+__device__ __forceinline__ double block512_sum_f64(double v, double *red8) {
+    v = wave_sum_f64(v);
+    if ((threadIdx.x & 63) == 0) red8[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return ((red8[0] + red8[1]) + (red8[2] + red8[3])) + ((red8[4] + red8[5]) + (red8[6] + red8[7]));
+}
+
+// Query of (sequence b, head h): qprep_body's Q8 path for R = 512, DN = 128, DR = 64, QD = 192
+// over 8 waves (wave w: latent tiles 4 (w & 1) .. +3 of qprep_body's wave w >> 1). scr: 2848 B.
+__device__ __forceinline__ void fq_qprep(const FqArgs &f, const AttnHot &hh, const SeqDesc &s, int b, int h,
+                                         uint8_t *scr) {
+    float *qn = (float *)scr, *qr = qn + 128, *ql = qr + 64, *red = ql + 512;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
+    const int w4 = w >> 1, t0 = 4 * (w & 1);
+    const uint16_t *ut = f.ukt + ((size_t)(h * 4 + w4) * 32 * 64 + l) * 8;
+    v8bf wa[4][4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) wa[tt][ks] = *(const v8bf *)(ut + (size_t)((t0 + tt) * 4 + ks) * 64 * 8);
+    const float *qh = f.y + (size_t)b * f.ldy + (size_t)h * 192;
+    if (tid < 192) {
+        const float v = sum_parts(qh + tid, kGemvKs, f.pstride);
+        if (tid < 128) qn[tid] = v;
+        else qr[tid - 128] = v;
+    }
+    const float2 csv = tid < 32 ? f.cs[(size_t)s.pos * 32 + tid] : float2{0.f, 0.f};
+    __syncthreads();
+    const int m0 = n == 0 ? -1 : 0, m1 = n == 1 ? -1 : 0;
+    v8bf qb[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const v4f x0 = *(const v4f *)(qn + 32 * ks + 8 * g), x1 = *(const v4f *)(qn + 32 * ks + 8 * g + 4);
+        v8bf hi, lo;
+        split8_cvt(x0, x1, hi, lo);
+        const v4i hv = __builtin_bit_cast(v4i, hi), lv = __builtin_bit_cast(v4i, lo);
+        qb[ks] = __builtin_bit_cast(v8bf, (hv & m0) | (lv & m1));
+    }
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+        v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) acc = mfma_bf16(wa[tt][ks], qb[ks], acc);
+        v4f v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = acc[i] + dpp_f32<0xB1>(acc[i]);  // quad_perm [1,0,3,2]
+        if (n == 0) {
+            const int r = 128 * w4 + 16 * (t0 + tt) + 4 * g;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ql[r + i] = v[i];
+        }
+    }
+    if (tid < 32) {
+        const int i = tid;
+        const float ev = qr[2 * i], od = qr[2 * i + 1];
+        const float ec = ev * csv.x, os = od * csv.y, oc = od * csv.x, es = ev * csv.y;
+        const float r0 = ec - os, r1 = oc + es;
+        const size_t o = ((size_t)b * 16 + h) * 64;
+        const float qsc = 1.0f / sqrtf(192.0f);
+        uint16_t hi, lo;
+        split_bf16(r0 * qsc, hi, lo);
+        st_sc1_b16((void *)(hh.qrhi + o + i), hi);
+        st_sc1_b16((void *)(hh.qrlo + o + i), lo);
+        split_bf16(r1 * qsc, hi, lo);
+        st_sc1_b16((void *)(hh.qrhi + o + 32 + i), hi);
+        st_sc1_b16((void *)(hh.qrlo + o + 32 + i), lo);
+    }
+    __syncthreads();
+    float m = 0.f;
+    v4f qv = {0.f, 0.f, 0.f, 0.f};
+    if (tid < 128) {
+        qv = *(const v4f *)(ql + 4 * tid);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(qv[i]));
+    }
+    const float amax = block512_max(m, red);
+    const bool ok = amax > 0.f && isfinite(amax);
+    const float inv = ok ? 127.0f / amax : 0.f;
+    if (tid < 128) {
+        uint32_t ph = 0, pl = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float v = qv[i] * inv;
+            float hi = rintf(v);
+            hi = fminf(fmaxf(hi, -127.f), 127.f);
+            float lo = rintf((v - hi) * 254.0f);
+            lo = fminf(fmaxf(lo, -127.f), 127.f);
+            ph |= (uint32_t)(uint8_t)(int8_t)hi << (8 * i);
+            pl |= (uint32_t)(uint8_t)(int8_t)lo << (8 * i);
+        }
+        const size_t o = ((size_t)b * 16 + h) * 512 + 4 * tid;
+        st_sc1_b32((void *)(hh.qhi + o), ph);
+        st_sc1_b32((void *)(hh.qlo + o), pl);
+    }
+    if (tid == 0) st_sc1_b32((void *)(hh.qs + (size_t)b * 16 + h), __float_as_uint(ok ? amax / 127.0f : 0.f));
+}
+
+// Row of sequence b: append_body's Q8 path for R = 512, DR = 64 over 8 waves (the RMSNorm sum
+// over the first 256 threads, two values each, as there). scr: 4448 B.
+__device__ __forceinline__ void fq_append(const FqArgs &f, const SeqDesc &s, int b, uint8_t *scr) {
+    float *kat = (float *)scr, *lat = kat + 576;
+    double *redd = (double *)(lat + 512);
+    float *redf = (float *)(redd + 8);
+    const int tid = threadIdx.x, pos = s.pos;
+    const float *ky = f.y + (size_t)b * f.ldy + f.koff;
+    const float kv0 = sum_parts(ky + tid, kGemvKs, f.pstride);
+    const float kv1 = tid < 64 ? sum_parts(ky + 512 + tid, kGemvKs, f.pstride) : 0.f;
+    const float nw = bf16_to_f32(f.norm[tid]);
+    const float2 csv = tid < 32 ? f.cs[(size_t)pos * 32 + tid] : float2{0.f, 0.f};
+    kat[tid] = kv0;
+    if (tid < 64) kat[512 + tid] = kv1;
+    __syncthreads();
+    double ss = 0.0;
+    if (tid < 256) {
+        for (int r = tid; r < 512; r += 256) {
+            const double v = (double)kat[r];
+            ss += v * v;
+        }
+    }
+    const float mean_sq = (float)(block512_sum_f64(ss, redd) / 512.0);
+    const float inv = 1.0f / sqrtf(mean_sq + f.eps);
+    const float t = kat[tid] * inv;
+    lat[tid] = t * nw;
+    __syncthreads();
+    const float amax = block512_max(fmaxf(0.f, fabsf(lat[tid])), redf);
+    const bool zero = !(amax > 0.0f) || !isfinite(amax);
+    const float scale = zero ? 1.0f : amax / 127.0f;
+    const float qinv = zero ? 0.0f : 1.0f / scale;
+    uint8_t *row_out = f.rows + (size_t)b * f.row_bytes;
+    if (tid < 128) {
+        uint32_t pk = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            int8_t q = 0;
+            if (!zero) {
+                float v = roundf(lat[4 * tid + i] * qinv);
+                v = v > 127.0f ? 127.0f : v;
+                v = v < -127.0f ? -127.0f : v;
+                q = (int8_t)v;
+            }
+            pk |= (uint32_t)(uint8_t)q << (8 * i);
+        }
+        st_sc1_b32((int8_t *)s.a + (size_t)pos * 512 + 4 * tid, pk);
+        *(uint32_t *)(row_out + 4 * tid) = pk;
+    }
+    if (tid == 0) {
+        st_sc1_b32((float *)s.b + pos, __float_as_uint(scale));
+        *(float *)(row_out + 512) = scale;
+    }
+    if (tid < 32) {
+        const int i = tid;
+        const float ev = kat[512 + 2 * i], od = kat[512 + 2 * i + 1];
+        const float ec = ev * csv.x, os = od * csv.y, oc = od * csv.x, es = ev * csv.y;
+        const uint16_t h0 = f32_to_bf16_rne(ec - os), h1 = f32_to_bf16_rne(oc + es);
+        uint16_t *rp = (uint16_t *)s.c + (size_t)pos * 64;
+        st_sc1_b16(rp + i, h0);
+        st_sc1_b16(rp + 32 + i, h1);
+        uint16_t *ro = (uint16_t *)(row_out + 516);
+        ro[i] = h0;
+        ro[32 + i] = h1;
+    }
+}
+
+// The producer task of this workgroup, if any (blocks [0, 17 B)), then its flag. Called by both
+// roles of the Q8 kernel at the same point of their barrier sequences (uniform per workgroup).
+__device__ __forceinline__ void fq_produce(const AttnArgs &a, const AttnHot &hh, uint8_t *scr) {
+    const int i = blockIdx.x, B = hh.nseq;
+    if (i >= 17 * B) return;
+    const DescLane dl = desc_lane(a.t);
+    const int b = i < 16 * B ? i >> 4 : i - 16 * B;
+    const SeqDesc s = desc_pick(dl, b);
+    if (i < 16 * B) fq_qprep(a.fq, hh, s, b, i & 15, scr);
+    else fq_append(a.fq, s, b, scr);
+    if (threadIdx.x < 128) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the storing waves
+    __syncthreads();
+    if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(i < 16 * B ? fq_qflag(a.fq, b) : fq_aflag(a.fq, b), 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Position of the quantised weight of (head h, chunk row r) within one level: 16-byte groups
 // of rows XOR-swizzled by the head, so the mix waves' 16-byte reads (one head, 16 rows per lane)
 // spread over the banks.
@@ -1993,8 +2235,9 @@ __device__ __forceinline__ void put_q8_weights(int8_t *wqc, const float *pv, flo
 // same LDS flags after A, so all eight take the same barriers. Everything the score waves read
 // per chunk (codes, RoPE keys, scales) arrives in LDS by the mix waves' DMA, so their steps
 // never wait on global-memory latency.
+template <bool FUSE>  // FUSE: the launch also prepares the queries and appends the rows (fq_produce)
 __device__ __forceinline__ void q8_score_role(const AttnArgs &a, const AttnHot &h, const SeqDesc &sd, uint8_t *smem, int w, int b,
-                                              int r0, int r1, int nch, int sid) {
+                                              int r0, int r1, int nch, int sid, int cpos) {
     int8_t *wq = (int8_t *)(smem + kQ8WqOff);
     int *oflag = (int *)(smem + kQ8FlagOff);
     float *mloc = (float *)(smem + kQ8MlOff);
@@ -2015,10 +2258,22 @@ __device__ __forceinline__ void q8_score_role(const AttnArgs &a, const AttnHot &
     v4i qh[8], ql[8];
     v8bf qrh[2], qrl[2];
     float qsd[4], m_run[4], l_lane[4];
-    // the query's int8 scales first: the first chunk's scores need them right after P
+    if constexpr (FUSE) {
+        // this workgroup's producer task, then (one poller, barrier Q) the 16 query heads of its
+        // sequence and, where the split holds the new row (whose scale the loads below read and
+        // whose chunk the mix waves request after Q), that row
+        fq_produce(a, h, smem + kQ8WqOff);
+        if (w == 0) {
+            fq_wait(a.fq, fq_qflag(a.fq, b), 16u);
+            if (cpos >= 0) fq_wait(a.fq, fq_aflag(a.fq, b), 1u);
+        }
+        lds_barrier();  // Q
+    }
+    // the query's int8 scales first: the first chunk's scores need them right after P (written in
+    // this launch when FUSE: read past the L2, whose line may hold another sequence's scales)
     float qsr[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qsr[i] = h.qs[(size_t)b * 16 + 4 * g + i];
+    for (int i = 0; i < 4; ++i) qsr[i] = FUSE ? ld_sc1_f32(h.qs + (size_t)b * 16 + 4 * g + i) : h.qs[(size_t)b * 16 + 4 * g + i];
     // the sequence's query operands (hi, lo codes: 8 KB each; RoPE hi, lo: 2 KB each) once into
     // code slot 3 by DMA (wave w: 1 KB pieces 5w .. 5w+4), read from there by all four waves
     const uint32_t qslot = lds_addr(smem) + 3 * kQ8CodeB;
@@ -2176,9 +2431,9 @@ __device__ __forceinline__ void q8_score_role(const AttnArgs &a, const AttnHot &
     }
 }
 
-template <bool ONCE>
+template <bool ONCE, bool FUSE>
 __device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const AttnHot &h, const SeqDesc &sd, uint8_t *smem, int mw, int b,
-                                            int r0, int r1, int nch, int sid) {
+                                            int r0, int r1, int nch, int sid, int cpos) {
     const int8_t *wq = (const int8_t *)(smem + kQ8WqOff);
     const int *oflag = (const int *)(smem + kQ8FlagOff);
     const float *abuf = (const float *)(smem + kQ8AlOff);
@@ -2252,12 +2507,43 @@ __device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const AttnHot &h,
     // prologue: codes of chunks 0 .. 2 and keys of chunks 0, 1 in flight, chunk 0 first (beside
     // the score waves' query DMA, before P0) and the rest after it; the issue order codes(c+1)
     // before keys(c) keeps the per-step wait count below uniform
-    issue_codes(0);
-    issue_rope(0);
-    lds_barrier();  // P0
-    if (nch > 1) issue_codes(1);
-    if (nch > 2) issue_codes(2);
-    if (nch > 1) issue_rope(1);
+    if constexpr (!FUSE) {
+        issue_codes(0);
+        issue_rope(0);
+        lds_barrier();  // P0
+        if (nch > 1) issue_codes(1);
+        if (nch > 2) issue_codes(2);
+        if (nch > 1) issue_rope(1);
+    } else {
+        // The same requests in the same order (codes 0, keys 0, codes 1, codes 2, keys 1), as many
+        // as possible ahead of barrier Q (the queries and the new row are ready, polled by score
+        // wave 0): a producer issues them after its task (its own loads go first), the others
+        // before it; from the first that touches the chunk holding the new row (cpos) on they
+        // wait for Q. Measured against chunk 0 only ahead of Q (headline step 1.510 ms): all
+        // three chunks before the task 1.490 ms, a producer's after its task 1.483 ms.
+        auto issue_item = [&](int it) __attribute__((always_inline)) {
+            if (it == 0) issue_codes(0);
+            else if (it == 1) issue_rope(0);
+            else if (it == 2) { if (nch > 1) issue_codes(1); }
+            else if (it == 3) { if (nch > 2) issue_codes(2); }
+            else if (nch > 1) issue_rope(1);
+        };
+        int it = 0;
+        auto issue_ahead = [&]() __attribute__((always_inline)) {
+            for (; it < 5; ++it) {
+                const int ch = it < 2 ? 0 : it == 2 ? 1 : it == 3 ? 2 : 1;
+                if (cpos >= 0 && ch >= cpos) break;
+                issue_item(it);
+            }
+        };
+        const bool prod = (int)blockIdx.x < 17 * h.nseq;
+        if (!prod) issue_ahead();
+        fq_produce(a, h, smem + kQ8WqOff);
+        if (prod) issue_ahead();
+        lds_barrier();  // Q
+        for (; it < 5; ++it) issue_item(it);
+        lds_barrier();  // P0
+    }
     wait_vm(nch > 1 ? (nch > 2 ? 16 : 8) + nrope : 0);
     lds_barrier();  // P
     const float smax = fmaxf(fmaxf(smx[0], smx[1]), fmaxf(smx[2], smx[3]));
@@ -2346,7 +2632,9 @@ __device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const AttnHot &h,
     }
 }
 
-template <bool ONCE>  // ONCE: each history row is read by one workgroup (non-temporal loads)
+// ONCE: each history row is read by one workgroup (non-temporal loads). FUSE: the launch
+// prepares the queries and appends the rows itself (fq_produce; no block launches).
+template <bool ONCE, bool FUSE = false>
 __global__ __launch_bounds__(512) void k_attn_q8_mfma(KVL_ATTN_HOT_PARAMS, AttnArgs a) {
     KVL_ATTN_HOT_INIT;
     __shared__ __attribute__((aligned(16))) uint8_t smem[kQ8SmemB];
@@ -2357,14 +2645,21 @@ __global__ __launch_bounds__(512) void k_attn_q8_mfma(KVL_ATTN_HOT_PARAMS, AttnA
     const int r0 = split * s.rps;
     const int r1 = split == s.nsplit - 1 ? s.len : r0 + s.rps;  // last split takes the rest
     const int nch = (r1 - r0 + kQ8Ch - 1) / kQ8Ch;
-    if (w >= 4) q8_mix_role<ONCE>(a, h, s, smem, w - 4, b, r0, r1, nch, pidx);
-    else q8_score_role(a, h, s, smem, w, b, r0, r1, nch, pidx);
+    // chunk of this split holding the row appended in this launch, or -1
+    const int cpos = FUSE && split == s.nsplit - 1 ? (s.pos - r0) / kQ8Ch : -1;
+    if (w >= 4) q8_mix_role<ONCE, FUSE>(a, h, s, smem, w - 4, b, r0, r1, nch, pidx, cpos);
+    else q8_score_role<FUSE>(a, h, s, smem, w, b, r0, r1, nch, pidx, cpos);
 }
 
 hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t, const Dims &d,
                             int rows_per_split, int total_splits, int lmax,
-                            const DecodeWork &w, int members) {
+                            const DecodeWork &w, int members, const FqArgs *fq) {
     AttnArgs a;
+    a.fq = fq ? *fq : FqArgs{};
+    if (fq && (kind != kAttnQ8Mfma || members > 0 || fmt != kFmtQ8 || d.NH != 16 || d.R != 512 || d.DR != 64 ||
+               d.DN != 128 || d.QD != 192 || 17 * t.n > total_splits || !fq->y || !fq->ukt || !fq->cs || !fq->norm ||
+               !fq->rows || !fq->flags || !fq->err))
+        return hipErrorInvalidValue;
     a.t = t;
     a.d = d;
     a.part = w.part;
@@ -2388,6 +2683,7 @@ hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t
     }
     if (kind == kAttnQ8Mfma) {
         if (a.members > 0) hipLaunchKernelGGL(k_attn_q8_mfma<false>, dim3(grid), dim3(512), 0, st, a.members, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);
+        else if (fq) hipLaunchKernelGGL((k_attn_q8_mfma<true, true>), dim3(grid), dim3(512), 0, st, a.members, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);
         else hipLaunchKernelGGL(k_attn_q8_mfma<true>, dim3(grid), dim3(512), 0, st, a.members, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);
     } else if (kind == kAttnF32Mfma) {
         if (a.members > 0) hipLaunchKernelGGL(k_attn_f32_mfma<false>, dim3(grid), dim3(256), 0, st, a.members, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);

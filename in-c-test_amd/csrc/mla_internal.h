@@ -87,9 +87,11 @@ hipError_t launch_gemv(hipStream_t st, float *Y, int ldy, const float *X, int ld
 // so history rows appended by decode equal those the state prefill writes.
 constexpr int kGemvKs = 4;
 bool gemv_ksplit_ok(int in, int ldx);
+// zero_flags (may be null): words kFqFlagStride * i, i < nzero, the launch clears (the readiness
+// flags of a fused Q8 attention launch that follows, FqArgs::flags).
 hipError_t launch_gemv_ksplit(hipStream_t st, float *Y, size_t pstride, int ldy, const float *X,
                               int ldx, int B, const uint16_t *W0, int out0, const uint16_t *W1,
-                              int out1, int in);
+                              int out1, int in, unsigned *zero_flags = nullptr, int nzero = 0);
 // The same kGemvKs partials (bit for bit) for S tokens given as bf16 planes XH, XL [S, in]
 // (k_split's rounding), tiled over 128 tokens so a weight tile serves many of them: the
 // prefill's kv_a projection and the state prefill. Shapes as launch_gemv_ksplit.
@@ -145,9 +147,31 @@ enum AttnKind : int { kAttnGeneric = 0, kAttnF32Mfma = 1, kAttnQ8Mfma = 2, kAttn
 // members > 0: the sequences are the members of one block (tokens of one sequence, each with
 // the split plan of its lone decode); the workgroups then go split-major, the members of a split
 // together on one XCD, so that they share the history rows in its L2.
+// What the Q8 attention launch needs to prepare the queries and append the rows itself (the
+// work of launch_append_qprep, Kimi shapes): the q_proj | kv_a partials of launch_gemv_ksplit,
+// W_UK^T in fragment order, the RoPE table, the kv_a norm weights, the caller's copy of the
+// appended rows, the readiness flags (word kFqFlagStride * i; i in [0, B): query heads done,
+// [kMaxBatch, kMaxBatch + B): row appended; zeroed by the launch_gemv_ksplit before it) and a
+// host-visible word set when a wait for them timed out.
+constexpr int kFqFlagStride = 32;  // FqArgs::flags: one 128-byte line per flag
+struct FqArgs {
+    const float *y;
+    const uint16_t *ukt;
+    const float2 *cs;
+    const uint16_t *norm;
+    uint8_t *rows;
+    unsigned *flags;
+    int *err;
+    size_t pstride;
+    int ldy, koff, row_bytes;
+    float eps;
+};
+// fq: null, or the fused form (kind == kAttnQ8Mfma, members == 0, Kimi shapes, at most one
+// round of workgroups, 17 B <= total_splits): blocks [0, 16 B) prepare one (sequence, head)
+// query each, blocks [16 B, 17 B) append one row each, before their own split.
 hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t, const Dims &d,
                             int rows_per_split, int total_splits, int lmax,
-                            const DecodeWork &w, int members = 0);
+                            const DecodeWork &w, int members = 0, const FqArgs *fq = nullptr);
 
 // Normalise the split partials into mix[(b*G + g), DVm] and, for the compressed formats,
 // apply W_UV: ho[b, h*DV + d] = sum_r kv_b[h*(DN+DV) + DN + d, r] * mix[b*NH + h, r].

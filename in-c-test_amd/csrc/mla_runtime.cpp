@@ -166,6 +166,12 @@ struct Ctx {
     DevBuf work, part, scores, prefill, fill, fillx, layer, sink;
     DevBuf rflag;  // int: raised by a stream-ordered prefill outside the MFMA route's range
     PinBuf pin_in, pin_out;
+    // fused Q8 decode (the attention launch prepares the queries and appends the rows): its
+    // readiness flags (device, 2 x kMaxBatch lines, cleared by the q_proj | kv_a GEMV of each
+    // call) and a host-visible word raised if one of its waits timed out
+    unsigned *fq_flags = nullptr;
+    int *fq_err = nullptr;
+    bool fq_on = true;  // KVL_MLA_NO_FUSED_QPREP=1 turns the fused form off (the two-launch form)
     bool capturing = false;
     // bumped by every release of library-owned device memory: a graph captured before a bump
     // may hold pointers to freed memory (kvl_mla_graph_launch refuses it)
@@ -218,6 +224,14 @@ int ensure_ready() {
         g_scratch[dev] = p;
     }
     HIP_TRY(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
+    HIP_TRY(hipMalloc(&c.fq_flags, 2 * kMaxBatch * kFqFlagStride * sizeof(unsigned)));
+    HIP_TRY(hipMemset(c.fq_flags, 0, 2 * kMaxBatch * kFqFlagStride * sizeof(unsigned)));
+    HIP_TRY(hipHostMalloc((void **)&c.fq_err, sizeof(int), hipHostMallocDefault));
+    *c.fq_err = 0;
+    {
+        const char *e = getenv("KVL_MLA_NO_FUSED_QPREP");
+        c.fq_on = !(e && e[0] == '1');
+    }
     c.device = dev;
     c.ncu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
     c.ready = true;
@@ -970,6 +984,15 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
     }
 
     const int ldy = d.QO + d.KVO;
+    // The fused form (see FqArgs): Q8 MFMA attention of independent sequences (no block members)
+    // at the Kimi shapes, one round of workgroups with room for the 17 B producer tasks, the
+    // k-split projection, W_UK^T in fragment order, two or more sequences; the no-allocation
+    // entry point keeps the two-launch form. Measured (headline stack, 8 x 32K Q8 rows, 27
+    // layers): 1.522 -> 1.483 ms per step; a lone 8K-row decode 29.5 -> 30.5 us (the 17 producer
+    // tasks hold up its 64 short splits), hence B >= 2.
+    const bool fuse = c.fq_on && B >= 2 && fmt == kFmtQ8 && kind == kAttnQ8Mfma && !solo && part_cap == 0 && kimi_attn(d) &&
+                      d.DN == 128 && d.QD == 192 && gemv_ksplit_ok(d.H, d.H) && ukt_shape(d) && dw.ukt &&
+                      17 * B <= total_splits && total_splits <= c.ncu && c.fq_flags && c.fq_err;
     {
         // q_proj | kv_a: k split over kGemvKs blocks where the shape allows (the consumers
         // add the partials), else one pass
@@ -982,7 +1005,7 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
             w.ynp = kGemvKs;
             w.ypstride = (size_t)B * ldy;
             HIP_TRY(launch_gemv_ksplit(st, w.y, w.ypstride, ldy, d_x, d.H, B, dw.q, d.QO, dw.kva,
-                                       d.KVO, d.H));
+                                       d.KVO, d.H, fuse ? c.fq_flags : nullptr, fuse ? 2 * kMaxBatch : 0));
         } else {
             w.ynp = 1;
             w.ypstride = 0;
@@ -1001,7 +1024,7 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
             StageTimer tm(2);
             HIP_TRY(launch_qprep(st, fmt, t, d, dw.kvb, cs, w, false));
         }
-    } else {
+    } else if (!fuse) {
         // append and query preparation in one launch (timed as stage 1)
         StageTimer tm(1);
         HIP_TRY(launch_append_qprep(st, fmt, t, d, w.y, ldy, d.QO, w.ynp, w.ypstride, dw.norm, eps, cs, dw.kvb,
@@ -1009,7 +1032,22 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
     }
     {
         StageTimer tm(3);
-        HIP_TRY(launch_attention(st, kind, fmt, t, d, rps, total_splits, lmax, w, solo ? B : 0));
+        FqArgs fq{};
+        if (fuse) {
+            fq.y = w.y;
+            fq.ukt = dw.ukt;
+            fq.cs = cs;
+            fq.norm = dw.norm;
+            fq.rows = w.rows;
+            fq.flags = c.fq_flags;
+            fq.err = c.fq_err;
+            fq.pstride = w.ypstride;
+            fq.ldy = ldy;
+            fq.koff = d.QO;
+            fq.row_bytes = d.R + 4 + 2 * d.DR;
+            fq.eps = eps;
+        }
+        HIP_TRY(launch_attention(st, kind, fmt, t, d, rps, total_splits, lmax, w, solo ? B : 0, fuse ? &fq : nullptr));
     }
     {
         StageTimer tm(4);
@@ -1133,6 +1171,12 @@ int decode_host(float *out, const float *x, const int *positions, int B, const K
         if (fmt == kFmtExp)
             HIP_TRY(hipMemcpyAsync(prows, wk.rows, (size_t)n * rb, hipMemcpyDeviceToHost, c.stream));
         HIP_TRY(hipStreamSynchronize(c.stream));
+        if (*c.fq_err) {
+            *c.fq_err = 0;
+            set_err("a wait of the fused query preparation timed out (results invalid); "
+                    "KVL_MLA_NO_FUSED_QPREP=1 selects the two-launch form");
+            return -1;
+        }
         memcpy(out + (size_t)g0 * d.H, c.pin_out.p, xin);
         for (int i = 0; i < n; ++i) {
             S *s = states[g0 + i];
@@ -2434,6 +2478,18 @@ int kvl_mla_timing_enable(int on) {
     ctx().timing = on != 0;
     ctx().timing_graph = on == 2;
     return 0;
+}
+
+int kvl_mla_set_fused_qprep(int on) {
+    Guard guard;
+    if (ensure_ready() != 0) return -1;
+    if (on != 0 && on != 1) {
+        set_err("kvl_mla_set_fused_qprep: on must be 0 or 1");
+        return -1;
+    }
+    const int prev = ctx().fq_on ? 1 : 0;
+    ctx().fq_on = on == 1;
+    return prev;
 }
 
 int kvl_mla_timing_stages(unsigned mask) {

@@ -258,6 +258,13 @@ int kvl_mla_graph_destroy(void *graph_exec);
  * kvl_mla_copy_kernel: a plain 16-byte vector copy kernel (bytes % 16 == 0), for calibrating
  * memory counters. */
 int kvl_mla_timing_enable(int on);
+/* Form of the Q8 decode of two or more independent sequences at the Kimi shapes (library
+ * extension, no counterpart in the reference): on = 1 (the default) prepares the queries and
+ * appends the rows inside the attention launch, on = 0 in a launch of their own before it (the
+ * form the block decode and the no-allocation entry point always use). The results are the same
+ * bit for bit. Returns the previous setting, or -1. The environment variable
+ * KVL_MLA_NO_FUSED_QPREP=1 sets 0 at initialisation. */
+int kvl_mla_set_fused_qprep(int on);
 int kvl_mla_timing_stages(unsigned mask);
 int kvl_mla_timing_read(double *ms, int *count);
 void *kvl_mla_event_record(void);

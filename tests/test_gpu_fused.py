@@ -1,0 +1,89 @@
+"""The Q8 decode of two or more independent sequences prepares the queries and appends the rows
+inside its attention launch (the launch's lowest-numbered workgroups work for the others, which
+wait for them on device flags); kvl_mla_set_fused_qprep(0) selects the two-launch form
+(k_append_qprep, then the attention). Both forms must give the same outputs, the same appended
+rows and the same states bit for bit (the parity of the two-launch form with the oracle is
+tested elsewhere, and the block decode, which always takes it, equals single decodes bit for
+bit). The cases cover the fused form's edges: eight long sequences (one round of workgroups),
+short sequences whose single split holds the new row in its first chunks (their requests wait
+for the append inside the prologue) beside long ones, and two consecutive steps (the flags are
+cleared by each step's projection launch)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from helpers import f32
+from kvl_mla import abi, inputs, lib
+
+pytestmark = pytest.mark.gpu
+
+L = lib.load()
+KIMI = dict(inputs.KIMI)
+
+# history rows per sequence; each case needs 17 x batch <= the launch's split count
+CASES = [(6000,) * 8, (100, 9000), (9000, 200, 130, 9000), (63, 9000, 9000)]
+
+
+def run(form, lens, cfg, w, x, steps):
+    prev = L.kvl_mla_set_fused_qprep(form)
+    assert prev in (0, 1)
+    try:
+        states = []
+        for i, n in enumerate(lens):
+            st = abi.KvlMlaCompressedQ8State()
+            lib.check(L.kvl_mla_compressed_q8_state_init(C.byref(st), C.byref(cfg), n + steps), "init")
+            lib.check(L.kvl_mla_compressed_q8_state_fill_synthetic(C.byref(st), 0, n, 0xF00 + i), "fill")
+            lib.check(L.kvl_mla_compressed_q8_state_pull(C.byref(st), 0, n), "pull")
+            states.append(st)
+        arr = (C.POINTER(abi.KvlMlaCompressedQ8State) * len(lens))(*[C.pointer(s) for s in states])
+        outs = []
+        for t in range(steps):
+            pos = np.ascontiguousarray([n + t for n in lens], dtype=np.int32)
+            out = np.zeros((len(lens), cfg.hidden_size), np.float32)
+            lib.check(L.kvl_mla_decode_compressed_q8_batch_bf16(f32(out), f32(np.ascontiguousarray(x[t])),
+                                                                pos.ctypes.data_as(C.POINTER(C.c_int)), len(lens),
+                                                                C.byref(cfg), C.byref(w), arr), f"step {t}")
+            outs.append(out)
+        rows = []
+        R, DR = cfg.kv_lora_rank, cfg.qk_rope_dim
+        for st, n in zip(states, lens):
+            m = n + steps
+            assert st.len == m
+            rows.append((np.ctypeslib.as_array(st.latent_q8, (m * R,)).copy(),
+                         np.ctypeslib.as_array(st.latent_scale, (m,)).copy(),
+                         np.ctypeslib.as_array(st.rope_bf16, (m * DR,)).copy()))
+        for st in states:
+            L.kvl_mla_compressed_q8_state_free(C.byref(st))
+        return outs, rows
+    finally:
+        L.kvl_mla_set_fused_qprep(prev)
+
+
+@pytest.mark.parametrize("lens", CASES, ids=["-".join(map(str, c)) for c in CASES])
+def test_fused_equals_two_launch_form(lens):
+    print(f"[fused] lens {lens}", flush=True)
+    cfg = inputs.config(**KIMI)
+    layer = inputs.make_layer(cfg, 0xF1)
+    w = layer.struct()
+    lib.check(L.kvl_mla_bind_weights(C.byref(cfg), C.byref(w)), "bind")
+    try:
+        steps = 2
+        x = np.stack([inputs.hidden(cfg, 0xF2 + t, len(lens)) for t in range(steps)])
+        fo, fr = run(1, lens, cfg, w, x, steps)
+        so, sr = run(0, lens, cfg, w, x, steps)
+        for t in range(steps):
+            assert np.isfinite(fo[t]).all()
+            np.testing.assert_array_equal(fo[t], so[t], err_msg=f"step {t} outputs")
+        for i in range(len(lens)):
+            for k, name in enumerate(("codes", "scales", "rope")):
+                np.testing.assert_array_equal(fr[i][k], sr[i][k], err_msg=f"sequence {i} {name}")
+    finally:
+        L.kvl_mla_release_weights(C.byref(w))
+
+
+def test_fused_switch_rejects_bad_values():
+    prev = L.kvl_mla_set_fused_qprep(1)
+    assert prev in (0, 1)
+    assert L.kvl_mla_set_fused_qprep(2) == -1
+    assert L.kvl_mla_set_fused_qprep(prev) == 1
