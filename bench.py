@@ -582,16 +582,22 @@ def main():
         d_po = L.kvl_mla_device_alloc(x32.nbytes)
 
         def time_prefill(xs):
+            # steady state: 3 warm-up calls, then the median of 5 trials of 10 back-to-back calls
+            # (a handful of calls right after the GPU idled read 5-10 % slower)
             lib.check(L.kvl_mla_copy_to_device(d_px, xs.ctypes.data, xs.nbytes), "h2d")
-            for _ in range(2):
+            for _ in range(3):
                 lib.check(L.kvl_mla_prefill_device(d_po, d_px, S, C.byref(cfg), C.byref(wstructs[0])), "prefill")
             lib.check(L.kvl_mla_synchronize(), "sync")
-            reps = 5
-            p0 = L.kvl_mla_event_record()
-            for _ in range(reps):
-                lib.check(L.kvl_mla_prefill_device(d_po, d_px, S, C.byref(cfg), C.byref(wstructs[0])), "prefill")
-            p1 = L.kvl_mla_event_record()
-            return L.kvl_mla_event_elapsed_ms(p0, p1) / reps
+            reps, trials = 10, []
+            for _ in range(5):
+                p0 = L.kvl_mla_event_record()
+                for _ in range(reps):
+                    lib.check(L.kvl_mla_prefill_device(d_po, d_px, S, C.byref(cfg), C.byref(wstructs[0])), "prefill")
+                p1 = L.kvl_mla_event_record()
+                trials.append(L.kvl_mla_event_elapsed_ms(p0, p1) / reps)
+                L.kvl_mla_event_destroy(p0)
+                L.kvl_mla_event_destroy(p1)
+            return float(np.median(trials))
 
         pms_32 = time_prefill(np.ascontiguousarray(x32))
         pms = time_prefill(xbf)

@@ -119,7 +119,8 @@ struct GemmArgs {
 // the keys of each 32-key group in vt_perm order.
 enum { kEpiPlain = 0, kEpiQ = 1, kEpiKV = 2 };
 struct GemmEpi {
-    _Float16 *qh, *ql, *kh;
+    _Float16 *qh, *kh;
+    uint8_t *ql8;  // bf8(Q lo x 2^11), the flash kernel's correction operand (kEpiQ)
     uint8_t *k8;
     _Float16 *vt;
     const float2 *cs;
@@ -312,22 +313,26 @@ __global__ __launch_bounds__(64 * (kGemmMath + kGemmDma)) void k_gemm16(GemmArgs
                 // lines the next kernels reuse (q GEMM 78 -> 70 us, kv_b GEMM 44 -> 40 us)
                 const int h = nl0 / QD, k0 = nl0 % QD;
                 const size_t o = ((size_t)h * e.Sp + t) * QD;
+                // Q hi as fp16 and Q lo only as the bf8 byte the flash kernel's correction takes
+                // (bf8(lo x 2^11)): 37.5 instead of 50 MB written at 4096 tokens
                 if (k0 < e.DN) {
-                    v4h hi, lo;
+                    v4h hi;
+                    uint32_t l8 = 0;
 #pragma unroll
                     for (int u = 0; u < 4; ++u) {
                         _Float16 hh, ll;
                         split_f16(v[u], hh, ll);
                         hi[u] = hh;
-                        lo[u] = ll;
+                        l8 |= bf8_lo_s11(ll) << (8 * u);
                     }
                     __builtin_nontemporal_store(hi, (v4h *)(e.qh + o + k0));
-                    __builtin_nontemporal_store(lo, (v4h *)(e.ql + o + k0));
+                    __builtin_nontemporal_store(l8, (uint32_t *)(e.ql8 + o + k0));
                 } else {
                     // pairs (ev, od) = (v[2p], v[2p+1]) of rope index i2 + p
                     const int i2 = (k0 - e.DN) >> 1;
                     const float2 *cs = e.cs + (size_t)t * half + i2;
-                    v2h h0, l0, h1, l1;
+                    v2h h0, h1;
+                    uint16_t l0 = 0, l1 = 0;
 #pragma unroll
                     for (int p = 0; p < 2; ++p) {
                         const float2 c = cs[p];
@@ -335,15 +340,15 @@ __global__ __launch_bounds__(64 * (kGemmMath + kGemmDma)) void k_gemm16(GemmArgs
                         _Float16 hh, ll;
                         split_f16(ev * c.x - od * c.y, hh, ll);
                         h0[p] = hh;
-                        l0[p] = ll;
+                        l0 |= (uint16_t)(bf8_lo_s11(ll) << (8 * p));
                         split_f16(od * c.x + ev * c.y, hh, ll);
                         h1[p] = hh;
-                        l1[p] = ll;
+                        l1 |= (uint16_t)(bf8_lo_s11(ll) << (8 * p));
                     }
                     __builtin_nontemporal_store(h0, (v2h *)(e.qh + o + e.DN + i2));
-                    __builtin_nontemporal_store(l0, (v2h *)(e.ql + o + e.DN + i2));
+                    __builtin_nontemporal_store(l0, (uint16_t *)(e.ql8 + o + e.DN + i2));
                     __builtin_nontemporal_store(h1, (v2h *)(e.qh + o + e.DN + half + i2));
-                    __builtin_nontemporal_store(l1, (v2h *)(e.ql + o + e.DN + half + i2));
+                    __builtin_nontemporal_store(l1, (uint16_t *)(e.ql8 + o + e.DN + half + i2));
                 }
             } else {  // kEpiKV, k_nope columns
                 const int h = nl0 / KH, k0 = nl0 % KH;
@@ -453,7 +458,9 @@ struct KvaPackArgs {
     const uint16_t *norm;
     const float2 *cs;
     uint16_t *lath, *latl;
-    _Float16 *qh, *ql, *kh;
+    _Float16 *qh;
+    uint8_t *ql8;
+    _Float16 *kh;
     uint8_t *k8;
     _Float16 *vt;
     size_t pstride;  // np partials of y, pstride floats apart, summed in order
@@ -473,7 +480,7 @@ __global__ __launch_bounds__(256) void k_kva_pack(KvaPackArgs a) {
             const size_t qo = ((size_t)h * a.Sp + t) * QD;
             for (int k = l; k < QD; k += 64) {
                 a.qh[qo + k] = 0;
-                a.ql[qo + k] = 0;
+                a.ql8[qo + k] = 0;
                 a.kh[qo + k] = 0;
             }
             for (int k = l; k < 96; k += 64) ((uint32_t *)(a.k8 + ((size_t)h * a.Sp + t) * 384))[k] = 0;
@@ -629,7 +636,8 @@ constexpr int kFSmem = 2 * 2 * kFKB + 2 * kFVB;
 constexpr float kFLazy = 8.0f;       // log2 headroom of the lazy max
 
 struct FlashArgs {
-    const _Float16 *qh, *ql, *kh;            // Q, K hi: [NH, Sp, 192]
+    const _Float16 *qh, *kh;                 // Q, K hi: [NH, Sp, 192]
+    const uint8_t *ql8;                      // bf8(Q lo x 2^11): [NH, Sp, 192]
     const uint8_t *k8;                       // K8 rows: [NH, Sp, 384 bytes]
     const _Float16 *vt;                      // V^T: [NH, 128, Sp]
     _Float16 *o;                             // [S, ldo] fp16 (input of the o_proj GEMM)
@@ -682,16 +690,18 @@ void k_flash_prefill(FlashArgs a) {
     const int qw = qt * kFQ + 32 * w;
     const size_t hq = (size_t)h * Sp;
 
-    // Q^T B operands: query qw + 16u + n, dims 32kb + 8g .. +7
-    v8h qa[2][6], qb[2][6];  // hi (main pass), lo (folded into the bf8 operands below)
+    // Q^T B operands: query qw + 16u + n, dims 32kb + 8g .. +7: hi as fp16 (main pass), lo as
+    // its bf8(lo x 2^11) bytes (the correction operand below, written so by the q GEMM)
+    v8h qa[2][6];
+    uint2 qb[2][6];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const _Float16 *ph = a.qh + (hq + qw + 16 * u + n) * 192 + 8 * g;
-        const _Float16 *pl = a.ql + (hq + qw + 16 * u + n) * 192 + 8 * g;
+        const uint8_t *pl = a.ql8 + (hq + qw + 16 * u + n) * 192 + 8 * g;
 #pragma unroll
         for (int kb = 0; kb < 6; ++kb) {
             qa[u][kb] = *(const v8h *)(ph + 32 * kb);
-            qb[u][kb] = *(const v8h *)(pl + 32 * kb);
+            qb[u][kb] = *(const uint2 *)(pl + 32 * kb);
         }
     }
 
@@ -750,7 +760,7 @@ void k_flash_prefill(FlashArgs a) {
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int kb = 0; kb < 6; ++kb) asm volatile("" : "+v"(qa[u][kb]), "+v"(qb[u][kb]));
+        for (int kb = 0; kb < 6; ++kb) asm volatile("" : "+v"(qa[u][kb]), "+v"(qb[u][kb].x), "+v"(qb[u][kb].y));
     wait_vmcnt<0>();
     // correction operands: per u, 96 bytes = bf8(Ql 2^11) then bf8(Qh), each in (k-block,
     // element) order, so that byte p meets byte p of the lane group's K8 bytes (hi, then lo);
@@ -763,13 +773,10 @@ void k_flash_prefill(FlashArgs a) {
         for (int kb = 0; kb < 6; ++kb)
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf) {
-                uint32_t lo = 0, hi = 0;
+                uint32_t hi = 0;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    lo |= bf8_lo_s11(qb[u][kb][4 * hf + i]) << (8 * i);
-                    hi |= f16_to_bf8(qa[u][kb][4 * hf + i]) << (8 * i);
-                }
-                wd[2 * kb + hf] = lo;
+                for (int i = 0; i < 4; ++i) hi |= f16_to_bf8(qa[u][kb][4 * hf + i]) << (8 * i);
+                wd[2 * kb + hf] = hf == 0 ? qb[u][kb].x : qb[u][kb].y;
                 wd[12 + 2 * kb + hf] = hi;
             }
 #pragma unroll
@@ -1229,12 +1236,12 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
         uint16_t *lath = (uint16_t *)take(2 * (size_t)S * d.R);
         uint16_t *latl = (uint16_t *)take(2 * (size_t)S * d.R);
         _Float16 *qh = (_Float16 *)take(2 * (size_t)d.NH * Sp * d.QD);
-        _Float16 *ql = (_Float16 *)take(2 * (size_t)d.NH * Sp * d.QD);
+        uint8_t *ql8 = (uint8_t *)take((size_t)d.NH * Sp * d.QD);
         _Float16 *kh = (_Float16 *)take(2 * (size_t)d.NH * Sp * d.QD);
         uint8_t *k8 = (uint8_t *)take((size_t)d.NH * Sp * 384);
         _Float16 *vt = (_Float16 *)take(2 * (size_t)d.NH * d.DV * Sp);
         _Float16 *heads = (_Float16 *)take(2 * (size_t)S * d.HO);
-        GemmEpi ep{qh, ql, kh, k8, vt, cs, Sp, d.DN, d.DR, d.DV};
+        GemmEpi ep{qh, kh, ql8, k8, vt, cs, Sp, d.DN, d.DR, d.DV};
         const float vscale = range ? range->vscale : 1.0f, oscale = range ? range->oscale : 1.0f;
         // flags[0] (any x lo word non-zero) is raised by k_split and cleared by k_kva_pack after
         // the q GEMM has read it, so no launch clears it first. A value left raised (a call
@@ -1258,7 +1265,7 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
                                     d.H, ep)) != hipSuccess) {
             return e;
         }
-        KvaPackArgs ka{ykva, wnorm, cs, lath, latl, qh, ql, kh, k8, vt, (size_t)S * d.KVO, np,
+        KvaPackArgs ka{ykva, wnorm, cs, lath, latl, qh, ql8, kh, k8, vt, (size_t)S * d.KVO, np,
                        S, Sp, d.NH, d.KVO, d.R, d.DN, d.DR, d.DV, eps, flags + 0};
         hipLaunchKernelGGL(k_kva_pack, dim3((Sp + 3) / 4), dim3(256), 0, st, ka);
         if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -1267,7 +1274,7 @@ hipError_t launch_prefill_all(hipStream_t st, const Dims &d, int S, float eps, c
         if ((e = gemm<kEpiKV>(st, lath, latl, nullptr, d.R, wkvb, d.KVB, nullptr, 0, d.R, nullptr, 0, S, d.R,
                               ep)) != hipSuccess)
             return e;
-        FlashArgs fa{qh, ql, kh, k8, vt, heads, flags + 1, range ? range->sticky : nullptr, S, Sp, d.NH, d.HO,
+        FlashArgs fa{qh, kh, ql8, k8, vt, heads, flags + 1, range ? range->sticky : nullptr, S, Sp, d.NH, d.HO,
                      smscale * 1.4426950408889634f};
         hipLaunchKernelGGL(k_flash_prefill, dim3(Sp / kFQ * d.NH), dim3(256), 0, st, fa);
         if ((e = hipGetLastError()) != hipSuccess) return e;
