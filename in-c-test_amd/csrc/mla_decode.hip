@@ -153,8 +153,9 @@ __global__ __launch_bounds__(1024) void k_gemv_ksplit(const float *X, const uint
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
     const int xcd = blockIdx.x & 7, rb = 2 * (blockIdx.x >> 3) + (xcd & 1);
     const int out = a.out0 + a.out1, kq = xcd >> 1, row0 = rb * 64, part = n >> 3;
-    // block 0 (row block 0 of k quarter 0, never empty) clears the next launch's flags
-    if (blockIdx.x == 0 && zf != nullptr && tid < nz) zf[(size_t)tid * kFqFlagStride] = 0u;
+    // block 0 (row block 0 of k quarter 0, never empty) clears the next launch's flags (the first
+    // 8 bytes of each line: the combine counters are 64 bits)
+    if (blockIdx.x == 0 && zf != nullptr && tid < nz) *(uint2 *)(zf + (size_t)tid * kFqFlagStride) = uint2{0u, 0u};
     if (row0 >= out) return;  // the whole block
     const uint16_t *wr[4];
 #pragma unroll
@@ -1320,9 +1321,22 @@ __device__ __forceinline__ int find_seq(const SeqTable &t, int bid) {
 // Sequence b's descriptor comes from desc_lane / desc_pick, b from a ballot over the lanes'
 // split0 (a lone decode's attention launch: 12.5 -> 10.3 us at 8K Q8 rows, 18.3 -> 16.5 us at
 // 32K against indexing the table by b once b is known).
+// XL (the Q8 launch that also combines, nseq a multiple of kXcds, every sequence with the same
+// split count ns, its splits consecutive): sequence-major per XCD, workgroup i takes sequence
+// i % kXcds + kXcds * ((i / kXcds) / ns), split (i / kXcds) % ns, so that all splits of a sequence
+// run on one XCD and its partials stay in that XCD's L2 for the combine (q8_comb_tail).
+template <bool XL = false>
 __device__ __forceinline__ bool seq_of(const AttnArgs &a, const AttnHot &h, int &b, int &split, int &pidx, SeqDesc &s) {
     const int sid = blockIdx.x, lane = threadIdx.x & 63;
     const DescLane m = desc_lane(a.t);
+    if constexpr (XL) {
+        const int ns = lane_pick(m.nsplit, 0), j = sid / kXcds;
+        b = sid % kXcds + kXcds * (j / ns);
+        split = j % ns;
+        s = desc_pick(m, b);
+        pidx = s.split0 + split;
+        return true;
+    }
     if (h.members > 0) {
         const int j = sid / kXcds;
         b = j % h.members;
@@ -2431,7 +2445,7 @@ __device__ __forceinline__ void q8_score_role(const AttnArgs &a, const AttnHot &
     }
 }
 
-template <bool ONCE, bool FUSE>
+template <bool ONCE, bool FUSE, bool COMB>
 __device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const AttnHot &h, const SeqDesc &sd, uint8_t *smem, int mw, int b,
                                             int r0, int r1, int nch, int sid, int cpos) {
     const int8_t *wq = (const int8_t *)(smem + kQ8WqOff);
@@ -2625,30 +2639,252 @@ __device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const AttnHot &h,
     for (int t = 0; t < 8; ++t) {
         const int r = 128 * mw + 16 * t + ne;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            __builtin_nontemporal_store(
-                wfac * fmaf((float)ahi[t][i], 64516.0f, fmaf((float)alo[t][i], 254.0f, (float)alo2[t][i])),
-                &P[(4 * ge + i) * 512 + r]);
+        for (int i = 0; i < 4; ++i) {
+            const float v = wfac * fmaf((float)ahi[t][i], 64516.0f, fmaf((float)alo[t][i], 254.0f, (float)alo2[t][i]));
+            // COMB: read by this XCD's workgroups in this launch (q8_comb_tail), from its L2
+            if constexpr (COMB) P[(4 * ge + i) * 512 + r] = v;
+            else __builtin_nontemporal_store(v, &P[(4 * ge + i) * 512 + r]);
+        }
+    }
+}
+
+// Position of latent column c of the merged mix in the combine's LDS row: 16-byte groups XOR-
+// swizzled by c / 32, so the 16 lanes of a W_UV row read distinct banks.
+__device__ __forceinline__ int mx_pos(int c) { return c ^ (((c >> 5) & 7) << 2); }
+constexpr int kCombPre = 8;  // split-partial loads a combine thread issues before its first wait
+
+// ---- the combine inside the Q8 attention launch ----------------------------------------------
+// With every split of a sequence on one XCD (seq_of<true>), its split partials are in that XCD's
+// L2 when the last split ends: each workgroup stores its partial with plain stores, waits until
+// the L2 has acknowledged them (vmcnt) and counts itself on the sequence's counter; workgroup
+// `split` < 32 then waits for the count to reach ns, invalidates its L1 and combines (head
+// split / 2, half split % 2) -- and further tasks split + ns, ... when ns < 32 -- with the
+// arithmetic of k_combine_r512, whose launch this replaces. The counter (64 bits, one 128-byte
+// line per sequence, after the query and row flags, cleared by the q_proj | kv_a launch of the
+// step) has one byte per XCC: a workgroup adds 1 << 8 * (its XCC id), so the waiters also see
+// that all the sequence's splits ran on one XCC, which the placement assumes (workgroup i on XCD
+// i % 8 + a per-launch offset); otherwise the partials would not all be in the reader's L2, and
+// the launch raises FqArgs::err (results invalid) instead of reading them. The waits are bounded
+// as fq_wait's are.
+__device__ __forceinline__ unsigned long long *fq_cflag(const FqArgs &f, int b) {
+    return (unsigned long long *)(f.flags + (size_t)kFqFlagStride * (2 * kMaxBatch + b));
+}
+__device__ __forceinline__ unsigned xcc_id() {
+    unsigned x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return x & 7;
+}
+// The counter's value by a returning atomic add of 0 (an atomic is never served from the L1).
+__device__ __forceinline__ unsigned long long cnt_poll(unsigned long long *p) {
+    unsigned long long v;
+    asm volatile("global_atomic_add_x2 %0, %1, %2, off sc0\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(p), "v"(0ull) : "memory");
+    return v;
+}
+// Sum of the eight byte fields (each <= ns <= 255, comb_ok).
+__device__ __forceinline__ unsigned cnt_total(unsigned long long v) {
+    unsigned t = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) t += (unsigned)(v >> (8 * i)) & 0xffu;
+    return t;
+}
+
+// One (head h, half) of the combine of a sequence whose ns split partials start at P, by the
+// 512 threads of the attention workgroup: thread t does the work of k_combine_r512's threads t
+// and t + 512 in the same order (split groups sg and sg + 4; W_UV rows dd and dd + 32), so the
+// outputs equal that kernel's bit for bit. wv: the thread's two W_UV row slices. lds: 27 KB.
+__device__ __forceinline__ void comb_task(const float *P, float *ho, uint16_t *hos, int n, int HO, int b, int h,
+                                          int half, int ns, const v4i (&wv)[2][4], uint8_t *lds) {
+    constexpr int NH = 16;
+    float *mx = (float *)lds;                      // 512 floats
+    float *wts = mx + 512;                         // kMaxSplits floats
+    v4f(*red)[128] = (v4f(*)[128])(wts + kMaxSplits);  // [8][128]
+    float *sinv = (float *)(red + 8);
+    const int tid = threadIdx.x;
+    const int sg = __builtin_amdgcn_readfirstlane(tid >> 7);  // split groups sg and sg + 4
+    const size_t stride = (size_t)NH * (512 + 2);
+    int c4 = tid & 127;
+    asm volatile("" : "+v"(c4));
+    const float *Pm = P + (size_t)NH * 512 + h;
+    float m0 = 0.f, l0 = 0.f;
+    if (tid < 64) {
+        const int i0 = min(tid, ns - 1);
+        m0 = Pm[(size_t)i0 * stride];
+        l0 = Pm[(size_t)i0 * stride + NH];
+    }
+    const float *Pg = P + (size_t)h * 512 + 4 * c4;
+    v4f pre[2][kCombPre];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < kCombPre; ++i)
+            pre[j][i] = sg + 4 * j + 8 * i < ns ? *(const v4f *)(Pg + (size_t)(sg + 4 * j + 8 * i) * stride)
+                                                : v4f{0.f, 0.f, 0.f, 0.f};
+    if (tid < 64) {
+        float m = tid < ns ? m0 : -INFINITY;
+        for (int i = tid + 64; i < ns; i += 64) m = fmaxf(m, Pm[(size_t)i * stride]);
+        m = wave_max(m);
+        float den = 0.f;
+        if (tid < ns) {
+            const float e = __expf(m0 - m);
+            wts[tid] = e;
+            den = l0 * e;
+        }
+        for (int i = tid + 64; i < ns; i += 64) {
+            const float e = __expf(Pm[(size_t)i * stride] - m);
+            wts[i] = e;
+            den = fmaf(Pm[(size_t)i * stride + NH], e, den);
+        }
+        den = wave_sum(den);
+        if (tid == 0) *sinv = 1.0f / den;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int g = sg + 4 * j;
+        v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < kCombPre; ++i) {
+            const int sp = g + 8 * i;
+            if (sp < ns) {
+                const float wt = wts[sp];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[e] = fmaf(pre[j][i][e], wt, acc[e]);
+            }
+        }
+        for (int sp = g + 8 * kCombPre; sp < ns; sp += 8 * kCombPre) {
+            v4f more[kCombPre];
+#pragma unroll
+            for (int i = 0; i < kCombPre; ++i)
+                more[i] = sp + 8 * i < ns ? *(const v4f *)(Pg + (size_t)(sp + 8 * i) * stride) : v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < kCombPre; ++i) {
+                if (sp + 8 * i < ns) {
+                    const float wt = wts[sp + 8 * i];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[e] = fmaf(more[i][e], wt, acc[e]);
+                }
+            }
+        }
+        red[g][c4] = acc;
+    }
+    __syncthreads();
+    {
+        const int cq = tid >> 2, e = tid & 3;
+        float v = red[0][cq][e];
+#pragma unroll
+        for (int g8 = 1; g8 < 8; ++g8) v += red[g8][cq][e];
+        mx[mx_pos(tid)] = v * *sinv;
+    }
+    __syncthreads();
+    const int q = tid & 15;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int dd = 64 * half + 32 * r + (tid >> 4);
+        float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const v4f m0v = *(const v4f *)(mx + mx_pos(32 * q + 8 * c));
+            const v4f m1v = *(const v4f *)(mx + mx_pos(32 * q + 8 * c + 4));
+            const uint32_t u0 = (uint32_t)wv[r][c][0], u1 = (uint32_t)wv[r][c][1];
+            const uint32_t u2 = (uint32_t)wv[r][c][2], u3 = (uint32_t)wv[r][c][3];
+            acc0 = fmaf(__uint_as_float(u0 << 16), m0v.x, acc0);
+            acc1 = fmaf(__uint_as_float(u0 & 0xffff0000u), m0v.y, acc1);
+            acc0 = fmaf(__uint_as_float(u1 << 16), m0v.z, acc0);
+            acc1 = fmaf(__uint_as_float(u1 & 0xffff0000u), m0v.w, acc1);
+            acc0 = fmaf(__uint_as_float(u2 << 16), m1v.x, acc0);
+            acc1 = fmaf(__uint_as_float(u2 & 0xffff0000u), m1v.y, acc1);
+            acc0 = fmaf(__uint_as_float(u3 << 16), m1v.z, acc0);
+            acc1 = fmaf(__uint_as_float(u3 & 0xffff0000u), m1v.w, acc1);
+        }
+        const float hsum = row16_sum(acc0 + acc1);  // the 16 lanes of row dd
+        if (q == 0) {
+            const size_t o = (size_t)b * HO + (size_t)h * 128 + dd;
+            ho[o] = hsum;
+            uint16_t hi, lo;
+            split_bf16(hsum, hi, lo);
+            hos[o] = hi;
+            hos[(size_t)n * HO + o] = lo;
+        }
+    }
+}
+
+// The W_UV row slices of task (h, half) for comb_task (kv_b: [NH][DN + 128][512] bf16, DN = 128).
+__device__ __forceinline__ void comb_wuv(const uint16_t *kv_b, int h, int half, v4i (&wv)[2][4]) {
+    const int tid = threadIdx.x, q = tid & 15;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int dd = 64 * half + 32 * r + (tid >> 4);
+        const uint16_t *row = kv_b + ((size_t)h * 256 + 128 + dd) * 512 + 32 * q;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) wv[r][c] = *(const v4i *)(row + 8 * c);
+    }
+}
+
+__device__ __forceinline__ void q8_comb_tail(const AttnArgs &a, const SeqDesc &s, int b, int split, uint8_t *smem) {
+    constexpr int kTasks = 32;  // (head, half) pairs of 16 heads
+    const int ns = s.nsplit, tid = threadIdx.x;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partial stores are in the L2
+    __syncthreads();
+    unsigned long long *cf = fq_cflag(a.fq, b);
+    const unsigned long long mine = 1ull << (8 * xcc_id());
+    if (tid == 0) __hip_atomic_fetch_add(cf, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    v4i wv[2][4];
+    if (split < kTasks) comb_wuv(a.fq.kvb, split >> 1, split & 1, wv);  // requested before the wait
+    if (tid == 0) {
+        if (split < kTasks) {
+            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+            unsigned long long v;
+            while (cnt_total(v = cnt_poll(cf)) < (unsigned)ns) {
+                if (__builtin_amdgcn_s_memrealtime() - t0 > kFqSpinTicks) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+            if (v != mine * (unsigned long long)ns)  // a timeout, or splits on another XCC
+                __hip_atomic_store(a.fq.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+    }
+    if (split >= kTasks) return;
+    __syncthreads();
+    asm volatile("buffer_inv sc0" ::: "memory");  // no L1 line of the partials from before the wait
+    const float *P = a.part + (size_t)s.split0 * 16 * 514;
+    for (int t = split;;) {
+        comb_task(P, a.fq.ho, a.fq.hos, a.nseq, a.d.HO, b, t >> 1, t & 1, ns, wv, smem);
+        t += ns;
+        if (t >= kTasks) break;
+        __syncthreads();  // the task's LDS is rewritten by the next
+        comb_wuv(a.fq.kvb, t >> 1, t & 1, wv);
     }
 }
 
 // ONCE: each history row is read by one workgroup (non-temporal loads). FUSE: the launch
 // prepares the queries and appends the rows itself (fq_produce; no block launches).
-template <bool ONCE, bool FUSE = false>
+template <bool ONCE, bool FUSE = false, bool COMB = false>
 __global__ __launch_bounds__(512) void k_attn_q8_mfma(KVL_ATTN_HOT_PARAMS, AttnArgs a) {
+    static_assert(!COMB || FUSE, "the combine tail is a form of the fused launch");
     KVL_ATTN_HOT_INIT;
     __shared__ __attribute__((aligned(16))) uint8_t smem[kQ8SmemB];
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int b, split, pidx;
     SeqDesc s;
-    if (!seq_of(a, h, b, split, pidx, s)) return;
+    if (!seq_of<COMB>(a, h, b, split, pidx, s)) return;
     const int r0 = split * s.rps;
     const int r1 = split == s.nsplit - 1 ? s.len : r0 + s.rps;  // last split takes the rest
     const int nch = (r1 - r0 + kQ8Ch - 1) / kQ8Ch;
     // chunk of this split holding the row appended in this launch, or -1
     const int cpos = FUSE && split == s.nsplit - 1 ? (s.pos - r0) / kQ8Ch : -1;
-    if (w >= 4) q8_mix_role<ONCE, FUSE>(a, h, s, smem, w - 4, b, r0, r1, nch, pidx, cpos);
+    if (w >= 4) q8_mix_role<ONCE, FUSE, COMB>(a, h, s, smem, w - 4, b, r0, r1, nch, pidx, cpos);
     else q8_score_role<FUSE>(a, h, s, smem, w, b, r0, r1, nch, pidx, cpos);
+    if constexpr (COMB) q8_comb_tail(a, s, b, split, smem);
+}
+
+bool comb_ok(const SeqTable &t, const Dims &d, int total_splits) {
+    if (t.n < kXcds || t.n % kXcds != 0 || d.NH != 16 || d.R != 512 || d.DN != 128 || d.DV != 128 ||
+        d.HO != 16 * 128)
+        return false;
+    const int ns = t.s[0].nsplit;
+    if (ns < 1 || ns > 255 || ns * t.n != total_splits) return false;  // 255: q8_comb_tail's byte counts
+    for (int i = 0; i < t.n; ++i)
+        if (t.s[i].nsplit != ns || t.s[i].split0 != i * ns) return false;
+    return true;
 }
 
 hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t, const Dims &d,
@@ -2658,7 +2894,8 @@ hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t
     a.fq = fq ? *fq : FqArgs{};
     if (fq && (kind != kAttnQ8Mfma || members > 0 || fmt != kFmtQ8 || d.NH != 16 || d.R != 512 || d.DR != 64 ||
                d.DN != 128 || d.QD != 192 || 17 * t.n > total_splits || !fq->y || !fq->ukt || !fq->cs || !fq->norm ||
-               !fq->rows || !fq->flags || !fq->err))
+               !fq->rows || !fq->flags || !fq->err ||
+               (fq->comb && (!comb_ok(t, d, total_splits) || !fq->kvb || !fq->ho || !fq->hos))))
         return hipErrorInvalidValue;
     a.t = t;
     a.d = d;
@@ -2683,6 +2920,7 @@ hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t
     }
     if (kind == kAttnQ8Mfma) {
         if (a.members > 0) hipLaunchKernelGGL(k_attn_q8_mfma<false>, dim3(grid), dim3(512), 0, st, a.members, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);
+        else if (fq && fq->comb) hipLaunchKernelGGL((k_attn_q8_mfma<true, true, true>), dim3(grid), dim3(512), 0, st, a.members, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);
         else if (fq) hipLaunchKernelGGL((k_attn_q8_mfma<true, true>), dim3(grid), dim3(512), 0, st, a.members, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);
         else hipLaunchKernelGGL(k_attn_q8_mfma<true>, dim3(grid), dim3(512), 0, st, a.members, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);
     } else if (kind == kAttnF32Mfma) {
@@ -2850,8 +3088,6 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
 // loaded once, so that the grid stays within one round of the CUs.
 // LDS position of mix column c: the 4-column groups of each 32-column row are XOR-permuted by the
 // row, so that the W_UV dot's reads (lane q: columns 32 q + 8 c' .. + 7) fall in distinct banks.
-__device__ __forceinline__ int mx_pos(int c) { return c ^ (((c >> 5) & 7) << 2); }
-constexpr int kCombPre = 8;
 constexpr int kCombBlocks = 256;  // k_combine_r512 grid target: one round on the CUs of an MI355X
 constexpr int kCombWide = 16;     // k_combine_r512x8: at most this many splits per sequence
 __global__ __launch_bounds__(1024) void k_combine_r512(const float *part_, const uint16_t *kv_b_, float *ho_, uint16_t *hos_, int spb_, int nh_, int dn_, int n_, int un_, CombineArgs a) {

@@ -87,8 +87,9 @@ hipError_t launch_gemv(hipStream_t st, float *Y, int ldy, const float *X, int ld
 // so history rows appended by decode equal those the state prefill writes.
 constexpr int kGemvKs = 4;
 bool gemv_ksplit_ok(int in, int ldx);
-// zero_flags (may be null): words kFqFlagStride * i, i < nzero, the launch clears (the readiness
-// flags of a fused Q8 attention launch that follows, FqArgs::flags).
+// zero_flags (may be null): words kFqFlagStride * i and kFqFlagStride * i + 1, i < nzero, the
+// launch clears (the readiness flags and combine counters of a fused Q8 attention launch that
+// follows, FqArgs::flags).
 hipError_t launch_gemv_ksplit(hipStream_t st, float *Y, size_t pstride, int ldy, const float *X,
                               int ldx, int B, const uint16_t *W0, int out0, const uint16_t *W1,
                               int out1, int in, unsigned *zero_flags = nullptr, int nzero = 0);
@@ -165,7 +166,17 @@ struct FqArgs {
     size_t pstride;
     int ldy, koff, row_bytes;
     float eps;
+    // comb != 0: the launch also combines the split partials into ho / hos (launch_combine's
+    // outputs, W_UV from kvb), with every split of a sequence on one XCD; needs t.n a multiple
+    // of 8 and every sequence with the same split count ns, sequence b's splits from b * ns
+    // (comb_ok), and flags words kFqFlagStride * (2 kMaxBatch + b), b < B, zeroed as the others.
+    int comb;
+    const uint16_t *kvb;
+    float *ho;
+    uint16_t *hos;
 };
+// True when a fused launch with this table and split count can combine in place (FqArgs::comb).
+bool comb_ok(const SeqTable &t, const Dims &d, int total_splits);
 // fq: null, or the fused form (kind == kAttnQ8Mfma, members == 0, Kimi shapes, at most one
 // round of workgroups, 17 B <= total_splits): blocks [0, 16 B) prepare one (sequence, head)
 // query each, blocks [16 B, 17 B) append one row each, before their own split.

@@ -166,12 +166,14 @@ struct Ctx {
     DevBuf work, part, scores, prefill, fill, fillx, layer, sink;
     DevBuf rflag;  // int: raised by a stream-ordered prefill outside the MFMA route's range
     PinBuf pin_in, pin_out;
-    // fused Q8 decode (the attention launch prepares the queries and appends the rows): its
-    // readiness flags (device, 2 x kMaxBatch lines, cleared by the q_proj | kv_a GEMV of each
-    // call) and a host-visible word raised if one of its waits timed out
+    // fused Q8 decode (the attention launch prepares the queries and appends the rows, and where
+    // comb_ok also combines): its readiness flags and combine counters (device, 3 x kMaxBatch
+    // lines, cleared by the q_proj | kv_a GEMV of each call) and a host-visible word raised if
+    // one of its waits timed out
     unsigned *fq_flags = nullptr;
     int *fq_err = nullptr;
-    bool fq_on = true;  // KVL_MLA_NO_FUSED_QPREP=1 turns the fused form off (the two-launch form)
+    bool fq_on = true;    // KVL_MLA_NO_FUSED_QPREP=1 turns the fused form off (the two-launch form)
+    bool comb_on = true;  // KVL_MLA_NO_FUSED_COMBINE=1: the fused form keeps the combine launch
     bool capturing = false;
     // bumped by every release of library-owned device memory: a graph captured before a bump
     // may hold pointers to freed memory (kvl_mla_graph_launch refuses it)
@@ -224,13 +226,15 @@ int ensure_ready() {
         g_scratch[dev] = p;
     }
     HIP_TRY(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
-    HIP_TRY(hipMalloc(&c.fq_flags, 2 * kMaxBatch * kFqFlagStride * sizeof(unsigned)));
-    HIP_TRY(hipMemset(c.fq_flags, 0, 2 * kMaxBatch * kFqFlagStride * sizeof(unsigned)));
+    HIP_TRY(hipMalloc(&c.fq_flags, 3 * kMaxBatch * kFqFlagStride * sizeof(unsigned)));
+    HIP_TRY(hipMemset(c.fq_flags, 0, 3 * kMaxBatch * kFqFlagStride * sizeof(unsigned)));
     HIP_TRY(hipHostMalloc((void **)&c.fq_err, sizeof(int), hipHostMallocDefault));
     *c.fq_err = 0;
     {
         const char *e = getenv("KVL_MLA_NO_FUSED_QPREP");
         c.fq_on = !(e && e[0] == '1');
+        e = getenv("KVL_MLA_NO_FUSED_COMBINE");
+        c.comb_on = !(e && e[0] == '1');
     }
     c.device = dev;
     c.ncu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
@@ -993,6 +997,11 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
     const bool fuse = c.fq_on && B >= 2 && fmt == kFmtQ8 && kind == kAttnQ8Mfma && !solo && part_cap == 0 && kimi_attn(d) &&
                       d.DN == 128 && d.QD == 192 && gemv_ksplit_ok(d.H, d.H) && ukt_shape(d) && dw.ukt &&
                       17 * B <= total_splits && total_splits <= c.ncu && c.fq_flags && c.fq_err;
+    // ... and the combine inside that launch (q8_comb_tail): eight sequences (or a multiple) with
+    // equal split counts, each sequence's splits on one XCD. Measured (headline stack): see the
+    // design notes on the fused combine.
+    const bool comb = fuse && c.comb_on && comb_ok(t, d, total_splits) && combine_writes_hos(fmt, d) &&
+                      gemv_xs_ok(d.HO);
     {
         // q_proj | kv_a: k split over kGemvKs blocks where the shape allows (the consumers
         // add the partials), else one pass
@@ -1005,7 +1014,7 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
             w.ynp = kGemvKs;
             w.ypstride = (size_t)B * ldy;
             HIP_TRY(launch_gemv_ksplit(st, w.y, w.ypstride, ldy, d_x, d.H, B, dw.q, d.QO, dw.kva,
-                                       d.KVO, d.H, fuse ? c.fq_flags : nullptr, fuse ? 2 * kMaxBatch : 0));
+                                       d.KVO, d.H, fuse ? c.fq_flags : nullptr, fuse ? 3 * kMaxBatch : 0));
         } else {
             w.ynp = 1;
             w.ypstride = 0;
@@ -1046,10 +1055,16 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
             fq.koff = d.QO;
             fq.row_bytes = d.R + 4 + 2 * d.DR;
             fq.eps = eps;
+            if (comb) {
+                fq.comb = 1;
+                fq.kvb = dw.kvb;
+                fq.ho = w.ho;
+                fq.hos = w.hos;
+            }
         }
         HIP_TRY(launch_attention(st, kind, fmt, t, d, rps, total_splits, lmax, w, solo ? B : 0, fuse ? &fq : nullptr));
     }
-    {
+    if (!comb) {
         StageTimer tm(4);
         HIP_TRY(launch_combine(st, fmt, t, d, dw.kvb, w));
     }
@@ -2489,6 +2504,18 @@ int kvl_mla_set_fused_qprep(int on) {
     }
     const int prev = ctx().fq_on ? 1 : 0;
     ctx().fq_on = on == 1;
+    return prev;
+}
+
+int kvl_mla_set_fused_combine(int on) {
+    Guard guard;
+    if (ensure_ready() != 0) return -1;
+    if (on != 0 && on != 1) {
+        set_err("kvl_mla_set_fused_combine: on must be 0 or 1");
+        return -1;
+    }
+    const int prev = ctx().comb_on ? 1 : 0;
+    ctx().comb_on = on == 1;
     return prev;
 }
 

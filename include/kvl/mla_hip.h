@@ -265,6 +265,13 @@ int kvl_mla_timing_enable(int on);
  * bit for bit. Returns the previous setting, or -1. The environment variable
  * KVL_MLA_NO_FUSED_QPREP=1 sets 0 at initialisation. */
 int kvl_mla_set_fused_qprep(int on);
+/* Extension, no counterpart in the reference. Where the fused form above runs for eight
+ * sequences with equal split counts (the batch-8 decode of long histories), the attention launch
+ * also merges the split partials and applies W_UV (the combine), each sequence's splits placed on
+ * one XCD so that its partials are read from that XCD's L2; 0 keeps the combine in a launch of
+ * its own. The results are the same bit for bit. Returns the previous setting, or -1.
+ * KVL_MLA_NO_FUSED_COMBINE=1 sets 0 at initialisation. */
+int kvl_mla_set_fused_combine(int on);
 int kvl_mla_timing_stages(unsigned mask);
 int kvl_mla_timing_read(double *ms, int *count);
 void *kvl_mla_event_record(void);

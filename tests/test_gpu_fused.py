@@ -7,7 +7,10 @@ tested elsewhere, and the block decode, which always takes it, equals single dec
 bit). The cases cover the fused form's edges: eight long sequences (one round of workgroups),
 short sequences whose single split holds the new row in its first chunks (their requests wait
 for the append inside the prologue) beside long ones, and two consecutive steps (the flags are
-cleared by each step's projection launch)."""
+cleared by each step's projection launch). For eight sequences with equal split counts the fused
+launch also combines the split partials (kvl_mla_set_fused_combine; each sequence's splits on one
+XCD): that form must equal the others bit for bit as well, with fewer splits than combine tasks
+(six thousand rows: 24 splits, so a workgroup takes two tasks)."""
 import ctypes as C
 
 import numpy as np
@@ -25,9 +28,11 @@ KIMI = dict(inputs.KIMI)
 CASES = [(6000,) * 8, (100, 9000), (9000, 200, 130, 9000), (63, 9000, 9000)]
 
 
-def run(form, lens, cfg, w, x, steps):
+def run(form, lens, cfg, w, x, steps, comb=1):
     prev = L.kvl_mla_set_fused_qprep(form)
     assert prev in (0, 1)
+    prev_comb = L.kvl_mla_set_fused_combine(comb)
+    assert prev_comb in (0, 1)
     try:
         states = []
         for i, n in enumerate(lens):
@@ -58,6 +63,7 @@ def run(form, lens, cfg, w, x, steps):
         return outs, rows
     finally:
         L.kvl_mla_set_fused_qprep(prev)
+        L.kvl_mla_set_fused_combine(prev_comb)
 
 
 @pytest.mark.parametrize("lens", CASES, ids=["-".join(map(str, c)) for c in CASES])
@@ -71,13 +77,16 @@ def test_fused_equals_two_launch_form(lens):
         steps = 2
         x = np.stack([inputs.hidden(cfg, 0xF2 + t, len(lens)) for t in range(steps)])
         fo, fr = run(1, lens, cfg, w, x, steps)
+        co, cr = run(1, lens, cfg, w, x, steps, comb=0)
         so, sr = run(0, lens, cfg, w, x, steps)
         for t in range(steps):
             assert np.isfinite(fo[t]).all()
             np.testing.assert_array_equal(fo[t], so[t], err_msg=f"step {t} outputs")
+            np.testing.assert_array_equal(co[t], so[t], err_msg=f"step {t} outputs (separate combine)")
         for i in range(len(lens)):
             for k, name in enumerate(("codes", "scales", "rope")):
                 np.testing.assert_array_equal(fr[i][k], sr[i][k], err_msg=f"sequence {i} {name}")
+                np.testing.assert_array_equal(cr[i][k], sr[i][k], err_msg=f"sequence {i} {name} (separate combine)")
     finally:
         L.kvl_mla_release_weights(C.byref(w))
 
@@ -87,3 +96,7 @@ def test_fused_switch_rejects_bad_values():
     assert prev in (0, 1)
     assert L.kvl_mla_set_fused_qprep(2) == -1
     assert L.kvl_mla_set_fused_qprep(prev) == 1
+    prev = L.kvl_mla_set_fused_combine(1)
+    assert prev in (0, 1)
+    assert L.kvl_mla_set_fused_combine(-1) == -1
+    assert L.kvl_mla_set_fused_combine(prev) == 1
