@@ -279,26 +279,58 @@ def main():
         else:
             L.kvl_mla_timing_read(ms, cnt)
     # The attention launch of this workload also prepares the queries and appends the rows
-    # (kvl_mla_set_fused_qprep): its algorithmic bytes are the history rows plus W_UK^T, the
-    # q_proj | kv_a partials it reads and the query operands and rows it writes.
+    # (kvl_mla_set_fused_qprep) and combines the split partials (kvl_mla_set_fused_combine): its
+    # algorithmic bytes are the history rows plus W_UK^T and W_UV, the q_proj | kv_a partials it
+    # reads, the query operands and rows it writes and the head outputs (fp32 and bf16 hi | lo).
+    # The split partials stay in the L2 of the XCD that combines them and are not counted.
     H_, NH_, R_, DN_, DR_ = cfg.hidden_size, cfg.num_heads, cfg.kv_lora_rank, cfg.qk_nope_dim, cfg.qk_rope_dim
-    QO_, KVO_ = NH_ * (DN_ + DR_), R_ + DR_
-    fused_extra = (2 * NH_ * R_ * DN_ + 4 * 4 * B * (QO_ + KVO_) + B * NH_ * (2 * R_ + 4 + 4 * DR_)
-                   + B * Q8_ROW)
+    QO_, KVO_, DV_ = NH_ * (DN_ + DR_), R_ + DR_, cfg.v_head_dim
+    fused_extra = (2 * NH_ * R_ * DN_ + 2 * NH_ * R_ * DV_ + 4 * 4 * B * (QO_ + KVO_)
+                   + B * NH_ * (2 * R_ + 4 + 4 * DR_) + B * Q8_ROW + B * NH_ * DV_ * (4 + 2 + 2))
     attn_bytes = hist_bytes + fused_extra
     attn_gbs = attn_bytes / (attn_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_bytes(B, CTX),
-                "kernel": "k_attn_q8_mfma<true, true> (attention with the query preparation and the "
-                          "row append of its sequences)",
+                "kernel": "k_attn_q8_mfma<true, true, true> (attention with the query preparation, the "
+                          "row append and the combine of its sequences)",
                 "algorithmic_bytes_per_launch": attn_bytes, "history_bytes_per_launch": hist_bytes,
                 "avg_launch_ms": round(attn_ms, 5), "timing": attn_src}
     if attn_only_ms is not None:
         roofline["avg_launch_ms_attention_events_only"] = round(attn_only_ms, 5)
 
+    # The step with the combine in a launch of its own (the query preparation still inside the
+    # attention launch): its step time.
+    sep_comb = None
+    if graph is not None:
+        prev_comb = L.kvl_mla_set_fused_combine(0)
+        try:
+            lib.check(L.kvl_mla_capture_begin(), "capture begin")
+            try:
+                step()
+            finally:
+                g4 = C.c_void_p()
+                rc = L.kvl_mla_capture_end(C.byref(g4))
+            lib.check(rc, "capture end (separate combine)")
+            for _ in range(max(1, args.warmup)):
+                lib.check(L.kvl_mla_graph_launch(g4), "graph launch")
+            lib.check(L.kvl_mla_synchronize(), "sync")
+            t0 = time.perf_counter()
+            for _ in range(K):
+                lib.check(L.kvl_mla_graph_launch(g4), "graph launch")
+            lib.check(L.kvl_mla_synchronize(), "sync")
+            sep_ms = (time.perf_counter() - t0) * 1e3 / K
+            L.kvl_mla_graph_destroy(g4)
+            sep_comb = {"ms_per_step": round(sep_ms, 4),
+                        "kernels": "k_attn_q8_mfma<true, true> then k_combine_r512"}
+            log(f"[bench] combine in its own launch: step {sep_ms:.3f} ms")
+        finally:
+            L.kvl_mla_set_fused_combine(prev_comb)
+    if sep_comb is not None:
+        roofline["separate_combine_form"] = sep_comb
+
     # The same step in the two-launch form (append + query preparation in a launch of their own,
-    # then the attention alone): its step time, and the attention kernel's rate over the history
-    # bytes, from the stage events inside the step graph as above.
+    # then the attention alone, then the combine): its step time, and the attention kernel's rate
+    # over the history bytes, from the stage events inside the step graph as above.
     two = None
     if graph is not None:
         prev_form = L.kvl_mla_set_fused_qprep(0)
