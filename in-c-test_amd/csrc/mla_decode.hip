@@ -242,12 +242,16 @@ __global__ __launch_bounds__(1024) void k_gemv_ksplit(const float *X, const uint
 // Requires in = NW * 32 * KPW.
 template <int NG, int KPW, int RB = 16, int NW = 16>
 __global__ __launch_bounds__(64 * NW) void k_gemv_xs(float *Y, const uint16_t *XS, const uint16_t *W0, int ldy, int B,
-                                                  int nout, int in, int acc) {
+                                                  int nout, int in, int acc, unsigned *zf, int nz) {
     // scalar arguments: preloaded into SGPRs at wave start (no argument round trip)
     const GemvSplitArgs a{Y, nullptr, XS, W0, nullptr, 0, ldy, 0, B, nout, 0, in, acc};
     static_assert(RB == 16 || RB == 8, "rows per block");
     __shared__ v4f red[NW][NG][64];
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
+    // block 0 clears the flags of the fused attention launch before it (the first 8 bytes of
+    // each line), for the next fused launch
+    if (blockIdx.x == 0 && blockIdx.z == 0 && zf != nullptr)
+        for (int k = tid; k < nz; k += 64 * NW) *(uint2 *)(zf + (size_t)k * kFqFlagStride) = uint2{0u, 0u};
     const int out = a.out0, part = n >> 3;
     const uint16_t *wrow = a.W0 + (size_t)min((int)blockIdx.x * RB + (n % RB), out - 1) * a.in;
     const int kbase = w * (32 * KPW) + g * 8;
@@ -567,8 +571,16 @@ hipError_t launch_kva_tok(hipStream_t st, float *Y, size_t pstride, int ldy, con
 
 bool gemv_xs_ok(int in) { return in == 2048 || in == 4096; }
 
+__global__ __launch_bounds__(256) void k_clear_flags(unsigned *zf, int nz) {
+    for (int k = threadIdx.x; k < nz; k += 256) *(uint2 *)(zf + (size_t)k * kFqFlagStride) = uint2{0u, 0u};
+}
+hipError_t launch_clear_flags(hipStream_t st, unsigned *flags, int nlines) {
+    hipLaunchKernelGGL(k_clear_flags, dim3(1), dim3(256), 0, st, flags, nlines);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemv_xs(hipStream_t st, float *Y, int ldy, const uint16_t *XS, int B,
-                          const uint16_t *W, int out, int in, bool accumulate) {
+                          const uint16_t *W, int out, int in, bool accumulate, unsigned *zf, int nz) {
     if (!gemv_xs_ok(in) || B < 1 || ((uintptr_t)XS % 16) != 0 || ((uintptr_t)W % 16) != 0 || out <= 0 ||
         (B + 15) / 16 > 65535)
         return hipErrorInvalidValue;
@@ -577,12 +589,12 @@ hipError_t launch_gemv_xs(hipStream_t st, float *Y, int ldy, const uint16_t *XS,
     if (in == 2048) {
         // four waves at every batch size: each output is the same sum in the same order whatever
         // the batch (a block decode's members equal lone decodes bit for bit)
-        if (two) hipLaunchKernelGGL((k_gemv_xs<2, 16, 16, 4>), grid, dim3(256), 0, st, Y, XS, W, ldy, B, out, in, accumulate ? 1 : 0);
-        else hipLaunchKernelGGL((k_gemv_xs<1, 16, 8, 4>), dim3((out + 7) / 8, 1, grid.z), dim3(256), 0, st, Y, XS, W, ldy, B, out, in, accumulate ? 1 : 0);
+        if (two) hipLaunchKernelGGL((k_gemv_xs<2, 16, 16, 4>), grid, dim3(256), 0, st, Y, XS, W, ldy, B, out, in, accumulate ? 1 : 0, zf, nz);
+        else hipLaunchKernelGGL((k_gemv_xs<1, 16, 8, 4>), dim3((out + 7) / 8, 1, grid.z), dim3(256), 0, st, Y, XS, W, ldy, B, out, in, accumulate ? 1 : 0, zf, nz);
     } else {
         // eight waves of 16 k-blocks (sixteen waves of 8 spill registers at NG = 2)
-        if (two) hipLaunchKernelGGL((k_gemv_xs<2, 16, 16, 8>), grid, dim3(512), 0, st, Y, XS, W, ldy, B, out, in, accumulate ? 1 : 0);
-        else hipLaunchKernelGGL((k_gemv_xs<1, 16, 16, 8>), grid, dim3(512), 0, st, Y, XS, W, ldy, B, out, in, accumulate ? 1 : 0);
+        if (two) hipLaunchKernelGGL((k_gemv_xs<2, 16, 16, 8>), grid, dim3(512), 0, st, Y, XS, W, ldy, B, out, in, accumulate ? 1 : 0, zf, nz);
+        else hipLaunchKernelGGL((k_gemv_xs<1, 16, 16, 8>), grid, dim3(512), 0, st, Y, XS, W, ldy, B, out, in, accumulate ? 1 : 0, zf, nz);
     }
     return hipGetLastError();
 }
@@ -2002,6 +2014,103 @@ __device__ __forceinline__ double block512_sum_f64(double v, double *red8) {
     return ((red8[0] + red8[1]) + (red8[2] + red8[3])) + ((red8[4] + red8[5]) + (red8[6] + red8[7]));
 }
 
+// Projection counts and the exit count (kFqFlagLines): line 3 kMaxBatch + i.
+__device__ __forceinline__ unsigned *fq_gflag(const FqArgs &f, int i) {
+    return f.flags + (size_t)kFqFlagStride * (3 * kMaxBatch + i);
+}
+// Thread 0 polls *flag until it reaches target (bounded, as fq_wait), then the whole workgroup
+// goes on.
+__device__ __forceinline__ void fq_wait_all(const FqArgs &f, const unsigned *flag, unsigned target) {
+    if (threadIdx.x == 0) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+            if (__builtin_amdgcn_s_memrealtime() - t0 > kFqSpinTicks) {
+                __hip_atomic_store(f.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
+    __syncthreads();
+}
+
+// The q_proj | kv_a projection block of k_gemv_ksplit<1, 1> with this workgroup's index (B <= 8
+// sequences, in = 2048, the same XCD-aware block -> (row block, k quarter) map), by the 512
+// threads of a fused attention workgroup: wave w does that kernel's waves w and w + 8 (k-blocks
+// kq 512 + 32 w and + 256), and the sixteen products are summed through LDS in that kernel's
+// wave order, in two halves (lds: 32 KB), so the partials written to y equal its outputs bit for
+// bit. They are stored with device-scope stores (read on other XCDs in this launch), and the
+// block counted on its head's counter (q rows: 192 per head) or the kv_a counter (index 16).
+// Called by both roles before any history request: its loads are then first in the CU's queue
+// and its waits cover nothing else. (Measured on the headline step: with the task on the score
+// waves only and the mix waves' history requests issued beside it, 1.404 ms against 1.378 ms.)
+__device__ __forceinline__ void fq_gemv(const FqArgs &f, int B, uint8_t *lds) {
+    const int i = blockIdx.x;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, n = l & 15, g = l >> 4;
+    const int xcd = i & 7, rb = 2 * (i >> 3) + (xcd & 1);
+    const int out = f.out0 + f.out1, kq = xcd >> 1, row0 = rb * 64, part = n >> 3;
+    if (!f.gemv || i >= kGemvTasks || row0 >= out) return;  // uniform per workgroup
+    v4f(*red)[4][64] = (v4f(*)[4][64])lds;                  // [8][4][64]
+    const uint16_t *wr[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int row = min(row0 + 16 * t + n, out - 1);  // rows past the end are never stored
+        wr[t] = row < f.out0 ? f.wq + (size_t)row * f.in : f.wkva + (size_t)(row - f.out0) * f.in;
+    }
+    v4i wa[2][4];
+    v4f xa[2], xb[2];
+    const float *xr = f.x + (size_t)min(n & 7, B - 1) * f.ldx;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int kbase = kq * 512 + (w + 8 * j) * 32 + g * 8;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) wa[j][t] = __builtin_nontemporal_load((const v4i *)(wr[t] + kbase));
+        xa[j] = *(const v4f *)(xr + kbase);
+        xb[j] = *(const v4f *)(xr + kbase + 4);
+    }
+    v4f acc[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const v8bf xv = split8_part(xa[j], xb[j], part);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            acc[j][t] = mfma_bf16(__builtin_bit_cast(v8bf, wa[j][t]), xv, v4f{0.f, 0.f, 0.f, 0.f});
+    }
+    v4f s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) red[w][t][l] = acc[j][t];
+        __syncthreads();
+        if (w < 4) {
+            // wave t sums row tile t over the sixteen waves in order (waves 8 j .. 8 j + 7 here)
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                if (j == 0 && q == 0) s = red[0][w][l];
+                else s += red[q][w][l];
+            }
+        }
+        __syncthreads();
+    }
+    if (w < 4) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[e] += dpp_f32<0x128>(s[e]);  // row_ror:8 = lane ^ 8
+        if (n < 8 && n < B) {
+            float *y = f.y + (size_t)kq * f.pstride + (size_t)n * f.ldy;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = row0 + 16 * w + 4 * g + e;
+                if (r < out) st_sc1_b32(y + r, __float_as_uint(s[e]));
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the stores have reached memory
+    }
+    __syncthreads();
+    if (tid == 0)
+        __hip_atomic_fetch_add(fq_gflag(f, row0 < f.out0 ? row0 / 192 : 16), 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Query of (sequence b, head h): qprep_body's Q8 path for R = 512, DN = 128, DR = 64, QD = 192
 // over 8 waves (wave w: latent tiles 4 (w & 1) .. +3 of qprep_body's wave w >> 1). scr: 2848 B.
 __device__ __forceinline__ void fq_qprep(const FqArgs &f, const AttnHot &hh, const SeqDesc &s, int b, int h,
@@ -2016,6 +2125,7 @@ __device__ __forceinline__ void fq_qprep(const FqArgs &f, const AttnHot &hh, con
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) wa[tt][ks] = *(const v8bf *)(ut + (size_t)((t0 + tt) * 4 + ks) * 64 * 8);
     const float *qh = f.y + (size_t)b * f.ldy + (size_t)h * 192;
+    if (f.gemv) fq_wait_all(f, fq_gflag(f, h), 12u);  // the 3 row blocks x 4 k quarters of head h
     if (tid < 192) {
         const float v = sum_parts(qh + tid, kGemvKs, f.pstride);
         if (tid < 128) qn[tid] = v;
@@ -2100,6 +2210,7 @@ __device__ __forceinline__ void fq_append(const FqArgs &f, const SeqDesc &s, int
     float *redf = (float *)(redd + 8);
     const int tid = threadIdx.x, pos = s.pos;
     const float *ky = f.y + (size_t)b * f.ldy + f.koff;
+    if (f.gemv) fq_wait_all(f, fq_gflag(f, 16), 36u);  // the 9 kv_a row blocks x 4 k quarters
     const float kv0 = sum_parts(ky + tid, kGemvKs, f.pstride);
     const float kv1 = tid < 64 ? sum_parts(ky + 512 + tid, kGemvKs, f.pstride) : 0.f;
     const float nw = bf16_to_f32(f.norm[tid]);
@@ -2273,9 +2384,11 @@ __device__ __forceinline__ void q8_score_role(const AttnArgs &a, const AttnHot &
     v8bf qrh[2], qrl[2];
     float qsd[4], m_run[4], l_lane[4];
     if constexpr (FUSE) {
-        // this workgroup's producer task, then (one poller, barrier Q) the 16 query heads of its
-        // sequence and, where the split holds the new row (whose scale the loads below read and
-        // whose chunk the mix waves request after Q), that row
+        // this workgroup's projection task (FqArgs::gemv; LDS: code slot 3, free until the
+        // query copy after Q), its producer task, then (one poller, barrier Q) the 16 query heads
+        // of its sequence and, where the split holds the new row (whose scale the loads below
+        // read and whose chunk the mix waves request after Q), that row
+        fq_gemv(a.fq, h.nseq, smem + 3 * kQ8CodeB);
         fq_produce(a, h, smem + kQ8WqOff);
         if (w == 0) {
             fq_wait(a.fq, fq_qflag(a.fq, b), 16u);
@@ -2551,6 +2664,8 @@ __device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const AttnHot &h,
             }
         };
         const bool prod = (int)blockIdx.x < 17 * h.nseq;
+        // a projection task goes before the history requests (fq_gemv)
+        fq_gemv(a.fq, h.nseq, smem + 3 * kQ8CodeB);
         if (!prod) issue_ahead();
         fq_produce(a, h, smem + kQ8WqOff);
         if (prod) issue_ahead();
@@ -2876,6 +2991,11 @@ __global__ __launch_bounds__(512) void k_attn_q8_mfma(KVL_ATTN_HOT_PARAMS, AttnA
     if constexpr (COMB) q8_comb_tail(a, s, b, split, smem);
 }
 
+bool gemv_fuse_ok(const Dims &d, int B, int total_splits) {
+    return B >= 1 && B <= 8 && d.H == 2048 && d.NH == 16 && d.QD == 192 && d.QO == 16 * 192 && d.KVO == 576 &&
+           total_splits >= kGemvTasks;
+}
+
 bool comb_ok(const SeqTable &t, const Dims &d, int total_splits) {
     if (t.n < kXcds || t.n % kXcds != 0 || d.NH != 16 || d.R != 512 || d.DN != 128 || d.DV != 128 ||
         d.HO != 16 * 128)
@@ -2895,7 +3015,10 @@ hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t
     if (fq && (kind != kAttnQ8Mfma || members > 0 || fmt != kFmtQ8 || d.NH != 16 || d.R != 512 || d.DR != 64 ||
                d.DN != 128 || d.QD != 192 || 17 * t.n > total_splits || !fq->y || !fq->ukt || !fq->cs || !fq->norm ||
                !fq->rows || !fq->flags || !fq->err ||
-               (fq->comb && (!comb_ok(t, d, total_splits) || !fq->kvb || !fq->ho || !fq->hos))))
+               (fq->comb && (!comb_ok(t, d, total_splits) || !fq->kvb || !fq->ho || !fq->hos)) ||
+               (fq->gemv && (!gemv_fuse_ok(d, t.n, total_splits) || !fq->x || !fq->wq || !fq->wkva ||
+                             fq->in != d.H || fq->out0 != d.QO || fq->out1 != d.KVO || (uintptr_t)fq->x % 16 != 0 ||
+                             fq->ldx % 4 != 0))))
         return hipErrorInvalidValue;
     a.t = t;
     a.d = d;

@@ -102,8 +102,12 @@ hipError_t launch_kva_tok(hipStream_t st, float *Y, size_t pstride, int ldy, con
 // launch_combine writes them (DecodeWork::hos). Shapes when gemv_xs_ok (in = 2048 or 4096),
 // any B.
 bool gemv_xs_ok(int in);
+// zf, nz (may be null): flag lines the launch clears (as launch_gemv_ksplit's zero_flags).
 hipError_t launch_gemv_xs(hipStream_t st, float *Y, int ldy, const uint16_t *XS, int B,
-                          const uint16_t *W, int out, int in, bool accumulate);
+                          const uint16_t *W, int out, int in, bool accumulate, unsigned *zf = nullptr,
+                          int nz = 0);
+// Clears the first 8 bytes of nlines flag lines (kFqFlagStride words apart).
+hipError_t launch_clear_flags(hipStream_t st, unsigned *flags, int nlines);
 
 // RMSNorm of katmp[b] (= y + koff) -> latent row; RoPE of katmp[b][R:] at s.pos. Writes the
 // row into the history at row s.pos (fmt Q8/F32/BF16) or, for kFmtExp, the normalised latent
@@ -156,7 +160,7 @@ enum AttnKind : int { kAttnGeneric = 0, kAttnF32Mfma = 1, kAttnQ8Mfma = 2, kAttn
 // host-visible word set when a wait for them timed out.
 constexpr int kFqFlagStride = 32;  // FqArgs::flags: one 128-byte line per flag
 struct FqArgs {
-    const float *y;
+    float *y;  // written by the launch's projection tasks when gemv
     const uint16_t *ukt;
     const float2 *cs;
     const uint16_t *norm;
@@ -174,9 +178,28 @@ struct FqArgs {
     const uint16_t *kvb;
     float *ho;
     uint16_t *hos;
+    // gemv != 0: the launch also computes the q_proj | kv_a partials into y (k_gemv_ksplit's
+    // blocks as tasks of its first kGemvTasks workgroups, the same arithmetic), from x [B, in]
+    // (16-byte aligned rows, ldx) and the weights wq [out0, in], wkva [out1, in]; needs B <= 8,
+    // in = 2048 and at least kGemvTasks workgroups (gemv_fuse_ok). Flags words
+    // kFqFlagStride * (3 kMaxBatch + i), i < kFqGemvFlags: per-head and kv_a task counts.
+    int gemv;
+    const float *x;
+    const uint16_t *wq, *wkva;
+    int ldx, in, out0, out1;
 };
+// Lines of the flags buffer: query, row, combine (kMaxBatch each), then the projection counts
+// (16 heads, kv_a). The o_proj launch after a fused launch clears them all (launch_gemv_xs's zf),
+// and so does the q_proj | kv_a launch before one (launch_gemv_ksplit's zero_flags).
+constexpr int kFqGemvFlags = 17;
+constexpr int kFqFlagLines = 3 * kMaxBatch + kFqGemvFlags;
+// Workgroups holding a projection task in the fused form: k_gemv_ksplit<1, 1>'s grid at the Kimi
+// shapes (57 row blocks of 64 rows x 4 k quarters, blocks placed XCD-aware).
+constexpr int kGemvTasks = 232;
 // True when a fused launch with this table and split count can combine in place (FqArgs::comb).
 bool comb_ok(const SeqTable &t, const Dims &d, int total_splits);
+// True when a fused launch can also compute the q_proj | kv_a projection (FqArgs::gemv).
+bool gemv_fuse_ok(const Dims &d, int B, int total_splits);
 // fq: null, or the fused form (kind == kAttnQ8Mfma, members == 0, Kimi shapes, at most one
 // round of workgroups, 17 B <= total_splits): blocks [0, 16 B) prepare one (sequence, head)
 // query each, blocks [16 B, 17 B) append one row each, before their own split.

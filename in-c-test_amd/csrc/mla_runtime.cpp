@@ -174,6 +174,10 @@ struct Ctx {
     int *fq_err = nullptr;
     bool fq_on = true;    // KVL_MLA_NO_FUSED_QPREP=1 turns the fused form off (the two-launch form)
     bool comb_on = true;  // KVL_MLA_NO_FUSED_COMBINE=1: the fused form keeps the combine launch
+    bool gemv_on = true;  // KVL_MLA_NO_FUSED_PROJECTION=1: the fused form keeps the projection launch
+    // a fused attention launch was enqueued and the o_proj launch that clears its flags was not
+    // (an error in between): the next launch that relies on clean flags clears them first
+    bool fq_dirty = false;
     bool capturing = false;
     // bumped by every release of library-owned device memory: a graph captured before a bump
     // may hold pointers to freed memory (kvl_mla_graph_launch refuses it)
@@ -226,8 +230,8 @@ int ensure_ready() {
         g_scratch[dev] = p;
     }
     HIP_TRY(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
-    HIP_TRY(hipMalloc(&c.fq_flags, 3 * kMaxBatch * kFqFlagStride * sizeof(unsigned)));
-    HIP_TRY(hipMemset(c.fq_flags, 0, 3 * kMaxBatch * kFqFlagStride * sizeof(unsigned)));
+    HIP_TRY(hipMalloc(&c.fq_flags, kFqFlagLines * kFqFlagStride * sizeof(unsigned)));
+    HIP_TRY(hipMemset(c.fq_flags, 0, kFqFlagLines * kFqFlagStride * sizeof(unsigned)));
     HIP_TRY(hipHostMalloc((void **)&c.fq_err, sizeof(int), hipHostMallocDefault));
     *c.fq_err = 0;
     {
@@ -235,6 +239,8 @@ int ensure_ready() {
         c.fq_on = !(e && e[0] == '1');
         e = getenv("KVL_MLA_NO_FUSED_COMBINE");
         c.comb_on = !(e && e[0] == '1');
+        e = getenv("KVL_MLA_NO_FUSED_PROJECTION");
+        c.gemv_on = !(e && e[0] == '1');
     }
     c.device = dev;
     c.ncu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
@@ -261,7 +267,7 @@ struct StageTimer {
     hipEvent_t a = nullptr, b = nullptr;
     explicit StageTimer(int s) : stage(s) {
         Ctx &c = ctx();
-        if (!c.timing || !((c.timing_mask >> s) & 1u) || (c.capturing && !c.timing_graph)) return;
+        if (s < 0 || !c.timing || !((c.timing_mask >> s) & 1u) || (c.capturing && !c.timing_graph)) return;  // s < 0: not timed
         a = ev_get();
         b = ev_get();
         // inside a capture, only an external record becomes a timestamped node of the graph
@@ -1002,11 +1008,18 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
     // design notes on the fused combine.
     const bool comb = fuse && c.comb_on && comb_ok(t, d, total_splits) && combine_writes_hos(fmt, d) &&
                       gemv_xs_ok(d.HO);
+    // ... and the q_proj | kv_a projection inside it too (fq_gemv): at most eight sequences, x
+    // 16-byte aligned, a launch of at least kGemvTasks workgroups.
+    const bool pfuse = fuse && c.gemv_on && gemv_fuse_ok(d, B, total_splits) && gemv_ksplit_ok(d.H, d.H) &&
+                       ((uintptr_t)d_x % 16) == 0;
     {
         // q_proj | kv_a: k split over kGemvKs blocks where the shape allows (the consumers
         // add the partials), else one pass
-        StageTimer tm(0);
-        if (gemv_ksplit_ok(d.H, d.H)) {
+        StageTimer tm(pfuse ? -1 : 0);
+        if (pfuse) {
+            w.ynp = kGemvKs;
+            w.ypstride = (size_t)B * ldy;
+        } else if (gemv_ksplit_ok(d.H, d.H)) {
             if (((uintptr_t)d_x % 16) != 0) {  // the kernel reads 16-byte vectors
                 HIP_TRY(hipMemcpyAsync(w.x, d_x, (size_t)B * d.H * sizeof(float), hipMemcpyDeviceToDevice, st));
                 d_x = w.x;
@@ -1014,7 +1027,7 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
             w.ynp = kGemvKs;
             w.ypstride = (size_t)B * ldy;
             HIP_TRY(launch_gemv_ksplit(st, w.y, w.ypstride, ldy, d_x, d.H, B, dw.q, d.QO, dw.kva,
-                                       d.KVO, d.H, fuse ? c.fq_flags : nullptr, fuse ? 3 * kMaxBatch : 0));
+                                       d.KVO, d.H, fuse ? c.fq_flags : nullptr, fuse ? kFqFlagLines : 0));
         } else {
             w.ynp = 1;
             w.ypstride = 0;
@@ -1039,6 +1052,10 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
         HIP_TRY(launch_append_qprep(st, fmt, t, d, w.y, ldy, d.QO, w.ynp, w.ypstride, dw.norm, eps, cs, dw.kvb,
                                     dw.ukt, w, kind == kAttnQ8Mfma));
     }
+    if (pfuse && c.fq_dirty) {
+        HIP_TRY(launch_clear_flags(st, c.fq_flags, kFqFlagLines));
+        c.fq_dirty = false;
+    }
     {
         StageTimer tm(3);
         FqArgs fq{};
@@ -1061,7 +1078,18 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
                 fq.ho = w.ho;
                 fq.hos = w.hos;
             }
+            if (pfuse) {
+                fq.gemv = 1;
+                fq.x = d_x;
+                fq.wq = dw.q;
+                fq.wkva = dw.kva;
+                fq.ldx = d.H;
+                fq.in = d.H;
+                fq.out0 = d.QO;
+                fq.out1 = d.KVO;
+            }
         }
+        if (fuse) c.fq_dirty = true;
         HIP_TRY(launch_attention(st, kind, fmt, t, d, rps, total_splits, lmax, w, solo ? B : 0, fuse ? &fq : nullptr));
     }
     if (!comb) {
@@ -1071,10 +1099,15 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
     {
         // o_proj: from the bf16 hi | lo planes of the head outputs when combine wrote them
         StageTimer tm(5);
-        if (combine_writes_hos(fmt, d) && gemv_xs_ok(d.HO))
-            HIP_TRY(launch_gemv_xs(st, d_out, d.H, w.hos, B, dw.o, d.H, d.HO, residual));
-        else
+        // after a fused launch, o_proj clears its flags for the next one (a fused launch that
+        // computes the projection itself has no q_proj | kv_a launch before it to do so)
+        if (combine_writes_hos(fmt, d) && gemv_xs_ok(d.HO)) {
+            HIP_TRY(launch_gemv_xs(st, d_out, d.H, w.hos, B, dw.o, d.H, d.HO, residual, fuse ? c.fq_flags : nullptr,
+                                   fuse ? kFqFlagLines : 0));
+            if (fuse) c.fq_dirty = false;
+        } else {
             HIP_TRY(launch_gemv(st, d_out, d.H, w.ho, d.HO, B, dw.o, d.H, nullptr, 0, d.HO, residual));
+        }
     }
     return 0;
 }
@@ -2392,7 +2425,12 @@ int kvl_mla_graph_launch(void *graph_exec) {
                 "(workspace or RoPE table growth, state free/re-init, weight release): capture it again");
         return -1;
     }
-    HIP_TRY(hipGraphLaunch(g->exec, ctx().stream));
+    Ctx &c = ctx();
+    if (c.fq_dirty && c.fq_flags) {  // a graph's fused launches expect clean flags
+        HIP_TRY(launch_clear_flags(c.stream, c.fq_flags, kFqFlagLines));
+        c.fq_dirty = false;
+    }
+    HIP_TRY(hipGraphLaunch(g->exec, c.stream));
     return 0;
 }
 
@@ -2516,6 +2554,18 @@ int kvl_mla_set_fused_combine(int on) {
     }
     const int prev = ctx().comb_on ? 1 : 0;
     ctx().comb_on = on == 1;
+    return prev;
+}
+
+int kvl_mla_set_fused_projection(int on) {
+    Guard guard;
+    if (ensure_ready() != 0) return -1;
+    if (on != 0 && on != 1) {
+        set_err("kvl_mla_set_fused_projection: on must be 0 or 1");
+        return -1;
+    }
+    const int prev = ctx().gemv_on ? 1 : 0;
+    ctx().gemv_on = on == 1;
     return prev;
 }
 

@@ -272,6 +272,13 @@ int kvl_mla_set_fused_qprep(int on);
  * its own. The results are the same bit for bit. Returns the previous setting, or -1.
  * KVL_MLA_NO_FUSED_COMBINE=1 sets 0 at initialisation. */
 int kvl_mla_set_fused_combine(int on);
+/* Extension, no counterpart in the reference. Where the fused form runs for at most eight
+ * sequences over at least 232 splits, the attention launch also computes the q_proj | kv_a
+ * projection (its first 232 workgroups each take one block of the projection GEMV, and the query
+ * preparation and the append wait for the blocks they read); 0 keeps the projection in a launch
+ * of its own. The results are the same bit for bit. Returns the previous setting, or -1.
+ * KVL_MLA_NO_FUSED_PROJECTION=1 sets 0 at initialisation. */
+int kvl_mla_set_fused_projection(int on);
 int kvl_mla_timing_stages(unsigned mask);
 int kvl_mla_timing_read(double *ms, int *count);
 void *kvl_mla_event_record(void);

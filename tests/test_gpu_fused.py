@@ -10,7 +10,11 @@ for the append inside the prologue) beside long ones, and two consecutive steps 
 cleared by each step's projection launch). For eight sequences with equal split counts the fused
 launch also combines the split partials (kvl_mla_set_fused_combine; each sequence's splits on one
 XCD): that form must equal the others bit for bit as well, with fewer splits than combine tasks
-(six thousand rows: 24 splits, so a workgroup takes two tasks)."""
+(six thousand rows: 24 splits, so a workgroup takes two tasks). With at least 232 splits for at
+most eight sequences the launch also computes the q_proj | kv_a projection
+(kvl_mla_set_fused_projection): eight sequences of 8000 rows (256 splits: projection and
+combine) and three sequences of 63, 30000 and 30000 rows (237 splits: projection only) cover it;
+every combination of the switches must give the same bits."""
 import ctypes as C
 
 import numpy as np
@@ -25,14 +29,16 @@ L = lib.load()
 KIMI = dict(inputs.KIMI)
 
 # history rows per sequence; each case needs 17 x batch <= the launch's split count
-CASES = [(6000,) * 8, (100, 9000), (9000, 200, 130, 9000), (63, 9000, 9000)]
+CASES = [(6000,) * 8, (100, 9000), (9000, 200, 130, 9000), (63, 9000, 9000), (8000,) * 8, (63, 30000, 30000)]
 
 
-def run(form, lens, cfg, w, x, steps, comb=1):
+def run(form, lens, cfg, w, x, steps, comb=1, proj=1):
     prev = L.kvl_mla_set_fused_qprep(form)
     assert prev in (0, 1)
     prev_comb = L.kvl_mla_set_fused_combine(comb)
     assert prev_comb in (0, 1)
+    prev_proj = L.kvl_mla_set_fused_projection(proj)
+    assert prev_proj in (0, 1)
     try:
         states = []
         for i, n in enumerate(lens):
@@ -64,6 +70,7 @@ def run(form, lens, cfg, w, x, steps, comb=1):
     finally:
         L.kvl_mla_set_fused_qprep(prev)
         L.kvl_mla_set_fused_combine(prev_comb)
+        L.kvl_mla_set_fused_projection(prev_proj)
 
 
 @pytest.mark.parametrize("lens", CASES, ids=["-".join(map(str, c)) for c in CASES])
@@ -76,17 +83,16 @@ def test_fused_equals_two_launch_form(lens):
     try:
         steps = 2
         x = np.stack([inputs.hidden(cfg, 0xF2 + t, len(lens)) for t in range(steps)])
-        fo, fr = run(1, lens, cfg, w, x, steps)
-        co, cr = run(1, lens, cfg, w, x, steps, comb=0)
         so, sr = run(0, lens, cfg, w, x, steps)
-        for t in range(steps):
-            assert np.isfinite(fo[t]).all()
-            np.testing.assert_array_equal(fo[t], so[t], err_msg=f"step {t} outputs")
-            np.testing.assert_array_equal(co[t], so[t], err_msg=f"step {t} outputs (separate combine)")
-        for i in range(len(lens)):
-            for k, name in enumerate(("codes", "scales", "rope")):
-                np.testing.assert_array_equal(fr[i][k], sr[i][k], err_msg=f"sequence {i} {name}")
-                np.testing.assert_array_equal(cr[i][k], sr[i][k], err_msg=f"sequence {i} {name} (separate combine)")
+        for comb, proj in ((1, 1), (1, 0), (0, 1), (0, 0)):
+            fo, fr = run(1, lens, cfg, w, x, steps, comb=comb, proj=proj)
+            form = f"fused, combine {comb}, projection {proj}"
+            for t in range(steps):
+                assert np.isfinite(fo[t]).all()
+                np.testing.assert_array_equal(fo[t], so[t], err_msg=f"step {t} outputs ({form})")
+            for i in range(len(lens)):
+                for k, name in enumerate(("codes", "scales", "rope")):
+                    np.testing.assert_array_equal(fr[i][k], sr[i][k], err_msg=f"sequence {i} {name} ({form})")
     finally:
         L.kvl_mla_release_weights(C.byref(w))
 
@@ -100,3 +106,7 @@ def test_fused_switch_rejects_bad_values():
     assert prev in (0, 1)
     assert L.kvl_mla_set_fused_combine(-1) == -1
     assert L.kvl_mla_set_fused_combine(prev) == 1
+    prev = L.kvl_mla_set_fused_projection(1)
+    assert prev in (0, 1)
+    assert L.kvl_mla_set_fused_projection(3) == -1
+    assert L.kvl_mla_set_fused_projection(prev) == 1
