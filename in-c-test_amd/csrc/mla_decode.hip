@@ -1306,7 +1306,7 @@ struct AttnHot {
     const int8_t *qhi, *qlo;
     const float *qs;
     const uint16_t *qrhi, *qrlo;
-    int members, nseq;
+    int members, nseq;  // members: > 0 a block launch (seq_of); a fused Q8 launch: -(its split count)
 };
 #define KVL_ATTN_HOT_PARAMS                                                                        \
     int members_, int nseq_, const int8_t *qhi_, const int8_t *qlo_, const uint16_t *qrhi_,         \
@@ -2360,7 +2360,11 @@ __device__ __forceinline__ void put_q8_weights(int8_t *wqc, const float *pv, flo
 // same LDS flags after A, so all eight take the same barriers. Everything the score waves read
 // per chunk (codes, RoPE keys, scales) arrives in LDS by the mix waves' DMA, so their steps
 // never wait on global-memory latency.
-template <bool FUSE>  // FUSE: the launch also prepares the queries and appends the rows (fq_produce)
+// Combine modes of the Q8 launch (FqArgs::comb): none; XCD-local (every split of a sequence on
+// one XCD, partials read from its L2); across XCDs (partials stored with device-scope stores,
+// read from memory).
+enum { kCombNone = 0, kCombXcd = 1, kCombCross = 2 };
+template <bool FUSE, int COMB>  // FUSE: the launch also prepares the queries and appends the rows (fq_produce)
 __device__ __forceinline__ void q8_score_role(const AttnArgs &a, const AttnHot &h, const SeqDesc &sd, uint8_t *smem, int w, int b,
                                               int r0, int r1, int nch, int sid, int cpos) {
     int8_t *wq = (int8_t *)(smem + kQ8WqOff);
@@ -2552,13 +2556,19 @@ __device__ __forceinline__ void q8_score_role(const AttnArgs &a, const AttnHot &
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int hh = 4 * g + i;
-            P[8192 + hh] = m_run[i];
-            P[8192 + 16 + hh] = (lsum[hh] + lsum[16 + hh]) + (lsum[32 + hh] + lsum[48 + hh]);
+            const float lv = (lsum[hh] + lsum[16 + hh]) + (lsum[32 + hh] + lsum[48 + hh]);
+            if constexpr (COMB == kCombCross) {  // read on other XCDs in this launch
+                st_sc1_b32(&P[8192 + hh], __float_as_uint(m_run[i]));
+                st_sc1_b32(&P[8192 + 16 + hh], __float_as_uint(lv));
+            } else {
+                P[8192 + hh] = m_run[i];
+                P[8192 + 16 + hh] = lv;
+            }
         }
     }
 }
 
-template <bool ONCE, bool FUSE, bool COMB>
+template <bool ONCE, bool FUSE, int COMB>
 __device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const AttnHot &h, const SeqDesc &sd, uint8_t *smem, int mw, int b,
                                             int r0, int r1, int nch, int sid, int cpos) {
     const int8_t *wq = (const int8_t *)(smem + kQ8WqOff);
@@ -2756,8 +2766,10 @@ __device__ __forceinline__ void q8_mix_role(const AttnArgs &a, const AttnHot &h,
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float v = wfac * fmaf((float)ahi[t][i], 64516.0f, fmaf((float)alo[t][i], 254.0f, (float)alo2[t][i]));
-            // COMB: read by this XCD's workgroups in this launch (q8_comb_tail), from its L2
-            if constexpr (COMB) P[(4 * ge + i) * 512 + r] = v;
+            // read in this launch (q8_comb_tail): by this XCD's workgroups from its L2, or by any
+            // XCD's past the L2s
+            if constexpr (COMB == kCombXcd) P[(4 * ge + i) * 512 + r] = v;
+            else if constexpr (COMB == kCombCross) st_sc1_b32(&P[(4 * ge + i) * 512 + r], __float_as_uint(v));
             else __builtin_nontemporal_store(v, &P[(4 * ge + i) * 512 + r]);
         }
     }
@@ -2935,6 +2947,7 @@ __device__ __forceinline__ void comb_wuv(const uint16_t *kv_b, int h, int half, 
     }
 }
 
+template <int COMB>
 __device__ __forceinline__ void q8_comb_tail(const AttnArgs &a, const SeqDesc &s, int b, int split, uint8_t *smem) {
     constexpr int kTasks = 32;  // (head, half) pairs of 16 heads
     const int ns = s.nsplit, tid = threadIdx.x;
@@ -2953,7 +2966,8 @@ __device__ __forceinline__ void q8_comb_tail(const AttnArgs &a, const SeqDesc &s
                 if (__builtin_amdgcn_s_memrealtime() - t0 > kFqSpinTicks) break;
                 __builtin_amdgcn_s_sleep(1);
             }
-            if (v != mine * (unsigned long long)ns)  // a timeout, or splits on another XCC
+            // a timeout, or (XCD-local mode) splits on another XCC
+            if (COMB == kCombXcd ? v != mine * (unsigned long long)ns : cnt_total(v) < (unsigned)ns)
                 __hip_atomic_store(a.fq.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
@@ -2972,28 +2986,42 @@ __device__ __forceinline__ void q8_comb_tail(const AttnArgs &a, const SeqDesc &s
 
 // ONCE: each history row is read by one workgroup (non-temporal loads). FUSE: the launch
 // prepares the queries and appends the rows itself (fq_produce; no block launches).
-template <bool ONCE, bool FUSE = false, bool COMB = false>
+template <bool ONCE, bool FUSE = false, int COMB = kCombNone>
 __global__ __launch_bounds__(512) void k_attn_q8_mfma(KVL_ATTN_HOT_PARAMS, AttnArgs a) {
-    static_assert(!COMB || FUSE, "the combine tail is a form of the fused launch");
+    static_assert(COMB == kCombNone || FUSE, "the combine tail is a form of the fused launch");
     KVL_ATTN_HOT_INIT;
     __shared__ __attribute__((aligned(16))) uint8_t smem[kQ8SmemB];
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // a fused launch with the projection may have more workgroups than splits (at least
+    // kGemvTasks): the ones past the splits only take their projection block. The split count
+    // comes in the members argument (-splits; a fused launch is never a block launch), which is
+    // preloaded: the argument block's copy would cost every workgroup a memory round trip first.
+    if (FUSE && (int)blockIdx.x >= -h.members) {
+        fq_gemv(a.fq, h.nseq, smem);
+        return;
+    }
     int b, split, pidx;
     SeqDesc s;
-    if (!seq_of<COMB>(a, h, b, split, pidx, s)) return;
+    if (!seq_of<COMB == kCombXcd>(a, h, b, split, pidx, s)) return;
     const int r0 = split * s.rps;
     const int r1 = split == s.nsplit - 1 ? s.len : r0 + s.rps;  // last split takes the rest
     const int nch = (r1 - r0 + kQ8Ch - 1) / kQ8Ch;
     // chunk of this split holding the row appended in this launch, or -1
     const int cpos = FUSE && split == s.nsplit - 1 ? (s.pos - r0) / kQ8Ch : -1;
     if (w >= 4) q8_mix_role<ONCE, FUSE, COMB>(a, h, s, smem, w - 4, b, r0, r1, nch, pidx, cpos);
-    else q8_score_role<FUSE>(a, h, s, smem, w, b, r0, r1, nch, pidx, cpos);
-    if constexpr (COMB) q8_comb_tail(a, s, b, split, smem);
+    else q8_score_role<FUSE, COMB>(a, h, s, smem, w, b, r0, r1, nch, pidx, cpos);
+    if constexpr (COMB != kCombNone) q8_comb_tail<COMB>(a, s, b, split, smem);
 }
 
-bool gemv_fuse_ok(const Dims &d, int B, int total_splits) {
-    return B >= 1 && B <= 8 && d.H == 2048 && d.NH == 16 && d.QD == 192 && d.QO == 16 * 192 && d.KVO == 576 &&
-           total_splits >= kGemvTasks;
+bool gemv_fuse_ok(const Dims &d, int B) {
+    return B >= 1 && B <= 8 && d.H == 2048 && d.NH == 16 && d.QD == 192 && d.QO == 16 * 192 && d.KVO == 576;
+}
+
+bool comb_cross_ok(const SeqTable &t, const Dims &d) {
+    if (t.n < 1 || d.NH != 16 || d.R != 512 || d.DN != 128 || d.DV != 128 || d.HO != 16 * 128) return false;
+    for (int i = 0; i < t.n; ++i)
+        if (t.s[i].nsplit < 16 || t.s[i].nsplit > 255) return false;  // at most two tasks per split
+    return true;
 }
 
 bool comb_ok(const SeqTable &t, const Dims &d, int total_splits) {
@@ -3015,8 +3043,10 @@ hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t
     if (fq && (kind != kAttnQ8Mfma || members > 0 || fmt != kFmtQ8 || d.NH != 16 || d.R != 512 || d.DR != 64 ||
                d.DN != 128 || d.QD != 192 || 17 * t.n > total_splits || !fq->y || !fq->ukt || !fq->cs || !fq->norm ||
                !fq->rows || !fq->flags || !fq->err ||
-               (fq->comb && (!comb_ok(t, d, total_splits) || !fq->kvb || !fq->ho || !fq->hos)) ||
-               (fq->gemv && (!gemv_fuse_ok(d, t.n, total_splits) || !fq->x || !fq->wq || !fq->wkva ||
+               (fq->comb == kCombXcd && !comb_ok(t, d, total_splits)) ||
+               (fq->comb == kCombCross && !comb_cross_ok(t, d)) || fq->comb < 0 || fq->comb > kCombCross ||
+               (fq->comb && (!fq->kvb || !fq->ho || !fq->hos)) || fq->splits != total_splits ||
+               (fq->gemv && (!gemv_fuse_ok(d, t.n) || !fq->x || !fq->wq || !fq->wkva ||
                              fq->in != d.H || fq->out0 != d.QO || fq->out1 != d.KVO || (uintptr_t)fq->x % 16 != 0 ||
                              fq->ldx % 4 != 0))))
         return hipErrorInvalidValue;
@@ -3036,6 +3066,7 @@ hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t
     a.members = kind == kAttnGeneric ? 0 : members;
     a.nseq = t.n;
     int grid = total_splits;
+    if (fq && fq->gemv) grid = max(grid, kGemvTasks);  // the projection's blocks
     if (a.members > 0) {
         int maxns = 0;
         for (int i = 0; i < t.n; ++i) maxns = max(maxns, t.s[i].nsplit);
@@ -3043,8 +3074,9 @@ hipError_t launch_attention(hipStream_t st, int kind, int fmt, const SeqTable &t
     }
     if (kind == kAttnQ8Mfma) {
         if (a.members > 0) hipLaunchKernelGGL(k_attn_q8_mfma<false>, dim3(grid), dim3(512), 0, st, a.members, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);
-        else if (fq && fq->comb) hipLaunchKernelGGL((k_attn_q8_mfma<true, true, true>), dim3(grid), dim3(512), 0, st, a.members, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);
-        else if (fq) hipLaunchKernelGGL((k_attn_q8_mfma<true, true>), dim3(grid), dim3(512), 0, st, a.members, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);
+        else if (fq && fq->comb == kCombXcd) hipLaunchKernelGGL((k_attn_q8_mfma<true, true, kCombXcd>), dim3(grid), dim3(512), 0, st, -total_splits, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);
+        else if (fq && fq->comb == kCombCross) hipLaunchKernelGGL((k_attn_q8_mfma<true, true, kCombCross>), dim3(grid), dim3(512), 0, st, -total_splits, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);
+        else if (fq) hipLaunchKernelGGL((k_attn_q8_mfma<true, true>), dim3(grid), dim3(512), 0, st, -total_splits, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);
         else hipLaunchKernelGGL(k_attn_q8_mfma<true>, dim3(grid), dim3(512), 0, st, a.members, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);
     } else if (kind == kAttnF32Mfma) {
         if (a.members > 0) hipLaunchKernelGGL(k_attn_f32_mfma<false>, dim3(grid), dim3(256), 0, st, a.members, a.nseq, a.qhi, a.qlo, a.qrhi, a.qrlo, a.qs, a.qf, a.part, a);

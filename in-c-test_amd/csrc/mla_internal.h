@@ -171,22 +171,26 @@ struct FqArgs {
     int ldy, koff, row_bytes;
     float eps;
     // comb != 0: the launch also combines the split partials into ho / hos (launch_combine's
-    // outputs, W_UV from kvb), with every split of a sequence on one XCD; needs t.n a multiple
-    // of 8 and every sequence with the same split count ns, sequence b's splits from b * ns
-    // (comb_ok), and flags words kFqFlagStride * (2 kMaxBatch + b), b < B, zeroed as the others.
+    // outputs, W_UV from kvb), split s of a sequence taking (head s / 2, half s % 2) and s + ns,
+    // ... (flags words kFqFlagStride * (2 kMaxBatch + b), b < B, zeroed as the others).
+    // comb = 1: every split of a sequence on one XCD, its partials read from that XCD's L2; needs
+    // t.n a multiple of 8 and every sequence with the same split count ns, sequence b's splits
+    // from b * ns (comb_ok). comb = 2: the partials stored past the L2s and read from memory;
+    // needs 16 .. 255 splits per sequence (comb_cross_ok).
     int comb;
     const uint16_t *kvb;
     float *ho;
     uint16_t *hos;
     // gemv != 0: the launch also computes the q_proj | kv_a partials into y (k_gemv_ksplit's
     // blocks as tasks of its first kGemvTasks workgroups, the same arithmetic), from x [B, in]
-    // (16-byte aligned rows, ldx) and the weights wq [out0, in], wkva [out1, in]; needs B <= 8,
-    // in = 2048 and at least kGemvTasks workgroups (gemv_fuse_ok). Flags words
+    // (16-byte aligned rows, ldx) and the weights wq [out0, in], wkva [out1, in]; needs B <= 8
+    // and in = 2048 (gemv_fuse_ok), and runs max(splits, kGemvTasks) workgroups. Flags words
     // kFqFlagStride * (3 kMaxBatch + i), i < kFqGemvFlags: per-head and kv_a task counts.
     int gemv;
     const float *x;
     const uint16_t *wq, *wkva;
     int ldx, in, out0, out1;
+    int splits;  // the launch's split count (with gemv the grid is max(splits, kGemvTasks))
 };
 // Lines of the flags buffer: query, row, combine (kMaxBatch each), then the projection counts
 // (16 heads, kv_a). The o_proj launch after a fused launch clears them all (launch_gemv_xs's zf),
@@ -199,7 +203,9 @@ constexpr int kGemvTasks = 232;
 // True when a fused launch with this table and split count can combine in place (FqArgs::comb).
 bool comb_ok(const SeqTable &t, const Dims &d, int total_splits);
 // True when a fused launch can also compute the q_proj | kv_a projection (FqArgs::gemv).
-bool gemv_fuse_ok(const Dims &d, int B, int total_splits);
+bool gemv_fuse_ok(const Dims &d, int B);
+// True when a fused launch can combine across XCDs (FqArgs::comb = 2).
+bool comb_cross_ok(const SeqTable &t, const Dims &d);
 // fq: null, or the fused form (kind == kAttnQ8Mfma, members == 0, Kimi shapes, at most one
 // round of workgroups, 17 B <= total_splits): blocks [0, 16 B) prepare one (sequence, head)
 // query each, blocks [16 B, 17 B) append one row each, before their own split.

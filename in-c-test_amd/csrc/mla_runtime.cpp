@@ -1000,18 +1000,25 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
     // entry point keeps the two-launch form. Measured (headline stack, 8 x 32K Q8 rows, 27
     // layers): 1.522 -> 1.483 ms per step; a lone 8K-row decode 29.5 -> 30.5 us (the 17 producer
     // tasks hold up its 64 short splits), hence B >= 2.
-    const bool fuse = c.fq_on && B >= 2 && fmt == kFmtQ8 && kind == kAttnQ8Mfma && !solo && part_cap == 0 && kimi_attn(d) &&
-                      d.DN == 128 && d.QD == 192 && gemv_ksplit_ok(d.H, d.H) && ukt_shape(d) && dw.ukt &&
-                      17 * B <= total_splits && total_splits <= c.ncu && c.fq_flags && c.fq_err;
-    // ... and the combine inside that launch (q8_comb_tail): eight sequences (or a multiple) with
-    // equal split counts, each sequence's splits on one XCD. Measured (headline stack): see the
-    // design notes on the fused combine.
-    const bool comb = fuse && c.comb_on && comb_ok(t, d, total_splits) && combine_writes_hos(fmt, d) &&
-                      gemv_xs_ok(d.HO);
+    const bool fuse_base = c.fq_on && fmt == kFmtQ8 && kind == kAttnQ8Mfma && !solo && part_cap == 0 &&
+                           kimi_attn(d) && d.DN == 128 && d.QD == 192 && gemv_ksplit_ok(d.H, d.H) && ukt_shape(d) &&
+                           dw.ukt && 17 * B <= total_splits && total_splits <= c.ncu && c.fq_flags && c.fq_err;
     // ... and the q_proj | kv_a projection inside it too (fq_gemv): at most eight sequences, x
-    // 16-byte aligned, a launch of at least kGemvTasks workgroups.
-    const bool pfuse = fuse && c.gemv_on && gemv_fuse_ok(d, B, total_splits) && gemv_ksplit_ok(d.H, d.H) &&
-                       ((uintptr_t)d_x % 16) == 0;
+    // 16-byte aligned, a launch of max(splits, kGemvTasks) <= CU count workgroups.
+    const bool pfuse_ok = fuse_base && c.gemv_on && gemv_fuse_ok(d, B) && gemv_ksplit_ok(d.H, d.H) &&
+                          ((uintptr_t)d_x % 16) == 0 && std::max(total_splits, kGemvTasks) <= c.ncu;
+    // ... and the combine inside it (q8_comb_tail): eight sequences (or a multiple) with equal
+    // split counts, each sequence's splits on one XCD (kCombXcd); or sequences of 16 or more
+    // splits each, their partials exchanged past the L2s (kCombCross). Measured (headline
+    // stack, lone decodes): see the design notes on the fused combine.
+    const bool comb_shape = c.comb_on && combine_writes_hos(fmt, d) && gemv_xs_ok(d.HO);
+    const int comb_mode = !comb_shape ? 0 : comb_ok(t, d, total_splits) ? 1 : comb_cross_ok(t, d) ? 2 : 0;
+    // A lone sequence takes the fused form only with the projection and the combine inside it
+    // (with the query preparation alone its 17 producer tasks held up its 64 short splits: a
+    // lone 8K-row decode 29.5 -> 30.5 us).
+    const bool fuse = fuse_base && (B >= 2 || (pfuse_ok && comb_mode != 0));
+    const bool pfuse = fuse && pfuse_ok;
+    const int comb = fuse ? comb_mode : 0;
     {
         // q_proj | kv_a: k split over kGemvKs blocks where the shape allows (the consumers
         // add the partials), else one pass
@@ -1072,8 +1079,9 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
             fq.koff = d.QO;
             fq.row_bytes = d.R + 4 + 2 * d.DR;
             fq.eps = eps;
+            fq.splits = total_splits;
             if (comb) {
-                fq.comb = 1;
+                fq.comb = comb;
                 fq.kvb = dw.kvb;
                 fq.ho = w.ho;
                 fq.hos = w.hos;

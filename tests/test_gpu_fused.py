@@ -14,7 +14,11 @@ XCD): that form must equal the others bit for bit as well, with fewer splits tha
 most eight sequences the launch also computes the q_proj | kv_a projection
 (kvl_mla_set_fused_projection): eight sequences of 8000 rows (256 splits: projection and
 combine) and three sequences of 63, 30000 and 30000 rows (237 splits: projection only) cover it;
-every combination of the switches must give the same bits."""
+every combination of the switches must give the same bits. Sequences of 16 or more splits each
+combine across XCDs (their partials stored past the L2s): a lone sequence of 9000 rows (64
+splits; the fused form of a lone sequence needs the projection and the combine inside the
+launch, so with either switch off it takes the two-launch form) and two of 20000 and 30000
+rows (79 + 118 splits)."""
 import ctypes as C
 
 import numpy as np
@@ -29,7 +33,8 @@ L = lib.load()
 KIMI = dict(inputs.KIMI)
 
 # history rows per sequence; each case needs 17 x batch <= the launch's split count
-CASES = [(6000,) * 8, (100, 9000), (9000, 200, 130, 9000), (63, 9000, 9000), (8000,) * 8, (63, 30000, 30000)]
+CASES = [(6000,) * 8, (100, 9000), (9000, 200, 130, 9000), (63, 9000, 9000), (8000,) * 8, (63, 30000, 30000),
+         (9000,), (20000, 30000)]
 
 
 def run(form, lens, cfg, w, x, steps, comb=1, proj=1):
