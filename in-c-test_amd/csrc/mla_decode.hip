@@ -2784,11 +2784,16 @@ constexpr int kCombPre = 8;  // split-partial loads a combine thread issues befo
 // With every split of a sequence on one XCD (seq_of<true>), its split partials are in that XCD's
 // L2 when the last split ends: each workgroup stores its partial with plain stores, waits until
 // the L2 has acknowledged them (vmcnt) and counts itself on the sequence's counter; workgroup
-// `split` < 32 then waits for the count to reach ns, invalidates its L1 and combines (head
-// split / 2, half split % 2) -- and further tasks split + ns, ... when ns < 32 -- with the
-// arithmetic of k_combine_r512, whose launch this replaces. The counter (64 bits, one 128-byte
-// line per sequence, after the query and row flags, cleared by the q_proj | kv_a launch of the
-// step) has one byte per XCC: a workgroup adds 1 << 8 * (its XCC id), so the waiters also see
+// `split` < 32 then waits for the count to reach ns and combines (head split / 2, half split %
+// 2) -- and further tasks split + ns, ... when ns < 32 -- with the arithmetic of k_combine_r512,
+// whose launch this replaces. Its first read of a partial line comes after the wait (the CU has
+// not read those lines in this launch, so its L1 holds no copy, and the launch began with the
+// caches invalidated): the read is served by the L2. (Polling a line that the CU keeps reading
+// does not work that way: the L1 keeps serving its first copy even with the sc0 bit on the load
+// or a buffer_inv sc0 before it, measured with per-split done words in one line, whose wait
+// never ended.) The counter (64 bits, one 128-byte line per sequence, after the query and row
+// flags, cleared before each fused launch) is updated and polled with atomics, which are not
+// served by the L1, and has one byte per XCC: a workgroup adds 1 << 8 * (its XCC id), so the waiters also see
 // that all the sequence's splits ran on one XCC, which the placement assumes (workgroup i on XCD
 // i % 8 + a per-launch offset); otherwise the partials would not all be in the reader's L2, and
 // the launch raises FqArgs::err (results invalid) instead of reading them. The waits are bounded
@@ -2973,7 +2978,7 @@ __device__ __forceinline__ void q8_comb_tail(const AttnArgs &a, const SeqDesc &s
     }
     if (split >= kTasks) return;
     __syncthreads();
-    asm volatile("buffer_inv sc0" ::: "memory");  // no L1 line of the partials from before the wait
+    asm volatile("buffer_inv sc0" ::: "memory");  // workgroup-scope invalidate (the reads are first reads)
     const float *P = a.part + (size_t)s.split0 * 16 * 514;
     for (int t = split;;) {
         comb_task(P, a.fq.ho, a.fq.hos, a.nseq, a.d.HO, b, t >> 1, t & 1, ns, wv, smem);
