@@ -278,21 +278,24 @@ def main():
             L.kvl_mla_graph_destroy(tg)
         else:
             L.kvl_mla_timing_read(ms, cnt)
-    # The attention launch of this workload also prepares the queries and appends the rows
+    # The attention launch of this workload also computes the q_proj | kv_a projection
+    # (kvl_mla_set_fused_projection), prepares the queries and appends the rows
     # (kvl_mla_set_fused_qprep) and combines the split partials (kvl_mla_set_fused_combine): its
-    # algorithmic bytes are the history rows plus W_UK^T and W_UV, the q_proj | kv_a partials it
-    # reads, the query operands and rows it writes and the head outputs (fp32 and bf16 hi | lo).
-    # The split partials stay in the L2 of the XCD that combines them and are not counted.
+    # algorithmic bytes are the history rows plus the projection weights, W_UK^T and W_UV, the
+    # layer input x, the q_proj | kv_a partials it writes and reads back, the query operands and
+    # rows it writes and the head outputs (fp32 and bf16 hi | lo). The split partials stay in the
+    # L2 of the XCD that combines them and are not counted.
     H_, NH_, R_, DN_, DR_ = cfg.hidden_size, cfg.num_heads, cfg.kv_lora_rank, cfg.qk_nope_dim, cfg.qk_rope_dim
     QO_, KVO_, DV_ = NH_ * (DN_ + DR_), R_ + DR_, cfg.v_head_dim
-    fused_extra = (2 * NH_ * R_ * DN_ + 2 * NH_ * R_ * DV_ + 4 * 4 * B * (QO_ + KVO_)
-                   + B * NH_ * (2 * R_ + 4 + 4 * DR_) + B * Q8_ROW + B * NH_ * DV_ * (4 + 2 + 2))
+    fused_extra = (2 * (QO_ + KVO_) * H_ + 4 * B * H_ + 2 * NH_ * R_ * DN_ + 2 * NH_ * R_ * DV_
+                   + 2 * 4 * 4 * B * (QO_ + KVO_) + B * NH_ * (2 * R_ + 4 + 4 * DR_) + B * Q8_ROW
+                   + B * NH_ * DV_ * (4 + 2 + 2))
     attn_bytes = hist_bytes + fused_extra
     attn_gbs = attn_bytes / (attn_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_bytes(B, CTX),
-                "kernel": "k_attn_q8_mfma<true, true, true> (attention with the query preparation, the "
-                          "row append and the combine of its sequences)",
+                "kernel": "k_attn_q8_mfma<true, true, kCombXcd> (the q_proj | kv_a projection, the query "
+                          "preparation, the row append, the attention and the combine of its sequences)",
                 "algorithmic_bytes_per_launch": attn_bytes, "history_bytes_per_launch": hist_bytes,
                 "avg_launch_ms": round(attn_ms, 5), "timing": attn_src}
     if attn_only_ms is not None:
