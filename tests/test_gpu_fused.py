@@ -17,8 +17,9 @@ combine) and three sequences of 63, 30000 and 30000 rows (237 splits: projection
 every combination of the switches must give the same bits. Sequences of 16 or more splits each
 combine across XCDs (their partials stored past the L2s): a lone sequence of 9000 rows (64
 splits; the fused form of a lone sequence needs the projection and the combine inside the
-launch, so with either switch off it takes the two-launch form) and two of 20000 and 30000
-rows (79 + 118 splits)."""
+launch, so with either switch off it takes the two-launch form), a lone sequence of 2100 rows
+(17 splits, the fewest the fused form takes: 15 of its workgroups combine two (head, half)
+pairs) and two of 20000 and 30000 rows (79 + 118 splits)."""
 import ctypes as C
 
 import numpy as np
@@ -34,7 +35,7 @@ KIMI = dict(inputs.KIMI)
 
 # history rows per sequence; each case needs 17 x batch <= the launch's split count
 CASES = [(6000,) * 8, (100, 9000), (9000, 200, 130, 9000), (63, 9000, 9000), (8000,) * 8, (63, 30000, 30000),
-         (9000,), (20000, 30000)]
+         (9000,), (20000, 30000), (2100,)]
 
 
 def run(form, lens, cfg, w, x, steps, comb=1, proj=1):
