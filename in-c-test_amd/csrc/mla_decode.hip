@@ -2014,7 +2014,8 @@ __device__ __forceinline__ double block512_sum_f64(double v, double *red8) {
     return ((red8[0] + red8[1]) + (red8[2] + red8[3])) + ((red8[4] + red8[5]) + (red8[6] + red8[7]));
 }
 
-// Projection counts and the exit count (kFqFlagLines): line 3 kMaxBatch + i.
+// Projection counts (kFqFlagLines): line 3 kMaxBatch + i, i < 16 the q rows of head i, i = 16
+// the kv_a rows.
 __device__ __forceinline__ unsigned *fq_gflag(const FqArgs &f, int i) {
     return f.flags + (size_t)kFqFlagStride * (3 * kMaxBatch + i);
 }

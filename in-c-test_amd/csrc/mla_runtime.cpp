@@ -167,9 +167,10 @@ struct Ctx {
     DevBuf rflag;  // int: raised by a stream-ordered prefill outside the MFMA route's range
     PinBuf pin_in, pin_out;
     // fused Q8 decode (the attention launch prepares the queries and appends the rows, and where
-    // comb_ok also combines): its readiness flags and combine counters (device, 3 x kMaxBatch
-    // lines, cleared by the q_proj | kv_a GEMV of each call) and a host-visible word raised if
-    // one of its waits timed out
+    // the shapes allow also computes the q_proj | kv_a projection and combines the splits): its
+    // readiness flags and counters (device, kFqFlagLines lines; cleared by the o_proj launch
+    // after each fused launch, or by the separate q_proj | kv_a launch before it) and a
+    // host-visible word raised if one of its waits timed out
     unsigned *fq_flags = nullptr;
     int *fq_err = nullptr;
     bool fq_on = true;    // KVL_MLA_NO_FUSED_QPREP=1 turns the fused form off (the two-launch form)
@@ -996,10 +997,9 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
     const int ldy = d.QO + d.KVO;
     // The fused form (see FqArgs): Q8 MFMA attention of independent sequences (no block members)
     // at the Kimi shapes, one round of workgroups with room for the 17 B producer tasks, the
-    // k-split projection, W_UK^T in fragment order, two or more sequences; the no-allocation
-    // entry point keeps the two-launch form. Measured (headline stack, 8 x 32K Q8 rows, 27
-    // layers): 1.522 -> 1.483 ms per step; a lone 8K-row decode 29.5 -> 30.5 us (the 17 producer
-    // tasks hold up its 64 short splits), hence B >= 2.
+    // k-split projection, W_UK^T in fragment order; the no-allocation entry point keeps the
+    // two-launch form. Measured with the query preparation alone inside (headline stack, 8 x 32K
+    // Q8 rows, 27 layers): 1.522 -> 1.483 ms per step.
     const bool fuse_base = c.fq_on && fmt == kFmtQ8 && kind == kAttnQ8Mfma && !solo && part_cap == 0 &&
                            kimi_attn(d) && d.DN == 128 && d.QD == 192 && gemv_ksplit_ok(d.H, d.H) && ukt_shape(d) &&
                            dw.ukt && 17 * B <= total_splits && total_splits <= c.ncu && c.fq_flags && c.fq_err;
