@@ -1229,6 +1229,7 @@ int decode_host(float *out, const float *x, const int *positions, int B, const K
         HIP_TRY(hipStreamSynchronize(c.stream));
         if (*c.fq_err) {
             *c.fq_err = 0;
+            c.fq_dirty = true;  // a timed-out wait may have left its counters behind
             set_err("a wait of the fused query preparation timed out (results invalid); "
                     "KVL_MLA_NO_FUSED_QPREP=1 selects the two-launch form");
             return -1;
@@ -2340,7 +2341,15 @@ void *kvl_mla_stream(void) {
 int kvl_mla_synchronize(void) {
     Guard guard;
     if (ensure_ready() != 0) return -1;
-    HIP_TRY(hipStreamSynchronize(ctx().stream));
+    Ctx &c = ctx();
+    HIP_TRY(hipStreamSynchronize(c.stream));
+    if (*c.fq_err) {  // a stream-ordered fused decode since the last check had a wait time out
+        *c.fq_err = 0;
+        c.fq_dirty = true;
+        set_err("a wait of a fused decode launch timed out (its results are invalid); "
+                "KVL_MLA_NO_FUSED_QPREP=1 selects the two-launch form");
+        return -1;
+    }
     return 0;
 }
 

@@ -227,7 +227,10 @@ int kvl_mla_prefill_compressed_bf16_state_device(float *d_out, const float *d_x,
                                                  const KvlMlaConfig *cfg, const KvlMlaBF16 *w,
                                                  KvlMlaCompressedBF16State *state);
 
-/* The library's HIP stream (hipStream_t) and helpers for callers without a HIP binding. */
+/* The library's HIP stream (hipStream_t) and helpers for callers without a HIP binding.
+ * kvl_mla_synchronize waits for the stream; it returns -1 when a stream-ordered fused decode
+ * enqueued since the last check had one of its bounded device waits time out (its outputs are
+ * invalid; kvl_mla_last_error says so). */
 void *kvl_mla_stream(void);
 int kvl_mla_synchronize(void);
 void *kvl_mla_device_alloc(size_t bytes);
