@@ -1962,7 +1962,6 @@ static_assert(kQ8SmemB <= 160 * 1024, "LDS of one CU");
 // for its append before that row's chunk is requested. Workgroups are dispatched in index order,
 // so the producers have started whenever anything waits on them; the waits are bounded anyway
 // (a timeout raises FqArgs::err and the launch ends with wrong values instead of hanging).
-constexpr uint64_t kFqSpinTicks = 2000000;  // 20 ms of the 100 MHz real-time counter
 
 __device__ __forceinline__ void st_sc1_b32(void *p, uint32_t v) {
     asm volatile("global_store_dword %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
@@ -1988,7 +1987,7 @@ __device__ __forceinline__ void fq_wait(const FqArgs &f, const unsigned *flag, u
     if ((threadIdx.x & 63) == 0) {
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-            if (__builtin_amdgcn_s_memrealtime() - t0 > kFqSpinTicks) {
+            if (__builtin_amdgcn_s_memrealtime() - t0 > (uint64_t)f.spin) {
                 __hip_atomic_store(f.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
                 break;
             }
@@ -2025,7 +2024,7 @@ __device__ __forceinline__ void fq_wait_all(const FqArgs &f, const unsigned *fla
     if (threadIdx.x == 0) {
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-            if (__builtin_amdgcn_s_memrealtime() - t0 > kFqSpinTicks) {
+            if (__builtin_amdgcn_s_memrealtime() - t0 > (uint64_t)f.spin) {
                 __hip_atomic_store(f.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
                 break;
             }
@@ -2969,7 +2968,7 @@ __device__ __forceinline__ void q8_comb_tail(const AttnArgs &a, const SeqDesc &s
             const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
             unsigned long long v;
             while (cnt_total(v = cnt_poll(cf)) < (unsigned)ns) {
-                if (__builtin_amdgcn_s_memrealtime() - t0 > kFqSpinTicks) break;
+                if (__builtin_amdgcn_s_memrealtime() - t0 > (uint64_t)a.fq.spin) break;
                 __builtin_amdgcn_s_sleep(1);
             }
             // a timeout, or (XCD-local mode) splits on another XCC

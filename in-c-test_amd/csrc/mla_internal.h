@@ -191,7 +191,9 @@ struct FqArgs {
     const uint16_t *wq, *wkva;
     int ldx, in, out0, out1;
     int splits;  // the launch's split count (with gemv the grid is max(splits, kGemvTasks))
+    unsigned spin;  // bound of every wait, in ticks of the 100 MHz real-time counter
 };
+constexpr unsigned kFqSpinTicks = 2000000;  // FqArgs::spin by default: 20 ms
 // Lines of the flags buffer: query, row, combine (kMaxBatch each), then the projection counts
 // (16 heads, kv_a). The o_proj launch after a fused launch clears them all (launch_gemv_xs's zf),
 // and so does the q_proj | kv_a launch before one (launch_gemv_ksplit's zero_flags).

@@ -176,6 +176,7 @@ struct Ctx {
     bool fq_on = true;    // KVL_MLA_NO_FUSED_QPREP=1 turns the fused form off (the two-launch form)
     bool comb_on = true;  // KVL_MLA_NO_FUSED_COMBINE=1: the fused form keeps the combine launch
     bool gemv_on = true;  // KVL_MLA_NO_FUSED_PROJECTION=1: the fused form keeps the projection launch
+    unsigned fq_spin = kFqSpinTicks;  // bound of the fused form's device waits (kvl_mla_set_fused_wait_limit)
     // a fused attention launch was enqueued and the o_proj launch that clears its flags was not
     // (an error in between): the next launch that relies on clean flags clears them first
     bool fq_dirty = false;
@@ -1080,6 +1081,7 @@ int decode_group(int fmt, const Dims &d, float eps, float theta, const DevWeight
             fq.row_bytes = d.R + 4 + 2 * d.DR;
             fq.eps = eps;
             fq.splits = total_splits;
+            fq.spin = c.fq_spin;
             if (comb) {
                 fq.comb = comb;
                 fq.kvb = dw.kvb;
@@ -2584,6 +2586,13 @@ int kvl_mla_set_fused_projection(int on) {
     const int prev = ctx().gemv_on ? 1 : 0;
     ctx().gemv_on = on == 1;
     return prev;
+}
+
+int kvl_mla_set_fused_wait_limit(unsigned ticks) {
+    Guard guard;
+    if (ensure_ready() != 0) return -1;
+    ctx().fq_spin = ticks == 0 ? kFqSpinTicks : ticks;
+    return 0;
 }
 
 int kvl_mla_timing_stages(unsigned mask) {

@@ -62,6 +62,7 @@ EXT_API = {
     "mla_set_fused_qprep": (C.c_int, [C.c_int]),
     "mla_set_fused_combine": (C.c_int, [C.c_int]),
     "mla_set_fused_projection": (C.c_int, [C.c_int]),
+    "mla_set_fused_wait_limit": (C.c_int, [C.c_uint]),
     "mla_timing_stages": (C.c_int, [C.c_uint]),
     "mla_timing_read": (C.c_int, [C.POINTER(C.c_double), C.POINTER(C.c_int)]),
     "mla_event_record": (C.c_void_p, []),

@@ -282,6 +282,13 @@ int kvl_mla_set_fused_combine(int on);
  * of its own. The results are the same bit for bit. Returns the previous setting, or -1.
  * KVL_MLA_NO_FUSED_PROJECTION=1 sets 0 at initialisation. */
 int kvl_mla_set_fused_projection(int on);
+/* Extension, no counterpart in the reference, for tests of the failure path: the bound of every
+ * device wait of the fused form above, in ticks of the GPU's 100 MHz real-time counter (0
+ * restores the default, 2,000,000 = 20 ms). A wait that reaches it ends, the launch runs to its
+ * end with invalid results, and the call reports it (a host-buffer call returns -1, a
+ * stream-ordered one through kvl_mla_synchronize); the next call clears the device flags and
+ * computes normally. Returns 0, or -1. */
+int kvl_mla_set_fused_wait_limit(unsigned ticks);
 int kvl_mla_timing_stages(unsigned mask);
 int kvl_mla_timing_read(double *ms, int *count);
 void *kvl_mla_event_record(void);

@@ -38,13 +38,20 @@ CASES = [(6000,) * 8, (100, 9000), (9000, 200, 130, 9000), (63, 9000, 9000), (80
          (9000,), (20000, 30000), (2100,)]
 
 
+def switches(form, comb, proj):
+    prev = (L.kvl_mla_set_fused_qprep(form), L.kvl_mla_set_fused_combine(comb), L.kvl_mla_set_fused_projection(proj))
+    assert all(p in (0, 1) for p in prev), prev
+    return prev
+
+
+def restore(prev):
+    L.kvl_mla_set_fused_qprep(prev[0])
+    L.kvl_mla_set_fused_combine(prev[1])
+    L.kvl_mla_set_fused_projection(prev[2])
+
+
 def run(form, lens, cfg, w, x, steps, comb=1, proj=1):
-    prev = L.kvl_mla_set_fused_qprep(form)
-    assert prev in (0, 1)
-    prev_comb = L.kvl_mla_set_fused_combine(comb)
-    assert prev_comb in (0, 1)
-    prev_proj = L.kvl_mla_set_fused_projection(proj)
-    assert prev_proj in (0, 1)
+    prev = switches(form, comb, proj)
     try:
         states = []
         for i, n in enumerate(lens):
@@ -74,9 +81,7 @@ def run(form, lens, cfg, w, x, steps, comb=1, proj=1):
             L.kvl_mla_compressed_q8_state_free(C.byref(st))
         return outs, rows
     finally:
-        L.kvl_mla_set_fused_qprep(prev)
-        L.kvl_mla_set_fused_combine(prev_comb)
-        L.kvl_mla_set_fused_projection(prev_proj)
+        restore(prev)
 
 
 @pytest.mark.parametrize("lens", CASES, ids=["-".join(map(str, c)) for c in CASES])
@@ -116,3 +121,79 @@ def test_fused_switch_rejects_bad_values():
     assert prev in (0, 1)
     assert L.kvl_mla_set_fused_projection(3) == -1
     assert L.kvl_mla_set_fused_projection(prev) == 1
+
+
+def test_fused_wait_timeout_is_reported_and_recovered():
+    """The failure path, forced from the host: with the fused launch's wait bound at one tick of
+    the 100 MHz counter its waits end before the work they wait for is done (every kernel still
+    runs to its end). The host-buffer call returns -1 with the timeout message and leaves the
+    states as they were; a stream-ordered call is reported by kvl_mla_synchronize. With the
+    default bound the next calls equal the two-launch form bit for bit (the flags left behind
+    are cleared)."""
+    print("[fused] forced wait timeouts, 8 x 8000 rows", flush=True)
+    lens = (8000,) * 8
+    cfg = inputs.config(**KIMI)
+    layer = inputs.make_layer(cfg, 0xF6)
+    w = layer.struct()
+    lib.check(L.kvl_mla_bind_weights(C.byref(cfg), C.byref(w)), "bind")
+    x = np.stack([inputs.hidden(cfg, 0xF7, len(lens))])
+    so, sr = run(0, lens, cfg, w, x, 1)
+    prev = switches(1, 1, 1)
+    states = []
+    d_x = d_o = None
+    try:
+        for i, n in enumerate(lens):
+            st = abi.KvlMlaCompressedQ8State()
+            lib.check(L.kvl_mla_compressed_q8_state_init(C.byref(st), C.byref(cfg), n + 1), "init")
+            lib.check(L.kvl_mla_compressed_q8_state_fill_synthetic(C.byref(st), 0, n, 0xF00 + i), "fill")
+            lib.check(L.kvl_mla_compressed_q8_state_pull(C.byref(st), 0, n), "pull")
+            states.append(st)
+        arr = (C.POINTER(abi.KvlMlaCompressedQ8State) * len(lens))(*[C.pointer(s) for s in states])
+        pos = np.ascontiguousarray(lens, dtype=np.int32)
+        xs = np.ascontiguousarray(x[0])
+        out = np.zeros((len(lens), cfg.hidden_size), np.float32)
+
+        def call():
+            return L.kvl_mla_decode_compressed_q8_batch_bf16(f32(out), f32(xs), pos.ctypes.data_as(C.POINTER(C.c_int)),
+                                                             len(lens), C.byref(cfg), C.byref(w), arr)
+
+        # host-buffer call
+        assert L.kvl_mla_set_fused_wait_limit(1) == 0
+        assert call() == -1
+        assert "timed out" in lib.last_error()
+        assert [s.len for s in states] == list(lens)
+        # stream-ordered call: enqueued, reported at the synchronisation
+        d_x = L.kvl_mla_device_alloc(xs.nbytes)
+        d_o = L.kvl_mla_device_alloc(out.nbytes)
+        assert d_x and d_o
+        lib.check(L.kvl_mla_copy_to_device(d_x, xs.ctypes.data, xs.nbytes), "h2d")
+        rc = L.kvl_mla_decode_compressed_q8_batch_device(d_o, d_x, len(lens), C.byref(cfg), C.byref(w), arr,
+                                                         lib.NO_ADVANCE)
+        assert rc == 0, lib.last_error()
+        assert L.kvl_mla_synchronize() == -1
+        assert "timed out" in lib.last_error()
+        # default bound: normal results again
+        assert L.kvl_mla_set_fused_wait_limit(0) == 0
+        rc = L.kvl_mla_decode_compressed_q8_batch_device(d_o, d_x, len(lens), C.byref(cfg), C.byref(w), arr,
+                                                         lib.NO_ADVANCE)
+        assert rc == 0, lib.last_error()
+        assert L.kvl_mla_synchronize() == 0, lib.last_error()
+        lib.check(call(), "host call after the timeouts")
+        np.testing.assert_array_equal(out, so[0], err_msg="outputs after the timeouts")
+        R, DR = cfg.kv_lora_rank, cfg.qk_rope_dim
+        for i, (st, n) in enumerate(zip(states, lens)):
+            m = n + 1
+            assert st.len == m
+            np.testing.assert_array_equal(np.ctypeslib.as_array(st.latent_q8, (m * R,)), sr[i][0])
+            np.testing.assert_array_equal(np.ctypeslib.as_array(st.latent_scale, (m,)), sr[i][1])
+            np.testing.assert_array_equal(np.ctypeslib.as_array(st.rope_bf16, (m * DR,)), sr[i][2])
+    finally:
+        L.kvl_mla_set_fused_wait_limit(0)
+        restore(prev)
+        if d_x:
+            L.kvl_mla_device_free(d_x)
+        if d_o:
+            L.kvl_mla_device_free(d_o)
+        for st in states:
+            L.kvl_mla_compressed_q8_state_free(C.byref(st))
+        L.kvl_mla_release_weights(C.byref(w))
